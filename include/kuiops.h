@@ -1,0 +1,236 @@
+/*
+ * kuiops.h -- C ABI of the MI355X (gfx950) kuiops hot path.
+ *
+ * Every entry point is a plain C function over device pointers, sizes and a
+ * HIP stream passed as `void *` (NULL = the legacy default stream).  Nothing
+ * here allocates device memory, synchronises the device or depends on torch:
+ * the caller owns every buffer (inputs, outputs and the optional workspace),
+ * and all work is enqueued asynchronously on the given stream, so every entry
+ * point may be recorded into a HIP graph.
+ *
+ * Return value: KUIOPS_OK (0) or a negative kuiops_status.  A negative status
+ * means nothing was enqueued.  KUIOPS_E_UNSUPPORTED means "shape/dtype outside
+ * what the kernels implement" (the caller falls back); KUIOPS_E_INVALID means
+ * inconsistent arguments (a bug in the caller).
+ *
+ * Reference interfaces replaced (panther03/kuiLLM):
+ *   - the per-instantiation host launchers `<Module>_<name>(uint32 dims...,
+ *     T* ptrs...)` that each pybind wrapper calls
+ *     (kuiops/mm/wrapper_mm.cu.j2:15-19, kuiops/addmm/wrapper_addmm.cu.j2:18-24,
+ *     kuiops/bmm/wrapper_bmm.cu.j2:16-20, kuiops/softmax/wrapper_softmax.cu.j2:14-16,
+ *     kuiops/sdpa/wrapper_sdpa.cu.j2:21-30, kuiops/gather/wrapper_gather.cu.j2:26-32);
+ *   - the libtorch glue of the reference's include/kuiops.h:11-36
+ *     (sync_current_stream / clone_in / index_to_u32), which has no counterpart
+ *     here because nothing is synchronised, cloned or narrowed.
+ */
+#ifndef KUIOPS_H_
+#define KUIOPS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KUIOPS_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define KUIOPS_API __attribute__((visibility("default")))
+#else
+#define KUIOPS_API
+#endif
+
+typedef enum kuiops_status {
+    KUIOPS_OK = 0,
+    KUIOPS_E_UNSUPPORTED = -1, /* outside the implemented shapes / dtypes   */
+    KUIOPS_E_INVALID = -2,     /* inconsistent or null arguments             */
+    KUIOPS_E_HIP = -3,         /* a HIP runtime call failed (launch error)   */
+    KUIOPS_E_WORKSPACE = -4    /* workspace missing or smaller than queried  */
+} kuiops_status;
+
+/* Element types.  Values are part of the ABI. */
+typedef enum kuiops_dtype {
+    KUIOPS_F32 = 0,
+    KUIOPS_F16 = 1,
+    KUIOPS_BF16 = 2,
+    KUIOPS_F64 = 3,
+    KUIOPS_I64 = 4,
+    KUIOPS_I32 = 5,
+    KUIOPS_I16 = 6,
+    KUIOPS_I8 = 7,
+    KUIOPS_U8 = 8,
+    KUIOPS_BOOL = 9
+} kuiops_dtype;
+
+/* Storage of the [K, N] right-hand operand B of a GEMM.
+ *   KUIOPS_B_ROW: element (k, n) at B[k * ldb + n]   (row-major [K, N])
+ *   KUIOPS_B_COL: element (k, n) at B[n * ldb + k]   (an nn.Linear weight
+ *                 [N, K] seen through .t(): K contiguous)                      */
+typedef enum kuiops_b_layout { KUIOPS_B_ROW = 0, KUIOPS_B_COL = 1 } kuiops_b_layout;
+
+/* Addend of addmm.
+ *   KUIOPS_C_NONE : out = alpha * A@B
+ *   KUIOPS_C_FULL : out = beta * Cin[M, N] + alpha * A@B   (Cin row stride ldcin)
+ *   KUIOPS_C_ROW  : out = beta * bias[N]   + alpha * A@B   (bias broadcast over rows) */
+typedef enum kuiops_c_kind { KUIOPS_C_NONE = 0, KUIOPS_C_FULL = 1, KUIOPS_C_ROW = 2 } kuiops_c_kind;
+
+/* Operation ids for kuiops_query_workspace. */
+typedef enum kuiops_op {
+    KUIOPS_OP_ADDMM = 1,
+    KUIOPS_OP_GEMV_SPLITK = 2,
+    KUIOPS_OP_SDPA_DECODE = 3,
+    KUIOPS_OP_TOPK = 4
+} kuiops_op;
+
+KUIOPS_API int kuiops_abi_version(void);
+KUIOPS_API const char *kuiops_status_string(int status);
+
+/* Bytes of workspace the given call needs (0 = none).  Arguments are the
+ * leading size arguments of that op:
+ *   ADDMM:        a = M, b = N, c = K
+ *   GEMV_SPLITK:  a = M, b = N, c = K
+ *   SDPA_DECODE:  a = batch * q_heads * q_len, b = kv_len, c = head_dim_v
+ *   TOPK:         a = rows, b = row length, c = k
+ * A workspace must be zero-filled once when it is allocated; every kernel
+ * that uses counters in it leaves them at zero again when it completes.
+ * Calls that share one workspace must be ordered on one stream.            */
+KUIOPS_API size_t kuiops_query_workspace(int op, int64_t a, int64_t b, int64_t c);
+
+/* ---------------------------------------------------------------- GEMM --
+ * C[M, N] = A[M, K] @ B[K, N]
+ * Replaces the mm launcher `(M, N, K, A, B, C)` of
+ * kuiops/mm/wrapper_mm.cu.j2:15-19 (family gate kuipy/kuiops.py:403-469).
+ * in_dtype: BF16, F16 or F32 (A and B share it).  out_dtype: same as
+ * in_dtype, or F32 for half inputs.  Accumulation is fp32 (fp64 for F64).
+ * A is row-major with row stride lda; B per b_layout; C row stride ldc.    */
+KUIOPS_API int kuiops_mm(int64_t M, int64_t N, int64_t K, int in_dtype,
+              const void *A, int64_t lda,
+              const void *B, int64_t ldb, int b_layout,
+              int out_dtype, void *C, int64_t ldc, void *stream);
+
+/* out[M, N] = beta * Cin + alpha * (A @ B), see kuiops_c_kind.
+ * Replaces the addmm launcher `(M, K, N, alpha, beta, A, B, C)` of
+ * kuiops/addmm/wrapper_addmm.cu.j2:18-24 (gate kuipy/kuiops.py:526-564),
+ * extended with the 1-D bias form the reference rejects
+ * (kuipy/kuiops.py:540, tests/test_jit_ops.py:82).
+ * splits: K-splits (0 = choose).  With splits > 1 fp32 partial tiles go to
+ * the workspace and are summed in split order 0..splits-1 (deterministic).
+ * `out` may alias Cin (in-place update, as the reference's wrapper does on a
+ * clone).                                                                  */
+KUIOPS_API int kuiops_addmm(int64_t M, int64_t K, int64_t N, double alpha, double beta,
+                 int in_dtype,
+                 const void *A, int64_t lda,
+                 const void *B, int64_t ldb, int b_layout,
+                 const void *Cin, int c_kind, int64_t ldcin,
+                 int out_dtype, void *out, int64_t ldo,
+                 int splits, void *workspace, size_t workspace_bytes,
+                 void *stream);
+
+/* C[b] = A[b] @ B[b] for b < batch (output overwritten, as comb2 in
+ * kuiops/bmm/Kuiops.Bmm.fst:10-23).  Replaces the bmm launcher
+ * `(Bn, M, K, N, A, B, C)` of kuiops/bmm/wrapper_bmm.cu.j2:16-20
+ * (gate kuipy/kuiops.py:481-511).  Batch strides in elements.             */
+KUIOPS_API int kuiops_bmm(int64_t batch, int64_t M, int64_t K, int64_t N, int in_dtype,
+               const void *A, int64_t stride_a, int64_t lda,
+               const void *B, int64_t stride_b, int64_t ldb, int b_layout,
+               int out_dtype, void *C, int64_t stride_c, int64_t ldc,
+               void *stream);
+
+/* Skinny (decode) GEMM: out[M, N] = x[M, K] @ W[K, N] (+ bias[N]) for
+ * 1 <= M <= 64, bf16/f16 in, fp32 accumulate, out_dtype = in or F32.
+ * K is split over `splits` work-groups (0 = choose); partials are summed in
+ * a fixed order by the last work-group of each column strip, so the result
+ * is bitwise repeatable.  Requires the workspace of
+ * kuiops_query_workspace(KUIOPS_OP_GEMV_SPLITK, M, N, K).  Serves the
+ * reference's mm/addmm families at decode shapes, which its gate rejects
+ * (`M % 64`, kuipy/kuiops.py:372-374).                                    */
+KUIOPS_API int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
+                       const void *x, int64_t ldx,
+                       const void *W, int64_t ldw, int w_layout,
+                       const void *bias,
+                       int out_dtype, void *out, int64_t ldo,
+                       int splits, void *workspace, size_t workspace_bytes,
+                       void *stream);
+
+/* ---------------------------------------------------------------- SDPA --
+ * Flash-attention forward: O = softmax(scale * Q K^T [+ causal mask]) V,
+ * LSE = logsumexp over keys (natural log, fp32, optional: pass NULL).
+ * Q (n, hq, l, e), K (n, hkv, s, e), V (n, hkv, s, ev); hq % hkv == 0
+ * (grouped-query heads share KV head h / (hq / hkv)).  Every tensor has a
+ * contiguous last dim; strides (in elements) are given for dims 0..2 as
+ * {batch, head, seq}.  O (n, hq, l, ev) with strides so[3]; LSE contiguous
+ * (n, hq, l).  Causal masking follows aten: query i sees keys j <= i (top
+ * left aligned; rows with no visible key output 0 and LSE = -inf).
+ * dtype BF16 or F16; e == ev, e in {64, 128}.
+ * Replaces the SDPA launcher of kuiops/sdpa/wrapper_sdpa.cu.j2:21-30
+ * (family kuipy/kuiops.py:627-681), which rejects is_causal.              */
+KUIOPS_API int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s,
+                    int64_t e, int64_t ev, int dtype,
+                    const void *Q, const int64_t sq[3],
+                    const void *K, const int64_t sk[3],
+                    const void *V, const int64_t sv[3],
+                    void *O, const int64_t so[3],
+                    float *lse, float scale, int causal, void *stream);
+
+/* Decode attention (l small, typically 1) over a KV cache, split over the
+ * key axis; same tensor conventions as kuiops_sdpa_fwd.  Causal masking with
+ * l > 1 aligns the queries to the END of the keys (query i sees keys
+ * j <= s - l + i), which is what a KV-cache decode step needs; pass
+ * causal = 0 for plain full attention.  Requires the workspace of
+ * kuiops_query_workspace(KUIOPS_OP_SDPA_DECODE, n*hq*l, s, ev).            */
+KUIOPS_API int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s,
+                       int64_t e, int64_t ev, int dtype,
+                       const void *Q, const int64_t sq[3],
+                       const void *K, const int64_t sk[3],
+                       const void *V, const int64_t sv[3],
+                       void *O, const int64_t so[3],
+                       float *lse, float scale, int causal,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------- sampling tail --
+ * Row softmax over the last dim of a contiguous [m, n] tensor:
+ * Y = exp(X - max) / sum.  in/out dtype F32, BF16, F16 or F64; X and Y may
+ * alias (the reference softmaxes a clone in place,
+ * kuiops/softmax/wrapper_softmax.cu.j2:8-18, kuipy/kuiops.py:607-610).     */
+KUIOPS_API int kuiops_softmax_lastdim(int64_t m, int64_t n, int dtype,
+                           const void *X, void *Y, void *stream);
+
+/* Top-k along the last dim of a contiguous [m, n] tensor (aten.topk with
+ * dim = -1).  values [m, k] (dtype of X), indices [m, k] int64.
+ * Ordering: largest (or smallest) first; NaN counts as larger than every
+ * number; equal values are ordered by ascending index, and a tie at the
+ * k-th place keeps the lowest indices.  `sorted` = 0 is accepted and also
+ * returns sorted output.  1 <= k <= min(n, 1024).  dtype F32, BF16, F16.
+ * No reference kernel exists (kuiops/topk/.gitkeep); aten.topk is the
+ * reference's result.                                                      */
+KUIOPS_API int kuiops_topk_lastdim(int64_t m, int64_t n, int64_t k, int dtype,
+                        const void *X, void *values, int64_t *indices,
+                        int largest, int sorted,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* out[x] = inp[x with axis `dim` replaced by idx[x]]  (torch.gather).
+ * Contiguous row-major tensors of rank 1..8; idx int64 with idx_shape
+ * pointwise <= inp_shape except along `dim`; elem_bytes 1, 2, 4 or 8.
+ * Negative or out-of-range indices write 0 and set *err_flag (device int,
+ * optional) to 1.  Replaces kuiops/gather/wrapper_gather.cu.j2:26-32 and
+ * the int64 -> u32 narrowing copy of the reference's include/kuiops.h:28-36
+ * (indices are read as int64 directly).                                    */
+KUIOPS_API int kuiops_gather(int rank, const int64_t *inp_shape, const int64_t *idx_shape,
+                  int dim, int elem_bytes, const void *inp, const int64_t *idx,
+                  void *out, int *err_flag, void *stream);
+
+/* aten.index.Tensor with one int64 index tensor at axis `dim` (every other
+ * axis sliced whole): out shape = inp[:dim] + idx_shape + inp[dim+1:], all
+ * contiguous.  Negative indices count from the end as in aten; indices out
+ * of range write 0 and set *err_flag.  inp is given as (outer, size, inner)
+ * = (prod inp[:dim], inp[dim], prod inp[dim+1:]).  No reference kernel
+ * exists (kuiops/index/.gitkeep).                                          */
+KUIOPS_API int kuiops_index(int64_t outer, int64_t size, int64_t inner, int64_t n_idx,
+                 int elem_bytes, const void *inp, const int64_t *idx,
+                 void *out, int *err_flag, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KUIOPS_H_ */

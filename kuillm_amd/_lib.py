@@ -1,0 +1,131 @@
+"""ctypes binding of ``libkuiops.so`` -- the C ABI declared in include/kuiops.h.
+
+This module is the only place that talks to the native library.  It loads the
+in-tree ``kuillm_amd/libkuiops.so`` (built by ``kuillm_amd.compile``), declares
+every entry point's argument types, and turns a negative status into a Python
+exception.  It never falls back to anything: if the library is missing or a
+call fails, the caller sees an error.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(os.environ.get("KUIOPS_LIB", Path(__file__).resolve().parent / "libkuiops.so"))
+
+# kuiops_status
+OK = 0
+E_UNSUPPORTED = -1
+E_INVALID = -2
+E_HIP = -3
+E_WORKSPACE = -4
+
+# kuiops_dtype
+F32, F16, BF16, F64, I64, I32, I16, I8, U8, BOOL = range(10)
+# kuiops_b_layout
+B_ROW, B_COL = 0, 1
+# kuiops_c_kind
+C_NONE, C_FULL, C_ROW = 0, 1, 2
+# kuiops_op
+OP_ADDMM, OP_GEMV_SPLITK, OP_SDPA_DECODE, OP_TOPK = 1, 2, 3, 4
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_dbl = ctypes.c_double
+_flt = ctypes.c_float
+_sz = ctypes.c_size_t
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes); mirrors include/kuiops.h one to one.
+SIGNATURES = {
+    "kuiops_abi_version": (_int, []),
+    "kuiops_status_string": (ctypes.c_char_p, [_int]),
+    "kuiops_query_workspace": (_sz, [_int, _i64, _i64, _i64]),
+    "kuiops_mm": (_int, [_i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _int, _int, _vp, _i64, _vp]),
+    "kuiops_addmm": (_int, [_i64, _i64, _i64, _dbl, _dbl, _int, _vp, _i64, _vp, _i64, _int,
+                            _vp, _int, _i64, _int, _vp, _i64, _int, _vp, _sz, _vp]),
+    "kuiops_bmm": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _vp, _i64, _i64, _int,
+                          _int, _vp, _i64, _i64, _vp]),
+    "kuiops_gemv_splitk": (_int, [_i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _int, _vp, _int,
+                                  _vp, _i64, _int, _vp, _sz, _vp]),
+    "kuiops_sdpa_fwd": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
+                               _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp]),
+    "kuiops_sdpa_decode": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
+                                  _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp, _sz, _vp]),
+    "kuiops_softmax_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp]),
+    "kuiops_topk_lastdim": (_int, [_i64, _i64, _i64, _int, _vp, _vp, _vp, _int, _int, _vp, _sz, _vp]),
+    "kuiops_gather": (_int, [_int, _i64p, _i64p, _int, _int, _vp, _vp, _vp, _vp, _vp]),
+    "kuiops_index": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
+}
+
+
+class KuiopsError(RuntimeError):
+    """A kuiops entry point returned a negative status."""
+
+    def __init__(self, name, status):
+        self.status = status
+        super().__init__(f"{name} failed: {status_string(status)} ({status})")
+
+
+class Unsupported(KuiopsError):
+    """KUIOPS_E_UNSUPPORTED: the shape / dtype is outside the kernels."""
+
+
+_lib = None
+
+
+def load(path: Path | str | None = None):
+    """Load (once) and return the ctypes library.  Raises if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"kuiops native library not built: {p} is missing "
+                           "(run `python -c 'import __graft_entry__ as g; g.build()'` "
+                           "or `make -C kuillm_amd/csrc`)")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.kuiops_abi_version() != 1:
+        raise RuntimeError("libkuiops ABI version mismatch")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def loaded() -> bool:
+    return _lib is not None
+
+
+def status_string(status: int) -> str:
+    try:
+        return load().kuiops_status_string(status).decode()
+    except Exception:
+        return str(status)
+
+
+def check(name: str, status: int) -> None:
+    if status == OK:
+        return
+    if status == E_UNSUPPORTED:
+        raise Unsupported(name, status)
+    raise KuiopsError(name, status)
+
+
+def call(name: str, *args) -> None:
+    """Call entry point ``name`` and raise on a negative status."""
+    check(name, getattr(load(), name)(*args))
+
+
+def strides3(*vals) -> ctypes.Array:
+    return (ctypes.c_int64 * 3)(*[int(v) for v in vals])
+
+
+def i64_array(vals) -> ctypes.Array:
+    vals = [int(v) for v in vals]
+    return (ctypes.c_int64 * max(1, len(vals)))(*vals)

@@ -1,0 +1,598 @@
+// Scaled dot-product attention for gfx950.
+//
+// fa_fwd_kernel -- flash-attention forward (prefill), bf16/f16, head dim 64/128.
+//   A work-group owns 128 queries of one (batch, head) and walks the keys in
+//   blocks of 64 staged through LDS (two stages, register prefetch).  Each of
+//   the 4 waves owns 32 queries and computes the TRANSPOSED score tile
+//   S^T = K Q^T with 32x32x16 MFMAs, so a lane holds 32 scores of a single
+//   query: the row max / row sum of the online softmax are in-lane reductions
+//   plus one cross-half swap (lane ^ 32).  The output is accumulated
+//   transposed as well, O^T += V^T P^T, with P^T taken straight from the
+//   score registers.  MFMA sums over K in any order, so the keys of one
+//   16-key step are numbered in the order the score accumulator holds them;
+//   V is transposed into LDS in that same order ([d][key], 4-key groups
+//   permuted 0,2,1,3 inside each 16) and one ds_read_b128 yields an operand.
+//   Softmax runs in the log2 domain (exp2 on the hardware exp unit) in fp32.
+//   Causal work-groups are dispatched heaviest-first and fully masked waves
+//   skip their MFMAs; all q-blocks of one head are mapped to one XCD so its
+//   K / V stay in that XCD's L2.
+//
+// fa_decode_kernel + fa_decode_combine_kernel -- decode (few queries per head)
+//   over a long KV cache: HBM-bound, so the keys are split over work-groups
+//   (split-KV); each work-group streams its key range once for all query rows
+//   that share the KV head (grouped-query attention), keeps fp32 online-softmax
+//   state per row, and writes (max, sum, unnormalised output) to the
+//   workspace.  The combine kernel merges the splits in split order.
+//
+// Semantics: aten scaled_dot_product_attention (the reference's fallthrough,
+// kuipy/kuiops.py:627-681 rejects is_causal; tests/test_jit_ops.py:173-193).
+#include "common.hpp"
+
+namespace kuiops {
+
+struct AttnArgs {
+    int64_t n, hq, hkv, l, s;
+    const void *Q, *K, *V;
+    void *O;
+    int64_t sq0, sq1, sq2, sk0, sk1, sk2, sv0, sv1, sv2, so0, so1, so2;
+    float *lse;
+    float scale_log2;   // softmax scale * log2(e)
+    int causal;
+    int nqb;            // query blocks per (batch, head)
+    // decode
+    int splits;
+    int64_t chunk;      // keys per split
+    int rows_per_group; // query rows handled by one work-group
+    int row_groups;
+    float *ws_ml;       // [rows_total][splits][2]
+    float *ws_o;        // [rows_total][splits][ev]
+};
+
+constexpr float kLn2 = 0.69314718055994530942f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ int swz8(int row) { return (row ^ (row >> 3)) & 7; }
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const float *v) {
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    t8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = from_f32<T>(v[i]);
+    return __builtin_bit_cast(u32x4, r);
+}
+
+template <typename T, int HD, bool CAUSAL>
+__global__ __launch_bounds__(256) void fa_fwd_kernel(AttnArgs a) {
+    constexpr int BQ = 128, BKV = 64, NCH = HD / 8;
+    constexpr int KCH = BKV * NCH / 256;            // K chunks per thread
+    constexpr int VBLK = (BKV / 4) * (HD / 8);      // 4x8 V blocks per tile
+    constexpr int VPT = (VBLK + 255) / 256;         // V blocks per thread
+    constexpr int DT = HD / 32;                     // 32-row d tiles of O^T
+    typedef typename Mfma<T>::frag frag;
+
+    __shared__ __attribute__((aligned(16))) T sK[2][BKV * HD];
+    __shared__ __attribute__((aligned(16))) T sV[2][HD * BKV];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lq = lane & 31, lh = lane >> 5;
+
+    // Work-group -> (batch*head, q-block): ids dispatched to one XCD form a
+    // contiguous range, which covers whole heads.
+    const int nblocks = gridDim.x, bid = blockIdx.x;
+    int w = bid;
+    if ((nblocks & 7) == 0) w = (bid & 7) * (nblocks >> 3) + (bid >> 3);
+    const int hb = w / a.nqb;
+    int qb = w - hb * a.nqb;
+    if (CAUSAL) qb = a.nqb - 1 - qb;
+    const int64_t b = hb / a.hq, h = hb - b * a.hq;
+    const int64_t hk = h / (a.hq / a.hkv);
+
+    const T *Qp = reinterpret_cast<const T *>(a.Q) + b * a.sq0 + h * a.sq1;
+    const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
+    const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
+
+    const int64_t q0 = (int64_t)qb * BQ;
+    const int64_t qw = q0 + wave * 32;
+    const int64_t myq = qw + lq;
+
+    frag qf[HD / 16];
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk) {
+        const int ch = 2 * kk + lh;
+        qf[kk] = as_frag<frag>(myq < a.l ? *reinterpret_cast<const u32x4 *>(Qp + myq * a.sq2 + ch * 8)
+                                         : u32x4{0, 0, 0, 0});
+    }
+
+    int64_t kv_end = a.s;
+    if (CAUSAL) kv_end = min(a.s, q0 + BQ);
+    const int nkv = (int)((kv_end + BKV - 1) / BKV);
+
+    u32x4 rk[KCH];
+    u32x4 rv[VPT * 4];
+    auto load_kv = [&](int64_t kv0) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + i * 256, r = c / NCH, ch = c % NCH;
+            const int64_t key = kv0 + r;
+            rk[i] = key < a.s ? *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + ch * 8) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int c = tid + i * 256;
+            const int sg = c % 16, dc = c / 16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t key = kv0 + sg * 4 + r;
+                rv[i * 4 + r] = (c < VBLK && key < a.s)
+                                    ? *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dc * 8)
+                                    : u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    auto store_kv = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = tid + i * 256, r = c / NCH, ch = c % NCH;
+            *reinterpret_cast<u32x4 *>(&sK[buf][r * HD + ((ch ^ (r & 7)) << 3)]) = rk[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int c = tid + i * 256;
+            if (c >= VBLK) continue;
+            const int sg = c % 16, dc = c / 16;
+            const int qd = sg & 3;
+            const int p0 = 16 * (sg >> 2) + 4 * ((qd == 1) ? 2 : (qd == 2) ? 1 : qd);
+            u32x2 t[8];
+            transpose4x8_b16(&rv[i * 4], t);
+#pragma unroll
+            for (int cc = 0; cc < 8; ++cc) {
+                const int d = dc * 8 + cc;
+                *reinterpret_cast<u32x2 *>(&sV[buf][d * BKV + (((p0 >> 3) ^ swz8(d)) << 3) + (p0 & 7)]) = t[cc];
+            }
+        }
+    };
+
+    f32x16 o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    if (nkv > 0) {
+        load_kv(0);
+        store_kv(0);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nkv; ++kt) {
+        const int buf = kt & 1;
+        const int64_t kv0 = (int64_t)kt * BKV;
+        if (kt + 1 < nkv) load_kv(kv0 + BKV);
+        const bool active = !(CAUSAL && kv0 > qw + 31) && qw < a.l;
+        if (active) {
+            const T *pk = sK[buf];
+            const T *pv = sV[buf];
+            f32x16 sc[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) sc[t][e] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < HD / 16; ++kk) {
+                const int ch = 2 * kk + lh;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int r = t * 32 + lq;
+                    const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4 *>(&pk[r * HD + ((ch ^ (r & 7)) << 3)]));
+                    sc[t] = Mfma<T>::m32(kf, qf[kk], sc[t]);
+                }
+            }
+            // Scale, mask, block max.  sc[t][e]: key kv0 + 32t + 8(e/4) + 4*lh + e%4, query myq.
+            const bool need_mask = (kv0 + BKV > a.s) || (CAUSAL && kv0 + BKV - 1 > qw);
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    float v = sc[t][e] * a.scale_log2;
+                    if (need_mask) {
+                        const int64_t key = kv0 + t * 32 + (e >> 2) * 8 + lh * 4 + (e & 3);
+                        if (key >= a.s || (CAUSAL && key > myq)) v = -INFINITY;
+                    }
+                    sc[t][e] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m_run, mx);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = fast_exp2(m_run - m_use);
+            float rs = 0.f;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float p = fast_exp2(sc[t][e] - m_use);
+                    sc[t][e] = p;
+                    rs += p;
+                }
+            l_run = l_run * alpha + rs;
+            m_run = m_new;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+            // O^T += V^T P^T over 4 steps of 16 keys.
+#pragma unroll
+            for (int b16 = 0; b16 < 4; ++b16) {
+                const int t = b16 >> 1, u = b16 & 1;
+                float pv8[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pv8[i] = sc[t][8 * u + i];
+                const frag pf = as_frag<frag>(pack8<T>(pv8));
+                const int ch = 2 * b16 + lh;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int d = dt * 32 + lq;
+                    const frag vf = as_frag<frag>(*reinterpret_cast<const u32x4 *>(&pv[d * BKV + ((ch ^ swz8(d)) << 3)]));
+                    o[dt] = Mfma<T>::m32(vf, pf, o[dt]);
+                }
+            }
+        }
+        if (kt + 1 < nkv) store_kv(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (myq < a.l) {
+        T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + h * a.so1 + myq * a.so2;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = dt * 32 + j * 8 + lh * 4;
+                typedef T t4 __attribute__((ext_vector_type(4)));
+                t4 v;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = from_f32<T>(o[dt][4 * j + i] * inv);
+                *reinterpret_cast<t4 *>(Op + d) = v;
+            }
+        if (a.lse && lh == 0)
+            a.lse[(b * a.hq + h) * a.l + myq] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+    }
+}
+
+// ------------------------------------------------------------------ decode
+
+// Merges online-softmax state (m2, l2, o2) into (m1, l1, o1).
+template <int ND>
+__device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, float m2, float l2, const float *o2) {
+    const float M = fmaxf(m1, m2);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    const float a1 = fast_exp2(m1 - Mu), a2 = fast_exp2(m2 - Mu);
+    l1 = l1 * a1 + l2 * a2;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) o1[d] = o1[d] * a1 + o2[d] * a2;
+    m1 = M;
+}
+
+template <typename T, int HD, int R>
+__global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
+    constexpr int LPK = HD / 8;       // lanes per key (8 d values each)
+    constexpr int KPW = 64 / LPK;     // keys per wave step
+    constexpr int NB = 4;             // keys per lane group per step
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kg = lane / LPK, dl = lane % LPK;
+    const int split = blockIdx.x;
+    const int hk = blockIdx.y / a.row_groups, rg = blockIdx.y % a.row_groups;
+    const int64_t b = blockIdx.z;
+    const int G = (int)(a.hq / a.hkv);
+    const int rows_kv = G * (int)a.l;            // query rows sharing this KV head
+    const int r0 = rg * a.rows_per_group;
+
+    const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
+    const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
+    const int64_t kbeg = (int64_t)split * a.chunk;
+    const int64_t kend = min(a.s, kbeg + a.chunk);
+
+    // Query rows: row r -> head hk*G + (r / l), query index r % l.
+    float q[R][8];
+    int64_t last_key[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int rr = r0 + r;
+        const bool ok = rr < rows_kv && r < a.rows_per_group;
+        const int64_t head = hk * G + (ok ? rr / a.l : 0);
+        const int64_t qi = ok ? rr % a.l : 0;
+        const T *Qp = reinterpret_cast<const T *>(a.Q) + b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8;
+        u32x4 raw = ok ? *reinterpret_cast<const u32x4 *>(Qp) : u32x4{0, 0, 0, 0};
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        t8 qv = __builtin_bit_cast(t8, raw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[r][e] = to_f32(qv[e]) * a.scale_log2;
+        // keys visible to this row (exclusive bound)
+        last_key[r] = ok ? (a.causal ? a.s - a.l + qi + 1 : a.s) : 0;
+    }
+
+    float m[R], lsum[R], o[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m[r] = -INFINITY;
+        lsum[r] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[r][e] = 0.f;
+    }
+
+    for (int64_t kb = kbeg + (int64_t)wave * KPW * NB; kb < kend; kb += 4 * KPW * NB) {
+        float s[R][NB];
+        u32x4 kr[NB], vr[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int64_t key = kb + j * KPW + kg;
+            const bool ok = key < kend;
+            kr[j] = ok ? *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + dl * 8) : u32x4{0, 0, 0, 0};
+            vr[j] = ok ? *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dl * 8) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            typedef T t8 __attribute__((ext_vector_type(8)));
+            t8 kv = __builtin_bit_cast(t8, kr[j]);
+            float kf[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kf[e] = to_f32(kv[e]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d += q[r][e] * kf[e];
+#pragma unroll
+                for (int off = 1; off < LPK; off <<= 1) d += __shfl_xor(d, off, 64);
+                s[r][j] = d;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float mb = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int64_t key = kb + j * KPW + kg;
+                if (key >= kend || key >= last_key[r]) s[r][j] = -INFINITY;
+                mb = fmaxf(mb, s[r][j]);
+            }
+            const float m_new = fmaxf(m[r], mb);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = fast_exp2(m[r] - m_use);
+            float p[NB], ps = 0.f;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                p[j] = fast_exp2(s[r][j] - m_use);
+                ps += p[j];
+            }
+            lsum[r] = lsum[r] * alpha + ps;
+            m[r] = m_new;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[r][e] *= alpha;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                typedef T t8 __attribute__((ext_vector_type(8)));
+                t8 vv = __builtin_bit_cast(t8, vr[j]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[r][e] += p[j] * to_f32(vv[e]);
+            }
+        }
+    }
+
+    // Merge the KPW key slots of the wave (lanes with equal dl), fixed butterfly order.
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float m2 = __shfl_xor(m[r], off, 64);
+            const float l2 = __shfl_xor(lsum[r], off, 64);
+            float o2[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o2[e] = __shfl_xor(o[r][e], off, 64);
+            // Order the operands by lane so both partners compute the same value.
+            if (lane & off) {
+                float mm = m2, ll = l2, oo[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) oo[e] = o2[e];
+                merge_state<8>(mm, ll, oo, m[r], lsum[r], o[r]);
+                m[r] = mm; lsum[r] = ll;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[r][e] = oo[e];
+            } else {
+                merge_state<8>(m[r], lsum[r], o[r], m2, l2, o2);
+            }
+        }
+    }
+
+    // Merge the 4 waves in wave order through LDS, then write the split's state.
+    __shared__ float sm[4][R], sl[4][R], so[4][R][HD];
+    if (kg == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (dl == 0) { sm[wave][r] = m[r]; sl[wave][r] = lsum[r]; }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) so[wave][r][dl * 8 + e] = o[r][e];
+        }
+    }
+    __syncthreads();
+    const int nrows = min(a.rows_per_group, rows_kv - r0);
+    for (int idx = tid; idx < R * HD; idx += 256) {
+        const int r = idx / HD, d = idx % HD;
+        if (r >= nrows) continue;
+        float mm = sm[0][r], ll = sl[0][r], oo = so[0][r][d];
+#pragma unroll
+        for (int wv = 1; wv < 4; ++wv) merge_state<1>(mm, ll, &oo, sm[wv][r], sl[wv][r], &so[wv][r][d]);
+        const int rr = r0 + r;
+        const int64_t head = hk * G + rr / a.l, qi = rr % a.l;
+        const int64_t grow = (b * a.hq + head) * a.l + qi;
+        a.ws_o[(grow * a.splits + split) * HD + d] = oo;
+        if (d == 0) {
+            a.ws_ml[(grow * a.splits + split) * 2 + 0] = mm;
+            a.ws_ml[(grow * a.splits + split) * 2 + 1] = ll;
+        }
+    }
+}
+
+// One wave per query row: merge the split states in split order.
+template <typename T, int HD>
+__global__ __launch_bounds__(64) void fa_decode_combine_kernel(AttnArgs a) {
+    const int64_t grow = blockIdx.x;            // (b * hq + head) * l + qi
+    const int lane = threadIdx.x;
+    const int64_t qi = grow % a.l, bh = grow / a.l;
+    const int64_t head = bh % a.hq, b = bh / a.hq;
+    float M = -INFINITY;
+    for (int z = 0; z < a.splits; ++z) M = fmaxf(M, a.ws_ml[(grow * a.splits + z) * 2]);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    constexpr int PER = HD / 64;
+    float acc[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) acc[i] = 0.f;
+    float L = 0.f;
+    for (int z = 0; z < a.splits; ++z) {
+        const float w = fast_exp2(a.ws_ml[(grow * a.splits + z) * 2] - Mu);
+        L += w * a.ws_ml[(grow * a.splits + z) * 2 + 1];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) acc[i] += w * a.ws_o[(grow * a.splits + z) * HD + lane + 64 * i];
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) Op[lane + 64 * i] = from_f32<T>(acc[i] * inv);
+    if (a.lse && lane == 0) a.lse[grow] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+}
+
+// ------------------------------------------------------------ host side
+
+static bool attn_common_ok(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, int64_t e, int64_t ev,
+                           int dtype, const void *Q, const int64_t *sq, const void *K, const int64_t *sk,
+                           const void *V, const int64_t *sv, void *O, const int64_t *so, int &status) {
+    status = KUIOPS_OK;
+    if (n < 0 || hq < 0 || hkv < 0 || l < 0 || s < 0 || e <= 0 || ev <= 0 || !sq || !sk || !sv || !so) {
+        status = KUIOPS_E_INVALID;
+        return false;
+    }
+    if (hkv == 0 || hq % hkv) { status = KUIOPS_E_INVALID; return false; }
+    if (!Q || !K || !V || !O) { status = KUIOPS_E_INVALID; return false; }
+    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) { status = KUIOPS_E_UNSUPPORTED; return false; }
+    if (e != ev || (e != 64 && e != 128)) { status = KUIOPS_E_UNSUPPORTED; return false; }
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) { status = KUIOPS_E_UNSUPPORTED; return false; }
+    for (int i = 0; i < 3; ++i)
+        if (sq[i] % 8 || sk[i] % 8 || sv[i] % 8 || so[i] % 4) { status = KUIOPS_E_UNSUPPORTED; return false; }
+    return true;
+}
+
+static void fill_args(AttnArgs &a, int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, const void *Q,
+                      const int64_t *sq, const void *K, const int64_t *sk, const void *V, const int64_t *sv,
+                      void *O, const int64_t *so, float *lse, float scale, int causal) {
+    a.n = n; a.hq = hq; a.hkv = hkv; a.l = l; a.s = s;
+    a.Q = Q; a.K = K; a.V = V; a.O = O;
+    a.sq0 = sq[0]; a.sq1 = sq[1]; a.sq2 = sq[2];
+    a.sk0 = sk[0]; a.sk1 = sk[1]; a.sk2 = sk[2];
+    a.sv0 = sv[0]; a.sv1 = sv[1]; a.sv2 = sv[2];
+    a.so0 = so[0]; a.so1 = so[1]; a.so2 = so[2];
+    a.lse = lse;
+    a.scale_log2 = scale * 1.44269504088896340736f;
+    a.causal = causal;
+}
+
+// Keys per split for the decode kernel: enough splits to fill the GPU, at
+// least 64 keys each.
+static int64_t decode_chunk(int64_t s) {
+    int64_t c = cdiv(cdiv(s, 32), 64) * 64;
+    return c < 64 ? 64 : c;
+}
+
+size_t decode_workspace_bytes(int64_t rows, int64_t kv_len, int64_t ev) {
+    const int64_t splits = cdiv(kv_len > 0 ? kv_len : 1, decode_chunk(kv_len));
+    return (size_t)rows * splits * (ev + 2) * sizeof(float) + 256;
+}
+
+template <typename T, int HD>
+static int launch_fwd(AttnArgs a, hipStream_t st) {
+    a.nqb = (int)cdiv(a.l, 128);
+    const int64_t blocks = (int64_t)a.nqb * a.n * a.hq;
+    if (blocks > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    return launch_status();
+}
+
+template <typename T, int HD>
+static int launch_decode(AttnArgs a, hipStream_t st) {
+    const int G = (int)(a.hq / a.hkv);
+    const int rows_kv = G * (int)a.l;
+    int R;
+    if (rows_kv <= 1) R = 1;
+    else if (rows_kv <= 2) R = 2;
+    else if (rows_kv <= 4) R = 4;
+    else R = 8;
+    a.rows_per_group = R;
+    a.row_groups = (int)cdiv(rows_kv, R);
+    dim3 grid((unsigned)a.splits, (unsigned)(a.hkv * a.row_groups), (unsigned)a.n);
+    switch (R) {
+        case 1: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 2>), grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 4>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 8>), grid, dim3(256), 0, st, a); break;
+    }
+    hipLaunchKernelGGL((fa_decode_combine_kernel<T, HD>), dim3((unsigned)(a.n * a.hq * a.l)), dim3(64), 0, st, a);
+    return launch_status();
+}
+
+}  // namespace kuiops
+
+using namespace kuiops;
+
+extern "C" int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, int64_t e, int64_t ev,
+                               int dtype, const void *Q, const int64_t sq[3], const void *K, const int64_t sk[3],
+                               const void *V, const int64_t sv[3], void *O, const int64_t so[3], float *lse,
+                               float scale, int causal, void *stream) {
+    int status;
+    if (!attn_common_ok(n, hq, hkv, l, s, e, ev, dtype, Q, sq, K, sk, V, sv, O, so, status)) {
+        if (status == KUIOPS_E_INVALID || n * hq * l != 0) return status;
+    }
+    if (n == 0 || hq == 0 || l == 0) return KUIOPS_OK;
+    if (hq > 65535 || n > 65535) return KUIOPS_E_UNSUPPORTED;
+    AttnArgs a{};
+    fill_args(a, n, hq, hkv, l, s, Q, sq, K, sk, V, sv, O, so, lse, scale, causal);
+    hipStream_t st = as_stream(stream);
+    if (dtype == KUIOPS_BF16) return e == 128 ? launch_fwd<bf16_t, 128>(a, st) : launch_fwd<bf16_t, 64>(a, st);
+    return e == 128 ? launch_fwd<f16_t, 128>(a, st) : launch_fwd<f16_t, 64>(a, st);
+}
+
+extern "C" int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, int64_t e,
+                                  int64_t ev, int dtype, const void *Q, const int64_t sq[3], const void *K,
+                                  const int64_t sk[3], const void *V, const int64_t sv[3], void *O,
+                                  const int64_t so[3], float *lse, float scale, int causal, void *workspace,
+                                  size_t workspace_bytes, void *stream) {
+    int status;
+    if (!attn_common_ok(n, hq, hkv, l, s, e, ev, dtype, Q, sq, K, sk, V, sv, O, so, status)) {
+        if (status == KUIOPS_E_INVALID || n * hq * l != 0) return status;
+    }
+    if (n == 0 || hq == 0 || l == 0) return KUIOPS_OK;
+    if (causal && l > s) return KUIOPS_E_UNSUPPORTED;
+    if (n > 65535 || hkv * cdiv((hq / hkv) * l, 8) > 65535) return KUIOPS_E_UNSUPPORTED;
+    AttnArgs a{};
+    fill_args(a, n, hq, hkv, l, s, Q, sq, K, sk, V, sv, O, so, lse, scale, causal);
+    const int64_t ss = s > 0 ? s : 1;
+    a.chunk = decode_chunk(ss);
+    a.splits = (int)cdiv(ss, a.chunk);
+    const int64_t rows = n * hq * l;
+    const size_t need = decode_workspace_bytes(rows, s, ev);
+    if (!workspace || workspace_bytes < need) return KUIOPS_E_WORKSPACE;
+    a.ws_ml = reinterpret_cast<float *>(workspace);
+    a.ws_o = a.ws_ml + rows * a.splits * 2;
+    if ((reinterpret_cast<uintptr_t>(a.ws_o) & 15) != 0) {
+        // keep o rows 16-byte aligned
+        a.ws_o = reinterpret_cast<float *>((reinterpret_cast<uintptr_t>(a.ws_o) + 15) & ~uintptr_t(15));
+    }
+    hipStream_t st = as_stream(stream);
+    if (dtype == KUIOPS_BF16) return e == 128 ? launch_decode<bf16_t, 128>(a, st) : launch_decode<bf16_t, 64>(a, st);
+    return e == 128 ? launch_decode<f16_t, 128>(a, st) : launch_decode<f16_t, 64>(a, st);
+}

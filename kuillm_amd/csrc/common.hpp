@@ -1,0 +1,155 @@
+// Shared device helpers for the gfx950 kuiops kernels: vector types, bf16/f16
+// conversions, MFMA wrappers, wave64 reductions and launch-status plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "kuiops.h"
+
+namespace kuiops {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- numerics
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(double x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+
+// Accumulation-type view of an element: fp64 stays fp64, everything else fp32.
+__device__ __forceinline__ float to_f32_or_self(float x) { return x; }
+__device__ __forceinline__ double to_f32_or_self(double x) { return x; }
+__device__ __forceinline__ float to_f32_or_self(bf16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32_or_self(f16_t x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ double from_f32<double>(float x) { return x; }
+// bf16 / f16 conversions round to nearest even (the hardware converts used by
+// the compiler on gfx950), matching torch's float -> bf16 / half casts.
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return (bf16_t)x; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return (f16_t)x; }
+
+// Two raw 16-bit floats packed in a dword -> fp32 (bf16 is the top half of fp32).
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// ------------------------------------------------------------------- MFMA
+// 32x32x16 and 16x16x32 half-precision MFMAs of CDNA4.  Operand lanes hold 8
+// consecutive K values; for 32x32: lane l -> row/col (l % 32), k 8*(l/32)..+7,
+// acc[4*j+i] -> row 8*j + 4*(l/32) + i, col l % 32.  For 16x16: lane l ->
+// row/col (l % 16), k 8*(l/16)..+7, acc[i] -> row 4*(l/16) + i, col l % 16.
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16_t> {
+    typedef bf16x8 frag;
+    static __device__ __forceinline__ f32x16 m32(frag a, frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 m16(frag a, frag b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma<f16_t> {
+    typedef f16x8 frag;
+    static __device__ __forceinline__ f32x16 m32(frag a, frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 m16(frag a, frag b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <typename F> __device__ __forceinline__ F as_frag(u32x4 v) {
+    return __builtin_bit_cast(F, v);
+}
+
+// 8x8 transpose of 16-bit elements held as 8 rows of 4 dwords: in[r] holds
+// row r (element c in half (c & 1) of dword c / 2); out[c] receives column c
+// (element r in half (r & 1) of dword r / 2).
+__device__ __forceinline__ void transpose8x8_b16(const u32x4 in[8], u32x4 out[8]) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t lo = in[2 * e][c >> 1];
+            uint32_t hi = in[2 * e + 1][c >> 1];
+            // v_perm_b32 selector: bytes of (hi:lo); pick the low or high half of each.
+            out[c][e] = (c & 1) ? __builtin_amdgcn_perm(hi, lo, 0x07060302u)
+                                : __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+    }
+}
+
+// 4x8 variant: in[r] (r < 4) rows of 8 elements; out[c] (c < 8) two dwords
+// holding column c's 4 elements.
+__device__ __forceinline__ void transpose4x8_b16(const u32x4 in[4], u32x2 out[8]) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            uint32_t lo = in[2 * e][c >> 1];
+            uint32_t hi = in[2 * e + 1][c >> 1];
+            out[c][e] = (c & 1) ? __builtin_amdgcn_perm(hi, lo, 0x07060302u)
+                                : __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+    }
+}
+
+// ------------------------------------------------------- wave64 reductions
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_max(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// --------------------------------------------------------------- host side
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? KUIOPS_OK : KUIOPS_E_HIP;
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+inline int dtype_bytes(int dt) {
+    switch (dt) {
+        case KUIOPS_F32: case KUIOPS_I32: return 4;
+        case KUIOPS_F16: case KUIOPS_BF16: case KUIOPS_I16: return 2;
+        case KUIOPS_F64: case KUIOPS_I64: return 8;
+        case KUIOPS_I8: case KUIOPS_U8: case KUIOPS_BOOL: return 1;
+        default: return 0;
+    }
+}
+
+}  // namespace kuiops

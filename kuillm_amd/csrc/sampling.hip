@@ -1,0 +1,292 @@
+// Sampling tail for gfx950: row softmax and row top-k over the last dim.
+//
+// softmax_kernel: one work-group per row; pass 1 keeps a per-thread online
+// (max, sum) pair, merged across the wave with shuffles and across waves in
+// LDS in a fixed order; pass 2 writes exp(x - max) / sum.  fp32 math (fp64 for
+// f64 input).  Semantics: aten._softmax (kuipy/kuiops.py:578-610,
+// tests/test_jit_ops.py:141-155).
+//
+// topk: one 1024-thread work-group per row.  Values are mapped to 32-bit keys
+// whose unsigned order is the requested order (NaN above +inf, as aten.topk
+// treats it).  k = 1 is a single arg-max pass.  Otherwise an MSB-first radix
+// select (4 passes of 8 bits, LDS histograms) finds the k-th key; the selected
+// elements are gathered in index order with block prefix sums (so ties at the
+// k-th place keep the lowest indices) and then bitonic-sorted in LDS by
+// (key descending, index ascending).  Values are copied bit-exactly.
+// There is no reference kernel (kuiops/topk/.gitkeep); aten.topk is the
+// reference's result.
+#include "common.hpp"
+
+namespace kuiops {
+
+// --------------------------------------------------------------- softmax
+
+template <typename T> struct AccT { typedef float type; };
+template <> struct AccT<double> { typedef double type; };
+
+__device__ __forceinline__ float acc_exp(float x) { return __expf(x); }
+__device__ __forceinline__ double acc_exp(double x) { return exp(x); }
+
+template <typename A>
+__device__ __forceinline__ void sm_merge(A &m, A &s, A m2, A s2) {
+    const A M = m > m2 ? m : m2;
+    if (M == -(A)INFINITY) return;            // both empty
+    s = s * acc_exp(m - M) + s2 * acc_exp(m2 - M);
+    m = M;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_kernel(int64_t n, const T *X, T *Y) {
+    typedef typename AccT<T>::type A;
+    const int64_t row = blockIdx.x;
+    const T *x = X + row * n;
+    T *y = Y + row * n;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    A m = -(A)INFINITY, s = 0;
+    for (int64_t i = tid; i < n; i += 256) {
+        const A v = (A)to_f32_or_self(x[i]);
+        if (v > m) {
+            s = (m == -(A)INFINITY ? (A)0 : s * acc_exp(m - v)) + (A)1;
+            m = v;
+        } else if (v != -(A)INFINITY) {
+            s += acc_exp(v - m);     // NaN propagates into s
+        }
+    }
+    // NaN inputs: keep NaN in m so the whole row becomes NaN, as aten does.
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const A m2 = __shfl_xor(m, off, 64), s2 = __shfl_xor(s, off, 64);
+        if (lane & off) { A mm = m2, ss = s2; sm_merge(mm, ss, m, s); m = mm; s = ss; }
+        else sm_merge(m, s, m2, s2);
+    }
+    __shared__ A sm_m[4], sm_s[4];
+    if (lane == 0) { sm_m[wave] = m; sm_s[wave] = s; }
+    __syncthreads();
+    A M = sm_m[0], S = sm_s[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) sm_merge(M, S, sm_m[w], sm_s[w]);
+    const A inv = (A)1 / S;
+    for (int64_t i = tid; i < n; i += 256) {
+        const A v = (A)to_f32_or_self(x[i]);
+        y[i] = (T)(acc_exp(v - M) * inv);
+    }
+}
+
+// ------------------------------------------------------------------ topk
+
+__device__ __forceinline__ uint32_t order_key(float v, bool largest) {
+    uint32_t b = __float_as_uint(v);
+    uint32_t k;
+    if (v != v) k = 0xffffffffu;                       // NaN: above everything
+    else k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return largest ? k : ~k;                           // smallest: NaN lands last
+}
+
+template <typename T> __device__ __forceinline__ float load_f(const T *p) { return to_f32(*p); }
+
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkMaxK = 1024;
+
+// Block-wide exclusive prefix sum of one int per thread (1024 threads).
+__device__ __forceinline__ int block_excl_scan(int v, int *s_warp, int &total) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) s_warp[wave] = x;
+    __syncthreads();
+    if (wave == 0) {
+        int w = lane < kTopkThreads / 64 ? s_warp[lane] : 0;
+        int ws = w;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(ws, off, 64);
+            if (lane >= off) ws += y;
+        }
+        if (lane < kTopkThreads / 64) s_warp[lane] = ws - w;   // exclusive per wave
+        if (lane == kTopkThreads / 64 - 1) s_warp[kTopkThreads / 64] = ws;
+    }
+    __syncthreads();
+    const int excl = s_warp[wave] + x - v;
+    total = s_warp[kTopkThreads / 64];
+    __syncthreads();
+    return excl;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(int64_t n, int k, const T *X, T *vals,
+                                                            int64_t *inds, int largest) {
+    const int64_t row = blockIdx.x;
+    const T *x = X + row * n;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool lg = largest != 0;
+
+    if (k == 1) {
+        // arg-max with lowest-index tie break: composite (key, ~index) maximum.
+        uint64_t best = 0;
+        for (int64_t i = tid; i < n; i += kTopkThreads) {
+            const uint64_t c = ((uint64_t)order_key(load_f(x + i), lg) << 32) | (uint32_t)~(uint32_t)i;
+            best = c > best ? c : best;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const uint64_t o = __shfl_xor(best, off, 64);
+            best = o > best ? o : best;
+        }
+        __shared__ uint64_t s_best[kTopkThreads / 64];
+        if (lane == 0) s_best[wave] = best;
+        __syncthreads();
+        if (tid == 0) {
+            uint64_t b = s_best[0];
+            for (int w = 1; w < kTopkThreads / 64; ++w) b = s_best[w] > b ? s_best[w] : b;
+            const int64_t idx = (int64_t)(uint32_t)~(uint32_t)(b & 0xffffffffu);
+            vals[row] = x[idx];
+            inds[row] = idx;
+        }
+        return;
+    }
+
+    __shared__ int hist[256];
+    __shared__ int s_scan[kTopkThreads / 64 + 1];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ int s_remaining;
+    __shared__ uint64_t s_sel[kTopkMaxK];
+
+    if (tid == 0) { s_prefix = 0; s_mask = 0; s_remaining = k; }
+    __syncthreads();
+    // Radix select: after the loop, keys > prefix are strictly selected and
+    // `remaining` keys equal to prefix complete the top k.
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+        for (int64_t i = tid; i < n; i += kTopkThreads) {
+            const uint32_t key = order_key(load_f(x + i), lg);
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // find the digit d (from 255 down) where the running count reaches `remaining`
+            const int rem = s_remaining;
+            // each lane owns 4 digits, highest digits in lane 0
+            int c[4], cs = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { c[j] = hist[255 - (lane * 4 + j)]; cs += c[j]; }
+            int incl = cs;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int y = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += y;
+            }
+            int before = incl - cs;   // count of keys in higher digits than this lane's
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (before < rem && before + c[j] >= rem) {
+                    const uint32_t d = 255 - (lane * 4 + j);
+                    s_prefix = prefix | (d << shift);
+                    s_mask = mask | (255u << shift);
+                    s_remaining = rem - before;
+                }
+                before += c[j];
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t thr = s_prefix;
+    const int n_eq_take = s_remaining;        // keys == thr to take (lowest indices)
+    const int n_gt = k - n_eq_take;
+
+    // Gather selected (key, index) in index order.
+    int gt_base = 0, eq_base = 0;
+    for (int64_t base = 0; base < n; base += kTopkThreads) {
+        const int64_t i = base + tid;
+        uint32_t key = 0;
+        int is_gt = 0, is_eq = 0;
+        if (i < n) {
+            key = order_key(load_f(x + i), lg);
+            is_gt = key > thr;
+            is_eq = key == thr;
+        }
+        int tot_gt, tot_eq;
+        const int pg = block_excl_scan(is_gt, s_scan, tot_gt);
+        const int pe = block_excl_scan(is_eq, s_scan, tot_eq);
+        const uint64_t comp = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
+        if (is_gt) s_sel[gt_base + pg] = comp;
+        if (is_eq && eq_base + pe < n_eq_take) s_sel[n_gt + eq_base + pe] = comp;
+        gt_base += tot_gt;
+        eq_base += tot_eq;
+        if (gt_base >= n_gt && eq_base >= n_eq_take) break;   // uniform across the block
+    }
+    __syncthreads();
+
+    // Bitonic sort (descending composite) over the next power of two >= k.
+    int P = 1;
+    while (P < k) P <<= 1;
+    for (int i = k + tid; i < P; i += kTopkThreads) s_sel[i] = 0;
+    __syncthreads();
+    for (int size = 2; size <= P; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < P / 2; i += kTopkThreads) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool desc = (lo & size) == 0;
+                const uint64_t a = s_sel[lo], b = s_sel[hi];
+                if ((a < b) == desc) { s_sel[lo] = b; s_sel[hi] = a; }
+            }
+            __syncthreads();
+        }
+    }
+    for (int j = tid; j < k; j += kTopkThreads) {
+        const int64_t idx = (int64_t)(uint32_t)~(uint32_t)(s_sel[j] & 0xffffffffu);
+        vals[row * k + j] = x[idx];
+        inds[row * k + j] = idx;
+    }
+}
+
+size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
+    (void)rows; (void)n; (void)k;
+    return 0;
+}
+
+}  // namespace kuiops
+
+using namespace kuiops;
+
+extern "C" int kuiops_softmax_lastdim(int64_t m, int64_t n, int dtype, const void *X, void *Y, void *stream) {
+    if (m < 0 || n < 0) return KUIOPS_E_INVALID;
+    if (m == 0 || n == 0) return KUIOPS_OK;
+    if (!X || !Y) return KUIOPS_E_INVALID;
+    if (m > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    dim3 grid((unsigned)m), block(256);
+    switch (dtype) {
+        case KUIOPS_F32: hipLaunchKernelGGL(softmax_kernel<float>, grid, block, 0, st, n, (const float *)X, (float *)Y); break;
+        case KUIOPS_BF16: hipLaunchKernelGGL(softmax_kernel<bf16_t>, grid, block, 0, st, n, (const bf16_t *)X, (bf16_t *)Y); break;
+        case KUIOPS_F16: hipLaunchKernelGGL(softmax_kernel<f16_t>, grid, block, 0, st, n, (const f16_t *)X, (f16_t *)Y); break;
+        case KUIOPS_F64: hipLaunchKernelGGL(softmax_kernel<double>, grid, block, 0, st, n, (const double *)X, (double *)Y); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
+extern "C" int kuiops_topk_lastdim(int64_t m, int64_t n, int64_t k, int dtype, const void *X, void *values,
+                                   int64_t *indices, int largest, int sorted, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
+    (void)sorted; (void)workspace; (void)workspace_bytes;
+    if (m < 0 || n < 0 || k < 0 || k > n) return KUIOPS_E_INVALID;
+    if (m == 0 || k == 0) return KUIOPS_OK;
+    if (!X || !values || !indices) return KUIOPS_E_INVALID;
+    if (k > kTopkMaxK || n >= (int64_t)UINT32_MAX || m > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    dim3 grid((unsigned)m), block(kTopkThreads);
+    switch (dtype) {
+        case KUIOPS_F32: hipLaunchKernelGGL(topk_kernel<float>, grid, block, 0, st, n, (int)k, (const float *)X, (float *)values, indices, largest); break;
+        case KUIOPS_BF16: hipLaunchKernelGGL(topk_kernel<bf16_t>, grid, block, 0, st, n, (int)k, (const bf16_t *)X, (bf16_t *)values, indices, largest); break;
+        case KUIOPS_F16: hipLaunchKernelGGL(topk_kernel<f16_t>, grid, block, 0, st, n, (int)k, (const f16_t *)X, (f16_t *)values, indices, largest); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    return launch_status();
+}

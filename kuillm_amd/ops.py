@@ -1,0 +1,379 @@
+"""Tensor-level API over the kuiops C ABI (include/kuiops.h).
+
+Each function checks shapes on the host, allocates its outputs with torch
+(PyTorch-ROCm is the device-memory and stream plumbing here), and enqueues the
+HIP kernels on the current torch stream through ``_lib``.  Nothing here
+synchronises the device, so every function can be recorded in a HIP graph
+(workspaces are allocated on first use, outside capture).
+
+There is no fallback in this module: a shape the kernels do not cover raises
+``_lib.Unsupported``; the ``kuiops`` op families decide whether to fall back to
+stock PyTorch (the reference's dispatch contract, kuipy/__init__.py:53-75).
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+
+from . import _lib
+from . import compile as _compile
+
+_DT = {
+    torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16,
+    torch.float64: _lib.F64, torch.int64: _lib.I64, torch.int32: _lib.I32,
+    torch.int16: _lib.I16, torch.int8: _lib.I8, torch.uint8: _lib.U8, torch.bool: _lib.BOOL,
+}
+HALF = (torch.bfloat16, torch.float16)
+CHECK_INDEX = os.environ.get("KUIOPS_CHECK_INDEX", "0") == "1"
+
+
+def _lib_handle():
+    return _compile.load_library()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dt(dtype) -> int:
+    try:
+        return _DT[dtype]
+    except KeyError:
+        raise _lib.Unsupported("dtype", _lib.E_UNSUPPORTED) from None
+
+
+# ----------------------------------------------------------------- workspace
+# One buffer per (device, kind).  "gemv" holds the split-K arrival counters,
+# which must start at zero: it is zero-filled when allocated and the kernel
+# leaves the counters at zero.  "scratch" is plain partial-result space.
+_WS = {}
+
+
+def workspace(device: torch.device, nbytes: int, kind: str = "scratch") -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), kind)
+    buf = _WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max(int(nbytes), 1 << 20)
+        size = (size + (1 << 20) - 1) // (1 << 20) * (1 << 20)
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WS[key] = buf
+    return buf
+
+
+# -------------------------------------------------------------------- layout
+
+def _rowmajor(A: torch.Tensor) -> torch.Tensor:
+    """A 2-D view with unit column stride and a row stride >= its width."""
+    if A.stride(-1) != 1 or (A.size(0) > 1 and A.stride(0) < A.size(1)):
+        A = A.contiguous()
+    return A
+
+
+def _b_operand(B: torch.Tensor):
+    """(tensor, ld, layout) for a [K, N] operand: N-contiguous or K-contiguous."""
+    K, N = B.shape
+    if B.stride(1) == 1 and (K <= 1 or B.stride(0) >= N):
+        return B, max(B.stride(0), N), _lib.B_ROW
+    if B.stride(0) == 1 and (N <= 1 or B.stride(1) >= K):
+        return B, max(B.stride(1), K), _lib.B_COL
+    B = B.contiguous()
+    return B, N, _lib.B_ROW
+
+
+# ---------------------------------------------------------------------- GEMM
+
+GEMV_MAX_M = 64
+
+
+def _gemv(x, B, ldb, layout, bias, out):
+    M, K = x.shape
+    N = B.shape[1]
+    lib = _lib_handle()
+    ws_bytes = lib.kuiops_query_workspace(_lib.OP_GEMV_SPLITK, M, N, K)
+    ws = workspace(x.device, ws_bytes, "gemv")
+    _lib.check("kuiops_gemv_splitk", lib.kuiops_gemv_splitk(
+        M, N, K, _dt(x.dtype), x.data_ptr(), x.stride(0), B.data_ptr(), ldb, layout,
+        _ptr(bias), _dt(out.dtype), out.data_ptr(), out.stride(0), 0, ws.data_ptr(), ws.numel(),
+        _stream(x.device)))
+    return out
+
+
+def mm(A: torch.Tensor, B: torch.Tensor, out_dtype=None) -> torch.Tensor:
+    """A[M, K] @ B[K, N] with fp32 accumulation (aten.mm semantics)."""
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0] or A.dtype != B.dtype:
+        raise _lib.KuiopsError("mm", _lib.E_INVALID)
+    A = _rowmajor(A)
+    B, ldb, layout = _b_operand(B)
+    M, K = A.shape
+    N = B.shape[1]
+    out = torch.empty((M, N), dtype=out_dtype or A.dtype, device=A.device)
+    if M == 0 or N == 0:
+        return out
+    if K == 0:
+        return out.zero_()
+    if A.dtype in HALF and M <= GEMV_MAX_M:
+        try:
+            return _gemv(A, B, ldb, layout, None, out)
+        except _lib.Unsupported:
+            pass
+    lib = _lib_handle()
+    _lib.check("kuiops_mm", lib.kuiops_mm(
+        M, N, K, _dt(A.dtype), A.data_ptr(), A.stride(0), B.data_ptr(), ldb, layout,
+        _dt(out.dtype), out.data_ptr(), out.stride(0), _stream(A.device)))
+    return out
+
+
+def addmm(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, beta=1.0, alpha=1.0) -> torch.Tensor:
+    """beta * C + alpha * (A @ B) with C broadcast to [M, N] (aten.addmm)."""
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0]:
+        raise _lib.KuiopsError("addmm", _lib.E_INVALID)
+    if not (A.dtype == B.dtype == C.dtype):
+        raise _lib.KuiopsError("addmm", _lib.E_INVALID)
+    A = _rowmajor(A)
+    B, ldb, layout = _b_operand(B)
+    M, K = A.shape
+    N = B.shape[1]
+    beta, alpha = float(beta), float(alpha)
+    if beta == 0.0:
+        c_kind, Cin, ldcin = _lib.C_NONE, None, 0
+    elif C.dim() == 1 and C.shape[0] == N or (C.dim() == 2 and C.shape[0] == 1 and C.shape[1] == N):
+        c_kind, Cin, ldcin = _lib.C_ROW, C.reshape(N).contiguous(), 0
+    else:
+        Cin = C.expand(M, N)
+        if Cin.stride(1) != 1 or Cin.stride(0) < N:
+            Cin = Cin.contiguous()
+        c_kind, ldcin = _lib.C_FULL, Cin.stride(0)
+    out = torch.empty((M, N), dtype=A.dtype, device=A.device)
+    if M == 0 or N == 0:
+        return out
+    if (A.dtype in HALF and M <= GEMV_MAX_M and alpha == 1.0 and K > 0
+            and (c_kind == _lib.C_NONE or (c_kind == _lib.C_ROW and beta == 1.0))):
+        try:
+            return _gemv(A, B, ldb, layout, Cin, out)
+        except _lib.Unsupported:
+            pass
+    lib = _lib_handle()
+    ws_bytes = lib.kuiops_query_workspace(_lib.OP_ADDMM, M, N, K)
+    ws = workspace(A.device, ws_bytes) if ws_bytes else None
+    _lib.check("kuiops_addmm", lib.kuiops_addmm(
+        M, K, N, alpha, beta, _dt(A.dtype), A.data_ptr(), A.stride(0), B.data_ptr(), ldb, layout,
+        _ptr(Cin), c_kind, ldcin, _dt(out.dtype), out.data_ptr(), out.stride(0),
+        0, _ptr(ws), 0 if ws is None else ws.numel(), _stream(A.device)))
+    return out
+
+
+def linear(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """x[..., K] @ W[N, K]^T (+ bias): nn.Linear with a K-contiguous weight."""
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if bias is None:
+        y = mm(x2, W.t())
+    else:
+        y = addmm(bias, x2, W.t())
+    return y.reshape(*lead, W.shape[0])
+
+
+def bmm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """C[b] = A[b] @ B[b] (aten.bmm)."""
+    if A.dim() != 3 or B.dim() != 3 or A.shape[0] != B.shape[0] or A.shape[2] != B.shape[1]:
+        raise _lib.KuiopsError("bmm", _lib.E_INVALID)
+    if A.dtype != B.dtype:
+        raise _lib.KuiopsError("bmm", _lib.E_INVALID)
+    Bn, M, K = A.shape
+    N = B.shape[2]
+    if A.stride(2) != 1 or (M > 1 and A.stride(1) < K):
+        A = A.contiguous()
+    if B.stride(2) == 1 and (K <= 1 or B.stride(1) >= N):
+        layout, ldb = _lib.B_ROW, max(B.stride(1), N)
+    elif B.stride(1) == 1 and (N <= 1 or B.stride(2) >= K):
+        layout, ldb = _lib.B_COL, max(B.stride(2), K)
+    else:
+        B = B.contiguous()
+        layout, ldb = _lib.B_ROW, N
+    out = torch.empty((Bn, M, N), dtype=A.dtype, device=A.device)
+    if out.numel() == 0:
+        return out
+    if K == 0:
+        return out.zero_()
+    lib = _lib_handle()
+    _lib.check("kuiops_bmm", lib.kuiops_bmm(
+        Bn, M, K, N, _dt(A.dtype), A.data_ptr(), A.stride(0), A.stride(1),
+        B.data_ptr(), B.stride(0), ldb, layout, _dt(out.dtype), out.data_ptr(),
+        out.stride(0), out.stride(1), _stream(A.device)))
+    return out
+
+
+# ---------------------------------------------------------------------- SDPA
+
+def _lastdim_contig(t):
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _attn_prep(q, k, v):
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise _lib.KuiopsError("sdpa", _lib.E_INVALID)
+    q, k, v = _lastdim_contig(q), _lastdim_contig(k), _lastdim_contig(v)
+    n, hq, l, e = q.shape
+    _, hkv, s, _ = k.shape
+    ev = v.shape[-1]
+    if k.shape[0] != n or v.shape[0] != n or v.shape[1] != hkv or v.shape[2] != s or k.shape[3] != e:
+        raise _lib.KuiopsError("sdpa", _lib.E_INVALID)
+    if hkv == 0 or hq % hkv:
+        raise _lib.KuiopsError("sdpa", _lib.E_INVALID)
+    return q, k, v, (n, hq, hkv, l, s, e, ev)
+
+
+def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=8):
+    """softmax(scale * q k^T [causal]) v  ->  (out, lse)   (aten SDPA semantics).
+
+    q (n, hq, l, e), k / v (n, hkv, s, e) with hq % hkv == 0; causal masking is
+    aten's top-left alignment (query i sees keys j <= i).  Non-causal calls
+    with few query rows per KV head use the split-KV decode kernel.
+    """
+    q, k, v, (n, hq, hkv, l, s, e, ev) = _attn_prep(q, k, v)
+    if scale is None:
+        scale = 1.0 / math.sqrt(e)
+    out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
+    lse = torch.empty((n, hq, l), dtype=torch.float32, device=q.device) if return_lse else None
+    if out.numel() == 0:
+        return out, lse
+    lib = _lib_handle()
+    sq = _lib.strides3(*q.stride()[:3])
+    sk = _lib.strides3(*k.stride()[:3])
+    sv = _lib.strides3(*v.stride()[:3])
+    so = _lib.strides3(*out.stride()[:3])
+    if not is_causal and (hq // hkv) * l <= decode_max_rows and s > 0:
+        ws_bytes = lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, n * hq * l, s, ev)
+        ws = workspace(q.device, ws_bytes)
+        _lib.check("kuiops_sdpa_decode", lib.kuiops_sdpa_decode(
+            n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), sq, k.data_ptr(), sk,
+            v.data_ptr(), sv, out.data_ptr(), so, _ptr(lse), float(scale), 0,
+            ws.data_ptr(), ws.numel(), _stream(q.device)))
+        return out, lse
+    _lib.check("kuiops_sdpa_fwd", lib.kuiops_sdpa_fwd(
+        n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), sq, k.data_ptr(), sk,
+        v.data_ptr(), sv, out.data_ptr(), so, _ptr(lse), float(scale), 1 if is_causal else 0,
+        _stream(q.device)))
+    return out, lse
+
+
+def sdpa_decode(q, k, v, scale=None, causal=True, return_lse=False):
+    """Decode attention over a KV cache: the l queries are the LAST l positions
+    of the s keys (query i sees keys j <= s - l + i when ``causal``)."""
+    q, k, v, (n, hq, hkv, l, s, e, ev) = _attn_prep(q, k, v)
+    if scale is None:
+        scale = 1.0 / math.sqrt(e)
+    out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
+    lse = torch.empty((n, hq, l), dtype=torch.float32, device=q.device) if return_lse else None
+    if out.numel() == 0:
+        return out, lse
+    lib = _lib_handle()
+    ws_bytes = lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, n * hq * l, s, ev)
+    ws = workspace(q.device, ws_bytes)
+    _lib.check("kuiops_sdpa_decode", lib.kuiops_sdpa_decode(
+        n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), _lib.strides3(*q.stride()[:3]),
+        k.data_ptr(), _lib.strides3(*k.stride()[:3]), v.data_ptr(), _lib.strides3(*v.stride()[:3]),
+        out.data_ptr(), _lib.strides3(*out.stride()[:3]), _ptr(lse), float(scale), 1 if causal else 0,
+        ws.data_ptr(), ws.numel(), _stream(q.device)))
+    return out, lse
+
+
+# ------------------------------------------------------------ sampling tail
+
+def softmax(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    """Softmax over the last dim (aten._softmax with half_to_float=False)."""
+    if x.dim() == 0 or (dim % x.dim()) != x.dim() - 1:
+        raise _lib.Unsupported("softmax", _lib.E_UNSUPPORTED)
+    xc = x.contiguous()
+    n = xc.shape[-1] if xc.dim() else 1
+    m = xc.numel() // n if n else 0
+    out = torch.empty_like(xc)
+    if xc.numel() == 0:
+        return out
+    lib = _lib_handle()
+    _lib.check("kuiops_softmax_lastdim", lib.kuiops_softmax_lastdim(
+        m, n, _dt(x.dtype), xc.data_ptr(), out.data_ptr(), _stream(x.device)))
+    return out
+
+
+def topk(x: torch.Tensor, k: int, dim: int = -1, largest: bool = True, sorted: bool = True):
+    """(values, int64 indices) of the k largest / smallest along ``dim``; ties
+    are ordered by ascending index and NaN is treated as the largest value."""
+    if x.dim() == 0:
+        raise _lib.Unsupported("topk", _lib.E_UNSUPPORTED)
+    dim = dim % x.dim()
+    moved = dim != x.dim() - 1
+    xc = (x.movedim(dim, -1) if moved else x).contiguous()
+    n = xc.shape[-1]
+    k = int(k)
+    if k < 0 or k > n:
+        raise _lib.KuiopsError("topk", _lib.E_INVALID)
+    m = xc.numel() // n if n else 0
+    vals = torch.empty((*xc.shape[:-1], k), dtype=x.dtype, device=x.device)
+    inds = torch.empty((*xc.shape[:-1], k), dtype=torch.int64, device=x.device)
+    if vals.numel():
+        lib = _lib_handle()
+        _lib.check("kuiops_topk_lastdim", lib.kuiops_topk_lastdim(
+            m, n, k, _dt(x.dtype), xc.data_ptr(), vals.data_ptr(), inds.data_ptr(),
+            1 if largest else 0, 1 if sorted else 0, None, 0, _stream(x.device)))
+    if moved:
+        vals, inds = vals.movedim(-1, dim), inds.movedim(-1, dim)
+    return vals, inds
+
+
+def _err_flag(device):
+    return torch.zeros(1, dtype=torch.int32, device=device) if CHECK_INDEX else None
+
+
+def _raise_if_flagged(flag, what):
+    if flag is not None and int(flag.item()) != 0:
+        raise IndexError(f"{what}: index out of range")
+
+
+def gather(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = None) -> torch.Tensor:
+    """torch.gather(inp, dim, idx) for contiguous int64 indices (bit-exact)."""
+    if idx.dtype != torch.int64 or idx.dim() != inp.dim() or inp.dim() < 1 or inp.dim() > 8:
+        raise _lib.Unsupported("gather", _lib.E_UNSUPPORTED)
+    dim = dim % inp.dim()
+    for d in range(inp.dim()):
+        if d != dim and idx.shape[d] > inp.shape[d]:
+            raise _lib.KuiopsError("gather", _lib.E_INVALID)
+    ic, xc = inp.contiguous(), idx.contiguous()
+    out = torch.empty(idx.shape, dtype=inp.dtype, device=inp.device)
+    if out.numel() == 0:
+        return out
+    flag = torch.zeros(1, dtype=torch.int32, device=inp.device) if (check or (check is None and CHECK_INDEX)) else None
+    lib = _lib_handle()
+    _lib.check("kuiops_gather", lib.kuiops_gather(
+        inp.dim(), _lib.i64_array(ic.shape), _lib.i64_array(xc.shape), dim, ic.element_size(),
+        ic.data_ptr(), xc.data_ptr(), out.data_ptr(), _ptr(flag), _stream(inp.device)))
+    _raise_if_flagged(flag, "gather")
+    return out
+
+
+def index(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = None) -> torch.Tensor:
+    """inp[(slice(None),) * dim + (idx,)] for one int64 index tensor
+    (aten.index.Tensor with a single index); negative indices wrap."""
+    if idx.dtype != torch.int64 or inp.dim() < 1:
+        raise _lib.Unsupported("index", _lib.E_UNSUPPORTED)
+    dim = dim % inp.dim()
+    ic, xc = inp.contiguous(), idx.contiguous()
+    outer = math.prod(ic.shape[:dim])
+    size = ic.shape[dim]
+    inner = math.prod(ic.shape[dim + 1:])
+    out = torch.empty((*ic.shape[:dim], *xc.shape, *ic.shape[dim + 1:]), dtype=inp.dtype, device=inp.device)
+    if out.numel() == 0:
+        return out
+    flag = torch.zeros(1, dtype=torch.int32, device=inp.device) if (check or (check is None and CHECK_INDEX)) else None
+    lib = _lib_handle()
+    _lib.check("kuiops_index", lib.kuiops_index(
+        outer, size, inner, xc.numel(), ic.element_size(), ic.data_ptr(), xc.data_ptr(),
+        out.data_ptr(), _ptr(flag), _stream(inp.device)))
+    _raise_if_flagged(flag, "index")
+    return out

@@ -1,0 +1,265 @@
+"""CPU oracle for the kuiops hot path -- TEST INFRASTRUCTURE ONLY.
+
+A plain numpy restatement of what the reference computes for each hot-path
+op.  Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU
+baseline may import it, and only as the checker: nothing in ``kuillm_amd``
+imports or calls this module, and the product path never routes through it.
+
+The reference (panther03/kuiLLM) dispatches aten ops to un-vendored,
+unpinned Kuiper kernels when its ``supported()`` gates accept them and to
+stock aten otherwise (kuipy/__init__.py:53-75, 161-164); its own tests check
+every op against stock torch (tests/test_jit_ops.py:34-43).  The oracle
+therefore restates aten semantics, op by op, citing the reference's family:
+
+  mm / addmm / bmm   kuipy/kuiops.py:403-564, kuiops/bmm/Kuiops.Bmm.fst:10-23
+  _softmax           kuipy/kuiops.py:578-610
+  SDPA (+ LSE)       kuipy/kuiops.py:627-681, kuiops/sdpa/Kuiops.Sdpa.fst.1:9-27
+  gather             kuipy/kuiops.py:717-754, kuiops/gather/Kuiops.Gather.fst:482-486
+  topk / index       no reference kernel (kuiops/topk/.gitkeep,
+                     kuiops/index/.gitkeep): aten.topk / aten.index.Tensor
+  verify metric      kuipy/__init__.py:193-225
+
+bf16 values travel as uint16 bit patterns (numpy has no bfloat16).
+
+How each function is pinned (tests/test_oracle.py):
+  * against golden vectors written by stock aten on CPU (tests/golden/);
+  * against closed forms and invariants chosen so that a dropped term, a
+    wrong sign / index or a transposed operand fails (identity and one-hot
+    operands, integer-valued products that are exact in fp32, softmax of a
+    constant row, attention with constant V, single-key attention, causal
+    row 0, brute-force sorting for topk, explicit loops for gather / index).
+No function here is "parity unpinned".
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+# ------------------------------------------------------------------- bf16
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Round fp32 to bf16 (round to nearest even, NaN kept quiet) -> uint16."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(x)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    out = rounded.astype(np.uint16)
+    out[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return out
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    b = np.asarray(b, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x) -> np.ndarray:
+    """fp32 values rounded to the nearest bf16, returned as fp32."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+def round_dtype(x, dtype: str) -> np.ndarray:
+    """Round to the storage dtype ('bf16', 'f16', 'f32', 'f64'), as fp32/fp64."""
+    if dtype == "bf16":
+        return round_bf16(np.asarray(x, dtype=np.float32))
+    if dtype == "f16":
+        return np.asarray(x, dtype=np.float16).astype(np.float32)
+    if dtype == "f32":
+        return np.asarray(x, dtype=np.float32)
+    return np.asarray(x, dtype=np.float64)
+
+
+# ------------------------------------------------------------------- GEMM
+
+
+def mm(A, B, acc="f64") -> np.ndarray:
+    """C = A @ B for [M, K] x [K, N] with the inputs taken exactly as given
+    (already rounded to their storage type) and a wide accumulator
+    (aten.mm; MmImpl kuipy/kuiops.py:403-469).  The product is not rounded:
+    callers round to the output dtype with ``round_dtype``."""
+    A = np.asarray(A, dtype=np.float64 if acc == "f64" else np.float32)
+    B = np.asarray(B, dtype=A.dtype)
+    if A.ndim != 2 or B.ndim != 2 or A.shape[1] != B.shape[0]:
+        raise ValueError("mm: shape mismatch")
+    return A @ B
+
+
+def addmm(C, A, B, alpha=1.0, beta=1.0) -> np.ndarray:
+    """beta * C + alpha * (A @ B), C broadcast to [M, N] (aten.addmm;
+    AddmmImpl kuipy/kuiops.py:520-564 with alpha/beta as in
+    kuiops/addmm/wrapper_addmm.cu.j2:7).  beta == 0 ignores C entirely."""
+    P = mm(A, B)
+    out = alpha * P
+    if beta != 0:
+        out = out + beta * np.broadcast_to(np.asarray(C, dtype=np.float64), P.shape)
+    return out
+
+
+def bmm(A, B) -> np.ndarray:
+    """C[b] = A[b] @ B[b], output overwritten (comb2, kuiops/bmm/Kuiops.Bmm.fst:10-23)."""
+    A = np.asarray(A, dtype=np.float64)
+    B = np.asarray(B, dtype=np.float64)
+    if A.ndim != 3 or B.ndim != 3 or A.shape[0] != B.shape[0] or A.shape[2] != B.shape[1]:
+        raise ValueError("bmm: shape mismatch")
+    return np.einsum("bmk,bkn->bmn", A, B)
+
+
+def splitk_mm(A, B, splits: int) -> np.ndarray:
+    """mm computed as fp32 partial products over `splits` K ranges, summed in
+    split order -- the deterministic split-K contract of kuiops_addmm /
+    kuiops_gemv_splitk (fixed-order reduction)."""
+    A = np.asarray(A, dtype=np.float32)
+    B = np.asarray(B, dtype=np.float32)
+    K = A.shape[1]
+    step = -(-K // splits)
+    acc = np.zeros((A.shape[0], B.shape[1]), dtype=np.float32)
+    for z in range(splits):
+        lo, hi = z * step, min(K, (z + 1) * step)
+        if lo < hi:
+            acc = acc + (A[:, lo:hi].astype(np.float64) @ B[lo:hi].astype(np.float64)).astype(np.float32)
+    return acc
+
+
+# ---------------------------------------------------------------- softmax
+
+
+def softmax(x, axis=-1) -> np.ndarray:
+    """exp(x - max) / sum over `axis` in fp64 (aten._softmax;
+    SoftmaxImpl kuipy/kuiops.py:572-610)."""
+    x = np.asarray(x, dtype=np.float64)
+    m = np.max(x, axis=axis, keepdims=True)
+    with np.errstate(invalid="ignore", over="ignore"):
+        e = np.exp(x - m)
+        return e / np.sum(e, axis=axis, keepdims=True)
+
+
+# ------------------------------------------------------------------- SDPA
+
+
+def sdpa(q, k, v, causal=False, scale=None, bias=None, align="top_left"):
+    """Attention in fp64: returns (out, lse).
+
+    q (n, hq, l, e), k (n, hkv, s, e), v (n, hkv, s, ev); hq % hkv == 0 and
+    query head h reads KV head h // (hq // hkv).  scores = scale * q k^T
+    (+ bias), the softmax-over-keys weights give out = P v and
+    lse = logsumexp(scores) (natural log).  Layouts (N, H, L, E) row-major
+    as kuiops/sdpa/Kuiops.Sdpa.fst.1:19-27; the bias is added after scaling
+    as aten does (the reference pre-divides it, kuipy/kuiops.py:673-676).
+    Causal: 'top_left' is aten's is_causal (query i sees keys j <= i);
+    'bottom_right' aligns the queries to the end of the keys (KV-cache
+    decode).  Rows with no visible key give out = 0 and lse = -inf.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    n, hq, l, e = q.shape
+    hkv, s = k.shape[1], k.shape[2]
+    if hq % hkv:
+        raise ValueError("sdpa: hq % hkv != 0")
+    g = hq // hkv
+    k = np.repeat(k, g, axis=1)
+    v = np.repeat(v, g, axis=1)
+    if scale is None:
+        scale = 1.0 / math.sqrt(e)
+    sc = scale * np.einsum("nhle,nhse->nhls", q, k)
+    if bias is not None:
+        sc = sc + np.asarray(bias, dtype=np.float64)
+    if causal:
+        i = np.arange(l)[:, None]
+        j = np.arange(s)[None, :]
+        visible = j <= i if align == "top_left" else j <= (s - l + i)
+        sc = np.where(visible, sc, -np.inf)
+    m = np.max(sc, axis=-1, keepdims=True)
+    m_safe = np.where(np.isfinite(m), m, 0.0)
+    p = np.exp(sc - m_safe)
+    denom = np.sum(p, axis=-1, keepdims=True)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        out = np.where(denom > 0, np.einsum("nhls,nhsv->nhlv", p, v) / np.where(denom > 0, denom, 1), 0.0)
+        lse = np.where(denom[..., 0] > 0, np.log(np.where(denom[..., 0] > 0, denom[..., 0], 1)) + m_safe[..., 0], -np.inf)
+    return out, lse
+
+
+# -------------------------------------------------------------------- topk
+
+
+def _order_key(x: np.ndarray) -> np.ndarray:
+    """Sort key with NaN above +inf (aten.topk's NaN convention)."""
+    x = np.asarray(x, dtype=np.float64)
+    return np.where(np.isnan(x), np.inf, x), np.isnan(x)
+
+
+def topk(x, k: int, largest=True):
+    """(values, int64 indices) of the k largest (smallest) entries of each row
+    of the last axis.  NaN ranks above every number; equal values are ordered
+    by ascending index (lowest indices win a tie at the k-th place).
+    aten.topk semantics on tie-free inputs; there is no reference kernel
+    (kuiops/topk/.gitkeep)."""
+    x = np.asarray(x)
+    flat = x.reshape(-1, x.shape[-1])
+    vals = np.empty((flat.shape[0], k), dtype=x.dtype)
+    inds = np.empty((flat.shape[0], k), dtype=np.int64)
+    for r in range(flat.shape[0]):
+        row = flat[r]
+        key, isnan = _order_key(row)
+        idx = np.arange(row.shape[0])
+        if largest:
+            # primary: NaN first, then value descending; secondary: index ascending
+            order = np.lexsort((idx, -key, ~isnan))
+        else:
+            order = np.lexsort((idx, key, isnan))
+        sel = order[:k]
+        vals[r] = row[sel]
+        inds[r] = sel
+    return vals.reshape(*x.shape[:-1], k), inds.reshape(*x.shape[:-1], k)
+
+
+# --------------------------------------------------------- gather / index
+
+
+def gather(inp, dim: int, idx) -> np.ndarray:
+    """out[x] = inp[x with axis `dim` replaced by idx[x]]
+    (kuiops/gather/Kuiops.Gather.fst:482-486; aten.gather)."""
+    inp = np.asarray(inp)
+    idx = np.asarray(idx, dtype=np.int64)
+    if np.any(idx < 0) or np.any(idx >= inp.shape[dim]):
+        raise IndexError("gather: index out of range")
+    coords = list(np.indices(idx.shape))
+    coords[dim] = idx
+    return inp[tuple(coords)]
+
+
+def index(inp, dim: int, idx) -> np.ndarray:
+    """inp[:, ..., idx, ...] with one int64 index tensor at axis `dim`
+    (aten.index.Tensor); negative indices count from the end."""
+    inp = np.asarray(inp)
+    idx = np.asarray(idx, dtype=np.int64)
+    size = inp.shape[dim]
+    if np.any(idx < -size) or np.any(idx >= size):
+        raise IndexError("index: index out of range")
+    idx = np.where(idx < 0, idx + size, idx)
+    return np.take(inp, idx, axis=dim)
+
+
+# ------------------------------------------------------------ verify metric
+
+
+def rel_frobenius(out, ref) -> float:
+    """||out - ref||_F / (||ref||_F + 1e-12) over positions finite in both
+    (kuipy/__init__.py:193-225)."""
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    fin = np.isfinite(o) & np.isfinite(r)
+    if not fin.any():
+        return 0.0
+    o, r = o[fin], r[fin]
+    return float(np.linalg.norm(o - r) / (np.linalg.norm(r) + 1e-12))
+
+
+def within(out, ref, rtol=1e-2, atol=1e-2) -> bool:
+    """Elementwise |out - ref| <= atol + rtol * |ref| (the north-star bf16
+    GEMM / SDPA tolerance)."""
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    return bool(np.all(np.abs(o - r) <= atol + rtol * np.abs(r)))

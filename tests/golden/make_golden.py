@@ -1,0 +1,104 @@
+"""Writes the golden fixtures in this directory from stock aten on CPU.
+
+The reference computes every hot-path op either with an un-vendored Kuiper
+kernel that its tests hold to stock torch (tests/test_jit_ops.py:34-43), or
+by falling through to stock aten (kuipy/__init__.py:161-164; always for
+topk / index / causal SDPA).  Stock aten on CPU is therefore the reference's
+own result for these ops.  Shapes follow the reference's tests
+(tests/test_jit_ops.py:51-230) plus BASELINE.json config 0 at reduced size.
+
+Fixtures are data only: inputs and aten outputs, bf16 stored as uint16 bits.
+Re-run with:  python tests/golden/make_golden.py
+"""
+import math
+from pathlib import Path
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+OUT = Path(__file__).resolve().parent / "golden.npz"
+
+
+def bits(t):
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def main():
+    g = {}
+    torch.manual_seed(0)
+    # mm (MmImpl; tests/test_jit_general.py:50-59 uses 128x64 @ 64x128 f32)
+    A = torch.randn(128, 64); B = torch.randn(64, 128)
+    g["mm_f32_A"], g["mm_f32_B"], g["mm_f32_C"] = A.numpy(), B.numpy(), torch.mm(A, B).numpy()
+    A = torch.randn(64, 96).bfloat16(); B = (torch.randn(96, 80) * 0.5).bfloat16()
+    g["mm_bf16_A"], g["mm_bf16_B"] = bits(A), bits(B)
+    g["mm_bf16_C32"] = (A.float() @ B.float()).numpy()          # fp32 accumulate, unrounded
+    g["mm_bf16_C"] = bits(torch.mm(A, B))                        # aten bf16 result
+    # addmm, test_jit_ops.py:98-112: 64^3, alpha/beta in {(1,1),(0.5,2)}, 2-D bias
+    for dt in ("f32", "bf16"):
+        tdt = torch.float32 if dt == "f32" else torch.bfloat16
+        A = torch.randn(64, 64, dtype=tdt); B = torch.randn(64, 64, dtype=tdt)
+        C2 = torch.randn(64, 64, dtype=tdt); C1 = torch.randn(64, dtype=tdt)
+        g[f"addmm_{dt}_A"], g[f"addmm_{dt}_B"], g[f"addmm_{dt}_C2"], g[f"addmm_{dt}_C1"] = bits(A), bits(B), bits(C2), bits(C1)
+        for tag, (al, be) in (("11", (1.0, 1.0)), ("052", (0.5, 2.0))):
+            g[f"addmm_{dt}_out2_{tag}"] = bits(torch.addmm(C2, A, B, alpha=al, beta=be))
+            g[f"addmm_{dt}_out1_{tag}"] = bits(torch.addmm(C1, A, B, alpha=al, beta=be))
+            g[f"addmm_{dt}_out2_{tag}_f32acc"] = (be * C2.float() + al * (A.float() @ B.float())).numpy()
+    # BASELINE config 0 (reduced rows): x~N(0,1), W~N(0,.02), bias~N(0,.02), fp32
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(8, 768, generator=gen); W = torch.randn(768, 3072, generator=gen) * 0.02
+    b = torch.randn(3072, generator=gen) * 0.02
+    g["cfg0_x"], g["cfg0_W"], g["cfg0_b"] = x.numpy(), W[:, :64].contiguous().numpy(), b[:64].contiguous().numpy()
+    g["cfg0_out"] = torch.addmm(b[:64], x, W[:, :64]).numpy()
+    # bmm, test_jit_ops.py:51-60
+    for dt in ("f32", "bf16"):
+        tdt = torch.float32 if dt == "f32" else torch.bfloat16
+        A = torch.randn(5, 17, 9, dtype=tdt); B = torch.randn(5, 9, 13, dtype=tdt)
+        g[f"bmm_{dt}_A"], g[f"bmm_{dt}_B"], g[f"bmm_{dt}_C"] = bits(A), bits(B), bits(torch.bmm(A, B))
+    # softmax, test_jit_ops.py:141-155
+    for shape in ((128, 64), (8, 5, 33)):
+        tag = "x".join(map(str, shape))
+        X = torch.randn(*shape)
+        g[f"softmax_{tag}_X"], g[f"softmax_{tag}_Y"] = X.numpy(), torch.softmax(X, -1).numpy()
+        Xb = X.bfloat16()
+        g[f"softmax_{tag}_Xb"], g[f"softmax_{tag}_Yb"] = bits(Xb), bits(torch.softmax(Xb, -1))
+    # sdpa: test_jit_ops.py:173-193 shape with a float bias, plus causal cases
+    N, H, L, S, E = 2, 3, 8, 10, 16
+    Q, K, V = torch.randn(N, H, L, E), torch.randn(N, H, S, E), torch.randn(N, H, S, E)
+    bias = torch.randn(N, H, L, S)
+    g["sdpa_Q"], g["sdpa_K"], g["sdpa_V"], g["sdpa_bias"] = Q.numpy(), K.numpy(), V.numpy(), bias.numpy()
+    g["sdpa_out_bias"] = F.scaled_dot_product_attention(Q, K, V, attn_mask=bias, scale=0.3).numpy()
+    g["sdpa_lse_bias"] = torch.logsumexp(Q @ K.transpose(-1, -2) * 0.3 + bias, -1).numpy()
+    g["sdpa_out_causal"] = F.scaled_dot_product_attention(Q, K, V, is_causal=True).numpy()
+    g["sdpa_out_full"] = F.scaled_dot_product_attention(Q, K, V).numpy()
+    Qb = torch.randn(1, 4, 70, 64).bfloat16(); Kb = torch.randn(1, 4, 70, 64).bfloat16(); Vb = torch.randn(1, 4, 70, 64).bfloat16()
+    g["sdpa_bf16_Q"], g["sdpa_bf16_K"], g["sdpa_bf16_V"] = bits(Qb), bits(Kb), bits(Vb)
+    g["sdpa_bf16_out_causal"] = F.scaled_dot_product_attention(Qb.float(), Kb.float(), Vb.float(), is_causal=True).numpy()
+    # topk: tie-free rows (distinct values), several k, both directions
+    X = torch.randperm(4 * 300).reshape(4, 300).float() / 7.0 - 80.0
+    g["topk_X"] = X.numpy()
+    for kk in (1, 5, 64, 300):
+        v, i = torch.topk(X, kk)
+        g[f"topk_{kk}_v"], g[f"topk_{kk}_i"] = v.numpy(), i.numpy()
+        v, i = torch.topk(X, kk, largest=False)
+        g[f"topk_{kk}_sv"], g[f"topk_{kk}_si"] = v.numpy(), i.numpy()
+    # gather, test_jit_ops.py:216-230
+    for shape, dim in (((8, 5), 1), ((8, 5), 0), ((4, 3, 6), 2)):
+        tag = "x".join(map(str, shape)) + f"_d{dim}"
+        Inp = torch.randn(*shape)
+        ish = list(shape); ish[dim] = max(1, shape[dim] - 1)
+        Idx = torch.randint(0, shape[dim], ish)
+        g[f"gather_{tag}_inp"], g[f"gather_{tag}_idx"], g[f"gather_{tag}_out"] = Inp.numpy(), Idx.numpy(), torch.gather(Inp, dim, Idx).numpy()
+    # index: embedding-row gather and a middle-axis index with negative entries
+    Emb = torch.randn(50, 12); ids = torch.randint(0, 50, (3, 7))
+    g["index_emb"], g["index_ids"], g["index_out"] = Emb.numpy(), ids.numpy(), Emb[ids].numpy()
+    T3 = torch.randn(2, 9, 4); ids2 = torch.tensor([[-1, 0, 3], [8, -9, 2]])
+    g["index3_inp"], g["index3_ids"], g["index3_out"] = T3.numpy(), ids2.numpy(), T3[:, ids2].numpy()
+    np.savez_compressed(OUT, **g)
+    print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(g)} arrays)")
+
+
+if __name__ == "__main__":
+    main()
