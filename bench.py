@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""Benchmark of the kuiops hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu-baseline]
+
+Headline (the JSON line's ``value``): BASELINE.json config 2, bf16 prefill
+addmm  out[4096,4096] = bias[4096] + A[4096,4096] @ B[4096,4096], A~N(0,1),
+B~N(0,0.02), fp32 accumulate, in bf16 TFLOP/s.  A "step" is one
+``kuillm_amd.ops.addmm`` call (one MFMA kernel launch) on inputs resident in
+HBM.  Each step is recorded once in a HIP graph and the graph is replayed, so
+the timed region holds device work only; HIP events on the launch stream
+bracket exactly K replays after W warm-up replays.
+
+``workloads`` (extra keys of the same line) measures the other BASELINE.json
+configs the same way: decode split-K GEMM (HBM GB/s), bmm, causal SDPA at
+S=2048/4096, decode SDPA, and the softmax + top-k sampling tail.  Each
+carries its own roofline fraction.
+
+``cpu_baseline``: the reference's CPU path -- stock torch aten on the host
+cores (the reference never offloads CPU tensors, kuipy/kuiops.py:531) -- on
+the same addmm in fp32 (CPU bf16 is not representative), timed for a bounded
+number of iterations.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
+    return ap.parse_args()
+
+
+def graph_time_ms(torch, fn, steps, warmup):
+    """Average device time of one `fn()` step: `fn` recorded once into a HIP
+    graph, W warm-up replays, then K replays between HIP events on the
+    current (launch) stream, with device synchronisation on both sides."""
+    fn()                                    # eager run: allocates workspaces outside capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def roofline(bound, achieved, unit, traffic=None):
+    peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def cpu_baseline(torch, seconds):
+    """Stock torch addmm on the host cores, fp32, same shape as the headline."""
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(0)
+    A = torch.randn(4096, 4096, generator=g)
+    B = torch.randn(4096, 4096, generator=g) * 0.02
+    bias = torch.randn(4096, generator=g) * 0.02
+    torch.addmm(bias, A, B)                      # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        torch.addmm(bias, A, B)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": round(2 * 4096 ** 3 / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"stock torch {torch.__version__} CPU fp32 addmm bias[4096] + A[4096,4096] @ "
+                      f"B[4096,4096], median of {len(times)} calls ({med * 1e3:.1f} ms each)"}
+
+
+def extra_workloads(torch, ops, steps, warmup, dev):
+    out = {}
+    bf = torch.bfloat16
+    torch.manual_seed(1)
+    # config 1: decode split-K GEMM, HBM-bound
+    W = (torch.randn(4096, 11008, device=dev) * 0.02).to(bf)
+    for M in (1, 4, 16):
+        x = torch.randn(M, 4096, device=dev).to(bf)
+        ms = graph_time_ms(torch, lambda: ops.mm(x, W), steps, warmup)
+        nbytes = 4096 * 11008 * 2 + M * 4096 * 2 + M * 11008 * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"decode_gemm_M{M}"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 5),
+                                    "roofline": roofline("hbm", gbs, "GB/s")}
+    del W
+    # config 2b: bmm 32 x [2048,128] @ [128,2048]
+    A3 = torch.randn(32, 2048, 128, device=dev).to(bf)
+    B3 = torch.randn(32, 128, 2048, device=dev).to(bf)
+    ms = graph_time_ms(torch, lambda: ops.bmm(A3, B3), steps, warmup)
+    tf = 2 * 32 * 2048 * 2048 * 128 / (ms * 1e-3) / 1e12
+    gbs = (2 * 32 * 2048 * 128 * 2 + 32 * 2048 * 2048 * 2) / (ms * 1e-3) / 1e9
+    out["bmm_32x2048x128x2048"] = {"value": round(tf, 1), "unit": "TFLOP/s", "ms": round(ms, 5),
+                                   "roofline": roofline("hbm", gbs, "GB/s"),
+                                   "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+    del A3, B3
+    # config 3: causal SDPA B=1, H=32, D=128
+    for S in (2048, 4096):
+        q = torch.randn(1, 32, S, 128, device=dev).to(bf)
+        k = torch.randn_like(q)
+        v = torch.randn_like(q)
+        ms = graph_time_ms(torch, lambda: ops.sdpa(q, k, v, is_causal=True), steps, warmup)
+        tf = 0.5 * 4 * 32 * S * S * 128 / (ms * 1e-3) / 1e12
+        out[f"sdpa_causal_S{S}"] = {"value": round(tf, 1), "unit": "TFLOP/s", "ms": round(ms, 5),
+                                    "roofline": roofline("mfma", tf, "TFLOP/s")}
+    # config 3b: decode SDPA, S_q = 1 over a 4096-token KV cache
+    qd = torch.randn(1, 32, 1, 128, device=dev).to(bf)
+    kc = torch.randn(1, 32, 4096, 128, device=dev).to(bf)
+    vc = torch.randn_like(kc)
+    ms = graph_time_ms(torch, lambda: ops.sdpa(qd, kc, vc), steps, warmup)
+    gbs = 2 * 32 * 4096 * 128 * 2 / (ms * 1e-3) / 1e9
+    out["sdpa_decode_kv4096"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 5),
+                                 "roofline": roofline("hbm", gbs, "GB/s")}
+    # sampling tail: softmax + top-1 / top-50 over a [1, 32000] fp32 logit row
+    logits = torch.randn(1, 32000, device=dev)
+    ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 1), steps, warmup)
+    out["sampling_softmax_top1_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
+    ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 50), steps, warmup)
+    out["sampling_softmax_top50_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the kuiops hot "
+              "path has no multi-GPU code -- run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from kuillm_amd import compile as _compile
+    from kuillm_amd import ops
+    _compile.load_library()                 # fails loudly when libkuiops.so is missing
+    dev = torch.device("cuda:0")
+
+    # ---- headline: BASELINE config 2, bf16 addmm 4096^3 with a 1-D bias
+    g = torch.Generator(device=dev).manual_seed(0)
+    A = torch.randn(4096, 4096, device=dev, generator=g).to(torch.bfloat16)
+    B = (torch.randn(4096, 4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    ms = graph_time_ms(torch, lambda: ops.addmm(bias, A, B), args.steps, args.warmup)
+    flops = 2 * 4096 ** 3
+    tflops = flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "bf16 TFLOP/s (GEMM, SDPA) + decode tokens/s, % of MI355X roofline",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) / N(0,0.02) tensors, resident in HBM)",
+        "config": {"workload": "prefill addmm bf16 bias[4096] + A[4096,4096] @ B[4096,4096], fp32 accumulate",
+                   "M": 4096, "N": 4096, "K": 4096, "b_layout": "row-major [K,N]", "parallelism": "single GPU"},
+        "roofline": roofline("mfma", tflops, "TFLOP/s"),
+    }
+    del A, B, bias
+    if not args.no_extra:
+        line["workloads"] = extra_workloads(torch, ops, args.steps, args.warmup, dev)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -439,32 +439,40 @@ __global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
     }
 }
 
-// One wave per query row: merge the split states in split order.
+// One work-group per query row: wave 0 turns the split maxima into weights
+// (splits <= 64, one per lane), then thread d sums weight * o[split][d] over
+// the splits in split order.
 template <typename T, int HD>
-__global__ __launch_bounds__(64) void fa_decode_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(128) void fa_decode_combine_kernel(AttnArgs a) {
     const int64_t grow = blockIdx.x;            // (b * hq + head) * l + qi
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
     const int64_t qi = grow % a.l, bh = grow / a.l;
     const int64_t head = bh % a.hq, b = bh / a.hq;
-    float M = -INFINITY;
-    for (int z = 0; z < a.splits; ++z) M = fmaxf(M, a.ws_ml[(grow * a.splits + z) * 2]);
-    const float Mu = (M == -INFINITY) ? 0.f : M;
-    constexpr int PER = HD / 64;
-    float acc[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) acc[i] = 0.f;
-    float L = 0.f;
-    for (int z = 0; z < a.splits; ++z) {
-        const float w = fast_exp2(a.ws_ml[(grow * a.splits + z) * 2] - Mu);
-        L += w * a.ws_ml[(grow * a.splits + z) * 2 + 1];
-#pragma unroll
-        for (int i = 0; i < PER; ++i) acc[i] += w * a.ws_o[(grow * a.splits + z) * HD + lane + 64 * i];
+    __shared__ float s_w[64];
+    __shared__ float s_M, s_L;
+    const float *ml = a.ws_ml + grow * a.splits * 2;
+    if (tid < 64) {
+        const float mz = tid < a.splits ? ml[2 * tid] : -INFINITY;
+        const float lz = tid < a.splits ? ml[2 * tid + 1] : 0.f;
+        const float M = wave_max(mz);
+        const float Mu = (M == -INFINITY) ? 0.f : M;
+        const float w = tid < a.splits ? fast_exp2(mz - Mu) : 0.f;
+        s_w[tid] = w;
+        const float L = wave_sum(w * lz);
+        if (tid == 0) { s_M = M; s_L = L; }
     }
+    __syncthreads();
+    const float L = s_L, M = s_M;
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) Op[lane + 64 * i] = from_f32<T>(acc[i] * inv);
-    if (a.lse && lane == 0) a.lse[grow] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+    if (tid < HD) {
+        const float *o = a.ws_o + grow * a.splits * HD + tid;
+        float acc = 0.f;
+#pragma unroll 8
+        for (int z = 0; z < a.splits; ++z) acc += s_w[z] * o[z * HD];
+        T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
+        Op[tid] = from_f32<T>(acc * inv);
+    }
+    if (a.lse && tid == 0) a.lse[grow] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
 }
 
 // ------------------------------------------------------------ host side
@@ -504,7 +512,7 @@ static void fill_args(AttnArgs &a, int64_t n, int64_t hq, int64_t hkv, int64_t l
 // Keys per split for the decode kernel: enough splits to fill the GPU, at
 // least 64 keys each.
 static int64_t decode_chunk(int64_t s) {
-    int64_t c = cdiv(cdiv(s, 32), 64) * 64;
+    int64_t c = cdiv(cdiv(s, 32), 64) * 64;   // at most 32 splits (combine handles 64)
     return c < 64 ? 64 : c;
 }
 
@@ -541,7 +549,7 @@ static int launch_decode(AttnArgs a, hipStream_t st) {
         case 4: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 4>), grid, dim3(256), 0, st, a); break;
         default: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 8>), grid, dim3(256), 0, st, a); break;
     }
-    hipLaunchKernelGGL((fa_decode_combine_kernel<T, HD>), dim3((unsigned)(a.n * a.hq * a.l)), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((fa_decode_combine_kernel<T, HD>), dim3((unsigned)(a.n * a.hq * a.l)), dim3(128), 0, st, a);
     return launch_status();
 }
 

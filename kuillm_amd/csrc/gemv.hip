@@ -13,10 +13,12 @@
 //     K-contiguous W ([N, K] storage): the same operand is one 16-byte load.
 //   * A work-group is 4 waves on one strip, interleaving their K steps; the
 //     four partial tiles are summed through LDS in wave order.
-//   * `splits` work-groups share a strip.  Each writes its fp32 partial to the
-//     workspace; the last to arrive (per-strip counter) sums the partials in
-//     split order 0..splits-1, adds the bias, converts and stores, then resets
-//     the counter to zero.  The result is independent of arrival order.
+//   * `splits` work-groups share a strip.  Each writes its fp32 partial tile to
+//     the workspace and a second kernel sums the partials in split order
+//     0..splits-1, adds the bias and converts, so the result is bitwise
+//     repeatable.  (Reducing in the last-arriving work-group instead would
+//     need device-scope fences, which on a chip with one L2 per XCD write
+//     back that L2.)
 #include "common.hpp"
 
 namespace kuiops {
@@ -30,7 +32,6 @@ struct GemvArgs {
     int splits;
     int64_t k_per_split;      // multiple of 128
     float *partial;           // [splits][M][N]
-    unsigned int *counters;   // [strips], zero between launches
 };
 
 constexpr int kGemvStrip = 128;
@@ -53,6 +54,7 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvArgs a) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc[mb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+#pragma unroll 2
     for (int64_t k0 = kbeg + (int64_t)wave * 32; k0 < kend; k0 += 4 * 32) {
         const int64_t kl = k0 + lg * 8;          // first of this lane's 8 k values
         const bool kin = kl < kend;               // K % 8 == 0: all 8 in or out
@@ -126,50 +128,51 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvArgs a) {
         return;
     }
 
+    // Split partials: this work-group's fp32 tile goes to the workspace; the
+    // reduce kernel sums the splits in order.
     const int64_t MN = a.M * a.N;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
         const int64_t row = mb * 16 + lg * 4 + wave;
         if (row >= a.M || !col_ok) continue;
-        float *dst = a.partial + split * MN + row * a.N;
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-            if (col0 + c < a.N) dst[col0 + c] = part[mb][c];
-    }
-    __threadfence();
-    __syncthreads();
-    __shared__ int s_last;
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&a.counters[strip], 1u);
-        s_last = (prev == (unsigned)(a.splits - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        const int64_t row = mb * 16 + lg * 4 + wave;
-        if (row >= a.M || !col_ok) continue;
-        float s[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) s[c] = 0.f;
-        for (int z = 0; z < a.splits; ++z) {
-            const float *src = a.partial + z * MN + row * a.N;
+        float *dst = a.partial + split * MN + row * a.N + col0;
+        if (col0 + 8 <= a.N) {
+            *reinterpret_cast<f32x4 *>(dst) = f32x4{part[mb][0], part[mb][1], part[mb][2], part[mb][3]};
+            *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{part[mb][4], part[mb][5], part[mb][6], part[mb][7]};
+        } else {
 #pragma unroll
             for (int c = 0; c < 8; ++c)
-                if (col0 + c < a.N) s[c] += src[col0 + c];
-        }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const int64_t col = col0 + c;
-            if (col >= a.N) break;
-            float v = s[c];
-            if (a.bias) v += to_f32(reinterpret_cast<const T *>(a.bias)[col]);
-            reinterpret_cast<Tout *>(a.out)[row * a.ldo + col] = from_f32<Tout>(v);
+                if (col0 + c < a.N) dst[c] = part[mb][c];
         }
     }
-    if (tid == 0) atomicExch(&a.counters[strip], 0u);
+}
+
+// out[m, n] = sum_{z = 0..splits-1} partial[z, m, n] (+ bias[n]), summed in
+// split order; 4 adjacent columns per thread.
+template <typename T, typename Tout>
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvArgs a) {
+    const int64_t MN = a.M * a.N;
+    const int64_t nq = (a.N + 3) / 4;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < a.M * nq; t += (int64_t)gridDim.x * 256) {
+        const int64_t row = t / nq, col0 = (t - row * nq) * 4;
+        const float *src = a.partial + row * a.N + col0;
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        const int nc = (int)min((int64_t)4, a.N - col0);
+        if (nc == 4 && (a.N & 3) == 0) {
+            for (int z = 0; z < a.splits; ++z) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(src + z * MN);
+                s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
+            }
+        } else {
+            for (int z = 0; z < a.splits; ++z)
+                for (int c = 0; c < nc; ++c) s[c] += src[z * MN + c];
+        }
+        for (int c = 0; c < nc; ++c) {
+            float v = s[c];
+            if (a.bias) v += to_f32(reinterpret_cast<const T *>(a.bias)[col0 + c]);
+            reinterpret_cast<Tout *>(a.out)[row * a.ldo + col0 + c] = from_f32<Tout>(v);
+        }
+    }
 }
 
 static int gemv_choose_splits(int64_t M, int64_t N, int64_t K) {
@@ -182,11 +185,9 @@ static int gemv_choose_splits(int64_t M, int64_t N, int64_t K) {
     return s < 1 ? 1 : (int)s;
 }
 
-static size_t counters_bytes(int64_t N) { return (size_t)cdiv(cdiv(N, kGemvStrip) * 4, 256) * 256; }
-
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     const int s = gemv_choose_splits(M, N, K);
-    return counters_bytes(N) + (s > 1 ? (size_t)s * M * N * sizeof(float) : 0);
+    return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
 template <typename T, typename Tout, int MB>
@@ -204,6 +205,11 @@ static int gemv_dispatch(const GemvArgs &a, bool wcol, hipStream_t st) {
         case 3: gemv_launch<T, Tout, 3>(a, wcol, st); break;
         case 4: gemv_launch<T, Tout, 4>(a, wcol, st); break;
         default: return KUIOPS_E_UNSUPPORTED;
+    }
+    if (a.splits > 1) {
+        int64_t blocks = cdiv(a.M * cdiv(a.N, 4), 256);
+        if (blocks > 2048) blocks = 2048;
+        hipLaunchKernelGGL((gemv_reduce_kernel<T, Tout>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     }
     return launch_status();
 }
@@ -238,10 +244,9 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
     a.splits = s;
     a.k_per_split = kps;
     if (s > 1) {
-        const size_t need = counters_bytes(N) + (size_t)s * M * N * sizeof(float);
-        if (!workspace || workspace_bytes < need) return KUIOPS_E_WORKSPACE;
-        a.counters = reinterpret_cast<unsigned int *>(workspace);
-        a.partial = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + counters_bytes(N));
+        const size_t need = (size_t)s * M * N * sizeof(float);
+        if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
+        a.partial = reinterpret_cast<float *>(workspace);
     }
     hipStream_t st = as_stream(stream);
     if (in_dtype == KUIOPS_BF16)

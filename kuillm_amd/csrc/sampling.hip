@@ -35,40 +35,116 @@ __device__ __forceinline__ void sm_merge(A &m, A &s, A m2, A s2) {
     m = M;
 }
 
+// Rows of at most 1024 elements: one wave per row, 4 rows per work-group,
+// the row held in registers (16 values per lane); one read, one write.
 template <typename T>
-__global__ __launch_bounds__(256) void softmax_kernel(int64_t n, const T *X, T *Y) {
+__global__ __launch_bounds__(256) void softmax_wave_kernel(int64_t m, int64_t n, const T *X, T *Y) {
+    typedef typename AccT<T>::type A;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const T *x = X + row * n;
+    T *y = Y + row * n;
+    A v[16];
+    A mx = -(A)INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int64_t i = lane + 64 * j;
+        v[j] = i < n ? (A)to_f32_or_self(x[i]) : -(A)INFINITY;
+        mx = v[j] > mx ? v[j] : mx;
+    }
+    // a NaN never wins `>`: carry it into the max explicitly so the row is NaN
+#pragma unroll
+    for (int j = 0; j < 16; ++j) if (v[j] != v[j]) mx = v[j];
+    mx = wave_max(mx);
+    A sum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        v[j] = acc_exp(v[j] - mx);
+        if (lane + 64 * j < n) sum += v[j];
+    }
+    sum = wave_sum(sum);
+    const A inv = (A)1 / sum;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int64_t i = lane + 64 * j;
+        if (i < n) y[i] = (T)(v[j] * inv);
+    }
+}
+
+// Longer rows: one 1024-thread work-group per row.  Rows of at most
+// 32 * 1024 elements stay in registers (one read); longer rows use an online
+// (max, sum) pass and a second read.
+constexpr int kSmThreads = 1024;
+constexpr int kSmCache = 32;
+
+template <typename T>
+__global__ __launch_bounds__(kSmThreads) void softmax_row_kernel(int64_t n, const T *X, T *Y) {
     typedef typename AccT<T>::type A;
     const int64_t row = blockIdx.x;
     const T *x = X + row * n;
     T *y = Y + row * n;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ A s_a[kSmThreads / 64], s_b[kSmThreads / 64];
+    const bool cached = n <= (int64_t)kSmThreads * kSmCache;
+    A v[kSmCache];
     A m = -(A)INFINITY, s = 0;
-    for (int64_t i = tid; i < n; i += 256) {
-        const A v = (A)to_f32_or_self(x[i]);
-        if (v > m) {
-            s = (m == -(A)INFINITY ? (A)0 : s * acc_exp(m - v)) + (A)1;
-            m = v;
-        } else if (v != -(A)INFINITY) {
-            s += acc_exp(v - m);     // NaN propagates into s
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < kSmCache; ++j) {
+            const int64_t i = tid + (int64_t)kSmThreads * j;
+            v[j] = i < n ? (A)to_f32_or_self(x[i]) : -(A)INFINITY;
+            m = (v[j] > m || v[j] != v[j]) ? v[j] : m;
+        }
+        m = wave_max(m);
+        if (lane == 0) s_a[wave] = m;
+        __syncthreads();
+        m = s_a[0];
+#pragma unroll
+        for (int w = 1; w < kSmThreads / 64; ++w) m = (s_a[w] > m || s_a[w] != s_a[w]) ? s_a[w] : m;
+#pragma unroll
+        for (int j = 0; j < kSmCache; ++j) {
+            v[j] = acc_exp(v[j] - m);
+            if (tid + (int64_t)kSmThreads * j < n) s += v[j];
+        }
+        s = wave_sum(s);
+        if (lane == 0) s_b[wave] = s;
+        __syncthreads();
+        s = 0;
+#pragma unroll
+        for (int w = 0; w < kSmThreads / 64; ++w) s += s_b[w];
+        const A inv = (A)1 / s;
+#pragma unroll
+        for (int j = 0; j < kSmCache; ++j) {
+            const int64_t i = tid + (int64_t)kSmThreads * j;
+            if (i < n) y[i] = (T)(v[j] * inv);
+        }
+        return;
+    }
+    for (int64_t i = tid; i < n; i += kSmThreads) {
+        const A e = (A)to_f32_or_self(x[i]);
+        if (e > m) {
+            s = (m == -(A)INFINITY ? (A)0 : s * acc_exp(m - e)) + (A)1;
+            m = e;
+        } else if (e != -(A)INFINITY) {
+            s += acc_exp(e - m);     // NaN propagates into s
         }
     }
-    // NaN inputs: keep NaN in m so the whole row becomes NaN, as aten does.
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
         const A m2 = __shfl_xor(m, off, 64), s2 = __shfl_xor(s, off, 64);
         if (lane & off) { A mm = m2, ss = s2; sm_merge(mm, ss, m, s); m = mm; s = ss; }
         else sm_merge(m, s, m2, s2);
     }
-    __shared__ A sm_m[4], sm_s[4];
-    if (lane == 0) { sm_m[wave] = m; sm_s[wave] = s; }
+    if (lane == 0) { s_a[wave] = m; s_b[wave] = s; }
     __syncthreads();
-    A M = sm_m[0], S = sm_s[0];
+    A M = s_a[0], S = s_b[0];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) sm_merge(M, S, sm_m[w], sm_s[w]);
+    for (int w = 1; w < kSmThreads / 64; ++w) sm_merge(M, S, s_a[w], s_b[w]);
     const A inv = (A)1 / S;
-    for (int64_t i = tid; i < n; i += 256) {
-        const A v = (A)to_f32_or_self(x[i]);
-        y[i] = (T)(acc_exp(v - M) * inv);
+    for (int64_t i = tid; i < n; i += kSmThreads) {
+        const A e = (A)to_f32_or_self(x[i]);
+        y[i] = (T)(acc_exp(e - M) * inv);
     }
 }
 
@@ -199,26 +275,32 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(int64_t n, int k, co
     const int n_eq_take = s_remaining;        // keys == thr to take (lowest indices)
     const int n_gt = k - n_eq_take;
 
-    // Gather selected (key, index) in index order.
-    int gt_base = 0, eq_base = 0;
-    for (int64_t base = 0; base < n; base += kTopkThreads) {
-        const int64_t i = base + tid;
-        uint32_t key = 0;
-        int is_gt = 0, is_eq = 0;
-        if (i < n) {
-            key = order_key(load_f(x + i), lg);
-            is_gt = key > thr;
-            is_eq = key == thr;
+    // Gather the selected (key, index) pairs in index order: thread t owns the
+    // contiguous segment [t * per, (t + 1) * per); two block scans of the
+    // per-thread counts place them.
+    {
+        const int64_t per = (n + kTopkThreads - 1) / kTopkThreads;
+        const int64_t lo = (int64_t)tid * per, hi = min(n, lo + per);
+        int cgt = 0, ceq = 0;
+        for (int64_t i = lo; i < hi; ++i) {
+            const uint32_t key = order_key(load_f(x + i), lg);
+            cgt += key > thr;
+            ceq += key == thr;
         }
-        int tot_gt, tot_eq;
-        const int pg = block_excl_scan(is_gt, s_scan, tot_gt);
-        const int pe = block_excl_scan(is_eq, s_scan, tot_eq);
-        const uint64_t comp = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
-        if (is_gt) s_sel[gt_base + pg] = comp;
-        if (is_eq && eq_base + pe < n_eq_take) s_sel[n_gt + eq_base + pe] = comp;
-        gt_base += tot_gt;
-        eq_base += tot_eq;
-        if (gt_base >= n_gt && eq_base >= n_eq_take) break;   // uniform across the block
+        // Tie counts only matter below n_eq_take <= 1024: clamping each thread's
+        // count to 1024 keeps every prefix exact below 1024 and >= 1024 above.
+        int total;
+        int pg = block_excl_scan(cgt, s_scan, total);
+        int pe = block_excl_scan(min(ceq, kTopkMaxK), s_scan, total);
+        for (int64_t i = lo; i < hi; ++i) {
+            const uint32_t key = order_key(load_f(x + i), lg);
+            const uint64_t comp = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
+            if (key > thr) s_sel[pg++] = comp;
+            else if (key == thr) {
+                if (pe < n_eq_take) s_sel[n_gt + pe] = comp;
+                ++pe;
+            }
+        }
     }
     __syncthreads();
 
@@ -255,18 +337,27 @@ size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
 
 using namespace kuiops;
 
+template <typename T>
+static void softmax_launch(int64_t m, int64_t n, const void *X, void *Y, hipStream_t st) {
+    if (n <= 1024)
+        hipLaunchKernelGGL(softmax_wave_kernel<T>, dim3((unsigned)cdiv(m, 4)), dim3(256), 0, st, m, n,
+                           (const T *)X, (T *)Y);
+    else
+        hipLaunchKernelGGL(softmax_row_kernel<T>, dim3((unsigned)m), dim3(kSmThreads), 0, st, n,
+                           (const T *)X, (T *)Y);
+}
+
 extern "C" int kuiops_softmax_lastdim(int64_t m, int64_t n, int dtype, const void *X, void *Y, void *stream) {
     if (m < 0 || n < 0) return KUIOPS_E_INVALID;
     if (m == 0 || n == 0) return KUIOPS_OK;
     if (!X || !Y) return KUIOPS_E_INVALID;
     if (m > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     hipStream_t st = as_stream(stream);
-    dim3 grid((unsigned)m), block(256);
     switch (dtype) {
-        case KUIOPS_F32: hipLaunchKernelGGL(softmax_kernel<float>, grid, block, 0, st, n, (const float *)X, (float *)Y); break;
-        case KUIOPS_BF16: hipLaunchKernelGGL(softmax_kernel<bf16_t>, grid, block, 0, st, n, (const bf16_t *)X, (bf16_t *)Y); break;
-        case KUIOPS_F16: hipLaunchKernelGGL(softmax_kernel<f16_t>, grid, block, 0, st, n, (const f16_t *)X, (f16_t *)Y); break;
-        case KUIOPS_F64: hipLaunchKernelGGL(softmax_kernel<double>, grid, block, 0, st, n, (const double *)X, (double *)Y); break;
+        case KUIOPS_F32: softmax_launch<float>(m, n, X, Y, st); break;
+        case KUIOPS_BF16: softmax_launch<bf16_t>(m, n, X, Y, st); break;
+        case KUIOPS_F16: softmax_launch<f16_t>(m, n, X, Y, st); break;
+        case KUIOPS_F64: softmax_launch<double>(m, n, X, Y, st); break;
         default: return KUIOPS_E_UNSUPPORTED;
     }
     return launch_status();

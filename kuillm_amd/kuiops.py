@@ -1,0 +1,359 @@
+"""Operator families: for each aten op, decide whether a kuiops kernel serves
+the call (``supported``) and run it (``run``).
+
+Same contract as the reference's families (kuipy/kuiops.py:27-43):
+
+* ``supported(func, args, kwargs) -> spec | None`` is pure and cheap (no GPU
+  work) and works on fake tensors too, so the Inductor pass can reuse it;
+* ``run(spec, args, kwargs) -> result`` returns what the aten op returns, or
+  ``None`` when the native gate refuses the call after all (the caller then
+  falls through to stock PyTorch);
+* ``tune_key`` / ``tune_params`` / ``tune(all)`` carry autotune parameters.
+
+The gates are wider than the reference's: the reference needs M, N multiples
+of 64 and 2-D addmm biases (kuipy/kuiops.py:365-394, 538-540) and rejects
+causal SDPA (:636-637); the kernels here take any shape, 1-D biases, causal
+and grouped-query attention, and add topk / index, which the reference never
+implemented (kuiops/topk/.gitkeep, kuiops/index/.gitkeep).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from . import ops
+from .config import log
+
+aten = torch.ops.aten
+
+_FLOAT_DTYPES = (torch.float16, torch.float32, torch.float64, torch.bfloat16)
+_HALF = (torch.float16, torch.bfloat16)
+_SIZE_LIMIT = 2 ** 31 - 1
+
+
+def _scalar(x):
+    """A Python scalar (or 0-d fp64 tensor) argument, else None
+    (kuipy/kuiops.py:14-21)."""
+    if isinstance(x, bool):
+        return None
+    if isinstance(x, (float, int)):
+        return x
+    if isinstance(x, torch.Tensor) and x.dim() == 0 and x.dtype == torch.float64 and not x.is_meta:
+        return float(x.item())
+    return None
+
+
+def _norm_dim(d, rank):
+    return d + rank if d < 0 else d
+
+
+def _is_dev(*ts):
+    return all(isinstance(t, torch.Tensor) and t.is_cuda for t in ts)
+
+
+class _Family:
+    tune_key = ""
+    tune_params = ()
+
+    def __init__(self, all_tune_params):
+        self.tune_params = all_tune_params.get(self.tune_key, self.tune_params)
+
+    def tune(self, all_tune_params):
+        all_tune_params[self.tune_key] = self.tune_params
+        return all_tune_params
+
+    def __repr__(self):
+        return f"{type(self).__name__}({self.tune_params!r})"
+
+
+# ---------------------------------------------------------------- GEMM
+
+class MmImpl(_Family):
+    """aten.mm -> kuiops_mm (MFMA) / kuiops_gemv_splitk for M <= gemv_max_m
+    (reference MmImpl kuipy/kuiops.py:397-469)."""
+    tune_key = "MM"
+    tune_params = {"impl": "auto", "gemv_max_m": ops.GEMV_MAX_M}
+
+    def supported(self, func, args, kwargs):
+        if len(args) != 2 or kwargs.get("alpha", 1) != 1:
+            return None
+        A, B = args
+        if not (_is_dev(A, B) and A.dim() == 2 and B.dim() == 2 and A.dtype == B.dtype
+                and A.dtype in _FLOAT_DTYPES):
+            return None
+        M, K = (int(x) for x in A.shape)
+        K2, N = (int(x) for x in B.shape)
+        if K != K2 or max(M, N, K) > _SIZE_LIMIT:
+            return None
+        return (A.dtype, M, N, K, [A, B])
+
+    def run(self, spec, args, kwargs):
+        _, _, _, _, (A, B) = spec
+        try:
+            return ops.mm(A, B)
+        except _lib.Unsupported:
+            return None
+
+
+class AddmmImpl(_Family):
+    """aten.addmm -> kuiops_addmm with a full or row-broadcast addend
+    (reference AddmmImpl kuipy/kuiops.py:520-564, which takes 2-D C only)."""
+    tune_key = "ADDMM"
+    tune_params = {"splitk": "auto"}
+
+    def supported(self, func, args, kwargs):
+        if len(args) != 3:
+            return None
+        Cin, A, B = args
+        if not (_is_dev(A, B, Cin) and A.dim() == 2 and B.dim() == 2 and Cin.dim() <= 2
+                and A.dtype == B.dtype == Cin.dtype and A.dtype in _FLOAT_DTYPES):
+            return None
+        M, K = (int(x) for x in A.shape)
+        K2, N = (int(x) for x in B.shape)
+        if K != K2:
+            return None
+        try:
+            torch.broadcast_shapes(tuple(Cin.shape), (M, N))
+        except RuntimeError:
+            return None
+        alpha = _scalar(kwargs.get("alpha", 1))
+        beta = _scalar(kwargs.get("beta", 1))
+        if alpha is None or beta is None:
+            return None
+        return (A.dtype, M, N, K, [Cin, A, B], float(alpha), float(beta))
+
+    def run(self, spec, args, kwargs):
+        _, _, _, _, (Cin, A, B), alpha, beta = spec
+        try:
+            return ops.addmm(Cin, A, B, beta=beta, alpha=alpha)
+        except _lib.Unsupported:
+            return None
+
+
+class BmmImpl(_Family):
+    """aten.bmm -> kuiops_bmm (reference BmmImpl kuipy/kuiops.py:475-511)."""
+    tune_key = "BMM"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) != 2:
+            return None
+        A, B = args
+        if not (_is_dev(A, B) and A.dim() == 3 and B.dim() == 3 and A.dtype == B.dtype
+                and A.dtype in _FLOAT_DTYPES):
+            return None
+        Bn, M, K = (int(x) for x in A.shape)
+        Bn2, K2, N = (int(x) for x in B.shape)
+        if Bn != Bn2 or K != K2 or Bn > 65535:
+            return None
+        return (A.dtype, [A, B])
+
+    def run(self, spec, args, kwargs):
+        try:
+            return ops.bmm(*spec[1])
+        except _lib.Unsupported:
+            return None
+
+
+# ------------------------------------------------------------ softmax
+
+class SoftmaxImpl(_Family):
+    """aten._softmax over the last dim (reference SoftmaxImpl
+    kuipy/kuiops.py:572-610)."""
+    tune_key = "SOFTMAX"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) != 3:
+            return None
+        X, dim, half_to_float = args
+        if not (_is_dev(X) and X.dtype in _FLOAT_DTYPES and not half_to_float):
+            return None
+        rank = X.dim()
+        if rank < 1 or _norm_dim(dim, rank) != rank - 1:
+            return None
+        n = int(X.shape[-1])
+        m = X.numel() // n if n else 0
+        if m > _SIZE_LIMIT:
+            return None
+        return (X.dtype, m, n, [X])
+
+    def run(self, spec, args, kwargs):
+        try:
+            return ops.softmax(spec[3][0])
+        except _lib.Unsupported:
+            return None
+
+
+# --------------------------------------------------------------- SDPA
+
+class SdpaImpl(_Family):
+    """aten._scaled_dot_product_efficient_attention and
+    _scaled_dot_product_flash_attention -> kuiops_sdpa_fwd / kuiops_sdpa_decode.
+
+    The reference family (kuipy/kuiops.py:621-681, disconnected at
+    kuipy/registry.py:27-28,59) needs a full additive bias and rejects
+    is_causal; here the bias must be absent (no masks beyond causal), and
+    causal, GQA head counts and decode shapes are served.  Returns the aten
+    output tuple with an fp32 (N, H, L) log-sum-exp."""
+    tune_key = "SDPA"
+    tune_params = {"decode_max_rows": 8}
+
+    def _parse(self, func, args, kwargs):
+        q, k, v = args[0], args[1], args[2]
+        if func == aten._scaled_dot_product_efficient_attention.default:
+            bias = args[3] if len(args) > 3 else kwargs.get("attn_bias")
+            need_lse = args[4] if len(args) > 4 else kwargs.get("compute_log_sumexp", False)
+            dropout = args[5] if len(args) > 5 else kwargs.get("dropout_p", 0.0)
+            causal = args[6] if len(args) > 6 else kwargs.get("is_causal", False)
+            debug = False
+        else:
+            bias = None
+            need_lse = True
+            dropout = args[3] if len(args) > 3 else kwargs.get("dropout_p", 0.0)
+            causal = args[4] if len(args) > 4 else kwargs.get("is_causal", False)
+            debug = args[5] if len(args) > 5 else kwargs.get("return_debug_mask", False)
+        return q, k, v, bias, bool(need_lse), float(dropout), bool(causal), bool(debug)
+
+    def supported(self, func, args, kwargs):
+        if len(args) < 3:
+            return None
+        q, k, v, bias, need_lse, dropout, causal, debug = self._parse(func, args, kwargs)
+        if bias is not None or dropout != 0.0 or debug:
+            return None
+        if not (_is_dev(q, k, v) and q.dim() == 4 and k.dim() == 4 and v.dim() == 4):
+            return None
+        if not (q.dtype == k.dtype == v.dtype and q.dtype in _HALF):
+            return None
+        n, hq, l, e = (int(x) for x in q.shape)
+        n2, hkv, s, e2 = (int(x) for x in k.shape)
+        n3, hkv3, s3, ev = (int(x) for x in v.shape)
+        if (n, e) != (n2, e2) or (n, hkv, s) != (n3, hkv3, s3) or hkv == 0 or hq % hkv:
+            return None
+        if e != ev or e not in (64, 128) or n > 65535 or hq > 65535:
+            return None
+        scale = kwargs.get("scale", None)
+        if scale is None:
+            scale = 1.0 / math.sqrt(e)
+        return (func, float(scale), causal, need_lse, [q, k, v])
+
+    def run(self, spec, args, kwargs):
+        func, scale, causal, need_lse, (q, k, v) = spec
+        try:
+            out, lse = ops.sdpa(q, k, v, is_causal=causal, scale=scale, return_lse=True,
+                                decode_max_rows=self.tune_params.get("decode_max_rows", 8)
+                                if isinstance(self.tune_params, dict) else 8)
+        except _lib.Unsupported:
+            return None
+        n, hq, l = out.shape[0], out.shape[1], out.shape[2]
+        empty = torch.empty([], dtype=torch.int64, device=q.device)
+        if func == aten._scaled_dot_product_efficient_attention.default:
+            if not need_lse:
+                lse = torch.empty((n, hq, 0), dtype=torch.float32, device=q.device)
+            return (out, lse, empty, empty)
+        none_t = torch.empty(0, dtype=torch.int32, device=q.device)
+        return (out, lse, none_t, none_t, int(l), int(k.shape[2]), empty, empty,
+                torch.empty(0, dtype=q.dtype, device=q.device))
+
+
+# ---------------------------------------------------- sampling: top-k
+
+class TopkImpl(_Family):
+    """aten.topk -> kuiops_topk_lastdim.  No reference kernel exists
+    (kuiops/topk/.gitkeep; KERNELS.md:58): the reference falls through to
+    aten.topk, which is what this matches (bit-exact on tie-free input)."""
+    tune_key = "TOPK"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) < 2:
+            return None
+        X, k = args[0], args[1]
+        dim = args[2] if len(args) > 2 else kwargs.get("dim", -1)
+        largest = args[3] if len(args) > 3 else kwargs.get("largest", True)
+        srt = args[4] if len(args) > 4 else kwargs.get("sorted", True)
+        if not (_is_dev(X) and X.dtype in (torch.float32, torch.bfloat16, torch.float16) and X.dim() >= 1):
+            return None
+        dim = _norm_dim(int(dim), X.dim())
+        n = int(X.shape[dim])
+        k = int(k)
+        if not (1 <= k <= min(n, 1024)) or n >= 2 ** 32 - 1:
+            return None
+        return (X, k, dim, bool(largest), bool(srt))
+
+    def run(self, spec, args, kwargs):
+        X, k, dim, largest, srt = spec
+        try:
+            return ops.topk(X, k, dim=dim, largest=largest, sorted=srt)
+        except _lib.Unsupported:
+            return None
+
+
+# ------------------------------------------------- gather / index
+
+class GatherImpl(_Family):
+    """aten.gather -> kuiops_gather (reference GatherImpl kuipy/kuiops.py:711-754;
+    its ``shape_le`` gate is relaxed to aten's: only the non-gather axes of
+    the index must fit the input)."""
+    tune_key = "GATHER"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) < 3 or kwargs.get("sparse_grad", False):
+            return None
+        Inp, dim, Idx = args[0], args[1], args[2]
+        if not (_is_dev(Inp, Idx) and Idx.dtype == torch.int64):
+            return None
+        rank = Inp.dim()
+        if Idx.dim() != rank or rank < 1 or rank > 8:
+            return None
+        dim = _norm_dim(int(dim), rank)
+        if not (0 <= dim < rank) or Inp.element_size() not in (1, 2, 4, 8):
+            return None
+        if any(int(Idx.shape[d]) > int(Inp.shape[d]) for d in range(rank) if d != dim):
+            return None
+        return (dim, [Inp, Idx])
+
+    def run(self, spec, args, kwargs):
+        dim, (Inp, Idx) = spec
+        try:
+            return ops.gather(Inp, dim, Idx)
+        except _lib.Unsupported:
+            return None
+
+
+class IndexImpl(_Family):
+    """aten.index.Tensor with exactly one int64 index tensor -> kuiops_index
+    (embedding-row gathers; no reference kernel, kuiops/index/.gitkeep)."""
+    tune_key = "INDEX"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) != 2:
+            return None
+        X, indices = args
+        if not _is_dev(X) or X.element_size() not in (1, 2, 4, 8):
+            return None
+        pos = [i for i, t in enumerate(indices) if t is not None]
+        if len(pos) != 1:
+            return None
+        d = pos[0]
+        idx = indices[d]
+        if not (isinstance(idx, torch.Tensor) and idx.dtype == torch.int64 and idx.is_cuda):
+            return None
+        if d >= X.dim():
+            return None
+        return (d, [X, idx])
+
+    def run(self, spec, args, kwargs):
+        d, (X, idx) = spec
+        try:
+            return ops.index(X, d, idx)
+        except _lib.Unsupported:
+            return None
+
+
+ALL_FAMILIES = (MmImpl, AddmmImpl, BmmImpl, SoftmaxImpl, SdpaImpl, TopkImpl, GatherImpl, IndexImpl)
+log(f"kuiops families: {[f.__name__ for f in ALL_FAMILIES]}")

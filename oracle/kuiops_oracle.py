@@ -171,7 +171,7 @@ def sdpa(q, k, v, causal=False, scale=None, bias=None, align="top_left"):
         j = np.arange(s)[None, :]
         visible = j <= i if align == "top_left" else j <= (s - l + i)
         sc = np.where(visible, sc, -np.inf)
-    m = np.max(sc, axis=-1, keepdims=True)
+    m = np.max(sc, axis=-1, keepdims=True, initial=-np.inf)
     m_safe = np.where(np.isfinite(m), m, 0.0)
     p = np.exp(sc - m_safe)
     denom = np.sum(p, axis=-1, keepdims=True)

@@ -1,0 +1,105 @@
+"""The C ABI library: loads, exports every symbol include/kuiops.h declares,
+and validates arguments on the host (no kernel launches, no GPU needed)."""
+import ctypes
+import re
+
+import pytest
+
+from kuillm_amd import _lib, compile as _compile, config as C
+
+HEADER = C.INCLUDE / "kuiops.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"KUIOPS_API\s+[\w\s\*]*?\b(kuiops_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not C.LIB_PATH.exists():
+        _compile.build_library()
+    return _lib.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    syms = declared_symbols()
+    for name in ("kuiops_mm", "kuiops_addmm", "kuiops_bmm", "kuiops_gemv_splitk", "kuiops_sdpa_fwd",
+                 "kuiops_sdpa_decode", "kuiops_softmax_lastdim", "kuiops_topk_lastdim", "kuiops_gather",
+                 "kuiops_index", "kuiops_query_workspace", "kuiops_status_string", "kuiops_abi_version"):
+        assert name in syms
+    # the ctypes table mirrors the header one to one
+    assert sorted(_lib.SIGNATURES) == syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(C.LIB_PATH))
+    for name in declared_symbols():
+        assert hasattr(raw, name), f"{name} not exported by {C.LIB_PATH.name}"
+
+
+def test_version_and_status_strings(lib):
+    assert lib.kuiops_abi_version() == 1
+    assert lib.kuiops_status_string(0) == b"ok"
+    assert b"unsupported" in lib.kuiops_status_string(-1)
+    assert b"invalid" in lib.kuiops_status_string(-2)
+    assert b"workspace" in lib.kuiops_status_string(-4)
+
+
+def test_workspace_queries(lib):
+    # gemv split-K partials: splits * M * N * 4 bytes, splits chosen from N and K
+    ws = lib.kuiops_query_workspace(_lib.OP_GEMV_SPLITK, 16, 11008, 4096)
+    assert ws > 0 and ws % (16 * 11008 * 4) == 0
+    assert lib.kuiops_query_workspace(_lib.OP_GEMV_SPLITK, 1, 11008, 4096) == ws // 16
+    # a 4096^3 GEMM fills the GPU without split-K
+    assert lib.kuiops_query_workspace(_lib.OP_ADDMM, 4096, 4096, 4096) == 0
+    # a few output tiles with a deep K do split
+    assert lib.kuiops_query_workspace(_lib.OP_ADDMM, 128, 128, 8192) > 0
+    assert lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, 32, 4096, 128) >= 32 * 32 * 130 * 4
+    assert lib.kuiops_query_workspace(99, 1, 1, 1) == 0
+    assert lib.kuiops_query_workspace(_lib.OP_ADDMM, -1, 1, 1) == 0
+
+
+def test_host_side_argument_validation(lib):
+    # invalid sizes are rejected before anything is enqueued
+    assert lib.kuiops_mm(-1, 4, 4, _lib.BF16, None, 4, None, 4, 0, _lib.BF16, None, 4, None) == _lib.E_INVALID
+    assert lib.kuiops_mm(4, 4, 4, _lib.BF16, None, 4, None, 4, 7, _lib.BF16, None, 4, None) == _lib.E_INVALID
+    assert lib.kuiops_mm(4, 4, 4, _lib.BF16, None, 4, None, 4, 0, _lib.BF16, None, 4, None) == _lib.E_INVALID
+    # empty problems are a no-op success
+    assert lib.kuiops_mm(0, 4, 4, _lib.BF16, None, 4, None, 4, 0, _lib.BF16, None, 4, None) == _lib.OK
+    assert lib.kuiops_softmax_lastdim(0, 10, _lib.F32, None, None, None) == _lib.OK
+    assert lib.kuiops_softmax_lastdim(-1, 10, _lib.F32, None, None, None) == _lib.E_INVALID
+    # gemv: M above 64 is outside the kernel
+    p = ctypes.c_void_p(16)
+    assert lib.kuiops_gemv_splitk(65, 8, 8, _lib.BF16, p, 8, p, 8, 0, None, _lib.BF16, p, 8, 0, None, 0,
+                                  None) == _lib.E_UNSUPPORTED
+    # gemv with a workspace that is too small
+    assert lib.kuiops_gemv_splitk(16, 11008, 4096, _lib.BF16, p, 4096, p, 11008, 0, None, _lib.BF16, p,
+                                  11008, 8, p, 16, None) == _lib.E_WORKSPACE
+    # topk: k > n is invalid, k > 1024 unsupported
+    assert lib.kuiops_topk_lastdim(1, 10, 11, _lib.F32, p, p, None, 1, 1, None, 0, None) == _lib.E_INVALID
+    assert lib.kuiops_topk_lastdim(1, 5000, 2000, _lib.F32, p, p, ctypes.cast(p, ctypes.POINTER(ctypes.c_int64)),
+                                   1, 1, None, 0, None) == _lib.E_UNSUPPORTED
+    # gather: rank out of range, dim out of range
+    shp = _lib.i64_array([2, 2])
+    assert lib.kuiops_gather(9, shp, shp, 0, 4, p, None, p, None, None) == _lib.E_INVALID
+    assert lib.kuiops_gather(2, shp, shp, 2, 4, p, None, p, None, None) == _lib.E_INVALID
+    # sdpa: head counts that do not divide, unsupported head dim
+    s3 = _lib.strides3(0, 0, 0)
+    assert lib.kuiops_sdpa_fwd(1, 3, 2, 4, 4, 64, 64, _lib.BF16, p, s3, p, s3, p, s3, p, s3, None, 1.0, 0,
+                               None) == _lib.E_INVALID
+    assert lib.kuiops_sdpa_fwd(1, 2, 2, 4, 4, 96, 96, _lib.BF16, p, s3, p, s3, p, s3, p, s3, None, 1.0, 0,
+                               None) == _lib.E_UNSUPPORTED
+
+
+def test_error_mapping():
+    with pytest.raises(_lib.Unsupported):
+        _lib.check("x", _lib.E_UNSUPPORTED)
+    with pytest.raises(_lib.KuiopsError):
+        _lib.check("x", _lib.E_HIP)
+    _lib.check("x", _lib.OK)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load(tmp_path / "libkuiops.so")

@@ -1,0 +1,125 @@
+"""Flash SDPA parity on the GPU against the fp64 numpy oracle and the aten
+golden fixtures.  Tolerance (north star): rel 1e-2 / abs 1e-2 elementwise on
+the output; the LSE (fp32) within 1e-3 absolute."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kuillm_amd import ops
+from oracle import kuiops_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def npy(t):
+    return t.detach().float().cpu().numpy()
+
+
+def gen(shape, dtype=torch.bfloat16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype)
+
+
+def close(out, ref, rtol=1e-2, atol=1e-2):
+    o = npy(out)
+    err = np.abs(o - ref) - (atol + rtol * np.abs(ref))
+    assert err.max() <= 0, f"max excess {err.max():.3e}"
+
+
+CASES = [  # n, hq, hkv, l, s, d, causal
+    (1, 2, 2, 128, 128, 128, False),
+    (1, 2, 2, 128, 128, 128, True),
+    (2, 4, 2, 200, 200, 64, True),
+    (1, 3, 3, 77, 300, 128, False),
+    (1, 4, 1, 65, 65, 64, True),
+    (2, 2, 2, 1, 1, 128, True),
+    (1, 2, 2, 300, 100, 64, True),       # more queries than keys: late rows see every key
+]
+
+
+@pytest.mark.parametrize("n,hq,hkv,l,s,d,causal", CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sdpa_fwd_vs_oracle(cuda, n, hq, hkv, l, s, d, causal, dtype):
+    q, k, v = gen((n, hq, l, d), dtype, 1), gen((n, hkv, s, d), dtype, 2), gen((n, hkv, s, d), dtype, 3)
+    out, lse = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda), is_causal=causal)
+    ref, lse_ref = O.sdpa(npy(q), npy(k), npy(v), causal=causal)
+    assert out.shape == (n, hq, l, d) and lse.shape == (n, hq, l) and lse.dtype == torch.float32
+    close(out, ref)
+    np.testing.assert_allclose(npy(lse), lse_ref, atol=1e-3, rtol=1e-4)
+
+
+def test_sdpa_golden(cuda, golden):
+    def tb(name):
+        return torch.from_numpy(golden[name].view(np.int16)).view(torch.bfloat16).to(cuda)
+    out, _ = ops.sdpa(tb("sdpa_bf16_Q"), tb("sdpa_bf16_K"), tb("sdpa_bf16_V"), is_causal=True)
+    close(out, golden["sdpa_bf16_out_causal"])
+    Q, K, V = (torch.from_numpy(golden[k]).to(cuda).to(torch.bfloat16) for k in ("sdpa_Q", "sdpa_K", "sdpa_V"))
+    # the golden head dim is 16: outside the kernels (head dim 64 / 128)
+    with pytest.raises(Exception):
+        ops.sdpa(Q, K, V)
+
+
+def test_sdpa_strided_views(cuda):
+    # (B, S, H, D) storage seen as (B, H, S, D): HF's layout, no copies needed
+    base = gen((2, 96, 4, 64), seed=4).to(cuda)
+    q = base.transpose(1, 2)
+    out, _ = ops.sdpa(q, q, q, is_causal=True)
+    ref, _ = O.sdpa(npy(q), npy(q), npy(q), causal=True)
+    close(out, ref)
+
+
+def test_sdpa_closed_forms(cuda):
+    q, k = gen((1, 2, 64, 128), seed=5).to(cuda), gen((1, 2, 256, 128), seed=6).to(cuda)
+    vrow = gen((1, 2, 1, 128), seed=7).to(cuda)
+    out, _ = ops.sdpa(q, k, vrow.expand(1, 2, 256, 128).contiguous())
+    close(out, np.broadcast_to(npy(vrow), out.shape))           # constant V -> V
+    v = gen((1, 2, 256, 128), seed=8).to(cuda)
+    out, _ = ops.sdpa(q, k, v, is_causal=True)
+    close(out[:, :, 0], npy(v[:, :, 0]))                        # causal row 0 -> V0
+
+
+@pytest.mark.parametrize("S", [2048, 4096])
+def test_sdpa_full_size_one_head(cuda, S):
+    """B=1, H=32, S, D=128 causal; heads 0 and 31 checked
+    against the oracle in full, every head for finiteness and row sums."""
+    torch.manual_seed(S)
+    q = torch.randn(1, 32, S, 128, device=cuda).to(torch.bfloat16)
+    k = torch.randn_like(q)
+    v = torch.randn_like(q)
+    out, lse = ops.sdpa(q, k, v, is_causal=True, scale=1 / math.sqrt(128))
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    for h in (0, 31):
+        ref, lref = O.sdpa(npy(q[:, h:h + 1]), npy(k[:, h:h + 1]), npy(v[:, h:h + 1]), causal=True)
+        close(out[:, h:h + 1], ref)
+        np.testing.assert_allclose(npy(lse[:, h:h + 1]), lref, atol=1e-3, rtol=1e-4)
+
+
+DECODE = [  # n, hq, hkv, l, s, d
+    (1, 32, 32, 1, 4096, 128),
+    (1, 32, 8, 1, 600, 64),
+    (2, 8, 2, 1, 77, 128),
+    (1, 4, 4, 1, 1, 64),
+]
+
+
+@pytest.mark.parametrize("n,hq,hkv,l,s,d", DECODE)
+def test_sdpa_decode_vs_oracle(cuda, n, hq, hkv, l, s, d):
+    q, k, v = gen((n, hq, l, d), seed=9), gen((n, hkv, s, d), seed=10), gen((n, hkv, s, d), seed=11)
+    out, lse = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda))          # non-causal -> split-KV kernel
+    ref, lref = O.sdpa(npy(q), npy(k), npy(v))
+    close(out, ref)
+    np.testing.assert_allclose(npy(lse), lref, atol=1e-3, rtol=1e-4)
+    again, _ = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda))
+    assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("l", [1, 2, 4])
+def test_sdpa_decode_bottom_right_causal(cuda, l):
+    # KV-cache decode step: the l new queries are the last l positions
+    q, k, v = gen((1, 32, l, 64), seed=12), gen((1, 8, 530, 64), seed=13), gen((1, 8, 530, 64), seed=14)
+    out, lse = ops.sdpa_decode(q.to(cuda), k.to(cuda), v.to(cuda), causal=True, return_lse=True)
+    ref, lref = O.sdpa(npy(q), npy(k), npy(v), causal=True, align="bottom_right")
+    close(out, ref)
+    np.testing.assert_allclose(npy(lse), lref, atol=1e-3, rtol=1e-4)

@@ -1,0 +1,202 @@
+"""GEMM parity on the GPU: mm / addmm / bmm / decode split-K against the numpy
+oracle on the same seeded inputs, the aten golden fixtures, and size-free
+properties at the BASELINE.json sizes.
+
+Tolerance (north star): bf16 / f16 results within rel 1e-2 / abs 1e-2 of the
+fp32-accumulate oracle, elementwise: |out - ref| <= 1e-2 + 1e-2 * |ref|.
+fp32 results: allclose(rtol=1e-3, atol=1e-3) as the reference's tests
+(tests/test_jit_ops.py:34-43)."""
+import numpy as np
+import pytest
+import torch
+
+from kuillm_amd import ops
+from oracle import kuiops_oracle as O
+
+pytestmark = pytest.mark.gpu
+RTOL = ATOL = 1e-2
+
+
+def npy(t):
+    return t.detach().float().cpu().numpy() if t.dtype != torch.float64 else t.detach().cpu().numpy()
+
+
+def gen(shape, dtype, scale=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def assert_tol(out, ref, dtype):
+    o = npy(out)
+    if dtype in (torch.float32, torch.float64):
+        np.testing.assert_allclose(o, ref, rtol=1e-3, atol=1e-3)
+    else:
+        err = np.abs(o - ref) - (ATOL + RTOL * np.abs(ref))
+        assert err.max() <= 0, f"max excess {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+SHAPES = [(64, 64, 64), (128, 128, 64), (256, 512, 320), (300, 260, 72), (129, 1000, 136), (96, 80, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_mm_vs_oracle(cuda, dtype, layout, M, N, K):
+    A = gen((M, K), dtype, seed=1)
+    B = gen((K, N), dtype, 0.5, seed=2)
+    ref = O.mm(npy(A), npy(B))
+    Bd = B.to(cuda) if layout == "row" else B.t().contiguous().to(cuda).t()
+    out = ops.mm(A.to(cuda), Bd)
+    assert out.dtype == dtype and out.shape == (M, N)
+    assert_tol(out, ref, dtype)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (17, 9, 13), (64, 64, 64)])
+def test_mm_f32_f64(cuda, M, N, K):
+    for dt in (torch.float32, torch.float64):
+        A, B = gen((M, K), dt, seed=3), gen((K, N), dt, seed=4)
+        out = ops.mm(A.to(cuda), B.to(cuda))
+        assert_tol(out, O.mm(npy(A), npy(B)), dt)
+
+
+def test_mm_golden(cuda, golden):
+    A, B = torch.from_numpy(golden["mm_f32_A"]), torch.from_numpy(golden["mm_f32_B"])
+    np.testing.assert_allclose(npy(ops.mm(A.to(cuda), B.to(cuda))), golden["mm_f32_C"], rtol=1e-3, atol=1e-3)
+    Ab = torch.from_numpy(golden["mm_bf16_A"].view(np.int16)).view(torch.bfloat16)
+    Bb = torch.from_numpy(golden["mm_bf16_B"].view(np.int16)).view(torch.bfloat16)
+    out = ops.mm(Ab.to(cuda), Bb.to(cuda))
+    assert_tol(out, golden["mm_bf16_C32"], torch.bfloat16)
+    # the kernel rounds the fp32 accumulator once: equal to the rounded oracle
+    # up to fp32 summation order (at most one bf16 ulp)
+    got = out.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.int32)
+    exp = O.f32_to_bf16_bits(golden["mm_bf16_C32"]).astype(np.int32)
+    assert np.abs(got - exp).max() <= 1
+
+
+def test_mm_closed_forms(cuda):
+    # integer-valued bf16 operands: every product and partial sum is exact in fp32
+    g = torch.Generator().manual_seed(5)
+    A = torch.randint(-4, 5, (256, 512), generator=g).to(torch.bfloat16)
+    B = torch.randint(-4, 5, (512, 384), generator=g).to(torch.bfloat16)
+    out = ops.mm(A.to(cuda), B.to(cuda)).float().cpu()
+    exact = A.double() @ B.double()
+    small = exact.abs() <= 256          # exactly representable in bf16
+    assert torch.equal(out[small], exact[small].float())
+    eye = torch.eye(512, dtype=torch.bfloat16)
+    assert torch.equal(ops.mm(A.to(cuda), eye.to(cuda)).cpu(), A)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("alpha,beta", [(1.0, 1.0), (0.5, 2.0)])
+def test_addmm_golden(cuda, golden, dtype, alpha, beta):
+    dt = "f32" if dtype == torch.float32 else "bf16"
+    tag = "11" if alpha == 1.0 else "052"
+
+    def t(name):
+        a = golden[f"addmm_{dt}_{name}"]
+        return (torch.from_numpy(a) if dt == "f32" else torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)).to(cuda)
+    A, B, C2, C1 = t("A"), t("B"), t("C2"), t("C1")
+    out2 = ops.addmm(C2, A, B, beta=beta, alpha=alpha)
+    out1 = ops.addmm(C1, A, B, beta=beta, alpha=alpha)
+    ref2 = O.addmm(npy(C2), npy(A), npy(B), alpha, beta)
+    ref1 = O.addmm(npy(C1), npy(A), npy(B), alpha, beta)
+    assert_tol(out2, ref2, dtype)
+    assert_tol(out1, ref1, dtype)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 8192), (64, 320, 4096), (256, 256, 2048)])
+def test_addmm_splitk_deterministic(cuda, M, N, K):
+    A, B = gen((M, K), torch.bfloat16, seed=6), gen((K, N), torch.bfloat16, 0.02, seed=7)
+    bias = gen((N,), torch.bfloat16, 0.02, seed=8)
+    Ad, Bd, bd = A.to(cuda), B.to(cuda), bias.to(cuda)
+    out = ops.addmm(bd, Ad, Bd)
+    again = ops.addmm(bd, Ad, Bd)
+    assert torch.equal(out, again)            # fixed-order split-K reduction
+    assert_tol(out, O.addmm(npy(bias), npy(A), npy(B)), torch.bfloat16)
+
+
+def test_addmm_config0_cpu_shape(cuda, golden):
+    # BASELINE config 0 (fp32 addmm, reduced columns) through the GPU kernels
+    x, W, b = (torch.from_numpy(golden[k]).to(cuda) for k in ("cfg0_x", "cfg0_W", "cfg0_b"))
+    np.testing.assert_allclose(npy(ops.addmm(b, x, W)), golden["cfg0_out"], rtol=1e-3, atol=1e-3)
+
+
+def test_addmm_full_size_prefill(cuda):
+    """A[4096,4096]~N(0,1), B~N(0,.02), bias[4096]: rows
+    sampled against the oracle, repeatability, and bias linearity."""
+    torch.manual_seed(0)
+    A = torch.randn(4096, 4096, device=cuda).to(torch.bfloat16)
+    B = (torch.randn(4096, 4096, device=cuda) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(4096, device=cuda) * 0.02).to(torch.bfloat16)
+    out = ops.addmm(bias, A, B)
+    assert torch.equal(out, ops.addmm(bias, A, B))
+    rows = torch.tensor([0, 1, 777, 2048, 4095])
+    ref = O.addmm(npy(bias), npy(A[rows]), npy(B))
+    assert_tol(out[rows], ref, torch.bfloat16)
+    # out(bias) - out(0) == bias up to output rounding
+    out0 = ops.mm(A, B)
+    d = (out.float() - out0.float() - bias.float()).abs()
+    assert d.max().item() <= 2 * 2 ** -8 * out0.float().abs().max().item() + 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_bmm_golden(cuda, golden, dtype):
+    dt = "f32" if dtype == torch.float32 else "bf16"
+
+    def t(name):
+        a = golden[f"bmm_{dt}_{name}"]
+        return (torch.from_numpy(a) if dt == "f32" else torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)).to(cuda)
+    out = ops.bmm(t("A"), t("B"))
+    assert out.shape == (5, 17, 13)
+    assert_tol(out, O.bmm(npy(t("A")), npy(t("B"))), dtype)
+
+
+@pytest.mark.parametrize("b,M,K,N", [(4, 64, 64, 64), (3, 130, 72, 200), (2, 256, 128, 512)])
+def test_bmm_vs_oracle(cuda, b, M, K, N):
+    A, B = gen((b, M, K), torch.bfloat16, seed=9), gen((b, K, N), torch.bfloat16, seed=10)
+    assert_tol(ops.bmm(A.to(cuda), B.to(cuda)), O.bmm(npy(A), npy(B)), torch.bfloat16)
+    # a K-contiguous B (transposed view) gives the same result
+    Bt = B.transpose(1, 2).contiguous().to(cuda).transpose(1, 2)
+    assert torch.equal(ops.bmm(A.to(cuda), Bt), ops.bmm(A.to(cuda), B.to(cuda)))
+
+
+def test_bmm_full_size(cuda):
+    """BASELINE config 2b: bmm 32 x [2048,128] x [128,2048]: sampled batches."""
+    torch.manual_seed(1)
+    A = torch.randn(32, 2048, 128, device=cuda).to(torch.bfloat16)
+    B = torch.randn(32, 128, 2048, device=cuda).to(torch.bfloat16)
+    out = ops.bmm(A, B)
+    for bi in (0, 31):
+        rows = slice(0, 2048, 97)
+        ref = O.mm(npy(A[bi, rows]), npy(B[bi]))
+        assert_tol(out[bi, rows], ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 33, 64])
+@pytest.mark.parametrize("layout", ["row", "col"])
+def test_decode_gemm_vs_oracle(cuda, M, layout):
+    """x[M,4096] @ W[4096,11008] (W~N(0,.02)), split-K."""
+    x = gen((M, 4096), torch.bfloat16, seed=11)
+    W = gen((4096, 11008), torch.bfloat16, 0.02, seed=12)
+    Wd = W.to(cuda) if layout == "row" else W.t().contiguous().to(cuda).t()
+    out = ops.mm(x.to(cuda), Wd)
+    assert torch.equal(out, ops.mm(x.to(cuda), Wd))          # bitwise repeatable
+    assert_tol(out, O.mm(npy(x), npy(W)), torch.bfloat16)
+
+
+def test_decode_gemm_bias_odd_shapes(cuda):
+    for (M, N, K) in [(3, 1000, 520), (1, 8, 8), (7, 4104, 4096)]:
+        x, W = gen((M, K), torch.bfloat16, seed=13), gen((K, N), torch.bfloat16, 0.1, seed=14)
+        b = gen((N,), torch.bfloat16, seed=15)
+        out = ops.addmm(b.to(cuda), x.to(cuda), W.to(cuda))
+        assert_tol(out, O.addmm(npy(b), npy(x), npy(W)), torch.bfloat16)
+        # fp32 output straight from the accumulator
+        o32 = ops.mm(x.to(cuda), W.to(cuda), out_dtype=torch.float32)
+        np.testing.assert_allclose(npy(o32), O.mm(npy(x), npy(W)), rtol=1e-4, atol=1e-4)
+
+
+def test_empty_and_degenerate(cuda):
+    A = torch.zeros(0, 8, device=cuda, dtype=torch.bfloat16)
+    assert ops.mm(A, torch.zeros(8, 4, device=cuda, dtype=torch.bfloat16)).shape == (0, 4)
+    z = ops.mm(torch.zeros(3, 0, device=cuda, dtype=torch.bfloat16), torch.zeros(0, 5, device=cuda, dtype=torch.bfloat16))
+    assert z.shape == (3, 5) and not z.any()

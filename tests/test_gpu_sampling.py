@@ -1,0 +1,143 @@
+"""Sampling tail parity on the GPU: softmax (tolerance), topk / gather /
+index (bit-exact) against the oracle and the aten golden fixtures."""
+import numpy as np
+import pytest
+import torch
+
+from kuillm_amd import ops
+from oracle import kuiops_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def npy(t):
+    return t.detach().cpu().numpy() if t.dtype not in (torch.bfloat16,) else t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("shape", [(128, 64), (8, 5, 33), (4, 32000), (2, 1025), (3, 40000), (1, 1)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
+def test_softmax_vs_oracle(cuda, shape, dtype):
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(*shape, generator=g) * 3).to(dtype)
+    out = ops.softmax(x.to(cuda))
+    ref = O.softmax(npy(x).astype(np.float64))
+    tol = 1e-3 if dtype == torch.bfloat16 else 1e-6
+    np.testing.assert_allclose(npy(out).astype(np.float64), ref, rtol=1e-2 if dtype == torch.bfloat16 else 1e-5,
+                               atol=tol)
+    np.testing.assert_allclose(npy(out).astype(np.float64).sum(-1), 1.0, atol=1e-3 if dtype != torch.bfloat16 else 3e-2)
+
+
+def test_softmax_golden(cuda, golden):
+    for tag in ("128x64", "8x5x33"):
+        out = ops.softmax(torch.from_numpy(golden[f"softmax_{tag}_X"]).to(cuda))
+        np.testing.assert_allclose(npy(out), golden[f"softmax_{tag}_Y"], rtol=1e-5, atol=1e-6)
+
+
+def test_softmax_special_values(cuda):
+    x = torch.tensor([[0.0, float("-inf"), 1.0, float("-inf")],
+                      [float("nan"), 0.0, 1.0, 2.0],
+                      [5.0, 5.0, 5.0, 5.0]], device=cuda)
+    out = ops.softmax(x).cpu()
+    ref = torch.softmax(x.cpu(), -1)
+    assert torch.allclose(out[0], ref[0]) and out[0, 1] == 0
+    assert torch.isnan(out[1]).all() and torch.isnan(ref[1]).all()
+    assert torch.allclose(out[2], torch.full((4,), 0.25))
+    big = torch.full((1, 50000), float("-inf"), device=cuda)
+    big[0, 1234] = 3.0
+    out = ops.softmax(big)
+    assert out[0, 1234] == 1 and out.sum() == 1
+
+
+def test_topk_golden(cuda, golden):
+    X = torch.from_numpy(golden["topk_X"]).to(cuda)
+    for kk in (1, 5, 64, 300):
+        v, i = ops.topk(X, kk)
+        assert np.array_equal(npy(v), golden[f"topk_{kk}_v"]) and np.array_equal(npy(i), golden[f"topk_{kk}_i"])
+        v, i = ops.topk(X, kk, largest=False)
+        assert np.array_equal(npy(v), golden[f"topk_{kk}_sv"]) and np.array_equal(npy(i), golden[f"topk_{kk}_si"])
+
+
+def tie_free_rows(m, n, dtype, seed):
+    """m rows of n distinct values, exactly representable in `dtype`."""
+    g = torch.Generator().manual_seed(seed)
+    if dtype == torch.bfloat16:
+        # distinct finite non-zero bf16 bit patterns of both signs
+        pats = torch.cat([torch.arange(1, 0x7F80), torch.arange(0x8001, 0xFF80)])
+        rows = [pats[torch.randperm(pats.numel(), generator=g)[:n]] for _ in range(m)]
+        return torch.stack(rows).to(torch.int16).view(torch.bfloat16)
+    vals = (torch.arange(n, dtype=torch.float32) - n / 2) / 1024
+    return torch.stack([vals[torch.randperm(n, generator=g)] for _ in range(m)])
+
+
+@pytest.mark.parametrize("m,n,k,dtype", [
+    (1, 32000, 1, torch.float32), (4, 32000, 50, torch.float32), (3, 1000, 1000, torch.float32),
+    (16, 777, 7, torch.float32), (2, 100000, 20, torch.float32),
+    (1, 32000, 1, torch.bfloat16), (4, 32000, 50, torch.bfloat16), (3, 1000, 1000, torch.bfloat16)])
+def test_topk_vs_oracle(cuda, m, n, k, dtype):
+    x = tie_free_rows(m, n, dtype, seed=n + k)
+    for largest in (True, False):
+        v, i = ops.topk(x.to(cuda), k, largest=largest)
+        rv, ri = O.topk(npy(x), k, largest=largest)
+        assert np.array_equal(npy(i), ri) and np.array_equal(npy(v), rv)
+        tv, ti = torch.topk(x.to(cuda), k, largest=largest)
+        assert torch.equal(i, ti) and torch.equal(v, tv)
+
+
+def test_topk_ties_and_nan(cuda):
+    x = torch.tensor([[1.0, 3.0, 3.0, -1.0, 3.0, float("nan"), 2.0]], device=cuda)
+    v, i = ops.topk(x, 4)
+    rv, ri = O.topk(npy(x), 4)
+    assert np.array_equal(npy(i), ri)          # NaN first, then ties by ascending index
+    assert np.isnan(npy(v)[0, 0]) and np.array_equal(npy(v)[0, 1:], rv[0, 1:])
+    v, i = ops.topk(x, 7, largest=False)
+    assert np.array_equal(npy(i), O.topk(npy(x), 7, largest=False)[1])
+    # a tie across the k-th place keeps the lowest indices
+    y = torch.zeros(1, 5000, device=cuda)
+    y[0, 4000:] = 1.0
+    v, i = ops.topk(y, 1020)
+    assert torch.equal(i[0, :1000].cpu(), torch.arange(4000, 5000))
+    assert torch.equal(i[0, 1000:].cpu(), torch.arange(0, 20))
+    with pytest.raises(Exception):
+        ops.topk(y, 1100)                      # k above 1024 is outside the kernel
+
+
+def test_topk_other_dim(cuda):
+    x = torch.randn(50, 3, device=cuda)
+    v, i = ops.topk(x, 5, dim=0)
+    tv, ti = torch.topk(x, 5, dim=0)
+    assert torch.equal(v, tv) and torch.equal(i, ti)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.int64, torch.uint8])
+def test_gather_vs_oracle(cuda, golden, dtype):
+    for shape, dim in (((8, 5), 1), ((8, 5), 0), ((4, 3, 6), 2)):
+        tag = "x".join(map(str, shape)) + f"_d{dim}"
+        inp = torch.from_numpy(golden[f"gather_{tag}_inp"] * 10).to(dtype)
+        idx = torch.from_numpy(golden[f"gather_{tag}_idx"])
+        out = ops.gather(inp.to(cuda), dim, idx.to(cuda))
+        assert torch.equal(out.cpu(), torch.gather(inp, dim, idx))
+        if dtype == torch.float32:
+            assert np.array_equal(npy(out), O.gather(npy(inp), dim, npy(idx)))
+    big = torch.randn(64, 32000, device=cuda)
+    idx = torch.randint(0, 32000, (64, 50), device=cuda)
+    assert torch.equal(ops.gather(big, 1, idx), torch.gather(big, 1, idx))
+
+
+def test_gather_out_of_range_flag(cuda):
+    inp = torch.randn(2, 3, device=cuda)
+    with pytest.raises(IndexError):
+        ops.gather(inp, 1, torch.tensor([[0, 3], [1, 2]], device=cuda), check=True)
+
+
+def test_index_vs_oracle(cuda, golden):
+    E = torch.from_numpy(golden["index_emb"])
+    ids = torch.from_numpy(golden["index_ids"])
+    assert np.array_equal(npy(ops.index(E.to(cuda), 0, ids.to(cuda))), golden["index_out"])
+    T3, ids2 = torch.from_numpy(golden["index3_inp"]), torch.from_numpy(golden["index3_ids"])
+    assert np.array_equal(npy(ops.index(T3.to(cuda), 1, ids2.to(cuda))), golden["index3_out"])
+    # embedding lookup at the Llama config: 16-byte row copies
+    emb = torch.randn(32000, 2048, device=cuda).to(torch.bfloat16)
+    tok = torch.randint(0, 32000, (1, 512), device=cuda)
+    assert torch.equal(ops.index(emb, 0, tok), emb[tok])
+    with pytest.raises(IndexError):
+        ops.index(emb, 0, torch.tensor([32000], device=cuda), check=True)
