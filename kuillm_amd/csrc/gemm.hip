@@ -1,26 +1,31 @@
 // GEMM family for gfx950: mm / addmm / bmm.
 //
-// Fast path (bf16 / f16 in, fp32 accumulate): LDS-tiled MFMA kernel.
-//   * Work-group tile BM x BN x 64, WM x WN waves, each wave a
-//     (BM/WM) x (BN/WN) sub-tile built from 32x32x16 MFMAs.
-//   * A and B tiles are staged K-contiguous in LDS ([row][64] with the 16-byte
-//     chunk index XOR-swizzled by the row), so one ds_read_b128 feeds one MFMA
-//     operand.  A row-major B ([K, N], N contiguous) is transposed on its way
-//     into LDS: each thread loads a 4(k) x 8(n) block and permutes it in
-//     registers; a K-contiguous B (nn.Linear weight seen through .t()) is
-//     copied like A.
-//   * Two LDS stages; the global loads of tile k+1 are issued before the
-//     MFMAs of tile k, one barrier per K step.
-//   * Work-group ids are remapped so that neighbouring output tiles run on the
-//     same XCD (dispatch is round-robin over the 8 XCDs) and are visited in
-//     groups of 8 tile-rows for L2 reuse.
-//   * Split-K writes fp32 partial tiles to the workspace; a second kernel
-//     sums them in split order (deterministic) and applies the epilogue.
-// Anything else (f32 / f64, unaligned or odd shapes) takes a plain LDS-tiled
-// SIMT kernel with the same epilogue.
+// Large bf16 / f16 GEMMs (K % 128 == 0, >= 128 output tiles of 256x256):
+// `gemm_dma_kernel` -- 256x256x64 work-group tiles, 8 waves (2 per SIMD) of
+// 128x64, 32x32x16 MFMAs, two LDS stages filled by buffer_load ... lds
+// (direct global -> LDS DMA, no VGPR staging).  Row-major B stays
+// N-contiguous in LDS and is read with ds_read_b64_tr_b16; A and a
+// K-contiguous B are read with ds_read_b128.  Each LDS stage is its own
+// __shared__ array so the compiler need not make LDS reads wait for DMA that
+// targets the other stage.
+//
+// Everything else bf16 / f16 (any M, N; K % 8 == 0): `gemm_mfma_kernel` --
+// BM x BN x 64 tiles (256x256 or 128x128), 4 waves, register-staged global
+// loads (a row-major B is transposed in registers on its way into LDS), two
+// LDS stages, optional split-K whose fp32 partials `splitk_reduce_kernel`
+// sums in split order (deterministic).
+//
+// Work-group ids are remapped so that neighbouring output tiles run on the
+// same XCD (dispatch is round-robin over the 8 XCDs, each with its own L2)
+// and are visited in groups of 8 tile-rows.
+//
+// f32 / f64 and unaligned operands take `gemm_simt_kernel`, a plain
+// LDS-tiled kernel with the same epilogue.
 //
 // Semantics follow aten mm / addmm / bmm (the reference's fallthrough and
 // test oracle, kuipy/kuiops.py:403-564, tests/test_jit_ops.py:51-112).
+#include <stdlib.h>
+
 #include "common.hpp"
 
 namespace kuiops {
@@ -235,6 +240,259 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_mfma_kernel(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------
+// gfx950 LDS-DMA kernel: 256x256x64 tiles, 4 waves (2x2), each wave 128x128
+// built from 32x32x16 MFMAs.  Global tiles go straight into LDS with
+// global_load_lds_dwordx4 (no VGPR staging, no ds_write): the LDS position a
+// lane fills is fixed (base + 16 * lane), so the XOR swizzle is applied by
+// choosing which 16-byte chunk each lane fetches.
+//   * A ([M, K], K contiguous) and a K-contiguous B: LDS rows of 64 k (128 B),
+//     chunk c stored at position c ^ (row & 7); operands are ds_read_b128.
+//   * Row-major B ([K, N]): kept N-contiguous in LDS (rows of 256 n, 512 B),
+//     chunk c of row k stored at c ^ fB(k); the MFMA operand (8 consecutive k
+//     of one column) is assembled by two ds_read_b64_tr_b16: within each group
+//     of 16 lanes, source lane q addresses row k0 + q/4, columns 4*(q%4)..+3,
+//     and output lane p receives rows k0..k0+3 of column p.
+// Requires K % 128 == 0 (the K loop is unrolled by the two LDS stages);
+// rows / columns past M / N are clamped on load and dropped on store.
+__device__ __forceinline__ int swzB(int k) { return ((k & 3) | (((k >> 3) & 1) << 2)) << 2; }
+
+typedef __attribute__((address_space(3))) char lds_char;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Generic -> LDS address-space cast.  A direct cast keeps the pointer's
+// provenance (an integer round trip would hide which LDS array it points
+// into, and the compiler would then make every LDS read wait for all
+// in-flight LDS-DMA loads).
+__device__ __forceinline__ lds_char *to_lds(const void *p) {
+    return (lds_char *)(const_cast<void *>(p));
+}
+
+// One global_load_lds_dwordx4: 16 bytes from `src` per lane into
+// dst + 16 * lane (dst is wave-uniform).  The source must reach the builtin
+// as `const void *`: a typed pointer makes the host compilation pass drop
+// the kernel's launch stub without a diagnostic.
+__device__ __forceinline__ void dma16(const void *src, const void *dst) {
+    __builtin_amdgcn_global_load_lds(src, to_lds(dst), 16, 0, 0);
+}
+
+// Buffer-resource form of the same copy: a wave-uniform descriptor (SGPRs),
+// a per-lane 32-bit byte offset and a uniform byte offset, so the K-step
+// advance costs no per-lane address registers.  Reads past `bytes` return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const void *dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)to_lds(dst), 16,
+                                             (int)voff, (int)soff, 0, 0);
+}
+
+// Epilogue of one 32x32 accumulator tile: lane holds column `col` and rows
+// row0 + 8 * (e / 4) + 4 * lk + e % 4.  The addend kind is wave-uniform.
+template <typename Tout>
+__device__ __forceinline__ void store_tile32(const GemmArgs &a, const f32x16 &acc, int64_t row0, int64_t col,
+                                             int lk) {
+    if (col >= a.N) return;
+    Tout *out = reinterpret_cast<Tout *>(a.out) + row0 * a.ldo + col;
+    const Tout *cin = reinterpret_cast<const Tout *>(a.cin);
+    const bool full_rows = row0 + 32 <= a.M;
+    float add[16];
+    if (a.c_kind == KUIOPS_C_ROW) {
+        const float b = a.beta * to_f32(cin[col]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) add[e] = b;
+    } else if (a.c_kind == KUIOPS_C_FULL) {
+        const Tout *c = cin + row0 * a.ldcin + col;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int r = (e >> 2) * 8 + lk * 4 + (e & 3);
+            add[e] = (full_rows || row0 + r < a.M) ? a.beta * to_f32(c[(int64_t)r * a.ldcin]) : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) add[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int r = (e >> 2) * 8 + lk * 4 + (e & 3);
+        if (full_rows || row0 + r < a.M) out[(int64_t)r * a.ldo] = from_f32<Tout>(a.alpha * acc[e] + add[e]);
+    }
+}
+
+// vmcnt-only wait (expcnt / lgkmcnt left at their maxima), N < 64.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <typename T, bool BCOL, typename Tout, int WM, int WN, int BK, int NS>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
+    constexpr int BM = 256, BN = 256;
+    constexpr int NW = WM * WN;                    // waves
+    constexpr int WTM = BM / WM, WTN = BN / WN;    // wave tile
+    constexpr int TM = WTM / 32, TN = WTN / 32;    // 32x32 tiles per wave
+    constexpr int KK = BK / 16;                    // MFMA k-steps per stage
+    constexpr int RB = BK * 2;                     // bytes per K-contiguous LDS row
+    constexpr int RPB = 1024 / RB;                 // such rows per 1 KB DMA block
+    constexpr int CPR = BK / 8;                    // 16-byte chunks per such row
+    constexpr int SBYTES = BM * BK * 2;            // bytes per operand per stage (BM == BN)
+    constexpr int DPW = SBYTES / 1024 / NW;        // DMA blocks per wave, per operand, per stage
+    static_assert(BK == 32 || BK == 64, "BK");
+    static_assert(NS >= 2 && NS <= 4, "stages");
+    static_assert(DPW >= 1, "DMA split");
+    typedef typename Mfma<T>::frag frag;
+    // One array per operand and stage: the compiler tracks LDS-DMA writes per
+    // underlying object, so reads of one stage need not wait for the DMA that
+    // is filling another.
+    __shared__ __attribute__((aligned(1024))) char sA0[SBYTES], sB0[SBYTES];
+    __shared__ __attribute__((aligned(1024))) char sA1[SBYTES], sB1[SBYTES];
+    __shared__ __attribute__((aligned(1024))) char sA2[NS > 2 ? SBYTES : 16], sB2[NS > 2 ? SBYTES : 16];
+    __shared__ __attribute__((aligned(1024))) char sA3[NS > 3 ? SBYTES : 16], sB3[NS > 3 ? SBYTES : 16];
+    char *const SA[4] = {sA0, sA1, sA2, sA3};
+    char *const SB[4] = {sB0, sB1, sB2, sB3};
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int nk = (int)(a.K / BK);                // multiple of NS
+
+    // K-contiguous rows: chunk c of row r sits at position c ^ swzK(r).
+    // 64 LDS banks: a ds_read_b128 serves 16 lanes (16 consecutive rows) per
+    // cycle, so the 16 (row parity, position) pairs of those rows must differ.
+    auto swzK = [](int r) { return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3); };
+
+    // Uniform tile bases plus 32-bit per-lane byte offsets (clamped rows /
+    // columns past M / N read valid memory; their results are not stored).
+    const char *baseA = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.A) + m0 * a.lda);
+    const char *baseB = BCOL ? reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.B) + n0 * a.ldb)
+                             : reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.B) + n0);
+    uint32_t goffA[DPW], goffB[DPW];
+#pragma unroll
+    for (int j = 0; j < DPW; ++j) {
+        const int blk = wave * DPW + j;
+        const int r = blk * RPB + lane / CPR;
+        const int c = (lane % CPR) ^ swzK(r);
+        goffA[j] = (uint32_t)((min((int64_t)r, a.M - 1 - m0) * a.lda + c * 8) * 2);
+        if constexpr (BCOL) {
+            goffB[j] = (uint32_t)((min((int64_t)r, a.N - 1 - n0) * a.ldb + c * 8) * 2);
+        } else {
+            const int kr = blk * 2 + (lane >> 5);   // B rows are 512 B: 2 per block
+            const int cb = (lane & 31) ^ swzB(kr);
+            goffB[j] = (uint32_t)(((int64_t)kr * a.ldb + min((int64_t)cb * 8, a.N - 8 - n0)) * 2);
+        }
+    }
+    const int64_t stepA = (int64_t)BK * 2;                          // bytes per K step
+    const int64_t stepB = BCOL ? (int64_t)BK * 2 : (int64_t)BK * a.ldb * 2;
+
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(baseA, 0xffffffffu);
+    const __amdgpu_buffer_rsrc_t rsB = make_rsrc(baseB, 0xffffffffu);
+    auto issue = [&](int kt, char *sa, char *sb) __attribute__((always_inline)) {
+        const uint32_t ka = (uint32_t)(kt * stepA), kb = (uint32_t)(kt * stepB);
+#pragma unroll
+        for (int j = 0; j < DPW; ++j) dma16_buf(rsA, goffA[j], ka, sa + (wave * DPW + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < DPW; ++j) dma16_buf(rsB, goffB[j], kb, sb + (wave * DPW + j) * 1024);
+    };
+
+    // LDS byte offsets of this lane's operand fragments.
+    const int lrow = lane & 31, lk = lane >> 5;
+    const int G = lane >> 4, q = lane & 15;
+    int offA[KK];                // per kk; tile i adds i * 32 rows
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        const int r = wm * WTM + lrow;
+        offA[kk] = r * RB + (((2 * kk + lk) ^ swzK(r)) << 4);
+    }
+    int offB[BCOL ? KK : TN];    // K-contiguous B: per kk like A; row-major B: per tile j
+    if constexpr (BCOL) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const int r = wn * WTN + lrow;
+            offB[kk] = r * RB + (((2 * kk + lk) ^ swzK(r)) << 4);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int kr = 8 * (G >> 1) + (q >> 2);                 // + 16 kk + 4 h
+            const int n = wn * WTN + j * 32 + 16 * (G & 1) + 4 * (q & 3);
+            offB[j] = kr * 512 + (((n >> 3) ^ swzB(kr)) << 4) + ((n >> 2) & 1) * 8;
+        }
+    }
+
+    auto load_frags = [&](const char *sa, const char *sb, int kk, frag *fa, frag *fb) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            fa[i] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(sa + offA[kk] + i * 32 * RB));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            if constexpr (BCOL) {
+                fb[j] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(sb + offB[kk] + j * 32 * RB));
+            } else {
+                const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4 *)to_lds(sb + offB[j] + kk * 16 * 512));
+                const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4 *)to_lds(sb + offB[j] + kk * 16 * 512 + 4 * 512));
+                const u32x2 h0 = __builtin_bit_cast(u32x2, t0), h1 = __builtin_bit_cast(u32x2, t1);
+                fb[j] = as_frag<frag>(u32x4{h0[0], h0[1], h1[0], h1[1]});
+            }
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    // MFMAs of one stage; fragments double-buffered (reads of kk + 1 are
+    // issued before the MFMAs of kk).
+    auto compute = [&](const char *sa, const char *sb) {
+        frag fa[2][TM], fb[2][TN];
+        load_frags(sa, sb, 0, fa[0], fb[0]);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            if (kk + 1 < KK) load_frags(sa, sb, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = Mfma<T>::m32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+        }
+    };
+
+    // Pipeline: stages 0..NS-2 are in flight before the loop.  Step kt waits
+    // for its own stage (the DMA of the younger stages may stay in flight),
+    // synchronises the work-group, refills the stage consumed at step kt - 1
+    // with step kt + NS - 1, then computes.
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+        if (s < nk) issue(s, SA[s], SB[s]);
+    for (int kt0 = 0; kt0 < nk; kt0 += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int kt = kt0 + s;
+            const int younger = min(NS - 2, nk - 1 - kt);      // stages issued after kt
+            if (younger >= 2) wait_vmcnt<2 * 2 * DPW>();
+            else if (younger == 1) wait_vmcnt<2 * DPW>();
+            else wait_vmcnt<0>();
+            __syncthreads();
+            if (kt + NS - 1 < nk) issue(kt + NS - 1, SA[(s + NS - 1) % NS], SB[(s + NS - 1) % NS]);
+            compute(SA[s], SB[s]);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            store_tile32<Tout>(a, acc[i][j], m0 + wm * WTM + i * 32, n0 + wn * WTN + j * 32 + lrow, lk);
+}
+
 // Sums split-K partials in split order, then applies alpha / beta / addend.
 template <typename Tout>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
@@ -348,9 +606,29 @@ static void launch_mfma(const GemmArgs &a, TileCfg t, bool bcol, int64_t gz, hip
 #undef KUIOPS_GEMM_LAUNCH
 }
 
+static bool dma_eligible(const GemmArgs &a, int64_t batch, bool bcol) {
+    // buffer offsets (tile rows x leading dim + K) must stay below 2^31 bytes
+    const int64_t lim = (int64_t)1 << 30;
+    if ((256 * a.lda + a.K) >= lim) return false;
+    if (bcol ? (256 * a.ldb + a.K) >= lim : (a.K * a.ldb + 256) >= lim) return false;
+    return batch == 1 && a.K % 128 == 0 && a.K > 0 && a.M >= 256 && a.N >= 256 &&
+           cdiv(a.M, 256) * cdiv(a.N, 256) >= 128;
+}
+
 template <typename T, typename Tout>
 static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *ws, size_t ws_bytes,
                     hipStream_t st) {
+    if (splits_req <= 1 && dma_eligible(a, batch, bcol)) {
+        a.tiles_m = (int)cdiv(a.M, 256);
+        a.tiles_n = (int)cdiv(a.N, 256);
+        dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+        // 8 waves (2 per SIMD, 128x64 each), BK = 64, two LDS stages: the best of
+        // the measured variants (4 waves x 128x128, BK = 32 with four stages,
+        // and an 8-wave ping-pong schedule were all slower at 4096^3 / 8192^3).
+        if (bcol) hipLaunchKernelGGL((gemm_dma_kernel<T, true, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((gemm_dma_kernel<T, false, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
+        return launch_status();
+    }
     TileCfg t = pick_tile(a.M, a.N, batch);
     a.tiles_m = (int)cdiv(a.M, t.bm);
     a.tiles_n = (int)cdiv(a.N, t.bn);

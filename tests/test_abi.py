@@ -103,3 +103,12 @@ def test_error_mapping():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load(tmp_path / "libkuiops.so")
+
+
+def test_no_kernel_launch_stub_left_undefined(lib):
+    # A kernel whose host-side launch stub is missing still links into the
+    # .so (dlopen then fails with "undefined symbol ...__device_stub__...");
+    # catch it at build time rather than on the GPU box.
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(C.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "__device_stub__" not in out
