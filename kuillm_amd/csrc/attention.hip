@@ -63,23 +63,52 @@ __device__ __forceinline__ u32x4 pack8(const float *v) {
     return __builtin_bit_cast(u32x4, r);
 }
 
+typedef __attribute__((address_space(3))) char lds_char;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Generic -> LDS pointer with provenance kept (see the GEMM kernels).
+__device__ __forceinline__ lds_char *to_lds(const void *p) { return (lds_char *)(const_cast<void *>(p)); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes per lane from (descriptor, lane offset, uniform offset) into
+// dst + 16 * lane; reads past the descriptor's size return zeros.
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const void *dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)to_lds(dst), 16,
+                                             (int)voff, (int)soff, 0, 0);
+}
+
+// Threshold (log2 domain) by which the running max may grow before O and l
+// are rescaled: probabilities stay below 2^8 meanwhile.
+constexpr float kRescaleSlack = 8.0f;
+
 template <typename T, int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) void fa_fwd_kernel(AttnArgs a) {
-    constexpr int BQ = 128, BKV = 64, NCH = HD / 8;
-    constexpr int KCH = BKV * NCH / 256;            // K chunks per thread
-    constexpr int VBLK = (BKV / 4) * (HD / 8);      // 4x8 V blocks per tile
-    constexpr int VPT = (VBLK + 255) / 256;         // V blocks per thread
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_fwd_kernel(AttnArgs a) {
+    constexpr int BQ = 128, BKV = 64;
+    constexpr int RB = HD * 2;                      // bytes per K / V row
+    constexpr int CPR = HD / 8;                     // 16-byte chunks per row
+    constexpr int TILE = BKV * RB;                  // bytes per K or V tile
+    constexpr int DPW = TILE / 1024 / 4;            // 1 KB DMA blocks per wave per tile
+    constexpr int RPB = 1024 / RB;                  // rows per DMA block
     constexpr int DT = HD / 32;                     // 32-row d tiles of O^T
     typedef typename Mfma<T>::frag frag;
+    static_assert(DPW >= 1, "tile split");
 
-    __shared__ __attribute__((aligned(16))) T sK[2][BKV * HD];
-    __shared__ __attribute__((aligned(16))) T sV[2][HD * BKV];
+    // LDS swizzles (64 banks = 256 bytes per cycle).  K rows, read with
+    // ds_read_b128 (16 consecutive rows per cycle): chunk c sits at c ^ kswz(r),
+    // which gives those 16 rows distinct 16-byte slots.  V rows, read with
+    // ds_read_b64_tr_b16 (8 rows x 64 bytes per instruction): chunk c sits at
+    // c ^ vswz(r), spreading each group of 4 rows over the whole bank width.
+    auto kswz = [](int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); };
+    auto vswz = [](int r) { return CPR == 16 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); };
+    __shared__ __attribute__((aligned(1024))) char sK0[TILE], sV0[TILE], sK1[TILE], sV1[TILE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lq = lane & 31, lh = lane >> 5;
+    const int G = lane >> 4, qq = lane & 15;
 
-    // Work-group -> (batch*head, q-block): ids dispatched to one XCD form a
-    // contiguous range, which covers whole heads.
     const int nblocks = gridDim.x, bid = blockIdx.x;
     int w = bid;
     if ((nblocks & 7) == 0) w = (bid & 7) * (nblocks >> 3) + (bid >> 3);
@@ -90,8 +119,13 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(AttnArgs a) {
     const int64_t hk = h / (a.hq / a.hkv);
 
     const T *Qp = reinterpret_cast<const T *>(a.Q) + b * a.sq0 + h * a.sq1;
-    const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
-    const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
+    const char *Kb = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1);
+    const char *Vb = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1);
+    // Descriptors end at the last key: the rows of a partial last block read 0.
+    const uint32_t kbytes = (uint32_t)min((int64_t)0x7fffffff, ((a.s - 1) * a.sk2 + HD) * 2);
+    const uint32_t vbytes = (uint32_t)min((int64_t)0x7fffffff, ((a.s - 1) * a.sv2 + HD) * 2);
+    const __amdgpu_buffer_rsrc_t rsK = make_rsrc(Kb, a.s > 0 ? kbytes : 0);
+    const __amdgpu_buffer_rsrc_t rsV = make_rsrc(Vb, a.s > 0 ? vbytes : 0);
 
     const int64_t q0 = (int64_t)qb * BQ;
     const int64_t qw = q0 + wave * 32;
@@ -109,140 +143,140 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(AttnArgs a) {
     if (CAUSAL) kv_end = min(a.s, q0 + BQ);
     const int nkv = (int)((kv_end + BKV - 1) / BKV);
 
-    u32x4 rk[KCH];
-    u32x4 rv[VPT * 4];
-    auto load_kv = [&](int64_t kv0) {
+    // Per-lane DMA byte offsets within a KV block (uniform part: block start).
+    uint32_t offK[DPW], offV[DPW];
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = tid + i * 256, r = c / NCH, ch = c % NCH;
-            const int64_t key = kv0 + r;
-            rk[i] = key < a.s ? *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + ch * 8) : u32x4{0, 0, 0, 0};
-        }
+    for (int j = 0; j < DPW; ++j) {
+        const int blk = wave * DPW + j;
+        const int r = blk * RPB + lane / CPR;
+        const int p = lane % CPR;
+        offK[j] = (uint32_t)((r * a.sk2 + ((p ^ kswz(r)) * 8)) * 2);
+        offV[j] = (uint32_t)((r * a.sv2 + ((p ^ vswz(r)) * 8)) * 2);
+    }
+    auto issue = [&](int kt, char *sk, char *sv) __attribute__((always_inline)) {
+        const uint32_t kb = (uint32_t)((int64_t)kt * BKV * a.sk2 * 2);
+        const uint32_t vb = (uint32_t)((int64_t)kt * BKV * a.sv2 * 2);
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int c = tid + i * 256;
-            const int sg = c % 16, dc = c / 16;
+        for (int j = 0; j < DPW; ++j) dma16_buf(rsK, offK[j], kb, sk + (wave * DPW + j) * 1024);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t key = kv0 + sg * 4 + r;
-                rv[i * 4 + r] = (c < VBLK && key < a.s)
-                                    ? *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dc * 8)
-                                    : u32x4{0, 0, 0, 0};
-            }
-        }
+        for (int j = 0; j < DPW; ++j) dma16_buf(rsV, offV[j], vb, sv + (wave * DPW + j) * 1024);
     };
-    auto store_kv = [&](int buf) {
+
+    // LDS offsets of this lane's operands.  K (A operand of S^T = K Q^T): key
+    // row 32t + lq, chunk 2kk + lh.  V^T (A operand of O^T += V^T P^T): d row
+    // 32dt + lq; the 8 key slots of lane half lh are keys 4lh..4lh+3 and
+    // 8+4lh..8+4lh+3 of each 16-key step (the order the score accumulator
+    // holds them), each 4 fetched by one transposing read.
+    int offKr[2];
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = tid + i * 256, r = c / NCH, ch = c % NCH;
-            *reinterpret_cast<u32x4 *>(&sK[buf][r * HD + ((ch ^ (r & 7)) << 3)]) = rk[i];
-        }
+    for (int t = 0; t < 2; ++t) offKr[t] = (t * 32 + lq) * RB;
+    const int kpos = kswz(lq);                      // == kswz(32t + lq)
+    int offVr[DT];
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int c = tid + i * 256;
-            if (c >= VBLK) continue;
-            const int sg = c % 16, dc = c / 16;
-            const int qd = sg & 3;
-            const int p0 = 16 * (sg >> 2) + 4 * ((qd == 1) ? 2 : (qd == 2) ? 1 : qd);
-            u32x2 t[8];
-            transpose4x8_b16(&rv[i * 4], t);
-#pragma unroll
-            for (int cc = 0; cc < 8; ++cc) {
-                const int d = dc * 8 + cc;
-                *reinterpret_cast<u32x2 *>(&sV[buf][d * BKV + (((p0 >> 3) ^ swz8(d)) << 3) + (p0 & 7)]) = t[cc];
-            }
-        }
-    };
+    for (int dt = 0; dt < DT; ++dt) {
+        const int krow = 4 * (G >> 1) + (qq >> 2);   // + 16 * step (+ 8 for the second read)
+        const int d = dt * 32 + 16 * (G & 1) + 4 * (qq & 3);
+        offVr[dt] = krow * RB + (((d >> 3) ^ vswz(krow)) << 4) + ((d >> 2) & 1) * 8;   // vswz(krow + 16s + 8h) == vswz(krow)
+    }
 
     f32x16 o[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_used = -INFINITY, l_run = 0.f;
 
-    if (nkv > 0) {
-        load_kv(0);
-        store_kv(0);
-    }
-    __syncthreads();
-
-    for (int kt = 0; kt < nkv; ++kt) {
-        const int buf = kt & 1;
-        const int64_t kv0 = (int64_t)kt * BKV;
-        if (kt + 1 < nkv) load_kv(kv0 + BKV);
-        const bool active = !(CAUSAL && kv0 > qw + 31) && qw < a.l;
-        if (active) {
-            const T *pk = sK[buf];
-            const T *pv = sV[buf];
-            f32x16 sc[2];
+    auto block = [&](const char *pk, const char *pv, int64_t kv0) __attribute__((always_inline)) {
+        f32x16 sc[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) sc[t][e] = 0.f;
+            for (int e = 0; e < 16; ++e) sc[t][e] = 0.f;
 #pragma unroll
-            for (int kk = 0; kk < HD / 16; ++kk) {
-                const int ch = 2 * kk + lh;
+        for (int kk = 0; kk < HD / 16; ++kk) {
+            const int pos = ((2 * kk + lh) ^ kpos) << 4;
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int r = t * 32 + lq;
-                    const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4 *>(&pk[r * HD + ((ch ^ (r & 7)) << 3)]));
-                    sc[t] = Mfma<T>::m32(kf, qf[kk], sc[t]);
-                }
+            for (int t = 0; t < 2; ++t) {
+                const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4 *>(pk + offKr[t] + pos));
+                sc[t] = Mfma<T>::m32(kf, qf[kk], sc[t]);
             }
-            // Scale, mask, block max.  sc[t][e]: key kv0 + 32t + 8(e/4) + 4*lh + e%4, query myq.
-            const bool need_mask = (kv0 + BKV > a.s) || (CAUSAL && kv0 + BKV - 1 > qw);
-            float mx = -INFINITY;
+        }
+        // sc[t][e]: key kv0 + 32t + 8(e/4) + 4lh + e%4, query myq.
+        const bool need_mask = (kv0 + BKV > a.s) || (CAUSAL && kv0 + BKV - 1 > qw);
+        if (need_mask) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    float v = sc[t][e] * a.scale_log2;
-                    if (need_mask) {
-                        const int64_t key = kv0 + t * 32 + (e >> 2) * 8 + lh * 4 + (e & 3);
-                        if (key >= a.s || (CAUSAL && key > myq)) v = -INFINITY;
-                    }
-                    sc[t][e] = v;
-                    mx = fmaxf(mx, v);
+                    const int64_t key = kv0 + t * 32 + (e >> 2) * 8 + lh * 4 + (e & 3);
+                    if (key >= a.s || (CAUSAL && key > myq)) sc[t][e] = -INFINITY;
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            const float alpha = fast_exp2(m_run - m_use);
-            float rs = 0.f;
+        }
+        float mx = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float p = fast_exp2(sc[t][e] - m_use);
-                    sc[t][e] = p;
-                    rs += p;
-                }
-            l_run = l_run * alpha + rs;
-            m_run = m_new;
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[t][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+        // Lazy rescale: move the reference max only when it grew by more
+        // than the slack (or is still -inf), for the whole wave at once.
+        if (__any(mx > m_used + kRescaleSlack)) {
+            const float m_new = fmaxf(m_used, mx);
+            const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_used - m_new);
+            l_run *= alpha;
 #pragma unroll
             for (int t = 0; t < DT; ++t)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
-            // O^T += V^T P^T over 4 steps of 16 keys.
+            m_used = m_new;
+        }
+        const float mref = (m_used == -INFINITY) ? 0.f : m_used;
+        float rs = 0.f;
 #pragma unroll
-            for (int b16 = 0; b16 < 4; ++b16) {
-                const int t = b16 >> 1, u = b16 & 1;
-                float pv8[8];
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) pv8[i] = sc[t][8 * u + i];
-                const frag pf = as_frag<frag>(pack8<T>(pv8));
-                const int ch = 2 * b16 + lh;
+            for (int e = 0; e < 16; ++e) {
+                const float p = fast_exp2(__builtin_fmaf(sc[t][e], a.scale_log2, -mref));
+                sc[t][e] = p;
+                rs += p;
+            }
+        l_run += rs;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const int d = dt * 32 + lq;
-                    const frag vf = as_frag<frag>(*reinterpret_cast<const u32x4 *>(&pv[d * BKV + ((ch ^ swz8(d)) << 3)]));
-                    o[dt] = Mfma<T>::m32(vf, pf, o[dt]);
-                }
+        for (int b16 = 0; b16 < 4; ++b16) {
+            const int t = b16 >> 1, u = b16 & 1;
+            float pv8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pv8[i] = sc[t][8 * u + i];
+            const frag pf = as_frag<frag>(pack8<T>(pv8));
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const char *vb = pv + offVr[dt] + b16 * 16 * RB;
+                const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4 *)to_lds(vb));
+                const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4 *)to_lds(vb + 8 * RB));
+                const u32x2 h0 = __builtin_bit_cast(u32x2, t0), h1 = __builtin_bit_cast(u32x2, t1);
+                const frag vf = as_frag<frag>(u32x4{h0[0], h0[1], h1[0], h1[1]});
+                o[dt] = Mfma<T>::m32(vf, pf, o[dt]);
             }
         }
-        if (kt + 1 < nkv) store_kv(buf ^ 1);
-        __syncthreads();
+    };
+
+    if (nkv > 0) issue(0, sK0, sV0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kt0 = 0; kt0 < nkv; kt0 += 2) {
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+            const int kt = kt0 + hs;
+            if (kt >= nkv) break;
+            const int64_t kv0 = (int64_t)kt * BKV;
+            if (kt + 1 < nkv) issue(kt + 1, hs ? sK0 : sK1, hs ? sV0 : sV1);
+            const bool active = !(CAUSAL && kv0 > qw + 31) && qw < a.l;
+            if (active) block(hs ? sK1 : sK0, hs ? sV1 : sV0, kv0);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -261,7 +295,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(AttnArgs a) {
                 *reinterpret_cast<t4 *>(Op + d) = v;
             }
         if (a.lse && lh == 0)
-            a.lse[(b * a.hq + h) * a.l + myq] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+            a.lse[(b * a.hq + h) * a.l + myq] = l_tot > 0.f ? (m_used + __log2f(l_tot)) * kLn2 : -INFINITY;
     }
 }
 
