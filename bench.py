@@ -45,10 +45,13 @@ def parse():
     return ap.parse_args()
 
 
-def graph_time_ms(torch, fn, steps, warmup):
-    """Average device time of one `fn()` step: `fn` recorded once into a HIP
-    graph, W warm-up replays, then K replays between HIP events on the
-    current (launch) stream, with device synchronisation on both sides."""
+def graph_time_ms(torch, fn, steps, warmup, reps=1):
+    """Average device time of one `fn()` step: `reps` back-to-back `fn()`
+    calls recorded into a HIP graph, W warm-up replays, then K replays between
+    HIP events on the current (launch) stream, with device synchronisation on
+    both sides; returns the time per call.  reps > 1 is for the
+    microsecond-scale decode kernels, whose graph-replay overhead (a few us)
+    would otherwise be timed as kernel time."""
     fn()                                    # eager run: allocates workspaces outside capture
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
@@ -58,7 +61,8 @@ def graph_time_ms(torch, fn, steps, warmup):
     torch.cuda.current_stream().wait_stream(side)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
+        for _ in range(reps):
+            fn()
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -69,7 +73,7 @@ def graph_time_ms(torch, fn, steps, warmup):
         g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return start.elapsed_time(end) / (steps * reps)
 
 
 def roofline(bound, achieved, unit, traffic=None):
@@ -107,7 +111,7 @@ def extra_workloads(torch, ops, steps, warmup, dev):
     W = (torch.randn(4096, 11008, device=dev) * 0.02).to(bf)
     for M in (1, 4, 16):
         x = torch.randn(M, 4096, device=dev).to(bf)
-        ms = graph_time_ms(torch, lambda: ops.mm(x, W), steps, warmup)
+        ms = graph_time_ms(torch, lambda: ops.mm(x, W), steps, warmup, reps=20)
         nbytes = 4096 * 11008 * 2 + M * 4096 * 2 + M * 11008 * 2
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"decode_gemm_M{M}"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 5),
@@ -136,15 +140,15 @@ def extra_workloads(torch, ops, steps, warmup, dev):
     qd = torch.randn(1, 32, 1, 128, device=dev).to(bf)
     kc = torch.randn(1, 32, 4096, 128, device=dev).to(bf)
     vc = torch.randn_like(kc)
-    ms = graph_time_ms(torch, lambda: ops.sdpa(qd, kc, vc), steps, warmup)
+    ms = graph_time_ms(torch, lambda: ops.sdpa(qd, kc, vc), steps, warmup, reps=20)
     gbs = 2 * 32 * 4096 * 128 * 2 / (ms * 1e-3) / 1e9
     out["sdpa_decode_kv4096"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 5),
                                  "roofline": roofline("hbm", gbs, "GB/s")}
     # sampling tail: softmax + top-1 / top-50 over a [1, 32000] fp32 logit row
     logits = torch.randn(1, 32000, device=dev)
-    ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 1), steps, warmup)
+    ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 1), steps, warmup, reps=20)
     out["sampling_softmax_top1_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
-    ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 50), steps, warmup)
+    ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 50), steps, warmup, reps=20)
     out["sampling_softmax_top50_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
     return out
 

@@ -19,6 +19,8 @@
 //     repeatable.  (Reducing in the last-arriving work-group instead would
 //     need device-scope fences, which on a chip with one L2 per XCD write
 //     back that L2.)
+#include <stdlib.h>
+
 #include "common.hpp"
 
 namespace kuiops {
@@ -31,6 +33,7 @@ struct GemvArgs {
     void *out; int64_t ldo;
     int splits;
     int64_t k_per_split;      // multiple of 128
+    int64_t k_part;           // strip kernel: k rows per wave (multiple of 32 * stages)
     float *partial;           // [splits][M][N]
 };
 
@@ -175,6 +178,207 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(GemvArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------
+// Strip variant (row-major W): one NW-wave work-group per (SW-column strip,
+// K range).  Enough work-groups to keep ~2 per CU resident matter more for
+// HBM throughput than long contiguous runs: 128-byte row segments stream at
+// full speed once ~600 work-groups are in flight.  Each wave owns
+// k_part rows of the strip and streams them through NS private LDS stages of
+// 32 rows with buffer_load ... lds (DMA, no VGPR staging, no barriers: a wave
+// only reads what it loaded itself).  The MFMA B operand (8 consecutive k of
+// one column) comes from two ds_read_b64_tr_b16 on W's natural row-major
+// layout; x is the A operand straight from global memory (it is tiny and
+// stays in L2).  The wave partials are summed in wave order through LDS; with
+// several K ranges, fp32 partials go to the workspace for gemv_reduce_kernel.
+typedef __attribute__((address_space(3))) char lds_char_g;
+typedef short s16x4g __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ lds_char_g *to_lds_g(const void *p) { return (lds_char_g *)(const_cast<void *>(p)); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_g() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <typename T, typename Tout, int SW, int NS, int MB, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
+    constexpr int RB = SW * 2;                      // bytes per LDS row (one W row of the strip)
+    constexpr int STG = 32 * RB;                    // bytes per stage per wave (32 k rows)
+    constexpr int DPS = STG / 1024;                 // 1 KB DMA blocks per stage
+    constexpr int RPB = 1024 / RB;                  // rows per DMA block
+    constexpr int CPR = RB / 16;                    // 16-byte chunks per row
+    constexpr int CG = SW / 16;                     // 16-column MFMA groups
+    static_assert(DPS >= 1 && CPR >= 2, "strip width");
+    typedef typename Mfma<T>::frag frag;
+    // one array per stage (distinct objects: see the GEMM kernels)
+    __shared__ __attribute__((aligned(1024))) char st0[NW * STG], st1[NW * STG];
+    __shared__ __attribute__((aligned(1024))) char st2[NS > 2 ? NW * STG : 16], st3[NS > 3 ? NW * STG : 16];
+    char *const ST[4] = {st0, st1, st2, st3};
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave-uniform by construction; readfirstlane lets the compiler keep the
+    // buffer descriptor built from it in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Strips handed to one XCD (dispatch is round-robin over the 8 XCDs) form
+    // a contiguous range of columns, so the work-groups running together on
+    // an XCD read adjacent segments of the same W rows.
+    const int nb = gridDim.x, bid = blockIdx.x;
+    const int xcd = bid & 7, q8 = nb >> 3, r8 = nb & 7;
+    const int strip = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
+    const int64_t n0 = (int64_t)strip * SW;
+    // K is cut into splits * NW parts of k_part rows: wave w of split s owns
+    // part s * NW + w.  The last parts may be short or empty; their rows past
+    // K lie outside the buffer range below and load as zeros.
+    const int split = blockIdx.y;
+    const int64_t kbeg = ((int64_t)split * NW + wave) * a.k_part;
+    const int64_t kend = min(a.K, kbeg + a.k_part);
+    const int nst = (int)(a.k_part / 32);
+    const T *x = reinterpret_cast<const T *>(a.x);
+
+    // chunk c of row r sits at c ^ swz(r).  One transposing read touches rows
+    // 8G + 4h + {0..3} (G = 0..3) x 32 bytes; swz spreads them over the
+    // 256-byte bank width (each 16-byte slot twice, the minimum for 512 bytes)
+    // and is the same for rows r and r + 4, which the second read (h = 1)
+    // relies on.
+    auto swz = [](int r) { return CPR == 8 ? 2 * ((r >> 3) & 3) : 2 * (((r >> 3) & 3) | ((r & 1) << 2)); };
+
+    const char *wbase = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.W) + kbeg * a.ldw + n0);
+    // the range ends after row kend - 1 (its columns up to N): row kend and
+    // beyond read zeros
+    const uint32_t wbytes =
+        kbeg < kend ? (uint32_t)min((int64_t)0x7fffffff, ((kend - 1 - kbeg) * a.ldw + (a.N - n0)) * 2) : 0u;
+    const __amdgpu_buffer_rsrc_t rsW = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(wbase), (short)0,
+                                                                         (int)wbytes, 0x00020000);
+    uint32_t goff[DPS];
+#pragma unroll
+    for (int j = 0; j < DPS; ++j) {
+        const int r = j * RPB + lane / CPR;
+        const int c = (lane % CPR) ^ swz(r);
+        // columns past N read the next row (or zeros past the end); not stored
+        goff[j] = (uint32_t)(((int64_t)r * a.ldw + c * 8) * 2);
+    }
+    const uint32_t step = (uint32_t)(32 * a.ldw * 2);
+    const int lc = lane & 15, G = lane >> 4;
+    // x fragments (A operand) travel with their stage's DMA: vmcnt counts in
+    // issue order, so a later, separate x load would make every wait drain
+    // all DMA in flight.
+    u32x4 xr[NS][MB];
+    auto issue = [&](int kt, char *st, u32x4 *xs) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < DPS; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsW, (__attribute__((address_space(3))) void *)to_lds_g(st + wave * STG + j * 1024), 16,
+                (int)(goff[j] + kt * step), 0, 0, 0);
+        const int64_t kl = min(kbeg + (int64_t)kt * 32 + 8 * G, a.K - 8);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            // unconditional load from a clamped row (no branch around the
+            // load); rows past M are zeroed where the fragment is used
+            const int64_t m = mb * 16 + lc;
+            xs[mb] = *reinterpret_cast<const u32x4 *>(x + min(m, a.M - 1) * a.ldx + kl);
+        }
+    };
+
+    // transposing-read offsets: lane group G holds k rows 8G..8G+7 of column
+    // 16cg + (lane % 16); read h covers rows 8G + 4h .. + 3.
+    const int q = lane & 15;
+    int offB[CG];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+        const int r = 8 * G + (q >> 2);
+        const int n = 16 * cg + 4 * (q & 3);
+        offB[cg] = r * RB + (((n >> 3) ^ swz(r)) << 4) + ((n >> 2) & 1) * 8;
+    }
+
+    f32x4 acc[MB][CG];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) acc[mb][cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int kt, const char *stg, const u32x4 *xs) __attribute__((always_inline)) {
+        // x columns of rows outside [kbeg, kend) meet zero W rows but are
+        // zeroed too, so an Inf or NaN there cannot leak into the sum
+        const bool kin = kbeg + (int64_t)kt * 32 + 8 * G < kend;
+        const char *sw = stg + wave * STG;
+        frag fb[CG];
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) {
+            const s16x4g t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4g *)to_lds_g(sw + offB[cg]));
+            const s16x4g t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4g *)to_lds_g(sw + offB[cg] + 4 * RB));
+            const u32x2 h0 = __builtin_bit_cast(u32x2, t0), h1 = __builtin_bit_cast(u32x2, t1);
+            fb[cg] = as_frag<frag>(u32x4{h0[0], h0[1], h1[0], h1[1]});
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const frag fa = as_frag<frag>(kin && mb * 16 + lc < a.M ? xs[mb] : u32x4{0, 0, 0, 0});
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) acc[mb][cg] = Mfma<T>::m16(fa, fb[cg], acc[mb][cg]);
+        }
+    };
+    constexpr int PER = DPS + MB;                   // vector-memory instructions per stage
+    // nst is a multiple of NS (k_part is a multiple of 32 * NS).  Straight-line code
+    // (no branch between issue and use) lets the compiler track which LDS
+    // array each DMA targets and keep NS - 1 stages in flight.
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s, ST[s], xr[s]);
+    for (int kt0 = 0; kt0 + NS < nst; kt0 += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            issue(kt0 + s + NS - 1, ST[(s + NS - 1) % NS], xr[(s + NS - 1) % NS]);
+            wait_vmcnt_g<(NS - 1) * PER>();
+            compute(kt0 + s, ST[s], xr[s]);
+        }
+    }
+    // last NS stages: one more issue, then drain
+    issue(nst - 1, ST[NS - 1], xr[NS - 1]);
+    wait_vmcnt_g<(NS - 1) * PER>();
+    compute(nst - NS, ST[0], xr[0]);
+#pragma unroll
+    for (int s = 1; s < NS; ++s) {
+        if (s == 1) wait_vmcnt_g<(NS - 2) * PER>();
+        else if (s == 2) wait_vmcnt_g<(NS > 3 ? (NS - 3) * PER : 0)>();
+        else wait_vmcnt_g<0>();
+        compute(nst - NS + s, ST[s], xr[s]);
+    }
+
+    // acc[mb][cg][i]: row 16mb + 4G + i, column n0 + 16cg + lc.  Sum the
+    // waves in wave order through LDS, one 16-row block at a time (the DMA
+    // stages are free: every wave waited for its last stage before its last
+    // reads, and the barrier orders them).
+    float *red = reinterpret_cast<float *>(st0);    // [wave][CG * 4][64] floats <= NW * STG bytes
+    constexpr int E = CG * 4;
+    static_assert(NW * E * 64 * 4 <= NW * STG, "reduction buffer");
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        __syncthreads();
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[(wave * E + cg * 4 + i) * 64 + lane] = acc[mb][cg][i];
+        __syncthreads();
+        for (int idx = tid; idx < E * 64; idx += NW * 64) {
+            const int e = idx / 64, l = idx % 64;
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) v += red[(w * E + e) * 64 + l];
+            const int cg = e / 4, i = e % 4;
+            const int64_t row = mb * 16 + 4 * (l >> 4) + i;
+            const int64_t col = n0 + 16 * cg + (l & 15);
+            if (row < a.M && col < a.N) {
+                if (a.splits > 1) {
+                    a.partial[((int64_t)split * a.M + row) * a.N + col] = v;
+                } else {
+                    if (a.bias) v += to_f32(reinterpret_cast<const T *>(a.bias)[col]);
+                    reinterpret_cast<Tout *>(a.out)[row * a.ldo + col] = from_f32<Tout>(v);
+                }
+            }
+        }
+    }
+}
+
 static int gemv_choose_splits(int64_t M, int64_t N, int64_t K) {
     (void)M;
     const int64_t strips = cdiv(N, kGemvStrip);
@@ -185,9 +389,13 @@ static int gemv_choose_splits(int64_t M, int64_t N, int64_t K) {
     return s < 1 ? 1 : (int)s;
 }
 
+static int strip_splits(int64_t N, int64_t K);
+
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     const int s = gemv_choose_splits(M, N, K);
-    return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+    const int s2 = strip_splits(N, K);
+    const int mx = s > s2 ? s : s2;
+    return mx > 1 ? (size_t)mx * M * N * sizeof(float) : 0;
 }
 
 template <typename T, typename Tout, int MB>
@@ -204,6 +412,62 @@ static int gemv_dispatch(const GemvArgs &a, bool wcol, hipStream_t st) {
         case 2: gemv_launch<T, Tout, 2>(a, wcol, st); break;
         case 3: gemv_launch<T, Tout, 3>(a, wcol, st); break;
         case 4: gemv_launch<T, Tout, 4>(a, wcol, st); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    if (a.splits > 1) {
+        int64_t blocks = cdiv(a.M * cdiv(a.N, 4), 256);
+        if (blocks > 2048) blocks = 2048;
+        hipLaunchKernelGGL((gemv_reduce_kernel<T, Tout>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
+    return launch_status();
+}
+
+constexpr int kStripW = 64;      // 128-byte row segments: narrower ones halve HBM efficiency
+// Work-group shape: up to 32 rows of x, 16 waves x 2 stages x 4 KB = 128 KB
+// LDS (one work-group per CU, 128 VGPRs per lane); 33..64 rows need more
+// accumulators, so 8 waves x 4 stages (256 VGPRs).  Both keep 32 stages of
+// 4 KB in flight per CU.
+constexpr int kStripWaves = 16, kStripStages = 2;
+constexpr int kStripWavesWide = 8, kStripStagesWide = 4;
+
+// K splits for the strip kernel.  A split costs a second (reduce) launch, so
+// one work-group per strip is kept while that still occupies >= 128 CUs
+// (N = 11008 gives 172 strips); narrower problems, once split anyway, are
+// split until every CU has a work-group.
+static int strip_splits(int64_t N, int64_t K) {
+    const int64_t strips = cdiv(N, kStripW);
+    if (strips >= 128) return 1;
+    int s = 1;
+    while (strips * s < 256 && s < 16 && K >= (int64_t)2 * s * 1024) s *= 2;
+    return s;
+}
+
+// rows per wave: K / (splits * NW) rounded up to whole pipelines (32 * NS)
+static int64_t strip_part(int64_t K, int splits, int nw, int ns) {
+    const int64_t g = 32 * ns;
+    return cdiv(cdiv(K, (int64_t)splits * nw), g) * g;
+}
+
+static bool strip_eligible(const GemvArgs &a, bool wcol) {
+    if (wcol || a.N % 8 || a.ldw % 8 || a.K % 8) return false;
+    if (cdiv(a.N, kStripW) * strip_splits(a.N, a.K) < 128) return false;
+    return ((a.K - 1) * a.ldw + a.N) * 2 < ((int64_t)1 << 31) && getenv("KUIOPS_GEMV_NO_STRIP") == nullptr;
+}
+
+template <typename T, typename Tout, int MB, int NW, int NS>
+static void strip_launch(GemvArgs a, hipStream_t st) {
+    a.k_part = strip_part(a.K, a.splits, NW, NS);
+    dim3 grid((unsigned)cdiv(a.N, kStripW), (unsigned)a.splits);
+    hipLaunchKernelGGL((gemv_strip_kernel<T, Tout, kStripW, NS, MB, NW>), grid, dim3(NW * 64), 0, st, a);
+}
+
+template <typename T, typename Tout>
+static int strip_dispatch(const GemvArgs &a, hipStream_t st) {
+    switch (cdiv(a.M, 16)) {
+        case 1: strip_launch<T, Tout, 1, kStripWaves, kStripStages>(a, st); break;
+        case 2: strip_launch<T, Tout, 2, kStripWaves, kStripStages>(a, st); break;
+        case 3: strip_launch<T, Tout, 3, kStripWavesWide, kStripStagesWide>(a, st); break;
+        case 4: strip_launch<T, Tout, 4, kStripWavesWide, kStripStagesWide>(a, st); break;
         default: return KUIOPS_E_UNSUPPORTED;
     }
     if (a.splits > 1) {
@@ -238,6 +502,18 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
     a.M = M; a.N = N; a.K = K;
     a.x = x; a.ldx = ldx; a.W = W; a.ldw = ldw; a.bias = bias;
     a.out = out; a.ldo = ldo;
+    hipStream_t st0 = as_stream(stream);
+    if (splits <= 0 && strip_eligible(a, wcol)) {
+        a.splits = strip_splits(N, K);
+        if (a.splits > 1) {
+            const size_t need = (size_t)a.splits * M * N * sizeof(float);
+            if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
+            a.partial = reinterpret_cast<float *>(workspace);
+        }
+        if (in_dtype == KUIOPS_BF16)
+            return out_dtype == KUIOPS_F32 ? strip_dispatch<bf16_t, float>(a, st0) : strip_dispatch<bf16_t, bf16_t>(a, st0);
+        return out_dtype == KUIOPS_F32 ? strip_dispatch<f16_t, float>(a, st0) : strip_dispatch<f16_t, f16_t>(a, st0);
+    }
     int s = splits > 0 ? splits : gemv_choose_splits(M, N, K);
     int64_t kps = cdiv(cdiv(K, s), 128) * 128;
     s = (int)cdiv(K, kps);
@@ -248,7 +524,7 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
         if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
         a.partial = reinterpret_cast<float *>(workspace);
     }
-    hipStream_t st = as_stream(stream);
+    hipStream_t st = st0;
     if (in_dtype == KUIOPS_BF16)
         return out_dtype == KUIOPS_F32 ? gemv_dispatch<bf16_t, float>(a, wcol, st)
                                        : gemv_dispatch<bf16_t, bf16_t>(a, wcol, st);

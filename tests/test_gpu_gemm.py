@@ -184,6 +184,23 @@ def test_decode_gemm_vs_oracle(cuda, M, layout):
     assert_tol(out, O.mm(npy(x), npy(W)), torch.bfloat16)
 
 
+@pytest.mark.parametrize("M,N,K", [(4, 4096, 11008), (16, 2048, 8192), (1, 8192, 2048), (64, 4096, 4104),
+                                   (5, 11008, 4104), (33, 11008, 1000)])
+def test_decode_gemm_ragged_k_and_splits(cuda, M, N, K):
+    """Row-major W shapes of the Llama decode projections: K not a multiple of
+    the per-wave pipeline (the last K parts are short or empty), one or several
+    K splits, and a W view with ldw > N."""
+    x = gen((M, K), torch.bfloat16, seed=16)
+    Wbig = gen((K, N + 64), torch.bfloat16, 0.02, seed=17)
+    for W in (Wbig[:, :N].contiguous(), Wbig[:, 32:32 + N]):
+        Wd = Wbig.to(cuda)[:, :N].contiguous() if W.is_contiguous() else Wbig.to(cuda)[:, 32:32 + N]
+        out = ops.mm(x.to(cuda), Wd)
+        assert torch.equal(out, ops.mm(x.to(cuda), Wd))
+        assert_tol(out, O.mm(npy(x), npy(W)), torch.bfloat16)
+        o32 = ops.mm(x.to(cuda), Wd, out_dtype=torch.float32)
+        np.testing.assert_allclose(npy(o32), O.mm(npy(x), npy(W)), rtol=1e-4, atol=1e-4)
+
+
 def test_decode_gemm_bias_odd_shapes(cuda):
     for (M, N, K) in [(3, 1000, 520), (1, 8, 8), (7, 4104, 4096)]:
         x, W = gen((M, K), torch.bfloat16, seed=13), gen((K, N), torch.bfloat16, 0.1, seed=14)
