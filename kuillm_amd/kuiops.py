@@ -10,6 +10,10 @@ Same contract as the reference's families (kuipy/kuiops.py:27-43):
   falls through to stock PyTorch);
 * ``tune_key`` / ``tune_params`` / ``tune(all)`` carry autotune parameters.
 
+``run`` calls the ``torch.ops.kuiops`` custom operators (kuillm_amd/library.py),
+the same ops the Inductor pass (kuillm_amd/inductor.py) puts into compiled
+graphs.
+
 The gates are wider than the reference's: the reference needs M, N multiples
 of 64 and 2-D addmm biases (kuipy/kuiops.py:365-394, 538-540) and rejects
 causal SDPA (:636-637); the kernels here take any shape, 1-D biases, causal
@@ -23,10 +27,12 @@ import math
 import torch
 
 from . import _lib
+from . import library  # noqa: F401  (defines torch.ops.kuiops)
 from . import ops
 from .config import log
 
 aten = torch.ops.aten
+K = torch.ops.kuiops      # the custom ops: HIP kernels behind the C ABI
 
 _FLOAT_DTYPES = (torch.float16, torch.float32, torch.float64, torch.bfloat16)
 _HALF = (torch.float16, torch.bfloat16)
@@ -92,7 +98,7 @@ class MmImpl(_Family):
     def run(self, spec, args, kwargs):
         _, _, _, _, (A, B) = spec
         try:
-            return ops.mm(A, B)
+            return K.mm(A, B)
         except _lib.Unsupported:
             return None
 
@@ -127,7 +133,7 @@ class AddmmImpl(_Family):
     def run(self, spec, args, kwargs):
         _, _, _, _, (Cin, A, B), alpha, beta = spec
         try:
-            return ops.addmm(Cin, A, B, beta=beta, alpha=alpha)
+            return K.addmm(Cin, A, B, beta, alpha)
         except _lib.Unsupported:
             return None
 
@@ -152,7 +158,7 @@ class BmmImpl(_Family):
 
     def run(self, spec, args, kwargs):
         try:
-            return ops.bmm(*spec[1])
+            return K.bmm(*spec[1])
         except _lib.Unsupported:
             return None
 
@@ -182,7 +188,7 @@ class SoftmaxImpl(_Family):
 
     def run(self, spec, args, kwargs):
         try:
-            return ops.softmax(spec[3][0])
+            return K.softmax(spec[3][0])
         except _lib.Unsupported:
             return None
 
@@ -242,9 +248,8 @@ class SdpaImpl(_Family):
     def run(self, spec, args, kwargs):
         func, scale, causal, need_lse, (q, k, v) = spec
         try:
-            out, lse = ops.sdpa(q, k, v, is_causal=causal, scale=scale, return_lse=True,
-                                decode_max_rows=self.tune_params.get("decode_max_rows", 8)
-                                if isinstance(self.tune_params, dict) else 8)
+            rows = self.tune_params.get("decode_max_rows", 8) if isinstance(self.tune_params, dict) else 8
+            out, lse = K.sdpa(q, k, v, causal, scale, int(rows))
         except _lib.Unsupported:
             return None
         n, hq, l = out.shape[0], out.shape[1], out.shape[2]
@@ -286,7 +291,7 @@ class TopkImpl(_Family):
     def run(self, spec, args, kwargs):
         X, k, dim, largest, srt = spec
         try:
-            return ops.topk(X, k, dim=dim, largest=largest, sorted=srt)
+            return K.topk(X, k, dim, largest, srt)
         except _lib.Unsupported:
             return None
 
@@ -319,7 +324,7 @@ class GatherImpl(_Family):
     def run(self, spec, args, kwargs):
         dim, (Inp, Idx) = spec
         try:
-            return ops.gather(Inp, dim, Idx)
+            return K.gather(Inp, dim, Idx)
         except _lib.Unsupported:
             return None
 
@@ -350,7 +355,7 @@ class IndexImpl(_Family):
     def run(self, spec, args, kwargs):
         d, (X, idx) = spec
         try:
-            return ops.index(X, d, idx)
+            return K.index(X, d, idx)
         except _lib.Unsupported:
             return None
 

@@ -1,0 +1,141 @@
+"""PyTorch custom operators ``torch.ops.kuiops.*`` over the kuiops C ABI.
+
+These are the callers the C ABI is built for: the ``kuiops`` op families
+(``KuiperMode``) and the Inductor pass both go through them.  Each op has
+  * a CUDA (HIP) kernel: the ``ops`` function, which enqueues the HIP
+    kernels of libkuiops.so on the current stream;
+  * a fake (meta) implementation, so the ops trace under ``torch.compile``,
+    ``make_fx`` and FakeTensorMode without touching the device.
+There is no CPU kernel: calling an op on CPU tensors raises
+``NotImplementedError`` from the dispatcher, as a product op must not fall
+back silently.
+
+Schemas follow the aten ops they replace (mm, addmm, bmm, _softmax over the
+last dim, scaled-dot-product attention returning (out, lse), topk, gather,
+single-tensor index) with the reference's argument meaning
+(kuipy/kuiops.py:403-754).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+_LIB = torch.library.Library("kuiops", "DEF")
+
+_SCHEMAS = {
+    "mm": "mm(Tensor A, Tensor B) -> Tensor",
+    "addmm": "addmm(Tensor C, Tensor A, Tensor B, float beta=1.0, float alpha=1.0) -> Tensor",
+    "bmm": "bmm(Tensor A, Tensor B) -> Tensor",
+    "softmax": "softmax(Tensor x) -> Tensor",
+    "sdpa": "sdpa(Tensor q, Tensor k, Tensor v, bool is_causal=False, float? scale=None, "
+            "int decode_max_rows=8) -> (Tensor, Tensor)",
+    "sdpa_decode": "sdpa_decode(Tensor q, Tensor k, Tensor v, bool causal=True, float? scale=None) -> Tensor",
+    "topk": "topk(Tensor x, int k, int dim=-1, bool largest=True, bool sorted=True) -> (Tensor, Tensor)",
+    "gather": "gather(Tensor inp, int dim, Tensor idx) -> Tensor",
+    "index": "index(Tensor inp, int dim, Tensor idx) -> Tensor",
+}
+for _s in _SCHEMAS.values():
+    _LIB.define(_s)
+
+
+# ------------------------------------------------------------ HIP kernels
+
+def _mm(A, B):
+    return ops.mm(A, B)
+
+
+def _addmm(C, A, B, beta=1.0, alpha=1.0):
+    return ops.addmm(C, A, B, beta=beta, alpha=alpha)
+
+
+def _bmm(A, B):
+    return ops.bmm(A, B)
+
+
+def _softmax(x):
+    return ops.softmax(x)
+
+
+def _sdpa(q, k, v, is_causal=False, scale=None, decode_max_rows=8):
+    return ops.sdpa(q, k, v, is_causal=is_causal, scale=scale, return_lse=True,
+                    decode_max_rows=decode_max_rows)
+
+
+def _sdpa_decode(q, k, v, causal=True, scale=None):
+    return ops.sdpa_decode(q, k, v, scale=scale, causal=causal)[0]
+
+
+def _topk(x, k, dim=-1, largest=True, sorted=True):
+    v, i = ops.topk(x, k, dim=dim, largest=largest, sorted=sorted)
+    return v.contiguous(), i.contiguous()      # the strides the fake kernel promises
+
+
+def _gather(inp, dim, idx):
+    return ops.gather(inp, dim, idx)
+
+
+def _index(inp, dim, idx):
+    return ops.index(inp, dim, idx)
+
+
+for _name, _fn in (("mm", _mm), ("addmm", _addmm), ("bmm", _bmm), ("softmax", _softmax),
+                   ("sdpa", _sdpa), ("sdpa_decode", _sdpa_decode), ("topk", _topk),
+                   ("gather", _gather), ("index", _index)):
+    _LIB.impl(_name, _fn, "CUDA")
+
+
+# ------------------------------------------------- fake (meta) kernels
+
+def _fake(name):
+    return torch.library.register_fake(f"kuiops::{name}", lib=_LIB)
+
+
+@_fake("mm")
+def _mm_fake(A, B):
+    return A.new_empty((A.shape[0], B.shape[1]))
+
+
+@_fake("addmm")
+def _addmm_fake(C, A, B, beta=1.0, alpha=1.0):
+    return A.new_empty((A.shape[0], B.shape[1]))
+
+
+@_fake("bmm")
+def _bmm_fake(A, B):
+    return A.new_empty((A.shape[0], A.shape[1], B.shape[2]))
+
+
+@_fake("softmax")
+def _softmax_fake(x):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+@_fake("sdpa")
+def _sdpa_fake(q, k, v, is_causal=False, scale=None, decode_max_rows=8):
+    n, hq, l, _ = q.shape
+    return (q.new_empty((n, hq, l, v.shape[-1])),
+            q.new_empty((n, hq, l), dtype=torch.float32))
+
+
+@_fake("sdpa_decode")
+def _sdpa_decode_fake(q, k, v, causal=True, scale=None):
+    return q.new_empty((*q.shape[:3], v.shape[-1]))
+
+
+@_fake("topk")
+def _topk_fake(x, k, dim=-1, largest=True, sorted=True):
+    shape = list(x.shape)
+    shape[dim % x.dim()] = k
+    return x.new_empty(shape), x.new_empty(shape, dtype=torch.int64)
+
+
+@_fake("gather")
+def _gather_fake(inp, dim, idx):
+    return inp.new_empty(idx.shape)
+
+
+@_fake("index")
+def _index_fake(inp, dim, idx):
+    dim = dim % inp.dim()
+    return inp.new_empty((*inp.shape[:dim], *idx.shape, *inp.shape[dim + 1:]))
