@@ -150,7 +150,88 @@ def extra_workloads(torch, ops, steps, warmup, dev):
     out["sampling_softmax_top1_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
     ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 50), steps, warmup, reps=20)
     out["sampling_softmax_top50_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
+    out["llama1b_greedy"] = llama_workload(torch, dev)
     return out
+
+
+LLAMA1B = dict(vocab=32000, d=2048, ffn=5632, layers=16, hq=32, hkv=8)
+
+
+def llama_state(torch, c, device, seed=0):
+    """Random-init Llama-style weights (transformers parameter names):
+    linear / embedding weights N(0, 0.02), norm weights 1."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    hd = c["d"] // c["hq"]
+
+    def w(o, i):
+        return (torch.randn(o, i, device=device, generator=g) * 0.02).to(torch.bfloat16)
+
+    st = {"model.embed_tokens.weight": w(c["vocab"], c["d"]), "lm_head.weight": w(c["vocab"], c["d"]),
+          "model.norm.weight": torch.ones(c["d"], device=device, dtype=torch.bfloat16)}
+    for i in range(c["layers"]):
+        p = f"model.layers.{i}."
+        st[p + "self_attn.q_proj.weight"] = w(c["hq"] * hd, c["d"])
+        st[p + "self_attn.k_proj.weight"] = w(c["hkv"] * hd, c["d"])
+        st[p + "self_attn.v_proj.weight"] = w(c["hkv"] * hd, c["d"])
+        st[p + "self_attn.o_proj.weight"] = w(c["d"], c["hq"] * hd)
+        st[p + "mlp.gate_proj.weight"] = w(c["ffn"], c["d"])
+        st[p + "mlp.up_proj.weight"] = w(c["ffn"], c["d"])
+        st[p + "mlp.down_proj.weight"] = w(c["d"], c["ffn"])
+        st[p + "input_layernorm.weight"] = torch.ones(c["d"], device=device, dtype=torch.bfloat16)
+        st[p + "post_attention_layernorm.weight"] = torch.ones(c["d"], device=device, dtype=torch.bfloat16)
+    return st
+
+
+def llama_decode_bytes(c, kv_tokens):
+    """HBM bytes one decode token must read: every weight but the embedding
+    table once (bf16) plus the K and V of kv_tokens cached positions."""
+    hd = c["d"] // c["hq"]
+    per_layer = c["d"] * (c["hq"] + 2 * c["hkv"]) * hd + c["hq"] * hd * c["d"] + 3 * c["d"] * c["ffn"]
+    weights = (c["layers"] * per_layer + c["d"] * c["vocab"]) * 2
+    return weights + c["layers"] * 2 * c["hkv"] * hd * 2 * kv_tokens
+
+
+def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3):
+    """random-init Llama-style 1B decoder (16 layers, d 2048,
+    32 q / 8 kv heads, head_dim 64, FFN 5632 SwiGLU, vocab 32000), bf16; a
+    512-token uniform-random prompt, then 128 greedy tokens (softmax + top-1).
+    Prefill runs eagerly; each decode step is one HIP-graph replay."""
+    from kuillm_amd.decoder import LlamaDecoder, LlamaShape
+    c = LLAMA1B
+    shape = LlamaShape(**c)
+    dec = LlamaDecoder(shape, llama_state(torch, c, dev), capacity=prompt_len + n_new, device=dev)
+    prompt = torch.randint(0, c["vocab"], (1, prompt_len), generator=torch.Generator().manual_seed(0))
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    dec.generate(prompt, n_new)                              # warm-up + graph capture
+    pre_ms, dec_ms = [], []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        a, b, e = ev(), ev(), ev()
+        a.record()
+        dec.prefill(prompt)
+        b.record()
+        dec.decode(n_new)
+        e.record()
+        torch.cuda.synchronize()
+        pre_ms.append(a.elapsed_time(b))
+        dec_ms.append(b.elapsed_time(e))
+    pre, dms = min(pre_ms), min(dec_ms)
+    step_ms = dms / (n_new - 1)
+    tok_s = 1e3 / step_ms
+    # bytes of the average step: KV grows from prompt_len + 1 to prompt_len + n_new - 1 keys
+    step_bytes = llama_decode_bytes(c, prompt_len + n_new / 2)
+    gbs = step_bytes * tok_s / 1e9
+    flops_prefill = 2 * prompt_len * (llama_decode_bytes(c, 0) / 2) + \
+        c["layers"] * 2 * 2 * c["hq"] * (c["d"] // c["hq"]) * prompt_len * prompt_len / 2
+    del dec
+    return {"value": round(tok_s, 1), "unit": "tokens/s", "decode_ms_per_token": round(step_ms, 4),
+            "prefill_ms": round(pre, 3), "prefill_tokens_per_s": round(prompt_len / pre * 1e3, 1),
+            "prefill_tflops": round(flops_prefill / (pre * 1e-3) / 1e12, 1),
+            "end_to_end_tokens_per_s": round(n_new / ((pre + dms) * 1e-3), 1),
+            "decode_bytes_per_token": int(step_bytes),
+            "roofline": roofline("hbm", gbs, "GB/s"),
+            "config": "random-init Llama-style 1B (16 x d2048, GQA 32/8, hd 64, FFN 5632, vocab 32000), "
+                      "bf16, batch 1, 512-token prompt, 128 greedy tokens"}
 
 
 def main():

@@ -176,15 +176,20 @@ KUIOPS_API int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, in
  * key axis; same tensor conventions as kuiops_sdpa_fwd.  Causal masking with
  * l > 1 aligns the queries to the END of the keys (query i sees keys
  * j <= s - l + i), which is what a KV-cache decode step needs; pass
- * causal = 0 for plain full attention.  Requires the workspace of
- * kuiops_query_workspace(KUIOPS_OP_SDPA_DECODE, n*hq*l, s, ev).            */
+ * causal = 0 for plain full attention.  kv_len (optional, device memory,
+ * int32[n]) gives each batch entry's key count s_b <= s, read when the
+ * kernel runs: a decode step recorded once in a HIP graph passes s = cache
+ * capacity and advances kv_len on the device.  Requires the workspace of
+ * kuiops_query_workspace(KUIOPS_OP_SDPA_DECODE, n*hq*l, s, ev).
+ * Replaces the decode use of the reference sdpa launcher
+ * (kuiops/sdpa/wrapper_sdpa.cu.j2:21-30), which has no KV-cache form.     */
 KUIOPS_API int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s,
                        int64_t e, int64_t ev, int dtype,
                        const void *Q, const int64_t sq[3],
                        const void *K, const int64_t sk[3],
                        const void *V, const int64_t sv[3],
                        void *O, const int64_t so[3],
-                       float *lse, float scale, int causal,
+                       float *lse, float scale, int causal, const int32_t *kv_len,
                        void *workspace, size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------- sampling tail --
@@ -228,6 +233,43 @@ KUIOPS_API int kuiops_gather(int rank, const int64_t *inp_shape, const int64_t *
 KUIOPS_API int kuiops_index(int64_t outer, int64_t size, int64_t inner, int64_t n_idx,
                  int elem_bytes, const void *inp, const int64_t *idx,
                  void *out, int *err_flag, void *stream);
+
+/* ---- decoder-layer glue (the elementwise / norm / cat work around the hot
+ * path; bf16 or f16, rows 16-byte aligned, n % 8 == 0) ------------------- */
+
+/* RMSNorm with an optional fused residual add, per row of [m, n]:
+ *   h = x (+ residual)      res_out = h (if non-null; may equal residual)
+ *   y = weight * round(h * rsqrt(mean(h^2) + eps)),  n <= 8192.
+ * Replaces the reference's elementwise chain pow / mean.dim / add / rsqrt /
+ * mul (ElementwiseImpl kuipy/kuiops.py:150-320, MeanImpl :860-921), one
+ * launch per aten op there.                                                */
+KUIOPS_API int kuiops_rmsnorm(int64_t m, int64_t n, int dtype, const void *x, int64_t ldx,
+                   const void *residual, int64_t ldr, void *res_out, int64_t ldro,
+                   const void *weight, float eps, void *y, int64_t ldy, void *stream);
+
+/* SwiGLU: out[m, n] = silu(gate) * up, where row i of gate_up is
+ * [gate (n) | up (n)] (one fused gate/up projection).  Replaces the
+ * reference's silu + mul elementwise launches (kuipy/kuiops.py:158,166). */
+KUIOPS_API int kuiops_silu_mul(int64_t m, int64_t n, int dtype, const void *gate_up, int64_t ldg,
+                    void *out, int64_t ldo, void *stream);
+
+/* Rotary embedding fused with the KV-cache append for t new tokens of n
+ * sequences.  Token (b, i)'s row of qkv (at qkv + b*ld_batch + i*ld_tok
+ * elements) is [q heads (hq*hd) | k heads (hkv*hd) | v heads (hkv*hd)];
+ * its position is pos0[b] + i (pos0: device int32[n], or null for 0).
+ * q is rotated into q_out[b, h, i, :] (strides sq = batch, head, token);
+ * rotated k and plain v are stored at cache position pos (strides
+ * sk / sv = batch, head, position) when pos < cache_cap.  inv_freq is a
+ * device fp32 array of hd/2 rotary frequencies.  Replaces the reference's
+ * rotary mul / neg / cat / add launches and the KV-cache cat
+ * (CatImpl kuipy/kuiops.py:810-857).                                      */
+KUIOPS_API int kuiops_rope_kv_append(int64_t n, int64_t t, int64_t hq, int64_t hkv, int64_t hd,
+                          int dtype, const void *qkv, int64_t ld_tok, int64_t ld_batch,
+                          const float *inv_freq, const int32_t *pos0,
+                          void *q_out, const int64_t sq[3],
+                          void *k_cache, const int64_t sk[3],
+                          void *v_cache, const int64_t sv[3], int64_t cache_cap,
+                          void *stream);
 
 #ifdef __cplusplus
 }

@@ -53,11 +53,15 @@ SIGNATURES = {
     "kuiops_sdpa_fwd": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
                                _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp]),
     "kuiops_sdpa_decode": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
-                                  _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp, _sz, _vp]),
+                                  _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp, _vp, _sz, _vp]),
     "kuiops_softmax_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp]),
     "kuiops_topk_lastdim": (_int, [_i64, _i64, _i64, _int, _vp, _vp, _vp, _int, _int, _vp, _sz, _vp]),
     "kuiops_gather": (_int, [_int, _i64p, _i64p, _int, _int, _vp, _vp, _vp, _vp, _vp]),
     "kuiops_index": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
+    "kuiops_rmsnorm": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _flt, _vp, _i64, _vp]),
+    "kuiops_silu_mul": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp]),
+    "kuiops_rope_kv_append": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _vp, _vp,
+                                     _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp]),
 }
 
 

@@ -46,6 +46,7 @@ struct AttnArgs {
     int row_groups;
     float *ws_ml;       // [rows_total][splits][2]
     float *ws_o;        // [rows_total][splits][ev]
+    const int32_t *kv_len;  // decode: per-batch key count in device memory (<= s), or null
 };
 
 constexpr float kLn2 = 0.69314718055994530942f;
@@ -329,8 +330,11 @@ __global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
 
     const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
     const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
+    // keys of this batch entry: s, or the cache length read from device
+    // memory (a graph-captured decode step keeps s at the cache capacity)
+    const int64_t s_b = a.kv_len ? max((int64_t)0, min((int64_t)a.kv_len[b], a.s)) : a.s;
     const int64_t kbeg = (int64_t)split * a.chunk;
-    const int64_t kend = min(a.s, kbeg + a.chunk);
+    const int64_t kend = min(s_b, kbeg + a.chunk);
 
     // Query rows: row r -> head hk*G + (r / l), query index r % l.
     float q[R][8];
@@ -348,7 +352,7 @@ __global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) q[r][e] = to_f32(qv[e]) * a.scale_log2;
         // keys visible to this row (exclusive bound)
-        last_key[r] = ok ? (a.causal ? a.s - a.l + qi + 1 : a.s) : 0;
+        last_key[r] = ok ? (a.causal ? s_b - a.l + qi + 1 : s_b) : 0;
     }
 
     float m[R], lsum[R], o[R][8];
@@ -611,8 +615,9 @@ extern "C" int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, in
 extern "C" int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, int64_t e,
                                   int64_t ev, int dtype, const void *Q, const int64_t sq[3], const void *K,
                                   const int64_t sk[3], const void *V, const int64_t sv[3], void *O,
-                                  const int64_t so[3], float *lse, float scale, int causal, void *workspace,
-                                  size_t workspace_bytes, void *stream) {
+                                  const int64_t so[3], float *lse, float scale, int causal,
+                                  const int32_t *kv_len, void *workspace, size_t workspace_bytes,
+                                  void *stream) {
     int status;
     if (!attn_common_ok(n, hq, hkv, l, s, e, ev, dtype, Q, sq, K, sk, V, sv, O, so, status)) {
         if (status == KUIOPS_E_INVALID || n * hq * l != 0) return status;
@@ -622,6 +627,7 @@ extern "C" int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l,
     if (n > 65535 || hkv * cdiv((hq / hkv) * l, 8) > 65535) return KUIOPS_E_UNSUPPORTED;
     AttnArgs a{};
     fill_args(a, n, hq, hkv, l, s, Q, sq, K, sk, V, sv, O, so, lse, scale, causal);
+    a.kv_len = kv_len;
     const int64_t ss = s > 0 ? s : 1;
     a.chunk = decode_chunk(ss);
     a.splits = (int)cdiv(ss, a.chunk);

@@ -1,0 +1,224 @@
+"""Llama-style decoder on the kuiops kernels: prefill + greedy decode with a
+KV cache, the decode step recorded once in a HIP graph and replayed per token.
+
+This is the model the reference runs through ``KuiperMode`` (infer.py:14-31:
+a transformers causal LM, bf16, greedy / sampled ``generate``), with every
+op of the step on a kuiops kernel:
+
+    embedding        kuiops_index                  (aten.index / embedding)
+    RMSNorm (+res)   kuiops_rmsnorm                (pow / mean / rsqrt / mul / add)
+    q, k, v          kuiops_gemv_splitk / mm       one fused [d, (hq+2hkv) hd] weight
+    rotary + cache   kuiops_rope_kv_append         (mul / neg / cat / add, cache cat)
+    attention        kuiops_sdpa_fwd (prefill), kuiops_sdpa_decode (decode,
+                     KV length read from device memory)
+    o, gate|up, down kuiops_gemv_splitk / mm       gate and up fused
+    SwiGLU           kuiops_silu_mul
+    LM head          kuiops_gemv_splitk / mm
+    sampling tail    kuiops_softmax_lastdim + kuiops_topk_lastdim (k = 1)
+
+Weights are stored [in, out] row-major (``W.t().contiguous()``): the decode
+GEMMs then stream W in 128-byte row segments, the layout the skinny GEMM
+kernel reads at HBM speed.  Numerics follow the transformers modules (each op
+rounds to bf16 where the stock module does), so greedy tokens match the stock
+model except where two logits tie within bf16 resolution.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+
+@dataclass
+class LlamaShape:
+    vocab: int
+    d: int
+    ffn: int
+    layers: int
+    hq: int
+    hkv: int
+    eps: float = 1e-5
+    theta: float = 10000.0
+
+    @property
+    def hd(self) -> int:
+        return self.d // self.hq
+
+    @classmethod
+    def from_hf(cls, c) -> "LlamaShape":
+        theta = getattr(c, "rope_theta", None)
+        if theta is None:
+            theta = (getattr(c, "rope_parameters", None) or {}).get("rope_theta", 10000.0)
+        return cls(vocab=c.vocab_size, d=c.hidden_size, ffn=c.intermediate_size, layers=c.num_hidden_layers,
+                   hq=c.num_attention_heads, hkv=c.num_key_value_heads, eps=c.rms_norm_eps, theta=float(theta))
+
+
+def rope_inv_freq(hd: int, theta: float) -> torch.Tensor:
+    """1 / theta^(2i / hd) in fp32, computed as the transformers default rotary init."""
+    return 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).float() / hd))
+
+
+class LlamaDecoder:
+    """Greedy generation for one batch of equal-length prompts.
+
+    ``state`` maps transformers parameter names (``model.layers.{i}.self_attn.q_proj.weight``
+    ...) to tensors; ``capacity`` is the KV-cache length (prompt + new tokens).
+    """
+
+    def __init__(self, shape: LlamaShape, state: dict, capacity: int, batch: int = 1,
+                 device="cuda", dtype=torch.bfloat16):
+        self.s = s = shape
+        self.cap = int(capacity)
+        self.n = int(batch)
+        self.dev = torch.device(device)
+        self.dtype = dtype
+        if s.hd not in (64, 128) or s.hq % s.hkv:
+            raise ValueError("head_dim must be 64 or 128 and hq a multiple of hkv")
+
+        def w(name):
+            return state[name].to(self.dev, dtype)
+
+        def kn(*names):       # nn.Linear weights [out, in] -> one [in, sum(out)] row-major matrix
+            return torch.cat([w(x) for x in names], 0).t().contiguous()
+
+        self.embed = w("model.embed_tokens.weight").contiguous()
+        self.layers = []
+        for i in range(s.layers):
+            p = f"model.layers.{i}."
+            self.layers.append(dict(
+                ln1=w(p + "input_layernorm.weight").contiguous(),
+                wqkv=kn(p + "self_attn.q_proj.weight", p + "self_attn.k_proj.weight", p + "self_attn.v_proj.weight"),
+                wo=kn(p + "self_attn.o_proj.weight"),
+                ln2=w(p + "post_attention_layernorm.weight").contiguous(),
+                wgu=kn(p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"),
+                wd=kn(p + "mlp.down_proj.weight"),
+            ))
+        self.norm = w("model.norm.weight").contiguous()
+        head = state.get("lm_head.weight", state["model.embed_tokens.weight"])
+        self.head = head.to(self.dev, dtype).t().contiguous()
+        self.inv_freq = rope_inv_freq(s.hd, s.theta).to(self.dev)
+        kv = (s.layers, self.n, s.hkv, self.cap, s.hd)
+        self.kcache = torch.zeros(kv, dtype=dtype, device=self.dev)
+        self.vcache = torch.zeros(kv, dtype=dtype, device=self.dev)
+        # device-side decode state: the token to feed, its position, the key count
+        self.tok = torch.zeros(self.n, dtype=torch.int64, device=self.dev)
+        self.pos = torch.zeros(self.n, dtype=torch.int32, device=self.dev)
+        self.kv_len = torch.zeros(self.n, dtype=torch.int32, device=self.dev)
+        self.graph = None
+        self.out_tokens = None
+
+    @classmethod
+    def from_hf(cls, model, capacity: int, batch: int = 1, device="cuda"):
+        return cls(LlamaShape.from_hf(model.config), model.state_dict(), capacity, batch, device)
+
+    # ------------------------------------------------------------ forward
+
+    def _layers(self, h, t, pos0, kv_len):
+        """Run every layer on h [n * t, d] (t new tokens per sequence at
+        positions pos0 ..); returns the final-norm input (last MLP output)
+        and the residual stream."""
+        s, n = self.s, self.n
+        res = h
+        pending = None
+        q = torch.empty((n, s.hq, t, s.hd), dtype=self.dtype, device=self.dev)
+        att = torch.empty((n, t, s.hq * s.hd), dtype=self.dtype, device=self.dev)
+        att4 = att.view(n, t, s.hq, s.hd).transpose(1, 2)            # [n, hq, t, hd] view
+        for i, L in enumerate(self.layers):
+            if pending is None:
+                x = ops.rmsnorm(res, L["ln1"], s.eps)
+            else:
+                x = ops.rmsnorm(pending, L["ln1"], s.eps, residual=res, res_out=res)
+            qkv = ops.mm(x, L["wqkv"]).view(n, t, -1)
+            kc, vc = self.kcache[i], self.vcache[i]
+            ops.rope_kv_append(qkv, s.hq, s.hkv, s.hd, self.inv_freq, pos0, q, kc, vc)
+            if t == 1:
+                ops.sdpa_decode(q, kc, vc, causal=True, kv_len=kv_len, out=att4)
+            else:
+                # prefill from position 0: the keys are the t just stored
+                ops.sdpa(q, kc[:, :, :t], vc[:, :, :t], is_causal=True, return_lse=False, out=att4)
+            o = ops.mm(att.view(n * t, -1), L["wo"])
+            x = ops.rmsnorm(o, L["ln2"], s.eps, residual=res, res_out=res)
+            a = ops.silu_mul(ops.mm(x, L["wgu"]))
+            pending = ops.mm(a, L["wd"])
+        return pending, res
+
+    def _head(self, pending, res, t):
+        """Greedy next token of each sequence from its last position."""
+        n = self.n
+        last = (lambda z: z.view(n, t, -1)[:, -1]) if t > 1 else (lambda z: z)
+        x = ops.rmsnorm(last(pending), self.norm, self.s.eps, residual=last(res))
+        logits = ops.mm(x, self.head)                               # bf16, as the stock LM head
+        probs = ops.softmax(logits.float())
+        _, idx = ops.topk(probs, 1)
+        return logits, idx.view(n)
+
+    def prefill(self, prompt: torch.Tensor):
+        """Run the prompt [n, t] (positions 0 .. t-1) and fill the KV cache;
+        returns (last-position logits [n, vocab], next tokens [n])."""
+        n, t = prompt.shape
+        if n != self.n or t > self.cap:
+            raise ValueError("prompt does not fit the batch / cache")
+        ids = prompt.to(self.dev).reshape(-1).contiguous()
+        h = ops.index(self.embed, 0, ids)
+        self.pos.zero_()
+        pending, res = self._layers(h, t, self.pos, None)
+        logits, nxt = self._head(pending, res, t)
+        self.tok.copy_(nxt)
+        self.pos.fill_(t)
+        self.kv_len.fill_(t + 1)
+        return logits, nxt
+
+    def _decode_step(self):
+        h = ops.index(self.embed, 0, self.tok)
+        pending, res = self._layers(h, 1, self.pos, self.kv_len)
+        logits, nxt = self._head(pending, res, 1)
+        self.tok.copy_(nxt)
+        self.pos.add_(1)
+        self.kv_len.add_(1)
+        return logits
+
+    def capture(self):
+        """Record one decode step (all its kernels) in a HIP graph.  The step
+        reads the token, position and key count from device memory and
+        advances them, so replays need no host work."""
+        saved = (self.tok.clone(), self.pos.clone(), self.kv_len.clone(),
+                 self.kcache.clone(), self.vcache.clone())
+        self._decode_step()                              # eager: allocates workspaces
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(self.dev)
+        side.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(side):
+            self._decode_step()
+        torch.cuda.current_stream(self.dev).wait_stream(side)
+        with torch.cuda.graph(g):
+            self.graph_logits = self._decode_step()
+        torch.cuda.synchronize(self.dev)
+        for dst, src in zip((self.tok, self.pos, self.kv_len, self.kcache, self.vcache), saved):
+            dst.copy_(src)
+        self.graph = g
+
+    def decode(self, n_new: int, use_graph: bool = True) -> torch.Tensor:
+        """Greedy-decode n_new tokens after ``prefill``; returns [n, n_new]
+        (the first is the token prefill chose)."""
+        out = torch.empty((n_new, self.n), dtype=torch.int64, device=self.dev)
+        if n_new == 0:
+            return out.t()
+        if int(self.pos[0]) + n_new - 1 > self.cap:
+            raise ValueError("KV cache too small")
+        if use_graph and self.graph is None:
+            self.capture()
+        out[0].copy_(self.tok)
+        for i in range(1, n_new):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self._decode_step()
+            out[i].copy_(self.tok)
+        return out.t()
+
+    def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True) -> torch.Tensor:
+        self.prefill(prompt)
+        return self.decode(n_new, use_graph)

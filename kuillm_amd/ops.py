@@ -229,17 +229,22 @@ def _attn_prep(q, k, v):
     return q, k, v, (n, hq, hkv, l, s, e, ev)
 
 
-def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=8):
+def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=8, out=None):
     """softmax(scale * q k^T [causal]) v  ->  (out, lse)   (aten SDPA semantics).
 
     q (n, hq, l, e), k / v (n, hkv, s, e) with hq % hkv == 0; causal masking is
     aten's top-left alignment (query i sees keys j <= i).  Non-causal calls
-    with few query rows per KV head use the split-KV decode kernel.
+    with few query rows per KV head use the split-KV decode kernel.  ``out``
+    ([n, hq, l, ev] with a unit last stride, e.g. a transposed view of an
+    [n, l, hq, ev] buffer) receives the result in place.
     """
     q, k, v, (n, hq, hkv, l, s, e, ev) = _attn_prep(q, k, v)
     if scale is None:
         scale = 1.0 / math.sqrt(e)
-    out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
+    if out is None:
+        out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (n, hq, l, ev) or out.stride(-1) != 1 or out.dtype != q.dtype:
+        raise _lib.KuiopsError("sdpa", _lib.E_INVALID)
     lse = torch.empty((n, hq, l), dtype=torch.float32, device=q.device) if return_lse else None
     if out.numel() == 0:
         return out, lse
@@ -253,7 +258,7 @@ def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=
         ws = workspace(q.device, ws_bytes)
         _lib.check("kuiops_sdpa_decode", lib.kuiops_sdpa_decode(
             n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), sq, k.data_ptr(), sk,
-            v.data_ptr(), sv, out.data_ptr(), so, _ptr(lse), float(scale), 0,
+            v.data_ptr(), sv, out.data_ptr(), so, _ptr(lse), float(scale), 0, None,
             ws.data_ptr(), ws.numel(), _stream(q.device)))
         return out, lse
     _lib.check("kuiops_sdpa_fwd", lib.kuiops_sdpa_fwd(
@@ -263,13 +268,23 @@ def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=
     return out, lse
 
 
-def sdpa_decode(q, k, v, scale=None, causal=True, return_lse=False):
+def sdpa_decode(q, k, v, scale=None, causal=True, return_lse=False, kv_len=None, out=None):
     """Decode attention over a KV cache: the l queries are the LAST l positions
-    of the s keys (query i sees keys j <= s - l + i when ``causal``)."""
+    of the s keys (query i sees keys j <= s - l + i when ``causal``).
+
+    ``kv_len`` (int32 [n] on the device) limits batch entry b to its first
+    kv_len[b] keys, read when the kernel runs; k / v may then be the whole
+    cache (s = capacity).  ``out`` ([n, hq, l, ev], any strides with a unit
+    last stride) receives the result in place."""
     q, k, v, (n, hq, hkv, l, s, e, ev) = _attn_prep(q, k, v)
     if scale is None:
         scale = 1.0 / math.sqrt(e)
-    out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
+    if kv_len is not None and (kv_len.dtype != torch.int32 or kv_len.numel() != n or not kv_len.is_contiguous()):
+        raise _lib.KuiopsError("sdpa_decode", _lib.E_INVALID)
+    if out is None:
+        out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (n, hq, l, ev) or out.stride(-1) != 1 or out.dtype != q.dtype:
+        raise _lib.KuiopsError("sdpa_decode", _lib.E_INVALID)
     lse = torch.empty((n, hq, l), dtype=torch.float32, device=q.device) if return_lse else None
     if out.numel() == 0:
         return out, lse
@@ -280,7 +295,7 @@ def sdpa_decode(q, k, v, scale=None, causal=True, return_lse=False):
         n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), _lib.strides3(*q.stride()[:3]),
         k.data_ptr(), _lib.strides3(*k.stride()[:3]), v.data_ptr(), _lib.strides3(*v.stride()[:3]),
         out.data_ptr(), _lib.strides3(*out.stride()[:3]), _ptr(lse), float(scale), 1 if causal else 0,
-        ws.data_ptr(), ws.numel(), _stream(q.device)))
+        _ptr(kv_len), ws.data_ptr(), ws.numel(), _stream(q.device)))
     return out, lse
 
 
@@ -377,3 +392,77 @@ def index(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = N
         out.data_ptr(), _ptr(flag), _stream(inp.device)))
     _raise_if_flagged(flag, "index")
     return out
+
+
+# ------------------------------------------------------ decoder-layer glue
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    """2-D [m, n] view with unit column stride (copy otherwise)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    return x2 if x2.stride(-1) == 1 else x2.contiguous()
+
+
+def rmsnorm(x, weight, eps, residual=None, res_out=None, out=None):
+    """weight * round(h * rsqrt(mean(h^2, -1) + eps)) with h = x (+ residual).
+
+    With ``res_out`` given, h (the updated residual stream) is stored there;
+    it may be ``residual`` itself.  Shapes: x, residual, res_out, out are
+    [..., n]; weight is [n]."""
+    n = x.shape[-1]
+    x2 = _rows(x)
+    m = x2.shape[0]
+    r2 = None if residual is None else residual.reshape(-1, n)
+    ro2 = None if res_out is None else res_out.reshape(-1, n)
+    for t in (r2, ro2):
+        if t is not None and (t.shape[0] != m or t.stride(-1) != 1 or t.dtype != x.dtype):
+            raise _lib.KuiopsError("rmsnorm", _lib.E_INVALID)
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    o2 = out.view(-1, n)
+    if weight.shape != (n,) or weight.dtype != x.dtype or not weight.is_contiguous():
+        raise _lib.KuiopsError("rmsnorm", _lib.E_INVALID)
+    lib = _lib_handle()
+    _lib.check("kuiops_rmsnorm", lib.kuiops_rmsnorm(
+        m, n, _dt(x.dtype), x2.data_ptr(), x2.stride(0),
+        _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(ro2), 0 if ro2 is None else ro2.stride(0),
+        weight.data_ptr(), float(eps), o2.data_ptr(), o2.stride(0), _stream(x.device)))
+    return out
+
+
+def silu_mul(gate_up, out=None):
+    """silu(gate_up[..., :n]) * gate_up[..., n:] for gate_up [..., 2n]."""
+    g2 = _rows(gate_up)
+    m, n2 = g2.shape
+    n = n2 // 2
+    if out is None:
+        out = torch.empty((*gate_up.shape[:-1], n), dtype=gate_up.dtype, device=gate_up.device)
+    o2 = out.view(-1, n)
+    lib = _lib_handle()
+    _lib.check("kuiops_silu_mul", lib.kuiops_silu_mul(
+        m, n, _dt(gate_up.dtype), g2.data_ptr(), g2.stride(0), o2.data_ptr(), o2.stride(0),
+        _stream(gate_up.device)))
+    return out
+
+
+def rope_kv_append(qkv, hq, hkv, hd, inv_freq, pos0, q_out, k_cache, v_cache):
+    """Rotate q / k of the new tokens and append k / v to the cache.
+
+    qkv [n, t, (hq + 2 hkv) hd] (rows with a unit last stride); pos0 int32 [n]
+    on the device (first position of the t tokens) or None for 0; q_out
+    [n, hq, t, hd]; k_cache / v_cache [n, hkv, capacity, hd]."""
+    n, t, w = qkv.shape
+    if w != (hq + 2 * hkv) * hd or qkv.stride(-1) != 1 or inv_freq.dtype != torch.float32:
+        raise _lib.KuiopsError("rope_kv_append", _lib.E_INVALID)
+    if tuple(q_out.shape) != (n, hq, t, hd) or q_out.stride(-1) != 1:
+        raise _lib.KuiopsError("rope_kv_append", _lib.E_INVALID)
+    for c in (k_cache, v_cache):
+        if c.dim() != 4 or tuple(c.shape[:2]) != (n, hkv) or c.shape[3] != hd or c.stride(-1) != 1:
+            raise _lib.KuiopsError("rope_kv_append", _lib.E_INVALID)
+    if pos0 is not None and (pos0.dtype != torch.int32 or pos0.numel() != n):
+        raise _lib.KuiopsError("rope_kv_append", _lib.E_INVALID)
+    lib = _lib_handle()
+    _lib.check("kuiops_rope_kv_append", lib.kuiops_rope_kv_append(
+        n, t, hq, hkv, hd, _dt(qkv.dtype), qkv.data_ptr(), qkv.stride(1), qkv.stride(0),
+        inv_freq.data_ptr(), _ptr(pos0), q_out.data_ptr(), _lib.strides3(*q_out.stride()[:3]),
+        k_cache.data_ptr(), _lib.strides3(*k_cache.stride()[:3]),
+        v_cache.data_ptr(), _lib.strides3(*v_cache.stride()[:3]), k_cache.shape[2], _stream(qkv.device)))

@@ -18,6 +18,12 @@ therefore restates aten semantics, op by op, citing the reference's family:
   topk / index       no reference kernel (kuiops/topk/.gitkeep,
                      kuiops/index/.gitkeep): aten.topk / aten.index.Tensor
   verify metric      kuipy/__init__.py:193-225
+  decoder glue       RMSNorm / SwiGLU / rotary + KV cache and a whole
+                     Llama-style decoder: the stock
+                     transformers modules the reference runs under
+                     KuiperMode (infer.py:14-31), whose elementwise, mean
+                     and cat ops it sends to ElementwiseImpl / MeanImpl /
+                     CatImpl (kuipy/kuiops.py:150-320, 810-921)
 
 bf16 values travel as uint16 bit patterns (numpy has no bfloat16).
 
@@ -27,7 +33,11 @@ How each function is pinned (tests/test_oracle.py):
     wrong sign / index or a transposed operand fails (identity and one-hot
     operands, integer-valued products that are exact in fp32, softmax of a
     constant row, attention with constant V, single-key attention, causal
-    row 0, brute-force sorting for topk, explicit loops for gather / index).
+    row 0, brute-force sorting for topk, explicit loops for gather / index);
+  * the decoder pieces against the transformers Llama modules run on the
+    CPU (RMSNorm, rotary embedding, MLP, the whole causal LM), plus closed
+    forms (constant-row RMSNorm, position-0 rotation = identity, rotation
+    preserves pair norms).
 No function here is "parity unpinned".
 """
 from __future__ import annotations
@@ -263,3 +273,97 @@ def within(out, ref, rtol=1e-2, atol=1e-2) -> bool:
     o = np.asarray(out, dtype=np.float64)
     r = np.asarray(ref, dtype=np.float64)
     return bool(np.all(np.abs(o - r) <= atol + rtol * np.abs(r)))
+
+
+# ------------------------------------------------- decoder-layer glue
+# bf16 rounding points follow the transformers Llama modules: every torch
+# op on a bf16 tensor rounds its result to bf16.
+
+
+def rmsnorm(x, w, eps, residual=None):
+    """(y, h): h = x (+ residual, rounded), y = w * round(h * rsqrt(mean(h^2) + eps))
+    (LlamaRMSNorm: variance in fp32, weight applied to the rounded value)."""
+    x = np.asarray(x, dtype=np.float32)
+    h = x if residual is None else round_bf16(x + np.asarray(residual, dtype=np.float32))
+    var = np.mean(h.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    inv = (1.0 / np.sqrt(var + eps)).astype(np.float32)
+    return round_bf16(np.asarray(w, dtype=np.float32) * round_bf16(h * inv)), h
+
+
+def silu_mul(gate_up):
+    """round(round(silu(gate)) * up) for gate_up = [gate | up] on the last axis."""
+    gu = np.asarray(gate_up, dtype=np.float32)
+    n = gu.shape[-1] // 2
+    g, u = gu[..., :n].astype(np.float64), gu[..., n:]
+    return round_bf16(round_bf16(g / (1.0 + np.exp(-g))) * u)
+
+
+def rope_inv_freq(hd: int, theta: float) -> np.ndarray:
+    """1 / theta^(2i / hd), i < hd / 2, in fp32 (LlamaRotaryEmbedding default init)."""
+    e = (np.arange(0, hd, 2, dtype=np.int64).astype(np.float32) / np.float32(hd)).astype(np.float64)
+    return (1.0 / (float(theta) ** e)).astype(np.float32)
+
+
+def rope(x, pos, inv_freq):
+    """Split-half rotary embedding of x[..., t, hd] at positions pos[t]:
+    (x1, x2) -> (x1 c - x2 s, x2 c + x1 s), angle = fp32(pos * inv_freq),
+    c / s rounded to bf16, every product and sum rounded."""
+    x = np.asarray(x, dtype=np.float32)
+    hd = x.shape[-1]
+    half = hd // 2
+    ang = (np.asarray(pos, dtype=np.float32)[:, None] * np.asarray(inv_freq, dtype=np.float32)[None, :])
+    c = round_bf16(np.cos(ang.astype(np.float64)).astype(np.float32))
+    s_ = round_bf16(np.sin(ang.astype(np.float64)).astype(np.float32))
+    x1, x2 = x[..., :half], x[..., half:]
+    o1 = round_bf16(round_bf16(x1 * c) + round_bf16(-x2 * s_))
+    o2 = round_bf16(round_bf16(x2 * c) + round_bf16(x1 * s_))
+    return np.concatenate([o1, o2], axis=-1)
+
+
+def linear(x, W):
+    """round(x @ W^T) for an nn.Linear weight W[out, in] (bf16 result)."""
+    return round_bf16(mm(x, np.asarray(W, dtype=np.float32).T).astype(np.float32))
+
+
+def llama_forward(p: dict, tokens, cfg: dict) -> np.ndarray:
+    """Logits (bf16 values as fp32) of every position of one sequence for a
+    Llama-style causal LM: embedding, cfg['layers'] x (RMSNorm, GQA attention
+    with rotary q / k, residual, RMSNorm, SwiGLU MLP, residual), final
+    RMSNorm, LM head.  p holds the transformers parameter names (weights as
+    fp32 arrays of bf16 values)."""
+    d, hq, hkv = cfg["d"], cfg["hq"], cfg["hkv"]
+    hd = d // hq
+    eps = cfg["eps"]
+    T = len(tokens)
+    inv = rope_inv_freq(hd, cfg["theta"])
+    pos = np.arange(T)
+    h = np.asarray(p["model.embed_tokens.weight"], dtype=np.float32)[np.asarray(tokens)]
+    for i in range(cfg["layers"]):
+        pre = f"model.layers.{i}."
+        x, _ = rmsnorm(h, p[pre + "input_layernorm.weight"], eps)
+        q = linear(x, p[pre + "self_attn.q_proj.weight"]).reshape(T, hq, hd).transpose(1, 0, 2)
+        k = linear(x, p[pre + "self_attn.k_proj.weight"]).reshape(T, hkv, hd).transpose(1, 0, 2)
+        v = linear(x, p[pre + "self_attn.v_proj.weight"]).reshape(T, hkv, hd).transpose(1, 0, 2)
+        q, k = rope(q, pos, inv), rope(k, pos, inv)
+        a, _ = sdpa(q[None], k[None], v[None], causal=True)
+        a = round_bf16(a[0].transpose(1, 0, 2).reshape(T, hq * hd).astype(np.float32))
+        h = round_bf16(h + linear(a, p[pre + "self_attn.o_proj.weight"]))
+        x, _ = rmsnorm(h, p[pre + "post_attention_layernorm.weight"], eps)
+        g = linear(x, p[pre + "mlp.gate_proj.weight"])
+        u = linear(x, p[pre + "mlp.up_proj.weight"])
+        h = round_bf16(h + linear(silu_mul(np.concatenate([g, u], -1)), p[pre + "mlp.down_proj.weight"]))
+    x, _ = rmsnorm(h, p["model.norm.weight"], eps)
+    return linear(x, p["lm_head.weight"])
+
+
+def llama_greedy(p: dict, prompt, n_new: int, cfg: dict):
+    """Greedy continuation: (tokens, per-step fp32 logits of the chosen
+    position), recomputing the full forward each step (tiny configs only)."""
+    toks = list(int(t) for t in prompt)
+    steps = []
+    for _ in range(n_new):
+        lg = llama_forward(p, toks, cfg)[-1]
+        steps.append(lg)
+        probs = softmax(lg)
+        toks.append(int(topk(probs, 1)[1][0]))
+    return toks[len(prompt):], steps
