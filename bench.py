@@ -7,9 +7,11 @@ Headline (the JSON line's ``value``): BASELINE.json config 2, bf16 prefill
 addmm  out[4096,4096] = bias[4096] + A[4096,4096] @ B[4096,4096], A~N(0,1),
 B~N(0,0.02), fp32 accumulate, in bf16 TFLOP/s.  A "step" is one
 ``kuillm_amd.ops.addmm`` call (one MFMA kernel launch) on inputs resident in
-HBM.  Each step is recorded once in a HIP graph and the graph is replayed, so
-the timed region holds device work only; HIP events on the launch stream
-bracket exactly K replays after W warm-up replays.
+HBM.  Ten back-to-back steps are recorded in a HIP graph and the graph is
+replayed, so the timed region holds device work only and the per-replay
+launch cost is spread over ten kernels; HIP events on the launch stream
+bracket exactly K replays after W warm-up replays, and ``ms_per_step`` is the
+time per kernel.
 
 ``workloads`` (extra keys of the same line) measures the other BASELINE.json
 configs the same way: decode split-K GEMM (HBM GB/s), bmm, causal SDPA at
@@ -42,6 +44,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="run only the dominant kernel of each workload 3x plus a 256 MiB copy "
+                         "(the byte-counter calibration), for rocprofv3 --pmc runs")
     return ap.parse_args()
 
 
@@ -76,10 +81,55 @@ def graph_time_ms(torch, fn, steps, warmup, reps=1):
     return start.elapsed_time(end) / (steps * reps)
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+
+
+def traffic_bytes(kernel):
+    """HBM bytes per launch of `kernel` measured by rocprofv3 --pmc FETCH_SIZE
+    and WRITE_SIZE over ``bench.py --profile-kernels``, each scaled by what
+    the counter reads for a 256 MiB copy (profiles/hbm_traffic.json); None if
+    not measured."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(kernel)
+    if not k:
+        return None
+    return int(k["fetch_kib"] * 1024 * t["fetch_scale"] + k["write_kib"] * 1024 * t["write_scale"])
+
+
 def roofline(bound, achieved, unit, traffic=None):
     peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def profile_kernels(torch, ops, dev):
+    """The dominant kernel of each measured workload, 3 launches each, then a
+    256 MiB device copy whose byte counts calibrate FETCH_SIZE / WRITE_SIZE."""
+    g = torch.Generator(device=dev).manual_seed(0)
+    A = torch.randn(4096, 4096, device=dev, generator=g).to(torch.bfloat16)
+    B = (torch.randn(4096, 4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    for _ in range(3):
+        ops.addmm(bias, A, B)
+    W = (torch.randn(4096, 11008, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(4, 4096, device=dev, generator=g).to(torch.bfloat16)
+    for _ in range(3):
+        ops.mm(x, W)
+    q, k, v = (torch.randn(1, 32, 4096, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    for _ in range(3):
+        ops.sdpa(q, k, v, is_causal=True)
+    qd = torch.randn(1, 32, 1, 128, device=dev, generator=g).to(torch.bfloat16)
+    for _ in range(3):
+        ops.sdpa(qd, k, v)
+    src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def cpu_baseline(torch, seconds):
@@ -115,12 +165,13 @@ def extra_workloads(torch, ops, steps, warmup, dev):
         nbytes = 4096 * 11008 * 2 + M * 4096 * 2 + M * 11008 * 2
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"decode_gemm_M{M}"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 5),
-                                    "roofline": roofline("hbm", gbs, "GB/s")}
+                                    "roofline": roofline("hbm", gbs, "GB/s",
+                                                         traffic_bytes("decode_gemm_M4") if M == 4 else None)}
     del W
     # config 2b: bmm 32 x [2048,128] @ [128,2048]
     A3 = torch.randn(32, 2048, 128, device=dev).to(bf)
     B3 = torch.randn(32, 128, 2048, device=dev).to(bf)
-    ms = graph_time_ms(torch, lambda: ops.bmm(A3, B3), steps, warmup)
+    ms = graph_time_ms(torch, lambda: ops.bmm(A3, B3), steps, warmup, reps=5)
     tf = 2 * 32 * 2048 * 2048 * 128 / (ms * 1e-3) / 1e12
     gbs = (2 * 32 * 2048 * 128 * 2 + 32 * 2048 * 2048 * 2) / (ms * 1e-3) / 1e9
     out["bmm_32x2048x128x2048"] = {"value": round(tf, 1), "unit": "TFLOP/s", "ms": round(ms, 5),
@@ -132,10 +183,11 @@ def extra_workloads(torch, ops, steps, warmup, dev):
         q = torch.randn(1, 32, S, 128, device=dev).to(bf)
         k = torch.randn_like(q)
         v = torch.randn_like(q)
-        ms = graph_time_ms(torch, lambda: ops.sdpa(q, k, v, is_causal=True), steps, warmup)
+        ms = graph_time_ms(torch, lambda: ops.sdpa(q, k, v, is_causal=True), steps, warmup, reps=5)
         tf = 0.5 * 4 * 32 * S * S * 128 / (ms * 1e-3) / 1e12
         out[f"sdpa_causal_S{S}"] = {"value": round(tf, 1), "unit": "TFLOP/s", "ms": round(ms, 5),
-                                    "roofline": roofline("mfma", tf, "TFLOP/s")}
+                                    "roofline": roofline("mfma", tf, "TFLOP/s",
+                                                         traffic_bytes("sdpa_causal_S4096") if S == 4096 else None)}
     # config 3b: decode SDPA, S_q = 1 over a 4096-token KV cache
     qd = torch.randn(1, 32, 1, 128, device=dev).to(bf)
     kc = torch.randn(1, 32, 4096, 128, device=dev).to(bf)
@@ -143,7 +195,7 @@ def extra_workloads(torch, ops, steps, warmup, dev):
     ms = graph_time_ms(torch, lambda: ops.sdpa(qd, kc, vc), steps, warmup, reps=20)
     gbs = 2 * 32 * 4096 * 128 * 2 / (ms * 1e-3) / 1e9
     out["sdpa_decode_kv4096"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 5),
-                                 "roofline": roofline("hbm", gbs, "GB/s")}
+                                 "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes("sdpa_decode_kv4096"))}
     # sampling tail: softmax + top-1 / top-50 over a [1, 32000] fp32 logit row
     logits = torch.randn(1, 32000, device=dev)
     ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 1), steps, warmup, reps=20)
@@ -249,13 +301,16 @@ def main():
     from kuillm_amd import ops
     _compile.load_library()                 # fails loudly when libkuiops.so is missing
     dev = torch.device("cuda:0")
+    if args.profile_kernels:
+        profile_kernels(torch, ops, dev)
+        return
 
     # ---- headline: BASELINE config 2, bf16 addmm 4096^3 with a 1-D bias
     g = torch.Generator(device=dev).manual_seed(0)
     A = torch.randn(4096, 4096, device=dev, generator=g).to(torch.bfloat16)
     B = (torch.randn(4096, 4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
     bias = (torch.randn(4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    ms = graph_time_ms(torch, lambda: ops.addmm(bias, A, B), args.steps, args.warmup)
+    ms = graph_time_ms(torch, lambda: ops.addmm(bias, A, B), args.steps, args.warmup, reps=10)
     flops = 2 * 4096 ** 3
     tflops = flops / (ms * 1e-3) / 1e12
     line = {
@@ -273,7 +328,7 @@ def main():
         "data": "synthetic (seeded N(0,1) / N(0,0.02) tensors, resident in HBM)",
         "config": {"workload": "prefill addmm bf16 bias[4096] + A[4096,4096] @ B[4096,4096], fp32 accumulate",
                    "M": 4096, "N": 4096, "K": 4096, "b_layout": "row-major [K,N]", "parallelism": "single GPU"},
-        "roofline": roofline("mfma", tflops, "TFLOP/s"),
+        "roofline": roofline("mfma", tflops, "TFLOP/s", traffic_bytes("addmm_4096")),
     }
     del A, B, bias
     if not args.no_extra:
