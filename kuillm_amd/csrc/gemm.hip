@@ -62,6 +62,27 @@ __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, i
     tn = in_group / gsz;
 }
 
+// Batched form: the linear id runs over batch x tiles; after the XCD remap
+// each batch entry's tiles are contiguous (so one XCD's L2 holds its A and
+// B), and tiles are grouped by 8 tile-rows within the entry.
+__device__ __forceinline__ void tile_coords_batched(int bid, int nblocks, int tiles_m, int tiles_n,
+                                                    int &tm, int &tn, int &bz) {
+    const int xcd = bid & 7, idx = bid >> 3;
+    const int q = nblocks >> 3, r = nblocks & 7;
+    const int pid = xcd * q + (xcd < r ? xcd : r) + idx;
+    const int per = tiles_m * tiles_n;
+    bz = pid / per;
+    const int t = pid - bz * per;
+    const int G = 8;
+    const int width = G * tiles_n;
+    const int group = t / width;
+    const int first_m = group * G;
+    const int gsz = min(tiles_m - first_m, G);
+    const int in_group = t - group * width;
+    tm = first_m + in_group % gsz;
+    tn = in_group / gsz;
+}
+
 template <typename Tout>
 __device__ __forceinline__ void epilogue_store(const GemmArgs &a, Tout *out, const Tout *cin,
                                                int64_t row, int64_t col, float acc) {
@@ -354,8 +375,11 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn);
+    int tm, tn, bz;
+    tile_coords_batched(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn, bz);
+    a.A = reinterpret_cast<const T *>(a.A) + bz * a.stride_a;
+    a.B = reinterpret_cast<const T *>(a.B) + bz * a.stride_b;
+    a.out = reinterpret_cast<Tout *>(a.out) + bz * a.stride_o;
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int nk = (int)(a.K / BK);                // multiple of NS
 
@@ -611,8 +635,10 @@ static bool dma_eligible(const GemmArgs &a, int64_t batch, bool bcol) {
     const int64_t lim = (int64_t)1 << 30;
     if ((256 * a.lda + a.K) >= lim) return false;
     if (bcol ? (256 * a.ldb + a.K) >= lim : (a.K * a.ldb + 256) >= lim) return false;
-    return batch == 1 && a.K % 128 == 0 && a.K > 0 && a.M >= 256 && a.N >= 256 &&
-           cdiv(a.M, 256) * cdiv(a.N, 256) >= 128;
+    // batched operands: the addend (addmm only) is not batched
+    if (batch > 1 && (a.c_kind != KUIOPS_C_NONE || a.stride_a % 8 || a.stride_b % 8)) return false;
+    return a.K % 128 == 0 && a.K > 0 && a.M >= 256 && a.N >= 256 &&
+           cdiv(a.M, 256) * cdiv(a.N, 256) * batch >= 128 && cdiv(a.M, 256) * cdiv(a.N, 256) * batch < INT32_MAX;
 }
 
 template <typename T, typename Tout>
@@ -621,7 +647,7 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
     if (splits_req <= 1 && dma_eligible(a, batch, bcol)) {
         a.tiles_m = (int)cdiv(a.M, 256);
         a.tiles_n = (int)cdiv(a.N, 256);
-        dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+        dim3 grid((unsigned)(a.tiles_m * a.tiles_n * batch));
         // 8 waves (2 per SIMD, 128x64 each), BK = 64, two LDS stages: the best of
         // the measured variants (4 waves x 128x128, BK = 32 with four stages,
         // and an 8-wave ping-pong schedule were all slower at 4096^3 / 8192^3).
