@@ -84,14 +84,14 @@ __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t vof
 // are rescaled: probabilities stay below 2^8 meanwhile.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename T, int HD, bool CAUSAL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <typename T, int HD, bool CAUSAL, int NWV>
+__global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(AttnArgs a) {
-    constexpr int BQ = 128, BKV = 64;
+    constexpr int BQ = 32 * NWV, BKV = 64;          // 32 queries per wave
     constexpr int RB = HD * 2;                      // bytes per K / V row
     constexpr int CPR = HD / 8;                     // 16-byte chunks per row
     constexpr int TILE = BKV * RB;                  // bytes per K or V tile
-    constexpr int DPW = TILE / 1024 / 4;            // 1 KB DMA blocks per wave per tile
+    constexpr int DPW = TILE / 1024 / NWV;          // 1 KB DMA blocks per wave per tile
     constexpr int RPB = 1024 / RB;                  // rows per DMA block
     constexpr int DT = HD / 32;                     // 32-row d tiles of O^T
     typedef typename Mfma<T>::frag frag;
@@ -154,11 +154,13 @@ void fa_fwd_kernel(AttnArgs a) {
         offK[j] = (uint32_t)((r * a.sk2 + ((p ^ kswz(r)) * 8)) * 2);
         offV[j] = (uint32_t)((r * a.sv2 + ((p ^ vswz(r)) * 8)) * 2);
     }
-    auto issue = [&](int kt, char *sk, char *sv) __attribute__((always_inline)) {
+    auto issue_k = [&](int kt, char *sk) __attribute__((always_inline)) {
         const uint32_t kb = (uint32_t)((int64_t)kt * BKV * a.sk2 * 2);
-        const uint32_t vb = (uint32_t)((int64_t)kt * BKV * a.sv2 * 2);
 #pragma unroll
         for (int j = 0; j < DPW; ++j) dma16_buf(rsK, offK[j], kb, sk + (wave * DPW + j) * 1024);
+    };
+    auto issue_v = [&](int kt, char *sv) __attribute__((always_inline)) {
+        const uint32_t vb = (uint32_t)((int64_t)kt * BKV * a.sv2 * 2);
 #pragma unroll
         for (int j = 0; j < DPW; ++j) dma16_buf(rsV, offV[j], vb, sv + (wave * DPW + j) * 1024);
     };
@@ -187,8 +189,8 @@ void fa_fwd_kernel(AttnArgs a) {
         for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
     float m_used = -INFINITY, l_run = 0.f;
 
-    auto block = [&](const char *pk, const char *pv, int64_t kv0) __attribute__((always_inline)) {
-        f32x16 sc[2];
+    // S^T block = K_blk Q^T: sc[t][e] = score of key kv0 + 32t + 8(e/4) + 4lh + e%4, query myq.
+    auto qk = [&](const char *pk, f32x16 *sc) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -202,22 +204,29 @@ void fa_fwd_kernel(AttnArgs a) {
                 sc[t] = Mfma<T>::m32(kf, qf[kk], sc[t]);
             }
         }
-        // sc[t][e]: key kv0 + 32t + 8(e/4) + 4lh + e%4, query myq.
+    };
+    // One pipeline step on score block `cur` (keys kv0 ..): mask and row
+    // max, lazy rescale, then exp(cur) interleaved with the MFMAs of the next
+    // block's scores (K slot `pk`, into `nxt`), then O^T += V^T P^T.
+    auto step = [&](f32x16 *cur, f32x16 *nxt, const char *pk, const char *pv, int64_t kv0)
+        __attribute__((always_inline)) {
         const bool need_mask = (kv0 + BKV > a.s) || (CAUSAL && kv0 + BKV - 1 > qw);
         if (need_mask) {
+            // key offset within the block of lane-slot (t, e) is 32t + 8(e/4) + 4lh + e%4
+            const int64_t last = CAUSAL ? min(myq, a.s - 1) : a.s - 1;   // last visible key
+            const int64_t lim = last - kv0 - 4 * lh;                       // its offset (minus 4lh)
+            const int lim32 = (int)max((int64_t)-1, min(lim, (int64_t)BKV));
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int64_t key = kv0 + t * 32 + (e >> 2) * 8 + lh * 4 + (e & 3);
-                    if (key >= a.s || (CAUSAL && key > myq)) sc[t][e] = -INFINITY;
-                }
+                for (int e = 0; e < 16; ++e)
+                    if (t * 32 + (e >> 2) * 8 + (e & 3) > lim32) cur[t][e] = -INFINITY;
         }
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[t][e]);
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, cur[t][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
         // Lazy rescale: move the reference max only when it grew by more
         // than the slack (or is still -inf), for the whole wave at once.
@@ -232,22 +241,36 @@ void fa_fwd_kernel(AttnArgs a) {
             m_used = m_new;
         }
         const float mref = (m_used == -INFINITY) ? 0.f : m_used;
-        float rs = 0.f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float p = fast_exp2(__builtin_fmaf(sc[t][e], a.scale_log2, -mref));
-                sc[t][e] = p;
+            for (int e = 0; e < 16; ++e) nxt[t][e] = 0.f;
+        float rs = 0.f;
+        constexpr int KS = HD / 16;                 // MFMA k-steps of one score block
+        constexpr int EPK = 32 / KS;                // exps per k-step
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            const int pos = ((2 * kk + lh) ^ kpos) << 4;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4 *>(pk + offKr[t] + pos));
+                nxt[t] = Mfma<T>::m32(kf, qf[kk], nxt[t]);
+            }
+#pragma unroll
+            for (int i = 0; i < EPK; ++i) {
+                const int idx = kk * EPK + i, t = idx >> 4, e = idx & 15;
+                const float p = fast_exp2(__builtin_fmaf(cur[t][e], a.scale_log2, -mref));
+                cur[t][e] = p;
                 rs += p;
             }
+        }
         l_run += rs;
 #pragma unroll
         for (int b16 = 0; b16 < 4; ++b16) {
             const int t = b16 >> 1, u = b16 & 1;
             float pv8[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) pv8[i] = sc[t][8 * u + i];
+            for (int i = 0; i < 8; ++i) pv8[i] = cur[t][8 * u + i];
             const frag pf = as_frag<frag>(pack8<T>(pv8));
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
@@ -263,20 +286,35 @@ void fa_fwd_kernel(AttnArgs a) {
         }
     };
 
-    if (nkv > 0) issue(0, sK0, sV0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int kt0 = 0; kt0 < nkv; kt0 += 2) {
+    // Software pipeline over KV blocks: step j runs the softmax of block j
+    // (VALU) interleaved with the score MFMAs of block j + 1, then
+    // O += P_j V_j, so each wave keeps both pipes fed.  LDS slots: K_j and
+    // V_j in slot j % 2.  Step j needs K_{j+1} and V_j; it refills slot j % 2
+    // with K_{j+2} (K_j was consumed at step j - 1) and slot (j + 1) % 2 with
+    // V_{j+1} (V_{j-1} was consumed at step j - 1).  The last step computes
+    // scores of a stale K slot, which are never used: no branch in the step.
+    // Waves whose queries are all masked in a block still run it (their
+    // probabilities are 0).
+    const bool live = qw < a.l;
+    f32x16 scA[2], scB[2];
+    if (nkv > 0) {
+        issue_k(0, sK0);
+        issue_v(0, sV0);
+        if (nkv > 1) issue_k(1, sK1);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (live) qk(sK0, scA);
+    }
+    for (int j0 = 0; j0 < nkv; j0 += 2) {
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs) {
-            const int kt = kt0 + hs;
-            if (kt >= nkv) break;
-            const int64_t kv0 = (int64_t)kt * BKV;
-            if (kt + 1 < nkv) issue(kt + 1, hs ? sK0 : sK1, hs ? sV0 : sV1);
-            const bool active = !(CAUSAL && kv0 > qw + 31) && qw < a.l;
-            if (active) block(hs ? sK1 : sK0, hs ? sV1 : sV0, kv0);
+            const int j = j0 + hs;
+            if (j >= nkv) break;
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
+            if (j + 2 < nkv) issue_k(j + 2, hs ? sK1 : sK0);
+            if (j + 1 < nkv) issue_v(j + 1, hs ? sV0 : sV1);
+            if (live) step(hs ? scB : scA, hs ? scA : scB, hs ? sK0 : sK1, hs ? sV1 : sV0, (int64_t)j * BKV);
         }
     }
 
@@ -561,11 +599,14 @@ size_t decode_workspace_bytes(int64_t rows, int64_t kv_len, int64_t ev) {
 
 template <typename T, int HD>
 static int launch_fwd(AttnArgs a, hipStream_t st) {
+    // 4 waves, 128 queries per work-group; 8-wave (256-query) blocks halve
+    // the L2 -> LDS traffic but measured no faster (causal: slower, from the
+    // coarser load balance).
     a.nqb = (int)cdiv(a.l, 128);
     const int64_t blocks = (int64_t)a.nqb * a.n * a.hq;
     if (blocks > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
-    if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     return launch_status();
 }
 
