@@ -75,6 +75,9 @@ typedef enum kuiops_b_layout { KUIOPS_B_ROW = 0, KUIOPS_B_COL = 1 } kuiops_b_lay
  *   KUIOPS_C_ROW  : out = beta * bias[N]   + alpha * A@B   (bias broadcast over rows) */
 typedef enum kuiops_c_kind { KUIOPS_C_NONE = 0, KUIOPS_C_FULL = 1, KUIOPS_C_ROW = 2 } kuiops_c_kind;
 
+/* Input stage fused into kuiops_decode_linear (see there). */
+typedef enum kuiops_x_kind { KUIOPS_X_PLAIN = 1, KUIOPS_X_RMSNORM = 2, KUIOPS_X_SWIGLU = 3 } kuiops_x_kind;
+
 /* Operation ids for kuiops_query_workspace. */
 typedef enum kuiops_op {
     KUIOPS_OP_ADDMM = 1,
@@ -270,6 +273,24 @@ KUIOPS_API int kuiops_rope_kv_append(int64_t n, int64_t t, int64_t hq, int64_t h
                           void *k_cache, const int64_t sk[3],
                           void *v_cache, const int64_t sv[3], int64_t cache_cap,
                           void *stream);
+
+/* Batch-1 decode projection with its input stage fused in (one launch):
+ * each work-group computes x[K] from `in`, then out[n] = dot(W[n, :], x)
+ * (+ bias[n]) for n < N, W stored [N, K] (an nn.Linear weight, K
+ * contiguous, row stride ldw).  No split-K: each output is one wave's dot
+ * product, written in dtype.
+ *   KUIOPS_X_PLAIN    x = in[K]
+ *   KUIOPS_X_RMSNORM  h = round(in + in_add) (in_add optional),
+ *                     x = norm_w * round(h * rsqrt(mean(h^2) + eps)); h is
+ *                     stored to h_out if non-null (h_out must not alias in)
+ *   KUIOPS_X_SWIGLU   x = round(silu(in[k])) * in[K + k]   (in = [gate | up])
+ * K <= 8192, K % 8 == 0.  Replaces, for a batch-1 decode step, the
+ * reference's mm / addmm launcher (kuiops/mm/wrapper_mm.cu.j2:15-19) plus the
+ * elementwise / mean launches of the RMSNorm or SwiGLU feeding it
+ * (kuipy/kuiops.py:150-320,860-921).                                      */
+KUIOPS_API int kuiops_decode_linear(int64_t N, int64_t K, int dtype, int x_kind, const void *in,
+                         const void *in_add, const void *norm_w, float eps, void *h_out,
+                         const void *W, int64_t ldw, const void *bias, void *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,8 @@ _sz = ctypes.c_size_t
 _i64p = ctypes.POINTER(ctypes.c_int64)
 
 # name -> (restype, argtypes); mirrors include/kuiops.h one to one.
+X_PLAIN, X_RMSNORM, X_SWIGLU = 1, 2, 3
+
 SIGNATURES = {
     "kuiops_abi_version": (_int, []),
     "kuiops_status_string": (ctypes.c_char_p, [_int]),
@@ -62,6 +64,8 @@ SIGNATURES = {
     "kuiops_silu_mul": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp]),
     "kuiops_rope_kv_append": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _vp, _vp,
                                      _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp]),
+    "kuiops_decode_linear": (_int, [_i64, _i64, _int, _int, _vp, _vp, _vp, _flt, _vp, _vp, _i64, _vp, _vp,
+                                    _vp]),
 }
 
 

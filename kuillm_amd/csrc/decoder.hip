@@ -132,45 +132,188 @@ struct RopeArgs {
     int64_t cap;                       // cache positions; tokens at pos >= cap are not stored
 };
 
-// One work-group per (token, batch entry).  Rotation is the split-half form
-// (x1, x2) -> (x1 cos - x2 sin, x2 cos + x1 sin) with angle pos * inv_freq[i]
-// in fp32, cos / sin rounded to the tensor dtype, and each product and the
-// sum rounded, as in the stock module code.
+// One 64-lane work-group per (token, batch entry, head) of the qkv row:
+// q and k heads are rotated (lane i < hd / 2 owns the pair (i, i + hd / 2)),
+// v heads are copied (lane i owns elements i, i + 64, ...).  Rotation is the
+// split-half form (x1, x2) -> (x1 cos - x2 sin, x2 cos + x1 sin) with angle
+// pos * inv_freq[i] in fp32, cos / sin rounded to the tensor dtype, and each
+// product and the sum rounded, as in the stock module code.
 template <typename T>
-__global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
-    const int64_t ti = blockIdx.x, b = blockIdx.y;
-    const int tid = threadIdx.x;
+__global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
+    const int64_t ti = blockIdx.x, b = blockIdx.y, h = blockIdx.z;
+    const int lane = threadIdx.x;
     const int64_t pos = (a.pos0 ? (int64_t)a.pos0[b] : 0) + ti;
     const bool store_kv = pos >= 0 && pos < a.cap;
     const T *row = reinterpret_cast<const T *>(a.qkv) + b * a.ld_batch + ti * a.ld_tok;
     const int64_t half = a.hd / 2;
-    const int64_t nrot = (a.hq + a.hkv) * half;
-    for (int64_t idx = tid; idx < nrot; idx += 256) {
-        const int64_t h = idx / half, i = idx % half;
-        const T *src = row + h * a.hd;
-        const float x1 = to_f32(src[i]), x2 = to_f32(src[i + half]);
-        const float ang = (float)pos * a.inv_freq[i];
-        const float c = rnd<T>(cosf(ang)), s = rnd<T>(sinf(ang));
-        const T o1 = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * s));
-        const T o2 = from_f32<T>(rnd<T>(x2 * c) + rnd<T>(x1 * s));
-        if (h < a.hq) {
-            T *q = reinterpret_cast<T *>(a.q) + b * a.sq0 + h * a.sq1 + ti * a.sq2;
-            q[i] = o1;
-            q[i + half] = o2;
-        } else if (store_kv) {
-            T *k = reinterpret_cast<T *>(a.kc) + b * a.sk0 + (h - a.hq) * a.sk1 + pos * a.sk2;
-            k[i] = o1;
-            k[i + half] = o2;
+    if (h < a.hq + a.hkv) {
+        if (h >= a.hq && !store_kv) return;
+        for (int64_t i = lane; i < half; i += 64) {
+            const float x1 = to_f32(row[h * a.hd + i]), x2 = to_f32(row[h * a.hd + i + half]);
+            const float ang = (float)pos * a.inv_freq[i];
+            const float c = rnd<T>(cosf(ang)), s = rnd<T>(sinf(ang));
+            const T o1 = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * s));
+            const T o2 = from_f32<T>(rnd<T>(x2 * c) + rnd<T>(x1 * s));
+            T *dst = h < a.hq ? reinterpret_cast<T *>(a.q) + b * a.sq0 + h * a.sq1 + ti * a.sq2
+                              : reinterpret_cast<T *>(a.kc) + b * a.sk0 + (h - a.hq) * a.sk1 + pos * a.sk2;
+            dst[i] = o1;
+            dst[i + half] = o2;
         }
+        return;
     }
     if (!store_kv) return;
-    const int64_t cph = a.hd / 8;                     // 16-byte chunks per head
-    const T *vsrc = row + (a.hq + a.hkv) * a.hd;
-    for (int64_t idx = tid; idx < a.hkv * cph; idx += 256) {
-        const int64_t h = idx / cph, c = idx % cph;
-        T *v = reinterpret_cast<T *>(a.vc) + b * a.sv0 + h * a.sv1 + pos * a.sv2 + c * 8;
-        *reinterpret_cast<u32x4 *>(v) = *reinterpret_cast<const u32x4 *>(vsrc + h * a.hd + c * 8);
+    const int64_t hv = h - a.hq - a.hkv;
+    T *v = reinterpret_cast<T *>(a.vc) + b * a.sv0 + hv * a.sv1 + pos * a.sv2;
+    for (int64_t i = lane; i < a.hd; i += 64) v[i] = row[h * a.hd + i];
+}
+
+// ------------------------------------- batch-1 decode projection
+
+constexpr int kXPlain = 1, kXRmsNorm = 2, kXSwiGlu = 3;   // kuiops_x_kind
+constexpr int kDecodeMaxK = 8192;
+
+struct DecLinArgs {
+    int64_t N, K;
+    const void *in, *in_add;           // x source; RMSNorm: h = round(in + in_add)
+    const void *norm_w;
+    float eps;
+    void *h_out;
+    const void *W; int64_t ldw;        // [N, K] rows, K contiguous
+    const void *bias;
+    void *out;
+    int rpw;                           // rows per wave
+};
+
+// out[n] = dot(W[n, :], x) (+ bias[n]) with x computed by every work-group
+// into LDS first (the fused input stage), then held in registers: lane l
+// owns 16-byte chunks l, l + 64, ... of x and of each W row, so a wave reads
+// a row as whole 1 KB segments and the row's dot product is a wave sum.  A
+// wave takes RG rows at a time (all their loads in flight together).
+//   kXPlain    x = in
+//   kXRmsNorm  h = round(in + in_add), x = round(w * round(h * rsqrt(mean(h^2) + eps)));
+//              work-group 0 stores h to h_out
+//   kXSwiGlu   x = round(round(silu(in[k])) * in[K + k])      (in = [gate | up])
+template <typename T, int XK, int KC>
+__global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
+    constexpr int RG = KC <= 4 ? 4 : (KC <= 8 ? 2 : 1);
+    constexpr int XCH = kDecodeMaxK / 8 / 256;      // x chunks per thread in the input stage
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    __shared__ u32x4 sx[kDecodeMaxK / 8];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = (int)(a.K / 8);
+    const T *in = reinterpret_cast<const T *>(a.in);
+
+    // ---- input stage
+    float h[XCH][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < XCH; ++c) {
+        const int ch = c * 256 + tid;
+        if (ch >= nch) continue;
+        unpack8<T>(*reinterpret_cast<const u32x4 *>(in + ch * 8), h[c]);
+        if constexpr (XK == kXRmsNorm) {
+            if (a.in_add) {
+                float o[8];
+                unpack8<T>(*reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.in_add) + ch * 8), o);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[c][e] = rnd<T>(h[c][e] + o[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += h[c][e] * h[c][e];
+        }
     }
+    float inv = 0.f;
+    if constexpr (XK == kXRmsNorm) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        inv = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.K + a.eps);
+    }
+    const bool store_h = XK == kXRmsNorm && a.h_out && blockIdx.x == 0;
+#pragma unroll
+    for (int c = 0; c < XCH; ++c) {
+        const int ch = c * 256 + tid;
+        if (ch >= nch) continue;
+        float xo[8];
+        if constexpr (XK == kXRmsNorm) {
+            float wv[8];
+            unpack8<T>(*reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.norm_w) + ch * 8), wv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xo[e] = wv[e] * rnd<T>(h[c][e] * inv);
+            if (store_h) *reinterpret_cast<u32x4 *>(reinterpret_cast<T *>(a.h_out) + ch * 8) = pack8f<T>(h[c]);
+        } else if constexpr (XK == kXSwiGlu) {
+            float uv[8];
+            unpack8<T>(*reinterpret_cast<const u32x4 *>(in + a.K + ch * 8), uv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xo[e] = rnd<T>(h[c][e] / (1.f + expf(-h[c][e]))) * uv[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xo[e] = h[c][e];
+        }
+        sx[ch] = pack8f<T>(xo);
+    }
+    __syncthreads();
+
+    // ---- rows
+    float xf[KC][8];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+        const int ch = j * 64 + lane;
+        if (ch < nch) unpack8<T>(sx[ch], xf[j]);
+        else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xf[j][e] = 0.f;
+        }
+    }
+    const T *W = reinterpret_cast<const T *>(a.W);
+    const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * a.rpw;
+    const int64_t r1 = min(a.N, r0 + a.rpw);
+    for (int64_t rb = r0; rb < r1; rb += RG) {
+        u32x4 wv[RG][KC];
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            const int64_t r = min(rb + g, a.N - 1);           // clamped: never stored
+#pragma unroll
+            for (int j = 0; j < KC; ++j) {
+                const int ch = j * 64 + lane;
+                wv[g][j] = ch < nch ? *reinterpret_cast<const u32x4 *>(W + r * a.ldw + ch * 8) : u32x4{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < KC; ++j) {
+                float w8[8];
+                unpack8<T>(wv[g][j], w8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w8[e], xf[j][e], acc);
+            }
+            acc = wave_sum(acc);
+            const int64_t r = rb + g;
+            if (lane == 0 && r < r1) {
+                if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
+                reinterpret_cast<T *>(a.out)[r] = from_f32<T>(acc);
+            }
+        }
+    }
+}
+
+template <typename T, int XK>
+static void decode_rows_launch(const DecLinArgs &a, unsigned grid, hipStream_t st) {
+    const int kc = (int)cdiv(a.K, 512);
+    if (kc <= 4) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 4>), dim3(grid), dim3(256), 0, st, a);
+    else if (kc <= 8) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 8>), dim3(grid), dim3(256), 0, st, a);
+    else if (kc <= 12) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 12>), dim3(grid), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_rows_kernel<T, XK, 16>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <typename T>
+static void decode_rows_dispatch(const DecLinArgs &a, int x_kind, unsigned grid, hipStream_t st) {
+    if (x_kind == kXPlain) decode_rows_launch<T, kXPlain>(a, grid, st);
+    else if (x_kind == kXRmsNorm) decode_rows_launch<T, kXRmsNorm>(a, grid, st);
+    else decode_rows_launch<T, kXSwiGlu>(a, grid, st);
 }
 
 }  // namespace kuiops
@@ -231,12 +374,36 @@ extern "C" int kuiops_rope_kv_append(int64_t n, int64_t t, int64_t hq, int64_t h
     if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
     if (hd % 8 || ld_tok % 8 || ld_batch % 8 || sv[0] % 8 || sv[1] % 8 || sv[2] % 8) return KUIOPS_E_UNSUPPORTED;
     if (!aligned16(qkv) || !aligned16(v_cache)) return KUIOPS_E_UNSUPPORTED;
-    if (t > INT32_MAX || n > 65535) return KUIOPS_E_UNSUPPORTED;
+    if (t > INT32_MAX || n > 65535 || hq + 2 * hkv > 65535) return KUIOPS_E_UNSUPPORTED;
     RopeArgs a{n, t, hq, hkv, hd, qkv, ld_tok, ld_batch, inv_freq, pos0,
                q_out, sq[0], sq[1], sq[2], k_cache, sk[0], sk[1], sk[2], v_cache, sv[0], sv[1], sv[2], cache_cap};
-    const dim3 grid((unsigned)t, (unsigned)n);
+    const dim3 grid((unsigned)t, (unsigned)n, (unsigned)(hq + 2 * hkv));
     hipStream_t st = as_stream(stream);
-    if (dtype == KUIOPS_BF16) hipLaunchKernelGGL((rope_kv_kernel<bf16_t>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((rope_kv_kernel<f16_t>), grid, dim3(256), 0, st, a);
+    if (dtype == KUIOPS_BF16) hipLaunchKernelGGL((rope_kv_kernel<bf16_t>), grid, dim3(64), 0, st, a);
+    else hipLaunchKernelGGL((rope_kv_kernel<f16_t>), grid, dim3(64), 0, st, a);
+    return launch_status();
+}
+
+extern "C" int kuiops_decode_linear(int64_t N, int64_t K, int dtype, int x_kind, const void *in, const void *in_add,
+                                    const void *norm_w, float eps, void *h_out, const void *W, int64_t ldw,
+                                    const void *bias, void *out, void *stream) {
+    if (N < 0 || K < 0) return KUIOPS_E_INVALID;
+    if (x_kind != kXPlain && x_kind != kXRmsNorm && x_kind != kXSwiGlu) return KUIOPS_E_INVALID;
+    if (N == 0) return KUIOPS_OK;
+    if (!in || !W || !out || (x_kind == kXRmsNorm && !norm_w)) return KUIOPS_E_INVALID;
+    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
+    if (K == 0 || K % 8 || K > kDecodeMaxK || ldw % 8 || ldw < K) return KUIOPS_E_UNSUPPORTED;
+    if (!aligned16(in) || !aligned16(W) || (in_add && !aligned16(in_add)) || (norm_w && !aligned16(norm_w)) ||
+        (h_out && !aligned16(h_out)))
+        return KUIOPS_E_UNSUPPORTED;
+    if (h_out && (h_out == in || h_out == in_add)) return KUIOPS_E_INVALID;
+    DecLinArgs a{N, K, in, in_add, norm_w, eps, h_out, W, ldw, bias, out, 1};
+    // about 2048 waves (8 per CU) in flight: rows per wave from N
+    a.rpw = (int)cdiv(N, 2048);
+    const int64_t grid = cdiv(N, 4 * (int64_t)a.rpw);
+    if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    if (dtype == KUIOPS_BF16) decode_rows_dispatch<bf16_t>(a, x_kind, (unsigned)grid, st);
+    else decode_rows_dispatch<f16_t>(a, x_kind, (unsigned)grid, st);
     return launch_status();
 }

@@ -531,3 +531,4 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
     return out_dtype == KUIOPS_F32 ? gemv_dispatch<f16_t, float>(a, wcol, st)
                                    : gemv_dispatch<f16_t, f16_t>(a, wcol, st);
 }
+

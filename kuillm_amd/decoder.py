@@ -7,18 +7,20 @@ op of the step on a kuiops kernel:
 
     embedding        kuiops_index                  (aten.index / embedding)
     RMSNorm (+res)   kuiops_rmsnorm                (pow / mean / rsqrt / mul / add)
-    q, k, v          kuiops_gemv_splitk / mm       one fused [d, (hq+2hkv) hd] weight
+    q, k, v          kuiops_decode_linear / mm     one fused [(hq+2hkv) hd, d] weight
     rotary + cache   kuiops_rope_kv_append         (mul / neg / cat / add, cache cat)
     attention        kuiops_sdpa_fwd (prefill), kuiops_sdpa_decode (decode,
                      KV length read from device memory)
-    o, gate|up, down kuiops_gemv_splitk / mm       gate and up fused
-    SwiGLU           kuiops_silu_mul
-    LM head          kuiops_gemv_splitk / mm
+    o, gate|up, down kuiops_decode_linear / mm     gate and up fused
+    SwiGLU           kuiops_silu_mul (fused into the down projection at decode)
+    LM head          kuiops_decode_linear / mm
     sampling tail    kuiops_softmax_lastdim + kuiops_topk_lastdim (k = 1)
 
-Weights are stored [in, out] row-major (``W.t().contiguous()``): the decode
-GEMMs then stream W in 128-byte row segments, the layout the skinny GEMM
-kernel reads at HBM speed.  Numerics follow the transformers modules (each op
+Weights stay in the nn.Linear layout [out, in] (q/k/v and gate/up fused
+along out).  A batch-1 decode step uses kuiops_decode_linear: every output
+is one wave's dot product over a contiguous weight row, with the RMSNorm or
+SwiGLU that feeds the projection computed in the same launch.  Prefill
+(and batch > 1) uses the MFMA GEMMs on the K-contiguous weights.  Numerics follow the transformers modules (each op
 rounds to bf16 where the stock module does), so greedy tokens match the stock
 model except where two logits tie within bf16 resolution.
 """
@@ -80,8 +82,8 @@ class LlamaDecoder:
         def w(name):
             return state[name].to(self.dev, dtype)
 
-        def kn(*names):       # nn.Linear weights [out, in] -> one [in, sum(out)] row-major matrix
-            return torch.cat([w(x) for x in names], 0).t().contiguous()
+        def kn(*names):       # nn.Linear weights [out, in], fused along out: [sum(out), in]
+            return torch.cat([w(x) for x in names], 0).contiguous()
 
         self.embed = w("model.embed_tokens.weight").contiguous()
         self.layers = []
@@ -97,7 +99,7 @@ class LlamaDecoder:
             ))
         self.norm = w("model.norm.weight").contiguous()
         head = state.get("lm_head.weight", state["model.embed_tokens.weight"])
-        self.head = head.to(self.dev, dtype).t().contiguous()
+        self.head = head.to(self.dev, dtype).contiguous()
         self.inv_freq = rope_inv_freq(s.hd, s.theta).to(self.dev)
         kv = (s.layers, self.n, s.hkv, self.cap, s.hd)
         self.kcache = torch.zeros(kv, dtype=dtype, device=self.dev)
@@ -107,7 +109,24 @@ class LlamaDecoder:
         self.pos = torch.zeros(self.n, dtype=torch.int32, device=self.dev)
         self.kv_len = torch.zeros(self.n, dtype=torch.int32, device=self.dev)
         self.graph = None
-        self.out_tokens = None
+        self.fused = self.n == 1 and max(s.d, s.ffn) <= 8192 and s.d % 8 == 0 and s.ffn % 8 == 0
+        if self.fused:
+            self._setup_fused()
+
+    def _setup_fused(self):
+        """Static buffers of the batch-1 decode step, whose projections carry
+        their RMSNorm / SwiGLU input stage (kuiops_decode_linear): 6 launches
+        per layer."""
+        s, dev = self.s, self.dev
+        bf = dict(dtype=self.dtype, device=dev)
+        self.h_buf = [torch.empty(s.d, **bf), torch.empty(s.d, **bf)]
+        self.qkv1 = torch.empty(1, 1, (s.hq + 2 * s.hkv) * s.hd, **bf)
+        self.q1 = torch.empty(1, s.hq, 1, s.hd, **bf)
+        self.att1 = torch.empty(1, 1, s.hq * s.hd, **bf)
+        self.o1 = torch.empty(s.d, **bf)
+        self.gu1 = torch.empty(2 * s.ffn, **bf)
+        self.down1 = torch.empty(s.d, **bf)
+        self.logits1 = torch.empty(s.vocab, **bf)
 
     @classmethod
     def from_hf(cls, model, capacity: int, batch: int = 1, device="cuda"):
@@ -130,7 +149,7 @@ class LlamaDecoder:
                 x = ops.rmsnorm(res, L["ln1"], s.eps)
             else:
                 x = ops.rmsnorm(pending, L["ln1"], s.eps, residual=res, res_out=res)
-            qkv = ops.mm(x, L["wqkv"]).view(n, t, -1)
+            qkv = ops.mm(x, L["wqkv"].t()).view(n, t, -1)
             kc, vc = self.kcache[i], self.vcache[i]
             ops.rope_kv_append(qkv, s.hq, s.hkv, s.hd, self.inv_freq, pos0, q, kc, vc)
             if t == 1:
@@ -138,10 +157,10 @@ class LlamaDecoder:
             else:
                 # prefill from position 0: the keys are the t just stored
                 ops.sdpa(q, kc[:, :, :t], vc[:, :, :t], is_causal=True, return_lse=False, out=att4)
-            o = ops.mm(att.view(n * t, -1), L["wo"])
+            o = ops.mm(att.view(n * t, -1), L["wo"].t())
             x = ops.rmsnorm(o, L["ln2"], s.eps, residual=res, res_out=res)
-            a = ops.silu_mul(ops.mm(x, L["wgu"]))
-            pending = ops.mm(a, L["wd"])
+            a = ops.silu_mul(ops.mm(x, L["wgu"].t()))
+            pending = ops.mm(a, L["wd"].t())
         return pending, res
 
     def _head(self, pending, res, t):
@@ -149,7 +168,7 @@ class LlamaDecoder:
         n = self.n
         last = (lambda z: z.view(n, t, -1)[:, -1]) if t > 1 else (lambda z: z)
         x = ops.rmsnorm(last(pending), self.norm, self.s.eps, residual=last(res))
-        logits = ops.mm(x, self.head)                               # bf16, as the stock LM head
+        logits = ops.mm(x, self.head.t())                           # bf16, as the stock LM head
         probs = ops.softmax(logits.float())
         _, idx = ops.topk(probs, 1)
         return logits, idx.view(n)
@@ -171,6 +190,8 @@ class LlamaDecoder:
         return logits, nxt
 
     def _decode_step(self):
+        if self.fused:
+            return self._decode_step_fused()
         h = ops.index(self.embed, 0, self.tok)
         pending, res = self._layers(h, 1, self.pos, self.kv_len)
         logits, nxt = self._head(pending, res, 1)
@@ -178,6 +199,39 @@ class LlamaDecoder:
         self.pos.add_(1)
         self.kv_len.add_(1)
         return logits
+
+    def _decode_step_fused(self):
+        """One batch-1 decode step, same arithmetic as ``_layers`` + ``_head``
+        (every rounding point kept), in 6 launches per layer: qkv (RMSNorm
+        stage) -> rotary + cache append -> attention (2) -> o -> gate|up
+        (RMSNorm stage) -> down (SwiGLU stage)."""
+        s = self.s
+        hb = self.h_buf
+        cur = 0
+        ops.index(self.embed, 0, self.tok, out=hb[0].view(1, -1))
+        att4 = self.att1.view(1, 1, s.hq, s.hd).transpose(1, 2)
+        down = None
+        for i, L in enumerate(self.layers):
+            kc, vc = self.kcache[i], self.vcache[i]
+            ops.decode_linear(hb[cur], L["wqkv"], "rmsnorm", in_add=down, norm_w=L["ln1"], eps=s.eps,
+                              h_out=hb[1 - cur], out=self.qkv1)
+            cur = 1 - cur
+            ops.rope_kv_append(self.qkv1, s.hq, s.hkv, s.hd, self.inv_freq, self.pos, self.q1, kc, vc)
+            ops.sdpa_decode(self.q1, kc, vc, causal=True, kv_len=self.kv_len, out=att4)
+            ops.decode_linear(self.att1, L["wo"], "plain", out=self.o1)
+            ops.decode_linear(hb[cur], L["wgu"], "rmsnorm", in_add=self.o1, norm_w=L["ln2"], eps=s.eps,
+                              h_out=hb[1 - cur], out=self.gu1)
+            cur = 1 - cur
+            ops.decode_linear(self.gu1, L["wd"], "swiglu", out=self.down1)
+            down = self.down1
+        ops.decode_linear(hb[cur], self.head, "rmsnorm", in_add=down, norm_w=self.norm, eps=s.eps,
+                          out=self.logits1)
+        probs = ops.softmax(self.logits1.view(1, -1).float())
+        _, idx = ops.topk(probs, 1)
+        self.tok.copy_(idx.view(1))
+        self.pos.add_(1)
+        self.kv_len.add_(1)
+        return self.logits1.view(1, -1)
 
     def capture(self):
         """Record one decode step (all its kernels) in a HIP graph.  The step

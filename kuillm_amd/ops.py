@@ -372,9 +372,10 @@ def gather(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = 
     return out
 
 
-def index(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = None) -> torch.Tensor:
+def index(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = None, out=None) -> torch.Tensor:
     """inp[(slice(None),) * dim + (idx,)] for one int64 index tensor
-    (aten.index.Tensor with a single index); negative indices wrap."""
+    (aten.index.Tensor with a single index); negative indices wrap.  ``out``
+    (contiguous, the result's shape and dtype) receives it in place."""
     if idx.dtype != torch.int64 or inp.dim() < 1:
         raise _lib.Unsupported("index", _lib.E_UNSUPPORTED)
     dim = dim % inp.dim()
@@ -382,7 +383,11 @@ def index(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = N
     outer = math.prod(ic.shape[:dim])
     size = ic.shape[dim]
     inner = math.prod(ic.shape[dim + 1:])
-    out = torch.empty((*ic.shape[:dim], *xc.shape, *ic.shape[dim + 1:]), dtype=inp.dtype, device=inp.device)
+    shape = (*ic.shape[:dim], *xc.shape, *ic.shape[dim + 1:])
+    if out is None:
+        out = torch.empty(shape, dtype=inp.dtype, device=inp.device)
+    elif tuple(out.shape) != shape or out.dtype != inp.dtype or not out.is_contiguous():
+        raise _lib.KuiopsError("index", _lib.E_INVALID)
     if out.numel() == 0:
         return out
     flag = torch.zeros(1, dtype=torch.int32, device=inp.device) if (check or (check is None and CHECK_INDEX)) else None
@@ -466,3 +471,36 @@ def rope_kv_append(qkv, hq, hkv, hd, inv_freq, pos0, q_out, k_cache, v_cache):
         inv_freq.data_ptr(), _ptr(pos0), q_out.data_ptr(), _lib.strides3(*q_out.stride()[:3]),
         k_cache.data_ptr(), _lib.strides3(*k_cache.stride()[:3]),
         v_cache.data_ptr(), _lib.strides3(*v_cache.stride()[:3]), k_cache.shape[2], _stream(qkv.device)))
+
+
+_X_KIND = {"plain": _lib.X_PLAIN, "rmsnorm": _lib.X_RMSNORM, "swiglu": _lib.X_SWIGLU}
+
+
+def decode_linear(x, W, x_kind="plain", in_add=None, norm_w=None, eps=1e-5, h_out=None, bias=None, out=None):
+    """Batch-1 decode projection out[N] = W @ f(x) with the input stage fused
+    in (one launch; see kuiops_decode_linear).  W is an nn.Linear weight
+    [N, K] (K contiguous).
+
+    * ``plain``:   f(x) = x[K]
+    * ``rmsnorm``: h = round(x + in_add), f = RMSNorm(h) * norm_w; h is written
+                   to ``h_out`` when given
+    * ``swiglu``:  x = [gate | up] (2K), f = silu(gate) * up
+    """
+    N, K = W.shape
+    xf = x.reshape(-1)
+    if x.dtype != W.dtype or W.stride(1) != 1 or not xf.is_contiguous():
+        raise _lib.KuiopsError("decode_linear", _lib.E_INVALID)
+    if xf.numel() != (2 * K if x_kind == "swiglu" else K):
+        raise _lib.KuiopsError("decode_linear", _lib.E_INVALID)
+    for t in (in_add, norm_w, h_out, bias):
+        if t is not None and (t.numel() != (N if t is bias else K) or not t.is_contiguous() or t.dtype != x.dtype):
+            raise _lib.KuiopsError("decode_linear", _lib.E_INVALID)
+    if out is None:
+        out = torch.empty(N, dtype=x.dtype, device=x.device)
+    elif out.numel() != N or not out.is_contiguous() or out.dtype != x.dtype:
+        raise _lib.KuiopsError("decode_linear", _lib.E_INVALID)
+    lib = _lib_handle()
+    _lib.check("kuiops_decode_linear", lib.kuiops_decode_linear(
+        N, K, _dt(x.dtype), _X_KIND[x_kind], xf.data_ptr(), _ptr(in_add), _ptr(norm_w), float(eps),
+        _ptr(h_out), W.data_ptr(), W.stride(0), _ptr(bias), out.data_ptr(), _stream(x.device)))
+    return out

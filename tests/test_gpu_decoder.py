@@ -194,3 +194,60 @@ def test_config5_decoder_vs_transformers(cuda):
             lg = f(gen.logits[i][0])
             assert lg[b] - lg[a] < 2 * noise, f"step {i}: token {a} vs {b}, gap {lg[b] - lg[a]:.3e}"
             break
+
+
+@pytest.mark.parametrize("kind", ["plain", "rmsnorm", "swiglu"])
+@pytest.mark.parametrize("N,K", [(3072, 2048), (2048, 5632), (32000, 2048), (104, 96), (8, 8192)])
+def test_decode_linear_vs_unfused(cuda, kind, N, K):
+    """kuiops_decode_linear (fused input stage) against the unfused kernels it
+    replaces: the input stage bit-exact (h_out), the projection within the
+    north-star tolerance of the oracle and fp32-reorder noise of mm."""
+    Kin = 2 * K if kind == "swiglu" else K
+    x = bf((Kin,), 20).to(cuda)
+    W = bf((N, K), 21, 0.02).to(cuda)
+    nw = (1.0 + bf((K,), 22, 0.1)).to(torch.bfloat16).to(cuda)
+    add = bf((K,), 23).to(cuda)
+    h_out = torch.empty(K, dtype=torch.bfloat16, device=cuda)
+    if kind == "rmsnorm":
+        out = ops.decode_linear(x, W, "rmsnorm", in_add=add, norm_w=nw, eps=1e-5, h_out=h_out)
+        res = x.clone()
+        xin = ops.rmsnorm(add.view(1, -1), nw, 1e-5, residual=res.view(1, -1), res_out=res.view(1, -1)).view(-1)
+        assert torch.equal(h_out, res)
+    elif kind == "swiglu":
+        out = ops.decode_linear(x, W, "swiglu")
+        xin = ops.silu_mul(x.view(1, -1)).view(-1)
+    else:
+        out = ops.decode_linear(x, W, "plain")
+        xin = x
+    ref32 = ops.mm(xin.view(1, -1), W.t(), out_dtype=torch.float32)[0]
+    close(f(out), O.mm(f(xin.view(1, -1)), f(W).T)[0])
+    close(f(out), f(ref32))
+    # every output is one dot product rounded once: within 1 bf16 ulp of mm's
+    assert (out.float() - ref32.to(torch.bfloat16).float()).abs().max() <= 2 ** -7 * ref32.abs().max()
+
+
+def test_fused_decode_step_matches_unfused(cuda):
+    """The 6-launch batch-1 decode step against the unfused one from the same
+    state, step by step: logits within fp32-reordering noise, the same next
+    token unless the top two logits tie within that noise."""
+    m = hf_model(TINY, cuda)
+    prompt = torch.randint(0, TINY["vocab"], (1, 24), generator=torch.Generator().manual_seed(6))
+    dec = LlamaDecoder.from_hf(m, capacity=64)
+    assert dec.fused
+    dec.prefill(prompt)
+    for step in range(8):
+        state = [t.clone() for t in (dec.tok, dec.pos, dec.kv_len, dec.kcache, dec.vcache)]
+        lf = dec._decode_step_fused().float().clone()
+        tok_f = dec.tok.clone()
+        after = [t.clone() for t in (dec.tok, dec.pos, dec.kv_len, dec.kcache, dec.vcache)]
+        for dst, src in zip((dec.tok, dec.pos, dec.kv_len, dec.kcache, dec.vcache), state):
+            dst.copy_(src)
+        dec.fused = False
+        lu = dec._decode_step().float()
+        dec.fused = True
+        close(f(lf), f(lu), 2e-2)
+        if not torch.equal(tok_f, dec.tok):
+            top2 = torch.topk(lu[0], 2).values
+            assert float(top2[0] - top2[1]) < 2e-2
+        for dst, src in zip((dec.tok, dec.pos, dec.kv_len, dec.kcache, dec.vcache), after):
+            dst.copy_(src)
