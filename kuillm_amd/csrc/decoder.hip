@@ -185,17 +185,18 @@ struct DecLinArgs {
 };
 
 // out[n] = dot(W[n, :], x) (+ bias[n]) with x computed by every work-group
-// into LDS first (the fused input stage), then held in registers: lane l
-// owns 16-byte chunks l, l + 64, ... of x and of each W row, so a wave reads
-// a row as whole 1 KB segments and the row's dot product is a wave sum.  A
-// wave takes RG rows at a time (all their loads in flight together).
+// into LDS (the fused input stage), then held in registers: lane l owns
+// 16-byte chunks l, l + 64, ... of x and of each W row, so a wave reads a row
+// as whole 1 KB segments and the row's dot product is a wave sum.  A wave
+// owns rpw <= RG rows; their W loads are issued before the input stage, so
+// the stage's own global reads and reduction hide under the W latency.
 //   kXPlain    x = in
 //   kXRmsNorm  h = round(in + in_add), x = round(w * round(h * rsqrt(mean(h^2) + eps)));
 //              work-group 0 stores h to h_out
 //   kXSwiGlu   x = round(round(silu(in[k])) * in[K + k])      (in = [gate | up])
 template <typename T, int XK, int KC>
 __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
-    constexpr int RG = KC <= 4 ? 4 : (KC <= 8 ? 2 : 1);
+    constexpr int RG = KC <= 4 ? 4 : (KC <= 8 ? 2 : 1);    // rows per wave at most (host: rpw <= RG)
     constexpr int XCH = kDecodeMaxK / 8 / 256;      // x chunks per thread in the input stage
     typedef T t8 __attribute__((ext_vector_type(8)));
     __shared__ u32x4 sx[kDecodeMaxK / 8];
@@ -203,6 +204,21 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nch = (int)(a.K / 8);
     const T *in = reinterpret_cast<const T *>(a.in);
+
+    // ---- this wave's W rows, in flight during the input stage
+    const T *W = reinterpret_cast<const T *>(a.W);
+    const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * a.rpw;
+    const int64_t r1 = min(a.N, r0 + a.rpw);
+    u32x4 wv[RG][KC];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+        const int64_t r = min(r0 + g, a.N - 1);                 // clamped: never stored
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            const int ch = j * 64 + lane;
+            wv[g][j] = ch < nch ? *reinterpret_cast<const u32x4 *>(W + r * a.ldw + ch * 8) : u32x4{0, 0, 0, 0};
+        }
+    }
 
     // ---- input stage
     float h[XCH][8];
@@ -266,36 +282,21 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
             for (int e = 0; e < 8; ++e) xf[j][e] = 0.f;
         }
     }
-    const T *W = reinterpret_cast<const T *>(a.W);
-    const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * a.rpw;
-    const int64_t r1 = min(a.N, r0 + a.rpw);
-    for (int64_t rb = r0; rb < r1; rb += RG) {
-        u32x4 wv[RG][KC];
 #pragma unroll
-        for (int g = 0; g < RG; ++g) {
-            const int64_t r = min(rb + g, a.N - 1);           // clamped: never stored
+    for (int g = 0; g < RG; ++g) {
+        float acc = 0.f;
 #pragma unroll
-            for (int j = 0; j < KC; ++j) {
-                const int ch = j * 64 + lane;
-                wv[g][j] = ch < nch ? *reinterpret_cast<const u32x4 *>(W + r * a.ldw + ch * 8) : u32x4{0, 0, 0, 0};
-            }
+        for (int j = 0; j < KC; ++j) {
+            float w8[8];
+            unpack8<T>(wv[g][j], w8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w8[e], xf[j][e], acc);
         }
-#pragma unroll
-        for (int g = 0; g < RG; ++g) {
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 0; j < KC; ++j) {
-                float w8[8];
-                unpack8<T>(wv[g][j], w8);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w8[e], xf[j][e], acc);
-            }
-            acc = wave_sum(acc);
-            const int64_t r = rb + g;
-            if (lane == 0 && r < r1) {
-                if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
-                reinterpret_cast<T *>(a.out)[r] = from_f32<T>(acc);
-            }
+        acc = wave_sum(acc);
+        const int64_t r = r0 + g;
+        if (lane == 0 && r < r1) {
+            if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
+            reinterpret_cast<T *>(a.out)[r] = from_f32<T>(acc);
         }
     }
 }
@@ -398,8 +399,10 @@ extern "C" int kuiops_decode_linear(int64_t N, int64_t K, int dtype, int x_kind,
         return KUIOPS_E_UNSUPPORTED;
     if (h_out && (h_out == in || h_out == in_add)) return KUIOPS_E_INVALID;
     DecLinArgs a{N, K, in, in_add, norm_w, eps, h_out, W, ldw, bias, out, 1};
-    // about 2048 waves (8 per CU) in flight: rows per wave from N
-    a.rpw = (int)cdiv(N, 2048);
+    // one register group of rows per wave, spread over at least ~2048 waves
+    const int kc = (int)cdiv(K, 512);
+    const int rg = kc <= 4 ? 4 : (kc <= 8 ? 2 : 1);
+    a.rpw = (int)min((int64_t)rg, cdiv(N, 2048));
     const int64_t grid = cdiv(N, 4 * (int64_t)a.rpw);
     if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     hipStream_t st = as_stream(stream);

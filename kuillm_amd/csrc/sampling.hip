@@ -192,6 +192,53 @@ __device__ __forceinline__ int block_excl_scan(int v, int *s_warp, int &total) {
     return excl;
 }
 
+// The largest key T such that at least `k` of the participating threads'
+// values are >= T (the k-th largest), by a 4-pass MSB radix select over one
+// value per thread.  Threads with part == false take no part.
+__device__ uint32_t block_kth_largest(uint32_t v, bool part, int k, int *hist, uint32_t *s_state) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) { s_state[0] = 0; s_state[1] = 0; s_state[2] = (uint32_t)k; }
+    __syncthreads();
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_state[0], mask = s_state[1];
+        if (part && (v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255], 1);
+        __syncthreads();
+        if (wave == 0) {
+            const int rem = (int)s_state[2];
+            int c[4], cs = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { c[j] = hist[255 - (lane * 4 + j)]; cs += c[j]; }
+            int incl = cs;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int y = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += y;
+            }
+            int before = incl - cs;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (before < rem && before + c[j] >= rem) {
+                    const uint32_t d = 255 - (lane * 4 + j);
+                    s_state[0] = prefix | (d << shift);
+                    s_state[1] = mask | (255u << shift);
+                    s_state[2] = (uint32_t)(rem - before);
+                }
+                before += c[j];
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t t = s_state[0];
+    __syncthreads();
+    return t;
+}
+
+constexpr int kTopkFastPer = 32;       // keys per thread held in registers (n <= 32768)
+constexpr int kTopkFastMaxK = 512;
+constexpr int kTopkCandCap = 2048;     // candidates the fast path sorts
+
 template <typename T>
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(int64_t n, int k, const T *X, T *vals,
                                                             int64_t *inds, int largest) {
@@ -230,6 +277,60 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(int64_t n, int k, co
     __shared__ uint32_t s_prefix, s_mask;
     __shared__ int s_remaining;
     __shared__ uint64_t s_sel[kTopkMaxK];
+
+    if (n <= (int64_t)kTopkThreads * kTopkFastPer && k <= kTopkFastMaxK) {
+        // Fast path: the row stays in registers (element j * 1024 + tid).
+        // T = the k-th largest of the per-thread maxima bounds the top k from
+        // below (k threads hold a key >= T), and usually few keys reach it:
+        // those candidates are gathered with one block scan and sorted.
+        __shared__ uint64_t s_cand[kTopkCandCap];
+        __shared__ uint32_t s_state[3];
+        uint32_t key[kTopkFastPer];
+        uint32_t mx = 0;
+        bool has = false;
+#pragma unroll
+        for (int j = 0; j < kTopkFastPer; ++j) {
+            const int64_t i = (int64_t)j * kTopkThreads + tid;
+            key[j] = i < n ? order_key(load_f(x + i), lg) : 0u;
+            if (i < n) { mx = has ? max(mx, key[j]) : key[j]; has = true; }
+        }
+        const uint32_t thr = block_kth_largest(mx, has, k, hist, s_state);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < kTopkFastPer; ++j) cnt += ((int64_t)j * kTopkThreads + tid < n) && key[j] >= thr;
+        int total;
+        int pos = block_excl_scan(cnt, s_scan, total);
+        if (total <= kTopkCandCap) {
+#pragma unroll
+            for (int j = 0; j < kTopkFastPer; ++j) {
+                const int64_t i = (int64_t)j * kTopkThreads + tid;
+                if (i < n && key[j] >= thr) s_cand[pos++] = ((uint64_t)key[j] << 32) | (uint32_t)~(uint32_t)i;
+            }
+            int P = 1;
+            while (P < total) P <<= 1;
+            for (int i = total + tid; i < P; i += kTopkThreads) s_cand[i] = 0;
+            __syncthreads();
+            for (int size = 2; size <= P; size <<= 1) {
+                for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                    for (int i = tid; i < P / 2; i += kTopkThreads) {
+                        const int lo = 2 * i - (i & (stride - 1));
+                        const int hi = lo + stride;
+                        const bool desc = (lo & size) == 0;
+                        const uint64_t a = s_cand[lo], b = s_cand[hi];
+                        if ((a < b) == desc) { s_cand[lo] = b; s_cand[hi] = a; }
+                    }
+                    __syncthreads();
+                }
+            }
+            for (int j = tid; j < k; j += kTopkThreads) {
+                const int64_t idx = (int64_t)(uint32_t)~(uint32_t)(s_cand[j] & 0xffffffffu);
+                vals[row * k + j] = x[idx];
+                inds[row * k + j] = idx;
+            }
+            return;
+        }
+        // too many keys tie at the threshold: the general path below
+    }
 
     if (tid == 0) { s_prefix = 0; s_mask = 0; s_remaining = k; }
     __syncthreads();

@@ -101,6 +101,25 @@ def test_topk_ties_and_nan(cuda):
         ops.topk(y, 1100)                      # k above 1024 is outside the kernel
 
 
+def test_topk_threshold_ties(cuda):
+    """The register-resident path (n <= 32768, k <= 512): ties at the k-th
+    place keep the lowest indices, and a row whose candidates overflow the
+    sort buffer (all equal) takes the general path with the same answer."""
+    y = torch.zeros(1, 5000, device=cuda)
+    y[0, 4000:] = 1.0
+    v, i = ops.topk(y, 300)
+    assert torch.equal(i[0].cpu(), torch.arange(4000, 4300)) and bool((v == 1).all())
+    z = torch.zeros(2, 32000, device=cuda)
+    v, i = ops.topk(z, 10)
+    assert torch.equal(i.cpu(), torch.arange(10).expand(2, 10))
+    # softmax probabilities of random logits (the sampling tail's input)
+    p = torch.softmax(torch.randn(3, 32000, generator=torch.Generator().manual_seed(9)), -1).to(cuda)
+    for k in (1, 20, 50, 512):
+        v, i = ops.topk(p, k)
+        tv, ti = torch.topk(p, k)
+        assert torch.equal(v, tv) and torch.equal(i, ti)
+
+
 def test_topk_other_dim(cuda):
     x = torch.randn(50, 3, device=cuda)
     v, i = ops.topk(x, 5, dim=0)
