@@ -95,8 +95,10 @@ KUIOPS_API const char *kuiops_status_string(int status);
  *   GEMV_SPLITK:  a = M, b = N, c = K
  *   SDPA_DECODE:  a = batch * q_heads * q_len, b = kv_len, c = head_dim_v
  *   TOPK:         a = rows, b = row length, c = k
- * Workspace contents need no initialisation; calls that share one
- * workspace must be ordered on one stream.                                 */
+ * Workspace contents need no initialisation, except GEMV_SPLITK's first
+ * 16 KB (arrival counters): zero before the first call, and every call
+ * leaves them zero.  Calls that share one workspace must be ordered on one
+ * stream.                                                                  */
 KUIOPS_API size_t kuiops_query_workspace(int op, int64_t a, int64_t b, int64_t c);
 
 /* ---------------------------------------------------------------- GEMM --
@@ -142,8 +144,9 @@ KUIOPS_API int kuiops_bmm(int64_t batch, int64_t M, int64_t K, int64_t N, int in
 /* Skinny (decode) GEMM: out[M, N] = x[M, K] @ W[K, N] (+ bias[N]) for
  * 1 <= M <= 64, bf16/f16 in, fp32 accumulate, out_dtype = in or F32.
  * K is split over `splits` work-groups (0 = choose); fp32 partials go to the
- * workspace and a second kernel sums them in split order, so the result is
- * bitwise repeatable.  Requires the workspace of
+ * workspace and are summed in split order (row-major W: by the last work-
+ * group of each column strip to finish, K-contiguous W: by a second
+ * kernel), so the result is bitwise repeatable.  Requires the workspace of
  * kuiops_query_workspace(KUIOPS_OP_GEMV_SPLITK, M, N, K).  Serves the
  * reference's mm/addmm families at decode shapes, which its gate rejects
  * (`M % 64`, kuipy/kuiops.py:372-374).                                    */

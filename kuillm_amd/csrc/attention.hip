@@ -248,14 +248,22 @@ void fa_fwd_kernel(AttnArgs a) {
         float rs = 0.f;
         constexpr int KS = HD / 16;                 // MFMA k-steps of one score block
         constexpr int EPK = 32 / KS;                // exps per k-step
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
+        // K fragments are read KPF k-steps ahead of their MFMAs (a ring of
+        // registers), so the LDS latency hides behind the MFMAs in flight.
+        constexpr int KPF = 3;
+        frag kr[KPF][2];
+        auto load_k = [&](int kk, frag *dst) __attribute__((always_inline)) {
             const int pos = ((2 * kk + lh) ^ kpos) << 4;
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const frag kf = as_frag<frag>(*reinterpret_cast<const u32x4 *>(pk + offKr[t] + pos));
-                nxt[t] = Mfma<T>::m32(kf, qf[kk], nxt[t]);
-            }
+            for (int t = 0; t < 2; ++t) dst[t] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(pk + offKr[t] + pos));
+        };
+#pragma unroll
+        for (int kk = 0; kk < KPF - 1; ++kk) load_k(kk, kr[kk]);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            if (kk + KPF - 1 < KS) load_k(kk + KPF - 1, kr[(kk + KPF - 1) % KPF]);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) nxt[t] = Mfma<T>::m32(kr[kk % KPF][t], qf[kk], nxt[t]);
 #pragma unroll
             for (int i = 0; i < EPK; ++i) {
                 const int idx = kk * EPK + i, t = idx >> 4, e = idx & 15;
@@ -265,24 +273,34 @@ void fa_fwd_kernel(AttnArgs a) {
             }
         }
         l_run += rs;
+        // V^T fragments (two transposing reads each), VPF MFMAs ahead.
+        constexpr int NV = 4 * DT, VPF = 3;
+        frag vr[VPF];
+        auto load_v = [&](int idx, frag &dst) __attribute__((always_inline)) {
+            const int b16 = idx / DT, dt = idx % DT;
+            const char *vb = pv + offVr[dt] + b16 * 16 * RB;
+            const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)to_lds(vb));
+            const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)to_lds(vb + 8 * RB));
+            const u32x2 h0 = __builtin_bit_cast(u32x2, t0), h1 = __builtin_bit_cast(u32x2, t1);
+            dst = as_frag<frag>(u32x4{h0[0], h0[1], h1[0], h1[1]});
+        };
 #pragma unroll
-        for (int b16 = 0; b16 < 4; ++b16) {
-            const int t = b16 >> 1, u = b16 & 1;
-            float pv8[8];
+        for (int i = 0; i < VPF - 1; ++i) load_v(i, vr[i]);
+        frag pf;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) pv8[i] = cur[t][8 * u + i];
-            const frag pf = as_frag<frag>(pack8<T>(pv8));
+        for (int idx = 0; idx < NV; ++idx) {
+            const int b16 = idx / DT, dt = idx % DT;
+            if (dt == 0) {
+                const int t = b16 >> 1, u = b16 & 1;
+                float pv8[8];
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const char *vb = pv + offVr[dt] + b16 * 16 * RB;
-                const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4 *)to_lds(vb));
-                const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4 *)to_lds(vb + 8 * RB));
-                const u32x2 h0 = __builtin_bit_cast(u32x2, t0), h1 = __builtin_bit_cast(u32x2, t1);
-                const frag vf = as_frag<frag>(u32x4{h0[0], h0[1], h1[0], h1[1]});
-                o[dt] = Mfma<T>::m32(vf, pf, o[dt]);
+                for (int i = 0; i < 8; ++i) pv8[i] = cur[t][8 * u + i];
+                pf = as_frag<frag>(pack8<T>(pv8));
             }
+            if (idx + VPF - 1 < NV) load_v(idx + VPF - 1, vr[(idx + VPF - 1) % VPF]);
+            o[dt] = Mfma<T>::m32(vr[idx % VPF], pf, o[dt]);
         }
     };
 

@@ -35,6 +35,7 @@ struct GemvArgs {
     int64_t k_per_split;      // multiple of 128
     int64_t k_part;           // strip kernel: k rows per wave (multiple of 32 * stages)
     float *partial;           // [splits][M][N]
+    unsigned *counters;       // strip kernel: per-strip arrival counters (zero between calls)
 };
 
 constexpr int kGemvStrip = 128;
@@ -369,12 +370,44 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
             const int64_t col = n0 + 16 * cg + (l & 15);
             if (row < a.M && col < a.N) {
                 if (a.splits > 1) {
-                    a.partial[((int64_t)split * a.M + row) * a.N + col] = v;
+                    // agent-coherent store (written through the XCD's L2):
+                    // the work-group that sums the partials may run on another XCD
+                    __hip_atomic_store(&a.partial[((int64_t)split * a.M + row) * a.N + col], v, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
                 } else {
                     if (a.bias) v += to_f32(reinterpret_cast<const T *>(a.bias)[col]);
                     reinterpret_cast<Tout *>(a.out)[row * a.ldo + col] = from_f32<Tout>(v);
                 }
             }
+        }
+    }
+    if (a.splits > 1) {
+        // The last work-group of the strip to arrive sums the partials in
+        // split order (bitwise repeatable whatever the arrival order).  The
+        // partials and the counter use agent-coherent accesses, so no
+        // device-scope fence (an L2 write-back per XCD) is needed: each
+        // thread waits for its stores to complete before the barrier that
+        // precedes the counter increment.
+        __shared__ int s_last;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(&a.counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(a.splits - 1);
+        __syncthreads();
+        if (s_last) {
+            for (int idx = tid; idx < MB * 16 * SW; idx += NW * 64) {
+                const int64_t row = idx / SW, col = n0 + idx % SW;
+                if (row >= a.M || col >= a.N) continue;
+                float v = 0.f;
+                for (int z = 0; z < a.splits; ++z)
+                    v += __hip_atomic_load(&a.partial[((int64_t)z * a.M + row) * a.N + col], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                if (a.bias) v += to_f32(reinterpret_cast<const T *>(a.bias)[col]);
+                reinterpret_cast<Tout *>(a.out)[row * a.ldo + col] = from_f32<Tout>(v);
+            }
+            if (tid == 0) __hip_atomic_store(&a.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -391,11 +424,16 @@ static int gemv_choose_splits(int64_t M, int64_t N, int64_t K) {
 
 static int strip_splits(int64_t N, int64_t K);
 
+// Workspace layout: the strip kernel's arrival counters (one per strip,
+// zero between calls) occupy a fixed head region that no call uses for
+// anything else; fp32 partials follow it.
+constexpr size_t kGemvCounterBytes = 16384;       // 4096 strips: N <= 262144
+
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     const int s = gemv_choose_splits(M, N, K);
     const int s2 = strip_splits(N, K);
     const int mx = s > s2 ? s : s2;
-    return mx > 1 ? (size_t)mx * M * N * sizeof(float) : 0;
+    return kGemvCounterBytes + (mx > 1 ? (size_t)mx * M * N * sizeof(float) : 0);
 }
 
 template <typename T, typename Tout, int MB>
@@ -449,7 +487,7 @@ static int64_t strip_part(int64_t K, int splits, int nw, int ns) {
 }
 
 static bool strip_eligible(const GemvArgs &a, bool wcol) {
-    if (wcol || a.N % 8 || a.ldw % 8 || a.K % 8) return false;
+    if (wcol || a.N % 8 || a.ldw % 8 || a.K % 8 || cdiv(a.N, kStripW) * 4 > (int64_t)kGemvCounterBytes) return false;
     if (cdiv(a.N, kStripW) * strip_splits(a.N, a.K) < 128) return false;
     return ((a.K - 1) * a.ldw + a.N) * 2 < ((int64_t)1 << 31) && getenv("KUIOPS_GEMV_NO_STRIP") == nullptr;
 }
@@ -469,11 +507,6 @@ static int strip_dispatch(const GemvArgs &a, hipStream_t st) {
         case 3: strip_launch<T, Tout, 3, kStripWavesWide, kStripStagesWide>(a, st); break;
         case 4: strip_launch<T, Tout, 4, kStripWavesWide, kStripStagesWide>(a, st); break;
         default: return KUIOPS_E_UNSUPPORTED;
-    }
-    if (a.splits > 1) {
-        int64_t blocks = cdiv(a.M * cdiv(a.N, 4), 256);
-        if (blocks > 2048) blocks = 2048;
-        hipLaunchKernelGGL((gemv_reduce_kernel<T, Tout>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     }
     return launch_status();
 }
@@ -506,9 +539,10 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
     if (splits <= 0 && strip_eligible(a, wcol)) {
         a.splits = strip_splits(N, K);
         if (a.splits > 1) {
-            const size_t need = (size_t)a.splits * M * N * sizeof(float);
+            const size_t need = kGemvCounterBytes + (size_t)a.splits * M * N * sizeof(float);
             if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
-            a.partial = reinterpret_cast<float *>(workspace);
+            a.counters = reinterpret_cast<unsigned *>(workspace);
+            a.partial = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + kGemvCounterBytes);
         }
         if (in_dtype == KUIOPS_BF16)
             return out_dtype == KUIOPS_F32 ? strip_dispatch<bf16_t, float>(a, st0) : strip_dispatch<bf16_t, bf16_t>(a, st0);
@@ -520,9 +554,9 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
     a.splits = s;
     a.k_per_split = kps;
     if (s > 1) {
-        const size_t need = (size_t)s * M * N * sizeof(float);
+        const size_t need = kGemvCounterBytes + (size_t)s * M * N * sizeof(float);
         if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
-        a.partial = reinterpret_cast<float *>(workspace);
+        a.partial = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + kGemvCounterBytes);
     }
     hipStream_t st = st0;
     if (in_dtype == KUIOPS_BF16)

@@ -201,6 +201,28 @@ def test_decode_gemm_ragged_k_and_splits(cuda, M, N, K):
         np.testing.assert_allclose(npy(o32), O.mm(npy(x), npy(W)), rtol=1e-4, atol=1e-4)
 
 
+def test_decode_gemm_split_sequence_keeps_counters_zero(cuda):
+    """Row-major decode GEMMs whose K split is summed by the last-arriving
+    work-group of each strip: alternating shapes (different split counts and
+    partial layouts over one workspace) stay exact and bitwise repeatable, and
+    leave the workspace's arrival counters at zero."""
+    shapes = [(16, 4096, 11008), (1, 2048, 8192), (4, 4096, 4096), (16, 2048, 8192), (1, 4096, 4096)]
+    firsts = {}
+    for rep in range(2):
+        for (M, N, K) in shapes:
+            x = gen((M, K), torch.bfloat16, seed=M + K)
+            W = gen((K, N), torch.bfloat16, 0.02, seed=N)
+            out = ops.mm(x.to(cuda), W.to(cuda))
+            if rep == 0:
+                assert_tol(out, O.mm(npy(x), npy(W)), torch.bfloat16)
+                firsts[(M, N, K)] = out
+            else:
+                assert torch.equal(out, firsts[(M, N, K)])
+    torch.cuda.synchronize()
+    ws = ops._WS[(cuda.index or 0, "gemv")]
+    assert not ws[:16384].any()
+
+
 def test_decode_gemm_bias_odd_shapes(cuda):
     for (M, N, K) in [(3, 1000, 520), (1, 8, 8), (7, 4104, 4096)]:
         x, W = gen((M, K), torch.bfloat16, seed=13), gen((K, N), torch.bfloat16, 0.1, seed=14)
