@@ -47,10 +47,12 @@ def test_version_and_status_strings(lib):
 
 
 def test_workspace_queries(lib):
-    # gemv split-K partials: splits * M * N * 4 bytes, splits chosen from N and K
+    # gemv split-K: a 16 KB counter head plus splits * M * N * 4 bytes of
+    # partials, splits chosen from N and K
+    head = 16384
     ws = lib.kuiops_query_workspace(_lib.OP_GEMV_SPLITK, 16, 11008, 4096)
-    assert ws > 0 and ws % (16 * 11008 * 4) == 0
-    assert lib.kuiops_query_workspace(_lib.OP_GEMV_SPLITK, 1, 11008, 4096) == ws // 16
+    assert ws > head and (ws - head) % (16 * 11008 * 4) == 0
+    assert lib.kuiops_query_workspace(_lib.OP_GEMV_SPLITK, 1, 11008, 4096) - head == (ws - head) // 16
     # a 4096^3 GEMM fills the GPU without split-K
     assert lib.kuiops_query_workspace(_lib.OP_ADDMM, 4096, 4096, 4096) == 0
     # a few output tiles with a deep K do split
