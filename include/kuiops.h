@@ -186,7 +186,11 @@ KUIOPS_API int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, in
  * int32[n]) gives each batch entry's key count s_b <= s, read when the
  * kernel runs: a decode step recorded once in a HIP graph passes s = cache
  * capacity and advances kv_len on the device.  Requires the workspace of
- * kuiops_query_workspace(KUIOPS_OP_SDPA_DECODE, n*hq*l, s, ev).
+ * kuiops_query_workspace(KUIOPS_OP_SDPA_DECODE, n*hq*l, s, ev), 16-byte
+ * aligned, whose first bytes hold the split arrival counters: they must be
+ * zero before the first call and every call leaves them zero (calls that
+ * share a workspace must not overlap).  One launch: the last split
+ * work-group of each query-row group merges the splits.
  * Replaces the decode use of the reference sdpa launcher
  * (kuiops/sdpa/wrapper_sdpa.cu.j2:21-30), which has no KV-cache form.     */
 KUIOPS_API int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s,
@@ -294,6 +298,38 @@ KUIOPS_API int kuiops_rope_kv_append(int64_t n, int64_t t, int64_t hq, int64_t h
 KUIOPS_API int kuiops_decode_linear(int64_t N, int64_t K, int dtype, int x_kind, const void *in,
                          const void *in_add, const void *norm_w, float eps, void *h_out,
                          const void *W, int64_t ldw, const void *bias, void *out, void *stream);
+
+/* Batch-1 decode gate/up projection with SwiGLU fused into its epilogue:
+ * W = [gate; up] stored [2*ffn, K] (rows ffn apart), x from the input stage
+ * as in kuiops_decode_linear (x_kind), and
+ *   out[i] = round(round(silu(g_i)) * u_i),  g_i, u_i = round(dot(W row, x))
+ * for i < ffn, the rounding of the stock gate_proj / silu / up_proj / mul
+ * chain.  No reference counterpart: it fuses the decoder glue around the
+ * mm launcher (kuiops/mm/wrapper_mm.cu.j2:15-19) with the silu and mul
+ * elementwise launches (kuipy/kuiops.py:158,166).  K <= 4096.              */
+KUIOPS_API int kuiops_decode_gate_up(int64_t ffn, int64_t K, int dtype, int x_kind, const void *in,
+                          const void *in_add, const void *norm_w, float eps, void *h_out,
+                          const void *W, int64_t ldw, void *out, void *stream);
+
+/* Batch-1 decode qkv projection with rotary embedding and the KV-cache
+ * append fused into its epilogue.  W is the fused [q; k; v] weight
+ * [(hq + 2*hkv)*hd, K]; x comes from the input stage of x_kind, reading
+ * `in` at row in_row[0] (device int64, clamped to [0, in_rows)) of stride
+ * ld_in when in_row is non-null (an embedding lookup), else `in` itself.
+ * At position p = pos[0] (device int32): q heads are rotated into
+ * q_out[hq*hd]; rotated k and plain v heads are stored at
+ * k_cache + kvh*sk_head + p*sk_pos (and v likewise) when p < cache_cap.
+ * Rotation and rounding as kuiops_rope_kv_append applied to the rounded
+ * projections.  No reference counterpart: it fuses the mm launcher with the
+ * rotary and KV-cache cat launches (CatImpl kuipy/kuiops.py:810-857) for a
+ * batch-1 decode step.  K <= 4096, hd even.                                 */
+KUIOPS_API int kuiops_decode_qkv_rope(int64_t hq, int64_t hkv, int64_t hd, int64_t K, int dtype, int x_kind,
+                           const void *in, const int64_t *in_row, int64_t ld_in, int64_t in_rows,
+                           const void *in_add, const void *norm_w, float eps, void *h_out,
+                           const void *W, int64_t ldw, const float *inv_freq, const int32_t *pos,
+                           void *q_out, void *k_cache, int64_t sk_head, int64_t sk_pos,
+                           void *v_cache, int64_t sv_head, int64_t sv_pos, int64_t cache_cap,
+                           void *stream);
 
 #ifdef __cplusplus
 }

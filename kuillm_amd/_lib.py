@@ -66,6 +66,10 @@ SIGNATURES = {
                                      _vp, _i64p, _vp, _i64p, _vp, _i64p, _i64, _vp]),
     "kuiops_decode_linear": (_int, [_i64, _i64, _int, _int, _vp, _vp, _vp, _flt, _vp, _vp, _i64, _vp, _vp,
                                     _vp]),
+    "kuiops_decode_gate_up": (_int, [_i64, _i64, _int, _int, _vp, _vp, _vp, _flt, _vp, _vp, _i64, _vp, _vp]),
+    "kuiops_decode_qkv_rope": (_int, [_i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _i64, _i64, _vp, _vp, _flt,
+                                      _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                      _vp]),
 }
 
 

@@ -17,12 +17,12 @@
 //   skip their MFMAs; all q-blocks of one head are mapped to one XCD so its
 //   K / V stay in that XCD's L2.
 //
-// fa_decode_kernel + fa_decode_combine_kernel -- decode (few queries per head)
-//   over a long KV cache: HBM-bound, so the keys are split over work-groups
-//   (split-KV); each work-group streams its key range once for all query rows
-//   that share the KV head (grouped-query attention), keeps fp32 online-softmax
-//   state per row, and writes (max, sum, unnormalised output) to the
-//   workspace.  The combine kernel merges the splits in split order.
+// fa_decode_kernel -- decode (few queries per head) over a long KV cache:
+//   HBM-bound, so the keys are split over work-groups (split-KV); each
+//   work-group streams its key range once for all query rows that share the
+//   KV head (grouped-query attention), keeps fp32 online-softmax state per
+//   row and writes (max, sum, unnormalised output) to the workspace; the last
+//   work-group of a row group to finish merges the splits in split order.
 //
 // Semantics: aten scaled_dot_product_attention (the reference's fallthrough,
 // kuipy/kuiops.py:627-681 rejects is_causal; tests/test_jit_ops.py:173-193).
@@ -46,6 +46,7 @@ struct AttnArgs {
     int row_groups;
     float *ws_ml;       // [rows_total][splits][2]
     float *ws_o;        // [rows_total][splits][ev]
+    unsigned *counters; // [n][hkv][row_groups] split arrival counters (zero between calls)
     const int32_t *kv_len;  // decode: per-batch key count in device memory (<= s), or null
 };
 
@@ -370,8 +371,9 @@ __device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, flo
     m1 = M;
 }
 
-template <typename T, int HD, int R>
-__global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
+template <typename T, int HD, int R, int NWV = 4>
+__global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
+    constexpr int NT = NWV * 64;
     constexpr int LPK = HD / 8;       // lanes per key (8 d values each)
     constexpr int KPW = 64 / LPK;     // keys per wave step
     constexpr int NB = 4;             // keys per lane group per step
@@ -420,7 +422,7 @@ __global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
         for (int e = 0; e < 8; ++e) o[r][e] = 0.f;
     }
 
-    for (int64_t kb = kbeg + (int64_t)wave * KPW * NB; kb < kend; kb += 4 * KPW * NB) {
+    for (int64_t kb = kbeg + (int64_t)wave * KPW * NB; kb < kend; kb += NWV * KPW * NB) {
         float s[R][NB];
         u32x4 kr[NB], vr[NB];
 #pragma unroll
@@ -504,8 +506,9 @@ __global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
         }
     }
 
-    // Merge the 4 waves in wave order through LDS, then write the split's state.
-    __shared__ float sm[4][R], sl[4][R], so[4][R][HD];
+    // Merge the waves in wave order through LDS; a single split writes the
+    // normalised output, otherwise the split's state goes to the workspace.
+    __shared__ float sm[NWV][R], sl[NWV][R], so[NWV][R][HD];
     if (kg == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -516,24 +519,136 @@ __global__ __launch_bounds__(256) void fa_decode_kernel(AttnArgs a) {
     }
     __syncthreads();
     const int nrows = min(a.rows_per_group, rows_kv - r0);
-    for (int idx = tid; idx < R * HD; idx += 256) {
+    for (int idx = tid; idx < R * HD; idx += NT) {
         const int r = idx / HD, d = idx % HD;
         if (r >= nrows) continue;
         float mm = sm[0][r], ll = sl[0][r], oo = so[0][r][d];
 #pragma unroll
-        for (int wv = 1; wv < 4; ++wv) merge_state<1>(mm, ll, &oo, sm[wv][r], sl[wv][r], &so[wv][r][d]);
+        for (int wv = 1; wv < NWV; ++wv) merge_state<1>(mm, ll, &oo, sm[wv][r], sl[wv][r], &so[wv][r][d]);
         const int rr = r0 + r;
         const int64_t head = hk * G + rr / a.l, qi = rr % a.l;
         const int64_t grow = (b * a.hq + head) * a.l + qi;
-        a.ws_o[(grow * a.splits + split) * HD + d] = oo;
+        if (a.splits == 1) {
+            T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
+            Op[d] = from_f32<T>(oo * (ll > 0.f ? 1.f / ll : 0.f));
+            if (a.lse && d == 0) a.lse[grow] = ll > 0.f ? (mm + __log2f(ll)) * kLn2 : -INFINITY;
+            continue;
+        }
+        if (!a.counters) {
+            // merged by the separate merge kernel
+            a.ws_o[(grow * a.splits + split) * HD + d] = oo;
+            if (d == 0) {
+                a.ws_ml[(grow * a.splits + split) * 2 + 0] = mm;
+                a.ws_ml[(grow * a.splits + split) * 2 + 1] = ll;
+            }
+            continue;
+        }
+        // agent-coherent stores (written through the XCD's L2): the
+        // work-group that merges the splits may run on another XCD
+        __hip_atomic_store(&a.ws_o[(grow * a.splits + split) * HD + d], oo, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
         if (d == 0) {
-            a.ws_ml[(grow * a.splits + split) * 2 + 0] = mm;
-            a.ws_ml[(grow * a.splits + split) * 2 + 1] = ll;
+            __hip_atomic_store(&a.ws_ml[(grow * a.splits + split) * 2 + 0], mm, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.ws_ml[(grow * a.splits + split) * 2 + 1], ll, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    if (a.splits == 1 || !a.counters) return;
+
+    // The last of the group's split work-groups to arrive merges the splits
+    // in split order (bitwise repeatable whatever the arrival order).  Each
+    // thread waits for its agent-coherent stores to complete before the
+    // barrier that precedes the counter increment, so no device-scope fence
+    // (an L2 write-back per XCD) is needed.
+    __shared__ int s_last;
+    __shared__ float s_w[R][64];
+    __shared__ float s_M[R], s_L[R];
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned *ctr = a.counters + (b * a.hkv + hk) * a.row_groups + rg;
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(a.splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // The split states are read with agent-coherent (sc1) buffer loads, which
+    // unlike atomics can be batched.  Wave w turns row w's split maxima into
+    // weights (splits <= 64, one per lane); thread (r, d) then sums
+    // weight * o[split][d] in split order.
+    const __amdgpu_buffer_rsrc_t rs_ml = __builtin_amdgcn_make_buffer_rsrc((void *)a.ws_ml, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc((void *)a.ws_o, (short)0, 0x7fffffff, 0x00020000);
+    constexpr int kSc1 = 16;                    // cache policy: system-coherent level 1 (agent scope)
+    auto grow_of = [&](int r) {
+        const int rr = r0 + r;
+        return (b * a.hq + hk * G + rr / a.l) * a.l + rr % a.l;
+    };
+    // Thread (r, d) = tid issues its o loads (at most 32 splits) before the
+    // weights are known, so both arrive in one memory round trip.
+    constexpr int kMaxSplits = 32;
+    float ov[kMaxSplits];
+    const bool pre = a.splits <= kMaxSplits && nrows * HD <= NT && tid < nrows * HD;
+    if (pre) {
+        const uint32_t base = (uint32_t)((grow_of(tid / HD) * a.splits * HD + tid % HD) * 4);
+#pragma unroll
+        for (int z = 0; z < kMaxSplits; ++z)
+            ov[z] = z < a.splits ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                       rs_o, base + (uint32_t)(z * HD * 4), 0, kSc1))
+                                 : 0.f;
+    }
+    for (int r = wave; r < nrows; r += NWV) {
+        const uint32_t base = (uint32_t)(grow_of(r) * a.splits * 2) * 4;
+        // (the b32 loads return raw bits)
+        const float mz = lane < a.splits
+                             ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs_ml, base + lane * 8, 0, kSc1))
+                             : -INFINITY;
+        const float lz = lane < a.splits
+                             ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs_ml, base + lane * 8 + 4, 0, kSc1))
+                             : 0.f;
+        const float M = wave_max(mz);
+        const float Mu = (M == -INFINITY) ? 0.f : M;
+        const float w = lane < a.splits ? fast_exp2(mz - Mu) : 0.f;
+        s_w[r][lane] = w;
+        const float L = wave_sum(w * lz);
+        if (lane == 0) { s_M[r] = M; s_L[r] = L; }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < nrows * HD; idx += NT) {
+        const int r = idx / HD, d = idx % HD;
+        const int64_t grow = grow_of(r);
+        float acc = 0.f;
+        if (pre) {
+#pragma unroll
+            for (int z = 0; z < kMaxSplits; ++z)
+                if (z < a.splits) acc += s_w[r][z] * ov[z];
+        } else {
+            const uint32_t base = (uint32_t)((grow * a.splits * HD + d) * 4);
+            for (int z0 = 0; z0 < a.splits; z0 += 8) {
+                float o8[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    o8[j] = z0 + j < a.splits ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                                    rs_o, base + (uint32_t)((z0 + j) * HD * 4), 0, kSc1))
+                                              : 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (z0 + j < a.splits) acc += s_w[r][z0 + j] * o8[j];
+            }
+        }
+        const float L = s_L[r];
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        const int rr = r0 + r;
+        const int64_t head = hk * G + rr / a.l, qi = rr % a.l;
+        T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
+        Op[d] = from_f32<T>(acc * inv);
+        if (a.lse && d == 0) a.lse[grow] = L > 0.f ? (s_M[r] + __log2f(L)) * kLn2 : -INFINITY;
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One work-group per query row: wave 0 turns the split maxima into weights
+// Separate merge for many splits (one work-group per query row; see the
+// host launch): wave 0 turns the split maxima into weights
 // (splits <= 64, one per lane), then thread d sums weight * o[split][d] over
 // the splits in split order.
 template <typename T, int HD>
@@ -605,14 +720,37 @@ static void fill_args(AttnArgs &a, int64_t n, int64_t hq, int64_t hkv, int64_t l
 
 // Keys per split for the decode kernel: enough splits to fill the GPU, at
 // least 64 keys each.
+constexpr int kFusedMergeMaxSplits = 16;
+
 static int64_t decode_chunk(int64_t s) {
-    int64_t c = cdiv(cdiv(s, 32), 64) * 64;   // at most 32 splits (combine handles 64)
+    int64_t c = cdiv(cdiv(s, 32), 64) * 64;   // at most 32 splits
     return c < 64 ? 64 : c;
 }
 
+// Query rows per work-group (the rows sharing a KV head, up to 8).
+static int decode_rows_per_group(int rows_kv) {
+    return rows_kv <= 1 ? 1 : rows_kv <= 2 ? 2 : rows_kv <= 4 ? 4 : 8;
+}
+
+// Waves of the single-split kernel (as many as the row state's registers allow).
+static int decode_single_waves(int R) { return R <= 2 ? 16 : (R == 4 ? 8 : 4); }
+
+// A cache that one work-group streams in a single step takes a single split
+// (no workspace round trip): keys per step = waves x keys per wave-step.
+// Longer caches are faster split: each step of a work-group is a dependent
+// memory round trip, while splits overlap theirs.
+static bool decode_single_split(int64_t s, int64_t ev, int R) {
+    const int64_t per_step = (int64_t)decode_single_waves(R) * (64 / (ev / 8)) * 4;
+    return s <= per_step;
+}
+
+// Workspace: split arrival counters (one per work-group row group, at most
+// one per query row; zero between calls), then the split states.
+static size_t decode_counter_bytes(int64_t rows) { return (size_t)cdiv(rows * 4, 256) * 256; }
+
 size_t decode_workspace_bytes(int64_t rows, int64_t kv_len, int64_t ev) {
     const int64_t splits = cdiv(kv_len > 0 ? kv_len : 1, decode_chunk(kv_len));
-    return (size_t)rows * splits * (ev + 2) * sizeof(float) + 256;
+    return decode_counter_bytes(rows) + (size_t)rows * splits * (ev + 2) * sizeof(float) + 256;
 }
 
 template <typename T, int HD>
@@ -632,21 +770,34 @@ template <typename T, int HD>
 static int launch_decode(AttnArgs a, hipStream_t st) {
     const int G = (int)(a.hq / a.hkv);
     const int rows_kv = G * (int)a.l;
-    int R;
-    if (rows_kv <= 1) R = 1;
-    else if (rows_kv <= 2) R = 2;
-    else if (rows_kv <= 4) R = 4;
-    else R = 8;
+    const int R = decode_rows_per_group(rows_kv);
     a.rows_per_group = R;
     a.row_groups = (int)cdiv(rows_kv, R);
     dim3 grid((unsigned)a.splits, (unsigned)(a.hkv * a.row_groups), (unsigned)a.n);
+    if (a.splits == 1) {
+        // short caches: one work-group per row group streams every key (no
+        // workspace round trip)
+        switch (R) {
+            case 1: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1, 16>), grid, dim3(1024), 0, st, a); break;
+            case 2: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 2, 16>), grid, dim3(1024), 0, st, a); break;
+            case 4: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 4, 8>), grid, dim3(512), 0, st, a); break;
+            default: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 8, 4>), grid, dim3(256), 0, st, a); break;
+        }
+        return launch_status();
+    }
+    // The last split work-group of a row group merges the splits in-kernel
+    // (one launch) when there are few; with many, each split work-group
+    // would wait for its write-through stores, so a second kernel merges.
+    const bool fused = a.splits <= kFusedMergeMaxSplits;
+    if (!fused) a.counters = nullptr;
     switch (R) {
         case 1: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1>), grid, dim3(256), 0, st, a); break;
         case 2: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 2>), grid, dim3(256), 0, st, a); break;
         case 4: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 4>), grid, dim3(256), 0, st, a); break;
         default: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 8>), grid, dim3(256), 0, st, a); break;
     }
-    hipLaunchKernelGGL((fa_decode_combine_kernel<T, HD>), dim3((unsigned)(a.n * a.hq * a.l)), dim3(128), 0, st, a);
+    if (!fused)
+        hipLaunchKernelGGL((fa_decode_combine_kernel<T, HD>), dim3((unsigned)(a.n * a.hq * a.l)), dim3(128), 0, st, a);
     return launch_status();
 }
 
@@ -689,11 +840,15 @@ extern "C" int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l,
     a.kv_len = kv_len;
     const int64_t ss = s > 0 ? s : 1;
     a.chunk = decode_chunk(ss);
+    if (decode_single_split(ss, ev, decode_rows_per_group((int)((hq / hkv) * l)))) a.chunk = ss;
     a.splits = (int)cdiv(ss, a.chunk);
     const int64_t rows = n * hq * l;
     const size_t need = decode_workspace_bytes(rows, s, ev);
+    if ((int64_t)(need - decode_counter_bytes(rows)) >= INT32_MAX) return KUIOPS_E_UNSUPPORTED;  // 32-bit offsets
     if (!workspace || workspace_bytes < need) return KUIOPS_E_WORKSPACE;
-    a.ws_ml = reinterpret_cast<float *>(workspace);
+    if (!aligned16(workspace)) return KUIOPS_E_WORKSPACE;
+    a.counters = reinterpret_cast<unsigned *>(workspace);
+    a.ws_ml = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + decode_counter_bytes(rows));
     a.ws_o = a.ws_ml + rows * a.splits * 2;
     if ((reinterpret_cast<uintptr_t>(a.ws_o) & 15) != 0) {
         // keep o rows 16-byte aligned

@@ -172,6 +172,8 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
 constexpr int kXPlain = 1, kXRmsNorm = 2, kXSwiGlu = 3;   // kuiops_x_kind
 constexpr int kDecodeMaxK = 8192;
 
+constexpr int kOutPlain = 0, kOutSwiGlu = 1, kOutRope = 2;   // decode_rows_kernel epilogues
+
 struct DecLinArgs {
     int64_t N, K;
     const void *in, *in_add;           // x source; RMSNorm: h = round(in + in_add)
@@ -182,7 +184,30 @@ struct DecLinArgs {
     const void *bias;
     void *out;
     int rpw;                           // rows per wave
+    // optional device row index of `in` (in += in_row[0] * ld_in, clamped to in_rows)
+    const int64_t *in_row; int64_t ld_in, in_rows;
+    // paired epilogues: logical row 2p + e is W row base(p) + e * pair_off
+    int64_t pair_off;
+    // rotary epilogue (kOutRope): rows are [q heads | k heads | v heads] of hd
+    int64_t hq, hkv, hd;
+    const float *inv_freq;
+    const int32_t *pos;                // device position of the token
+    void *kc; int64_t sk1, sk2;        // k cache: head, position strides
+    void *vc; int64_t sv1, sv2;
+    int64_t cap;
 };
+
+// W row of logical row j: identity, or the pair mapping of the paired
+// epilogues (SwiGLU: rows p and p + ffn; rotary: rows i and i + hd/2 of a
+// head, so that one wave holds both halves of each rotated pair).
+template <int OK>
+__device__ __forceinline__ int64_t dec_row(const DecLinArgs &a, int64_t j) {
+    if constexpr (OK == kOutPlain) return j;
+    const int64_t p = j >> 1, e = j & 1;
+    if constexpr (OK == kOutSwiGlu) return p + e * a.pair_off;
+    const int64_t half = a.pair_off, head = p / half;
+    return head * a.hd + (p - head * half) + e * half;
+}
 
 // out[n] = dot(W[n, :], x) (+ bias[n]) with x computed by every work-group
 // into LDS (the fused input stage), then held in registers: lane l owns
@@ -194,9 +219,17 @@ struct DecLinArgs {
 //   kXRmsNorm  h = round(in + in_add), x = round(w * round(h * rsqrt(mean(h^2) + eps)));
 //              work-group 0 stores h to h_out
 //   kXSwiGlu   x = round(round(silu(in[k])) * in[K + k])      (in = [gate | up])
-template <typename T, int XK, int KC>
+// Epilogues (OK):
+//   kOutPlain   out[n] = round(dot) (+ bias)
+//   kOutSwiGlu  rows (p, p + ffn) of a [gate; up] weight: out[p] = round(round(silu(g)) * u),
+//               g, u the rounded projections (as silu_mul_kernel)
+//   kOutRope    rows (i, i + hd/2) of each head of a fused qkv weight: q and k
+//               pairs rotated at position pos (as rope_kv_kernel), q to out
+//               [hq * hd], k and v stored into the caches at pos (if < cap)
+template <typename T, int XK, int KC, int OK = kOutPlain>
 __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
     constexpr int RG = KC <= 4 ? 4 : (KC <= 8 ? 2 : 1);    // rows per wave at most (host: rpw <= RG)
+    static_assert(OK == kOutPlain || RG % 2 == 0, "paired epilogues need two rows per wave");
     constexpr int XCH = kDecodeMaxK / 8 / 256;      // x chunks per thread in the input stage
     typedef T t8 __attribute__((ext_vector_type(8)));
     __shared__ u32x4 sx[kDecodeMaxK / 8];
@@ -204,6 +237,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nch = (int)(a.K / 8);
     const T *in = reinterpret_cast<const T *>(a.in);
+    if (a.in_row) in += max((int64_t)0, min(a.in_row[0], a.in_rows - 1)) * a.ld_in;
 
     // ---- this wave's W rows, in flight during the input stage
     const T *W = reinterpret_cast<const T *>(a.W);
@@ -212,14 +246,13 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
     u32x4 wv[RG][KC];
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
-        const int64_t r = min(r0 + g, a.N - 1);                 // clamped: never stored
+        const int64_t r = dec_row<OK>(a, min(r0 + g, a.N - 1));   // clamped: never stored
 #pragma unroll
         for (int j = 0; j < KC; ++j) {
             const int ch = j * 64 + lane;
             wv[g][j] = ch < nch ? *reinterpret_cast<const u32x4 *>(W + r * a.ldw + ch * 8) : u32x4{0, 0, 0, 0};
         }
     }
-
     // ---- input stage
     float h[XCH][8];
     float ss = 0.f;
@@ -282,6 +315,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
             for (int e = 0; e < 8; ++e) xf[j][e] = 0.f;
         }
     }
+    float accs[RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
         float acc = 0.f;
@@ -292,29 +326,101 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w8[e], xf[j][e], acc);
         }
-        acc = wave_sum(acc);
-        const int64_t r = r0 + g;
-        if (lane == 0 && r < r1) {
-            if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
-            reinterpret_cast<T *>(a.out)[r] = from_f32<T>(acc);
+        accs[g] = wave_sum(acc);
+    }
+    if (lane != 0) return;
+    if constexpr (OK == kOutPlain) {
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            const int64_t r = r0 + g;
+            if (r < r1) {
+                float acc = accs[g];
+                if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
+                reinterpret_cast<T *>(a.out)[r] = from_f32<T>(acc);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < RG; g += 2) {
+            const int64_t r = r0 + g;                    // even: rows r, r + 1 form pair r / 2
+            if (r + 1 >= r1) continue;
+            const int64_t p = r >> 1;
+            const float x1 = rnd<T>(accs[g]), x2 = rnd<T>(accs[g + 1]);
+            if constexpr (OK == kOutSwiGlu) {
+                reinterpret_cast<T *>(a.out)[p] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
+            } else {
+                const int64_t half = a.pair_off, head = p / half, i = p - head * half;
+                const int64_t pos = a.pos ? (int64_t)a.pos[0] : 0;
+                const bool store_kv = pos >= 0 && pos < a.cap;
+                if (head < a.hq + a.hkv) {
+                    const float ang = (float)pos * a.inv_freq[i];
+                    const float c = rnd<T>(cosf(ang)), sn = rnd<T>(sinf(ang));
+                    const T o1 = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * sn));
+                    const T o2 = from_f32<T>(rnd<T>(x2 * c) + rnd<T>(x1 * sn));
+                    T *dst;
+                    if (head < a.hq) {
+                        dst = reinterpret_cast<T *>(a.out) + head * a.hd;
+                    } else {
+                        if (!store_kv) continue;
+                        dst = reinterpret_cast<T *>(a.kc) + (head - a.hq) * a.sk1 + pos * a.sk2;
+                    }
+                    dst[i] = o1;
+                    dst[i + half] = o2;
+                } else if (store_kv) {
+                    T *dst = reinterpret_cast<T *>(a.vc) + (head - a.hq - a.hkv) * a.sv1 + pos * a.sv2;
+                    dst[i] = from_f32<T>(x1);
+                    dst[i + half] = from_f32<T>(x2);
+                }
+            }
         }
     }
 }
 
-template <typename T, int XK>
+template <typename T, int XK, int OK>
 static void decode_rows_launch(const DecLinArgs &a, unsigned grid, hipStream_t st) {
     const int kc = (int)cdiv(a.K, 512);
-    if (kc <= 4) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 4>), dim3(grid), dim3(256), 0, st, a);
-    else if (kc <= 8) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 8>), dim3(grid), dim3(256), 0, st, a);
-    else if (kc <= 12) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 12>), dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((decode_rows_kernel<T, XK, 16>), dim3(grid), dim3(256), 0, st, a);
+    if (kc <= 4) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 4, OK>), dim3(grid), dim3(256), 0, st, a);
+    else if (kc <= 8) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 8, OK>), dim3(grid), dim3(256), 0, st, a);
+    else if constexpr (OK == kOutPlain) {
+        if (kc <= 12) hipLaunchKernelGGL((decode_rows_kernel<T, XK, 12, OK>), dim3(grid), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((decode_rows_kernel<T, XK, 16, OK>), dim3(grid), dim3(256), 0, st, a);
+    }
 }
 
-template <typename T>
+template <typename T, int OK>
 static void decode_rows_dispatch(const DecLinArgs &a, int x_kind, unsigned grid, hipStream_t st) {
-    if (x_kind == kXPlain) decode_rows_launch<T, kXPlain>(a, grid, st);
-    else if (x_kind == kXRmsNorm) decode_rows_launch<T, kXRmsNorm>(a, grid, st);
-    else decode_rows_launch<T, kXSwiGlu>(a, grid, st);
+    if (x_kind == kXPlain) decode_rows_launch<T, kXPlain, OK>(a, grid, st);
+    else if (x_kind == kXRmsNorm) decode_rows_launch<T, kXRmsNorm, OK>(a, grid, st);
+    else decode_rows_launch<T, kXSwiGlu, OK>(a, grid, st);
+}
+
+// Shared host path of the decode projections: argument checks, rows per
+// wave (one register group of rows per wave, spread over at least ~2048
+// waves; an even count for the paired epilogues) and the launch.
+template <int OK>
+static int decode_linear_run(DecLinArgs a, int dtype, int x_kind, void *stream) {
+    if (a.N < 0 || a.K < 0) return KUIOPS_E_INVALID;
+    if (x_kind != kXPlain && x_kind != kXRmsNorm && x_kind != kXSwiGlu) return KUIOPS_E_INVALID;
+    if (a.N == 0) return KUIOPS_OK;
+    if (!a.in || !a.W || !a.out || (x_kind == kXRmsNorm && !a.norm_w)) return KUIOPS_E_INVALID;
+    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
+    if (a.K == 0 || a.K % 8 || a.K > kDecodeMaxK || a.ldw % 8 || a.ldw < a.K) return KUIOPS_E_UNSUPPORTED;
+    if (!aligned16(a.in) || !aligned16(a.W) || (a.in_add && !aligned16(a.in_add)) ||
+        (a.norm_w && !aligned16(a.norm_w)) || (a.h_out && !aligned16(a.h_out)))
+        return KUIOPS_E_UNSUPPORTED;
+    if (a.in_row && (a.ld_in % 8 || a.in_rows <= 0)) return KUIOPS_E_UNSUPPORTED;
+    if (a.h_out && (a.h_out == a.in || a.h_out == a.in_add)) return KUIOPS_E_INVALID;
+    const int kc = (int)cdiv(a.K, 512);
+    const int rg = kc <= 4 ? 4 : (kc <= 8 ? 2 : 1);
+    if (OK != kOutPlain && rg < 2) return KUIOPS_E_UNSUPPORTED;
+    a.rpw = (int)min((int64_t)rg, cdiv(a.N, 2048));
+    if (OK != kOutPlain && (a.rpw & 1)) a.rpw += 1;
+    const int64_t grid = cdiv(a.N, 4 * (int64_t)a.rpw);
+    if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    if (dtype == KUIOPS_BF16) decode_rows_dispatch<bf16_t, OK>(a, x_kind, (unsigned)grid, st);
+    else decode_rows_dispatch<f16_t, OK>(a, x_kind, (unsigned)grid, st);
+    return launch_status();
 }
 
 }  // namespace kuiops
@@ -388,25 +494,36 @@ extern "C" int kuiops_rope_kv_append(int64_t n, int64_t t, int64_t hq, int64_t h
 extern "C" int kuiops_decode_linear(int64_t N, int64_t K, int dtype, int x_kind, const void *in, const void *in_add,
                                     const void *norm_w, float eps, void *h_out, const void *W, int64_t ldw,
                                     const void *bias, void *out, void *stream) {
-    if (N < 0 || K < 0) return KUIOPS_E_INVALID;
-    if (x_kind != kXPlain && x_kind != kXRmsNorm && x_kind != kXSwiGlu) return KUIOPS_E_INVALID;
-    if (N == 0) return KUIOPS_OK;
-    if (!in || !W || !out || (x_kind == kXRmsNorm && !norm_w)) return KUIOPS_E_INVALID;
-    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
-    if (K == 0 || K % 8 || K > kDecodeMaxK || ldw % 8 || ldw < K) return KUIOPS_E_UNSUPPORTED;
-    if (!aligned16(in) || !aligned16(W) || (in_add && !aligned16(in_add)) || (norm_w && !aligned16(norm_w)) ||
-        (h_out && !aligned16(h_out)))
-        return KUIOPS_E_UNSUPPORTED;
-    if (h_out && (h_out == in || h_out == in_add)) return KUIOPS_E_INVALID;
-    DecLinArgs a{N, K, in, in_add, norm_w, eps, h_out, W, ldw, bias, out, 1};
-    // one register group of rows per wave, spread over at least ~2048 waves
-    const int kc = (int)cdiv(K, 512);
-    const int rg = kc <= 4 ? 4 : (kc <= 8 ? 2 : 1);
-    a.rpw = (int)min((int64_t)rg, cdiv(N, 2048));
-    const int64_t grid = cdiv(N, 4 * (int64_t)a.rpw);
-    if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
-    hipStream_t st = as_stream(stream);
-    if (dtype == KUIOPS_BF16) decode_rows_dispatch<bf16_t>(a, x_kind, (unsigned)grid, st);
-    else decode_rows_dispatch<f16_t>(a, x_kind, (unsigned)grid, st);
-    return launch_status();
+    DecLinArgs a{};
+    a.N = N; a.K = K; a.in = in; a.in_add = in_add; a.norm_w = norm_w; a.eps = eps; a.h_out = h_out;
+    a.W = W; a.ldw = ldw; a.bias = bias; a.out = out;
+    return decode_linear_run<kOutPlain>(a, dtype, x_kind, stream);
+}
+
+extern "C" int kuiops_decode_gate_up(int64_t ffn, int64_t K, int dtype, int x_kind, const void *in,
+                                     const void *in_add, const void *norm_w, float eps, void *h_out, const void *W,
+                                     int64_t ldw, void *out, void *stream) {
+    if (ffn < 0) return KUIOPS_E_INVALID;
+    DecLinArgs a{};
+    a.N = 2 * ffn; a.K = K; a.in = in; a.in_add = in_add; a.norm_w = norm_w; a.eps = eps; a.h_out = h_out;
+    a.W = W; a.ldw = ldw; a.out = out; a.pair_off = ffn;
+    return decode_linear_run<kOutSwiGlu>(a, dtype, x_kind, stream);
+}
+
+extern "C" int kuiops_decode_qkv_rope(int64_t hq, int64_t hkv, int64_t hd, int64_t K, int dtype, int x_kind,
+                                      const void *in, const int64_t *in_row, int64_t ld_in, int64_t in_rows,
+                                      const void *in_add, const void *norm_w, float eps, void *h_out,
+                                      const void *W, int64_t ldw, const float *inv_freq, const int32_t *pos,
+                                      void *q_out, void *k_cache, int64_t sk_head, int64_t sk_pos, void *v_cache,
+                                      int64_t sv_head, int64_t sv_pos, int64_t cache_cap, void *stream) {
+    if (hq < 0 || hkv < 0 || hd <= 0 || hd % 2 || cache_cap < 0) return KUIOPS_E_INVALID;
+    if (!inv_freq || !k_cache || !v_cache) return KUIOPS_E_INVALID;
+    DecLinArgs a{};
+    a.N = (hq + 2 * hkv) * hd; a.K = K; a.in = in; a.in_add = in_add; a.norm_w = norm_w; a.eps = eps;
+    a.h_out = h_out; a.W = W; a.ldw = ldw; a.out = q_out;
+    a.in_row = in_row; a.ld_in = ld_in; a.in_rows = in_rows;
+    a.pair_off = hd / 2; a.hq = hq; a.hkv = hkv; a.hd = hd; a.inv_freq = inv_freq; a.pos = pos;
+    a.kc = k_cache; a.sk1 = sk_head; a.sk2 = sk_pos; a.vc = v_cache; a.sv1 = sv_head; a.sv2 = sv_pos;
+    a.cap = cache_cap;
+    return decode_linear_run<kOutRope>(a, dtype, x_kind, stream);
 }

@@ -106,27 +106,29 @@ class LlamaDecoder:
         self.vcache = torch.zeros(kv, dtype=dtype, device=self.dev)
         # device-side decode state: the token to feed, its position, the key count
         self.tok = torch.zeros(self.n, dtype=torch.int64, device=self.dev)
-        self.pos = torch.zeros(self.n, dtype=torch.int32, device=self.dev)
-        self.kv_len = torch.zeros(self.n, dtype=torch.int32, device=self.dev)
+        # position and key count share one buffer, so a decode step advances
+        # both with one launch
+        self.step_state = torch.zeros((2, self.n), dtype=torch.int32, device=self.dev)
+        self.pos, self.kv_len = self.step_state[0], self.step_state[1]
         self.graph = None
-        self.fused = self.n == 1 and max(s.d, s.ffn) <= 8192 and s.d % 8 == 0 and s.ffn % 8 == 0
+        self.fused = self.n == 1 and s.d <= 4096 and s.ffn <= 8192 and s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0
         if self.fused:
             self._setup_fused()
 
     def _setup_fused(self):
         """Static buffers of the batch-1 decode step, whose projections carry
-        their RMSNorm / SwiGLU input stage (kuiops_decode_linear): 6 launches
-        per layer."""
+        their input stage (RMSNorm) and epilogue (rotary + KV append, SwiGLU):
+        5 launches per layer."""
         s, dev = self.s, self.dev
         bf = dict(dtype=self.dtype, device=dev)
         self.h_buf = [torch.empty(s.d, **bf), torch.empty(s.d, **bf)]
-        self.qkv1 = torch.empty(1, 1, (s.hq + 2 * s.hkv) * s.hd, **bf)
         self.q1 = torch.empty(1, s.hq, 1, s.hd, **bf)
         self.att1 = torch.empty(1, 1, s.hq * s.hd, **bf)
         self.o1 = torch.empty(s.d, **bf)
-        self.gu1 = torch.empty(2 * s.ffn, **bf)
+        self.a1 = torch.empty(s.ffn, **bf)
         self.down1 = torch.empty(s.d, **bf)
         self.logits1 = torch.empty(s.vocab, **bf)
+        self.top_v = torch.empty(1, 1, dtype=torch.float32, device=dev)
 
     @classmethod
     def from_hf(cls, model, capacity: int, batch: int = 1, device="cuda"):
@@ -196,41 +198,38 @@ class LlamaDecoder:
         pending, res = self._layers(h, 1, self.pos, self.kv_len)
         logits, nxt = self._head(pending, res, 1)
         self.tok.copy_(nxt)
-        self.pos.add_(1)
-        self.kv_len.add_(1)
+        self.step_state.add_(1)
         return logits
 
     def _decode_step_fused(self):
         """One batch-1 decode step, same arithmetic as ``_layers`` + ``_head``
-        (every rounding point kept), in 6 launches per layer: qkv (RMSNorm
-        stage) -> rotary + cache append -> attention (2) -> o -> gate|up
-        (RMSNorm stage) -> down (SwiGLU stage)."""
+        (every rounding point kept), in 5 launches per layer: qkv (embedding
+        lookup / RMSNorm stage, rotary + cache append epilogue) -> attention
+        -> o -> gate|up (RMSNorm stage, SwiGLU epilogue) -> down."""
         s = self.s
         hb = self.h_buf
         cur = 0
-        ops.index(self.embed, 0, self.tok, out=hb[0].view(1, -1))
         att4 = self.att1.view(1, 1, s.hq, s.hd).transpose(1, 2)
         down = None
         for i, L in enumerate(self.layers):
             kc, vc = self.kcache[i], self.vcache[i]
-            ops.decode_linear(hb[cur], L["wqkv"], "rmsnorm", in_add=down, norm_w=L["ln1"], eps=s.eps,
-                              h_out=hb[1 - cur], out=self.qkv1)
+            src = self.embed if i == 0 else hb[cur]
+            ops.decode_qkv_rope(src, L["wqkv"], s.hq, s.hkv, s.hd, self.inv_freq, self.pos, self.q1, kc[0], vc[0],
+                                x_kind="rmsnorm", row=self.tok if i == 0 else None, in_add=down,
+                                norm_w=L["ln1"], eps=s.eps, h_out=hb[1 - cur])
             cur = 1 - cur
-            ops.rope_kv_append(self.qkv1, s.hq, s.hkv, s.hd, self.inv_freq, self.pos, self.q1, kc, vc)
             ops.sdpa_decode(self.q1, kc, vc, causal=True, kv_len=self.kv_len, out=att4)
             ops.decode_linear(self.att1, L["wo"], "plain", out=self.o1)
-            ops.decode_linear(hb[cur], L["wgu"], "rmsnorm", in_add=self.o1, norm_w=L["ln2"], eps=s.eps,
-                              h_out=hb[1 - cur], out=self.gu1)
+            ops.decode_gate_up(hb[cur], L["wgu"], "rmsnorm", in_add=self.o1, norm_w=L["ln2"], eps=s.eps,
+                               h_out=hb[1 - cur], out=self.a1)
             cur = 1 - cur
-            ops.decode_linear(self.gu1, L["wd"], "swiglu", out=self.down1)
+            ops.decode_linear(self.a1, L["wd"], "plain", out=self.down1)
             down = self.down1
         ops.decode_linear(hb[cur], self.head, "rmsnorm", in_add=down, norm_w=self.norm, eps=s.eps,
                           out=self.logits1)
         probs = ops.softmax(self.logits1.view(1, -1).float())
-        _, idx = ops.topk(probs, 1)
-        self.tok.copy_(idx.view(1))
-        self.pos.add_(1)
-        self.kv_len.add_(1)
+        ops.topk(probs, 1, out=(self.top_v, self.tok.view(1, 1)))
+        self.step_state.add_(1)
         return self.logits1.view(1, -1)
 
     def capture(self):

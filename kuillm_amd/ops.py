@@ -49,9 +49,9 @@ def _dt(dtype) -> int:
 
 
 # ----------------------------------------------------------------- workspace
-# One buffer per (device, kind).  "gemv" holds the split-K arrival counters,
-# which must start at zero: it is zero-filled when allocated and the kernel
-# leaves the counters at zero.  "scratch" is plain partial-result space.
+# One buffer per (device, kind).  "gemv" and "attn" hold split arrival
+# counters (decode GEMM, decode attention), which must start at zero: they
+# are zero-filled when allocated and the kernels leave the counters at zero.  "scratch" is plain partial-result space.
 _WS = {}
 
 
@@ -255,7 +255,7 @@ def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=
     so = _lib.strides3(*out.stride()[:3])
     if not is_causal and (hq // hkv) * l <= decode_max_rows and s > 0:
         ws_bytes = lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, n * hq * l, s, ev)
-        ws = workspace(q.device, ws_bytes)
+        ws = workspace(q.device, ws_bytes, "attn")
         _lib.check("kuiops_sdpa_decode", lib.kuiops_sdpa_decode(
             n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), sq, k.data_ptr(), sk,
             v.data_ptr(), sv, out.data_ptr(), so, _ptr(lse), float(scale), 0, None,
@@ -290,7 +290,7 @@ def sdpa_decode(q, k, v, scale=None, causal=True, return_lse=False, kv_len=None,
         return out, lse
     lib = _lib_handle()
     ws_bytes = lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, n * hq * l, s, ev)
-    ws = workspace(q.device, ws_bytes)
+    ws = workspace(q.device, ws_bytes, "attn")
     _lib.check("kuiops_sdpa_decode", lib.kuiops_sdpa_decode(
         n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), _lib.strides3(*q.stride()[:3]),
         k.data_ptr(), _lib.strides3(*k.stride()[:3]), v.data_ptr(), _lib.strides3(*v.stride()[:3]),
@@ -317,9 +317,11 @@ def softmax(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
     return out
 
 
-def topk(x: torch.Tensor, k: int, dim: int = -1, largest: bool = True, sorted: bool = True):
+def topk(x: torch.Tensor, k: int, dim: int = -1, largest: bool = True, sorted: bool = True, out=None):
     """(values, int64 indices) of the k largest / smallest along ``dim``; ties
-    are ordered by ascending index and NaN is treated as the largest value."""
+    are ordered by ascending index and NaN is treated as the largest value.
+    ``out`` = (values, indices): contiguous buffers of the result's shape
+    (last dim only) written in place."""
     if x.dim() == 0:
         raise _lib.Unsupported("topk", _lib.E_UNSUPPORTED)
     dim = dim % x.dim()
@@ -330,8 +332,16 @@ def topk(x: torch.Tensor, k: int, dim: int = -1, largest: bool = True, sorted: b
     if k < 0 or k > n:
         raise _lib.KuiopsError("topk", _lib.E_INVALID)
     m = xc.numel() // n if n else 0
-    vals = torch.empty((*xc.shape[:-1], k), dtype=x.dtype, device=x.device)
-    inds = torch.empty((*xc.shape[:-1], k), dtype=torch.int64, device=x.device)
+    if out is not None:
+        vals, inds = out
+        shape = (*xc.shape[:-1], k)
+        if moved or vals.numel() != m * k or inds.numel() != m * k or vals.dtype != x.dtype or \
+                inds.dtype != torch.int64 or not vals.is_contiguous() or not inds.is_contiguous():
+            raise _lib.KuiopsError("topk", _lib.E_INVALID)
+        vals, inds = vals.view(shape), inds.view(shape)
+    else:
+        vals = torch.empty((*xc.shape[:-1], k), dtype=x.dtype, device=x.device)
+        inds = torch.empty((*xc.shape[:-1], k), dtype=torch.int64, device=x.device)
     if vals.numel():
         lib = _lib_handle()
         _lib.check("kuiops_topk_lastdim", lib.kuiops_topk_lastdim(
@@ -504,3 +514,61 @@ def decode_linear(x, W, x_kind="plain", in_add=None, norm_w=None, eps=1e-5, h_ou
         N, K, _dt(x.dtype), _X_KIND[x_kind], xf.data_ptr(), _ptr(in_add), _ptr(norm_w), float(eps),
         _ptr(h_out), W.data_ptr(), W.stride(0), _ptr(bias), out.data_ptr(), _stream(x.device)))
     return out
+
+
+def decode_gate_up(x, W, x_kind="rmsnorm", in_add=None, norm_w=None, eps=1e-5, h_out=None, out=None):
+    """Batch-1 gate/up projection with SwiGLU in the epilogue (one launch;
+    see kuiops_decode_gate_up): W = [gate; up] as one nn.Linear weight
+    [2 ffn, K]; returns round(silu(gate(x))) * up(x) rounded, [ffn]."""
+    N2, K = W.shape
+    ffn = N2 // 2
+    xf = x.reshape(-1)
+    if N2 % 2 or x.dtype != W.dtype or W.stride(1) != 1 or not xf.is_contiguous() or xf.numel() != K:
+        raise _lib.KuiopsError("decode_gate_up", _lib.E_INVALID)
+    for t in (in_add, norm_w, h_out):
+        if t is not None and (t.numel() != K or not t.is_contiguous() or t.dtype != x.dtype):
+            raise _lib.KuiopsError("decode_gate_up", _lib.E_INVALID)
+    if out is None:
+        out = torch.empty(ffn, dtype=x.dtype, device=x.device)
+    elif out.numel() != ffn or not out.is_contiguous() or out.dtype != x.dtype:
+        raise _lib.KuiopsError("decode_gate_up", _lib.E_INVALID)
+    lib = _lib_handle()
+    _lib.check("kuiops_decode_gate_up", lib.kuiops_decode_gate_up(
+        ffn, K, _dt(x.dtype), _X_KIND[x_kind], xf.data_ptr(), _ptr(in_add), _ptr(norm_w), float(eps),
+        _ptr(h_out), W.data_ptr(), W.stride(0), out.data_ptr(), _stream(x.device)))
+    return out
+
+
+def decode_qkv_rope(x, W, hq, hkv, hd, inv_freq, pos, q_out, k_cache, v_cache, x_kind="rmsnorm", row=None,
+                    in_add=None, norm_w=None, eps=1e-5, h_out=None):
+    """Batch-1 qkv projection + rotary + KV-cache append (one launch; see
+    kuiops_decode_qkv_rope).  W is the fused [q; k; v] nn.Linear weight
+    [(hq + 2 hkv) hd, K]; x is [K], or a [rows, K] table read at device row
+    ``row`` (int64 [1], an embedding lookup); pos is int32 [1] on the device;
+    q_out [hq * hd]; k_cache / v_cache [hkv, capacity, hd]."""
+    N, K = W.shape
+    if N != (hq + 2 * hkv) * hd or x.dtype != W.dtype or W.stride(1) != 1 or inv_freq.dtype != torch.float32:
+        raise _lib.KuiopsError("decode_qkv_rope", _lib.E_INVALID)
+    if row is None:
+        xf, ld_in, rows = x.reshape(-1), 0, 1
+        if not xf.is_contiguous() or xf.numel() != K:
+            raise _lib.KuiopsError("decode_qkv_rope", _lib.E_INVALID)
+    else:
+        if x.dim() != 2 or x.shape[1] != K or x.stride(1) != 1 or row.dtype != torch.int64 or row.numel() < 1:
+            raise _lib.KuiopsError("decode_qkv_rope", _lib.E_INVALID)
+        xf, ld_in, rows = x, x.stride(0), x.shape[0]
+    if pos.dtype != torch.int32 or q_out.numel() != hq * hd or not q_out.is_contiguous():
+        raise _lib.KuiopsError("decode_qkv_rope", _lib.E_INVALID)
+    for c in (k_cache, v_cache):
+        if c.dim() != 3 or c.shape[0] != hkv or c.shape[2] != hd or c.stride(-1) != 1 or c.dtype != x.dtype:
+            raise _lib.KuiopsError("decode_qkv_rope", _lib.E_INVALID)
+    for t in (in_add, norm_w, h_out):
+        if t is not None and (t.numel() != K or not t.is_contiguous() or t.dtype != x.dtype):
+            raise _lib.KuiopsError("decode_qkv_rope", _lib.E_INVALID)
+    lib = _lib_handle()
+    _lib.check("kuiops_decode_qkv_rope", lib.kuiops_decode_qkv_rope(
+        hq, hkv, hd, K, _dt(x.dtype), _X_KIND[x_kind], xf.data_ptr(), _ptr(row), ld_in, rows, _ptr(in_add),
+        _ptr(norm_w), float(eps), _ptr(h_out), W.data_ptr(), W.stride(0), inv_freq.data_ptr(), pos.data_ptr(),
+        q_out.data_ptr(), k_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), v_cache.data_ptr(),
+        v_cache.stride(0), v_cache.stride(1), k_cache.shape[1], _stream(x.device)))
+    return q_out

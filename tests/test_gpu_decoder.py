@@ -251,3 +251,84 @@ def test_fused_decode_step_matches_unfused(cuda):
             assert float(top2[0] - top2[1]) < 2e-2
         for dst, src in zip((dec.tok, dec.pos, dec.kv_len, dec.kcache, dec.vcache), after):
             dst.copy_(src)
+
+
+@pytest.mark.parametrize("ffn,K", [(5632, 2048), (64, 96), (2816, 4096)])
+def test_decode_gate_up_matches_unfused(cuda, ffn, K):
+    """kuiops_decode_gate_up (SwiGLU epilogue) is bit-identical to the
+    decode projection of the fused [gate; up] weight followed by silu_mul:
+    each output is the same dot product, rounded at the same points."""
+    x = bf((K,), 30).to(cuda)
+    W = bf((2 * ffn, K), 31, 0.02).to(cuda)
+    nw = (1.0 + bf((K,), 32, 0.1)).to(torch.bfloat16).to(cuda)
+    add = bf((K,), 33).to(cuda)
+    h1 = torch.empty(K, dtype=torch.bfloat16, device=cuda)
+    h2 = torch.empty(K, dtype=torch.bfloat16, device=cuda)
+    out = ops.decode_gate_up(x, W, "rmsnorm", in_add=add, norm_w=nw, eps=1e-5, h_out=h1)
+    gu = ops.decode_linear(x, W, "rmsnorm", in_add=add, norm_w=nw, eps=1e-5, h_out=h2)
+    ref = ops.silu_mul(gu.view(1, -1)).view(-1)
+    assert torch.equal(h1, h2)
+    assert torch.equal(out, ref)
+    # and against the oracle chain
+    xin, _ = O.rmsnorm(f(x).reshape(1, -1), f(nw), 1e-5, residual=f(add).reshape(1, -1))
+    g = O.linear(xin, f(W[:ffn]))
+    u = O.linear(xin, f(W[ffn:]))
+    close(f(out), O.silu_mul(np.concatenate([g, u], -1))[0])
+
+
+@pytest.mark.parametrize("hq,hkv,hd,K,pos", [(32, 8, 64, 2048, 517), (4, 2, 128, 256, 3), (8, 8, 64, 512, 0)])
+def test_decode_qkv_rope_matches_unfused(cuda, hq, hkv, hd, K, pos):
+    """kuiops_decode_qkv_rope (rotary + cache-append epilogue, optional
+    embedding-row input) is bit-identical to the decode projection followed
+    by rope_kv_append; a position past the cache stores nothing."""
+    N = (hq + 2 * hkv) * hd
+    cap = 600
+    table = bf((50, K), 40).to(cuda)
+    W = bf((N, K), 41, 0.02).to(cuda)
+    nw = (1.0 + bf((K,), 42, 0.1)).to(torch.bfloat16).to(cuda)
+    inv = torch.from_numpy(O.rope_inv_freq(hd, 10000.0)).to(cuda)
+    row = torch.tensor([17], dtype=torch.int64, device=cuda)
+    p = torch.tensor([pos], dtype=torch.int32, device=cuda)
+    kc1 = torch.zeros(hkv, cap, hd, dtype=torch.bfloat16, device=cuda)
+    vc1, kc2, vc2 = kc1.clone(), kc1.clone(), kc1.clone()
+    q1 = torch.empty(hq * hd, dtype=torch.bfloat16, device=cuda)
+    h1 = torch.empty(K, dtype=torch.bfloat16, device=cuda)
+    ops.decode_qkv_rope(table, W, hq, hkv, hd, inv, p, q1, kc1, vc1, row=row, norm_w=nw, eps=1e-5, h_out=h1)
+    x = table[17].contiguous()
+    qkv = ops.decode_linear(x, W, "rmsnorm", norm_w=nw, eps=1e-5)
+    q2 = torch.empty(1, hq, 1, hd, dtype=torch.bfloat16, device=cuda)
+    ops.rope_kv_append(qkv.view(1, 1, -1), hq, hkv, hd, inv, p, q2, kc2.view(1, hkv, cap, hd),
+                       vc2.view(1, hkv, cap, hd))
+    assert torch.equal(h1, x)
+    assert torch.equal(q1, q2.view(-1))
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert kc1[:, pos].abs().sum() > 0 and vc1[:, pos].abs().sum() > 0
+    # plain input, position past the cache: q only
+    kc3 = torch.zeros_like(kc1)
+    vc3 = torch.zeros_like(vc1)
+    ops.decode_qkv_rope(x, W, hq, hkv, hd, inv, torch.tensor([cap], dtype=torch.int32, device=cuda), q1, kc3, vc3,
+                        norm_w=nw, eps=1e-5)
+    assert not kc3.any() and not vc3.any()
+
+
+def test_sdpa_decode_split_merge_keeps_counters_zero(cuda):
+    """Decode attention merges its splits in the last-arriving work-group:
+    alternating shapes over one workspace stay within tolerance, are
+    bitwise repeatable, and leave the arrival counters at zero."""
+    shapes = [(1, 32, 8, 1, 4096, 128), (2, 8, 8, 1, 700, 64), (1, 32, 8, 1, 64, 64), (1, 4, 1, 2, 300, 128)]
+    firsts = {}
+    for rep in range(2):
+        for (n, hq, hkv, l, s, d) in shapes:
+            q = bf((n, hq, l, d), 50 + s).to(cuda)
+            k = bf((n, hkv, s, d), 51 + s).to(cuda)
+            v = bf((n, hkv, s, d), 52 + s).to(cuda)
+            out, _ = ops.sdpa(q, k, v)                      # few rows per KV head: split-KV decode
+            if rep == 0:
+                ref, _ = O.sdpa(f(q), f(k), f(v))
+                close(f(out), ref)
+                firsts[s] = out
+            else:
+                assert torch.equal(out, firsts[s])
+    torch.cuda.synchronize()
+    ws = ops._WS[(cuda.index or 0, "attn")]
+    assert not ws[:256].any()            # counters: 4 bytes per query row, 256-byte aligned
