@@ -40,6 +40,7 @@ struct GemmArgs {
     int64_t k_per_split;   // multiple of 64
     int splits;
     int tiles_m, tiles_n;
+    int vec_store;         // gemm_dma_kernel: 16-byte row-segment epilogue (ldo, N % 8 == 0, aligned out)
     float *partial;        // split-K workspace [splits][M][N]
 };
 
@@ -510,6 +511,63 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
         }
     }
 
+    if constexpr (sizeof(Tout) == 2 && WM == 2 && TM * 32 == WTM) {
+        if (a.vec_store) {
+            // Staged epilogue: the tile goes out as whole 512-byte row segments
+            // (16 bytes per lane) instead of the accumulator layout's 64-byte
+            // pieces.  Pass p stages rows 32p.. of each wave row (wm) band in
+            // the freed stage buffers (sA0 for wm = 0, sB0 for wm = 1), rows
+            // 528 bytes apart (16 bytes of padding: the two row halves a
+            // store instruction covers fall on different banks).
+            constexpr int RS = BN * 2 + 16;
+            static_assert(32 * RS <= SBYTES, "staging band");
+            char *band = wm == 0 ? sA0 : sB0;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                __syncthreads();                 // stage buffers (or the previous band) free
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int64_t col = n0 + wn * WTN + j * 32 + lrow;
+                    const int64_t row0 = m0 + wm * WTM + i * 32;
+                    float add[16];
+                    if (a.c_kind == KUIOPS_C_ROW) {
+                        const float bv = col < a.N ? a.beta * to_f32(reinterpret_cast<const Tout *>(a.cin)[col]) : 0.f;
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) add[e] = bv;
+                    } else if (a.c_kind == KUIOPS_C_FULL) {
+                        const Tout *c = reinterpret_cast<const Tout *>(a.cin);
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            const int64_t r = row0 + (e >> 2) * 8 + lk * 4 + (e & 3);
+                            add[e] = (r < a.M && col < a.N) ? a.beta * to_f32(c[r * a.ldcin + col]) : 0.f;
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) add[e] = 0.f;
+                    }
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int r = (e >> 2) * 8 + lk * 4 + (e & 3);
+                        *reinterpret_cast<Tout *>(band + r * RS + (wn * WTN + j * 32 + lrow) * 2) =
+                            from_f32<Tout>(a.alpha * acc[i][j][e] + add[e]);
+                    }
+                }
+                __syncthreads();
+                // 2 bands x 32 rows x 32 chunks of 16 bytes over 512 threads
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int idx = rr * NW * 64 + tid;
+                    const int bnd = idx >> 10, row = (idx >> 5) & 31, ch = idx & 31;
+                    const int64_t grow = m0 + bnd * WTM + i * 32 + row;
+                    const int64_t gcol = n0 + ch * 8;
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>((bnd ? sB0 : sA0) + row * RS + ch * 16);
+                    if (grow < a.M && gcol < a.N)
+                        *reinterpret_cast<u32x4 *>(reinterpret_cast<Tout *>(a.out) + grow * a.ldo + gcol) = v;
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -647,6 +705,7 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
     if (splits_req <= 1 && dma_eligible(a, batch, bcol)) {
         a.tiles_m = (int)cdiv(a.M, 256);
         a.tiles_n = (int)cdiv(a.N, 256);
+        a.vec_store = sizeof(Tout) == 2 && a.N % 8 == 0 && a.ldo % 8 == 0 && a.stride_o % 8 == 0 && aligned16(a.out);
         dim3 grid((unsigned)(a.tiles_m * a.tiles_n * batch));
         // 8 waves (2 per SIMD, 128x64 each), BK = 64, two LDS stages: the best of
         // the measured variants (4 waves x 128x128, BK = 32 with four stages,
