@@ -359,6 +359,20 @@ void fa_fwd_kernel(AttnArgs a) {
 
 // ------------------------------------------------------------------ decode
 
+// Sum over aligned groups of N (2, 4, 8 or 16) lanes with DPP lane moves
+// (no LDS round trip): quad swaps, then the half-row and row mirrors.  Each
+// step adds two partial sums that are equal in both lanes of a pair, so every
+// lane of a group ends with the bitwise same total.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+    if (N >= 4) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // lane ^ 2
+    if (N >= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)); // 7 - lane (in 8)
+    if (N >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)); // 15 - lane (in 16)
+    return v;
+}
+
 // Merges online-softmax state (m2, l2, o2) into (m1, l1, o1).
 template <int ND>
 __device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, float m2, float l2, const float *o2) {
@@ -422,15 +436,27 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
         for (int e = 0; e < 8; ++e) o[r][e] = 0.f;
     }
 
-    for (int64_t kb = kbeg + (int64_t)wave * KPW * NB; kb < kend; kb += NWV * KPW * NB) {
+    // The loop runs over the split's keys within the capacity s (known at
+    // launch), not over the device key count: the K / V loads then need not
+    // wait for kv_len.  Keys at or past kend are masked after loading.
+    const int64_t kend_cap = min(a.s, kbeg + a.chunk);
+    for (int64_t kb = kbeg + (int64_t)wave * KPW * NB; kb < kend_cap; kb += NWV * KPW * NB) {
         float s[R][NB];
         u32x4 kr[NB], vr[NB];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int64_t key = kb + j * KPW + kg;
-            const bool ok = key < kend;
-            kr[j] = ok ? *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + dl * 8) : u32x4{0, 0, 0, 0};
-            vr[j] = ok ? *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dl * 8) : u32x4{0, 0, 0, 0};
+            const int64_t key = min(kb + j * KPW + kg, kend_cap - 1);    // in-bounds address
+            kr[j] = *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + dl * 8);
+            vr[j] = *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dl * 8);
+        }
+        // keys past the device count are zeroed (their scores are masked
+        // below; a zero V keeps a NaN in unused cache rows out of the sum)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            if (kb + j * KPW + kg >= kend) {
+                kr[j] = u32x4{0, 0, 0, 0};
+                vr[j] = u32x4{0, 0, 0, 0};
+            }
         }
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
@@ -444,8 +470,7 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
                 float d = 0.f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) d += q[r][e] * kf[e];
-#pragma unroll
-                for (int off = 1; off < LPK; off <<= 1) d += __shfl_xor(d, off, 64);
+                d = group_sum<LPK>(d);
                 s[r][j] = d;
             }
         }
@@ -481,40 +506,18 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
         }
     }
 
-    // Merge the KPW key slots of the wave (lanes with equal dl), fixed butterfly order.
-#pragma unroll
-    for (int off = LPK; off < 64; off <<= 1) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float m2 = __shfl_xor(m[r], off, 64);
-            const float l2 = __shfl_xor(lsum[r], off, 64);
-            float o2[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o2[e] = __shfl_xor(o[r][e], off, 64);
-            // Order the operands by lane so both partners compute the same value.
-            if (lane & off) {
-                float mm = m2, ll = l2, oo[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) oo[e] = o2[e];
-                merge_state<8>(mm, ll, oo, m[r], lsum[r], o[r]);
-                m[r] = mm; lsum[r] = ll;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[r][e] = oo[e];
-            } else {
-                merge_state<8>(m[r], lsum[r], o[r], m2, l2, o2);
-            }
-        }
-    }
-
-    // Merge the waves in wave order through LDS; a single split writes the
-    // normalised output, otherwise the split's state goes to the workspace.
-    __shared__ float sm[NWV][R], sl[NWV][R], so[NWV][R][HD];
-    if (kg == 0) {
+    // Merge the key slots (KPW per wave, lanes with equal dl) of all waves
+    // through LDS, in slot order; a single split writes the normalised
+    // output, otherwise the split's state goes to the workspace.
+    constexpr int NSL = NWV * KPW;
+    __shared__ float sm[NSL][R], sl[NSL][R], so[NSL][R][HD];
+    {
+        const int slot = wave * KPW + kg;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (dl == 0) { sm[wave][r] = m[r]; sl[wave][r] = lsum[r]; }
+            if (dl == 0) { sm[slot][r] = m[r]; sl[slot][r] = lsum[r]; }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) so[wave][r][dl * 8 + e] = o[r][e];
+            for (int e = 0; e < 8; ++e) so[slot][r][dl * 8 + e] = o[r][e];
         }
     }
     __syncthreads();
@@ -522,9 +525,17 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     for (int idx = tid; idx < R * HD; idx += NT) {
         const int r = idx / HD, d = idx % HD;
         if (r >= nrows) continue;
-        float mm = sm[0][r], ll = sl[0][r], oo = so[0][r][d];
-#pragma unroll
-        for (int wv = 1; wv < NWV; ++wv) merge_state<1>(mm, ll, &oo, sm[wv][r], sl[wv][r], &so[wv][r][d]);
+        // max over the slots, then one weight per slot for its sum and output
+        // (independent terms, summed in slot order)
+        float mm = -INFINITY;
+        for (int sv = 0; sv < NSL; ++sv) mm = fmaxf(mm, sm[sv][r]);
+        const float mu = (mm == -INFINITY) ? 0.f : mm;
+        float ll = 0.f, oo = 0.f;
+        for (int sv = 0; sv < NSL; ++sv) {
+            const float wgt = fast_exp2(sm[sv][r] - mu);
+            ll = __builtin_fmaf(sl[sv][r], wgt, ll);
+            oo = __builtin_fmaf(so[sv][r][d], wgt, oo);
+        }
         const int rr = r0 + r;
         const int64_t head = hk * G + rr / a.l, qi = rr % a.l;
         const int64_t grow = (b * a.hq + head) * a.l + qi;
