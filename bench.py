@@ -202,6 +202,11 @@ def extra_workloads(torch, ops, steps, warmup, dev):
     out["sampling_softmax_top1_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
     ms = graph_time_ms(torch, lambda: ops.topk(ops.softmax(logits), 50), steps, warmup, reps=20)
     out["sampling_softmax_top50_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
+    # HF top-p tail (sort, softmax, cumsum, scatter, mask, softmax, multinomial)
+    # over a [1, 32000] row, uniforms resident on the device
+    u = torch.rand(1, 1, device=dev)
+    ms = graph_time_ms(torch, lambda: ops.sample_top_p(logits, 0.9, uniforms=u), steps, warmup, reps=10)
+    out["sampling_top_p_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
     out["llama1b_greedy"] = llama_workload(torch, dev)
     return out
 

@@ -83,7 +83,8 @@ typedef enum kuiops_op {
     KUIOPS_OP_ADDMM = 1,
     KUIOPS_OP_GEMV_SPLITK = 2,
     KUIOPS_OP_SDPA_DECODE = 3,
-    KUIOPS_OP_TOPK = 4
+    KUIOPS_OP_TOPK = 4,
+    KUIOPS_OP_SORT = 5          /* (m, n, 0): rows x row length */
 } kuiops_op;
 
 KUIOPS_API int kuiops_abi_version(void);
@@ -233,6 +234,46 @@ KUIOPS_API int kuiops_topk_lastdim(int64_t m, int64_t n, int64_t k, int dtype,
 KUIOPS_API int kuiops_gather(int rank, const int64_t *inp_shape, const int64_t *idx_shape,
                   int dim, int elem_bytes, const void *inp, const int64_t *idx,
                   void *out, int *err_flag, void *stream);
+
+/* aten.scatter.src: for every x of idx's shape,
+ *   out[x with axis `dim` replaced by idx[x]] = src[x],
+ * out being a contiguous copy of self (the caller clones self into out
+ * first).  src and idx are contiguous with idx_shape, pointwise <= out_shape
+ * except along `dim`; rank 1..8; elem_bytes 1, 2, 4 or 8.  Out-of-range
+ * indices write nothing and set *err_flag.  Where indices repeat along `dim`
+ * the value that lands is unspecified (as in aten).  Replaces the reference's
+ * scatter launcher (ScatterImpl kuipy/kuiops.py:757-807,
+ * kuiops/scatter/wrapper_scatter.cu.j2), which returns the updated clone.   */
+KUIOPS_API int kuiops_scatter(int rank, const int64_t *out_shape, const int64_t *idx_shape, int dim,
+                   int elem_bytes, const void *src, const int64_t *idx, void *out,
+                   int *err_flag, void *stream);
+
+/* Row sort of X[m, n] along the last dim (aten.sort, stable): values and
+ * int64 indices [m, n]; ascending or descending; NaN counts as the largest
+ * value, -0 equals +0, equal values keep index order.  dtype F32, BF16, F16;
+ * n < 2^32.  Workspace: kuiops_query_workspace(KUIOPS_OP_SORT, m, n, 0)
+ * bytes (0 for n <= 2048).  No reference kernel (KERNELS.md row
+ * aten.sort.default): aten.sort is the reference's result.                 */
+KUIOPS_API int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *X, void *values,
+                        int64_t *indices, int descending, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/* Inclusive prefix sum of X[m, n] along the last dim into Y (aten.cumsum):
+ * dtype F32 (fp32 accumulate), F64, I64 (exact).  No reference kernel
+ * (KERNELS.md rows aten.cumsum.default).                                   */
+KUIOPS_API int kuiops_cumsum_lastdim(int64_t m, int64_t n, int dtype, const void *X, void *Y, void *stream);
+
+/* Multinomial sampling with replacement from non-negative weights P[m, n]
+ * (rows need not sum to 1): out[r, s] = the first index i whose running
+ * weight sum (fp64) exceeds uniforms[r, s] * row total (inverse CDF), so a
+ * zero weight is never drawn.  uniforms: device fp32 [m, num_samples] in
+ * [0, 1), the caller's random numbers (the draws are a deterministic
+ * function of them).  A row with a negative, NaN or infinite weight or a
+ * zero total draws index 0 and sets *err_flag (aten raises).  dtype F32,
+ * F64, BF16, F16.  No reference kernel (KERNELS.md row
+ * aten.multinomial.default).                                               */
+KUIOPS_API int kuiops_multinomial(int64_t m, int64_t n, int dtype, const void *probs, int64_t num_samples,
+                       const float *uniforms, int64_t *out, int *err_flag, void *stream);
 
 /* aten.index.Tensor with one int64 index tensor at axis `dim` (every other
  * axis sliced whole): out shape = inp[:dim] + idx_shape + inp[dim+1:], all

@@ -28,7 +28,7 @@ B_ROW, B_COL = 0, 1
 # kuiops_c_kind
 C_NONE, C_FULL, C_ROW = 0, 1, 2
 # kuiops_op
-OP_ADDMM, OP_GEMV_SPLITK, OP_SDPA_DECODE, OP_TOPK = 1, 2, 3, 4
+OP_ADDMM, OP_GEMV_SPLITK, OP_SDPA_DECODE, OP_TOPK, OP_SORT = 1, 2, 3, 4, 5
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -59,6 +59,10 @@ SIGNATURES = {
     "kuiops_softmax_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp]),
     "kuiops_topk_lastdim": (_int, [_i64, _i64, _i64, _int, _vp, _vp, _vp, _int, _int, _vp, _sz, _vp]),
     "kuiops_gather": (_int, [_int, _i64p, _i64p, _int, _int, _vp, _vp, _vp, _vp, _vp]),
+    "kuiops_scatter": (_int, [_int, _i64p, _i64p, _int, _int, _vp, _vp, _vp, _vp, _vp]),
+    "kuiops_sort_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp, _int, _vp, _sz, _vp]),
+    "kuiops_cumsum_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp]),
+    "kuiops_multinomial": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
     "kuiops_index": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "kuiops_rmsnorm": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _flt, _vp, _i64, _vp]),
     "kuiops_silu_mul": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp]),

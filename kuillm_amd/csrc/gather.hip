@@ -1,10 +1,12 @@
-// Index data movement for gfx950: torch.gather and single-tensor aten.index.
+// Index data movement for gfx950: torch.gather, aten.scatter.src and
+// single-tensor aten.index.
 // Pure data movement (bit-exact): each thread copies whole elements, and
 // aten.index copies 16-byte chunks of the trailing (inner) block when the
 // element run allows it.  Indices are consumed as int64 directly (no u32
 // narrowing pass as in the reference's include/kuiops.h:28-36).
 // Semantics: aten.gather (kuipy/kuiops.py:717-754,
-// kuiops/gather/Kuiops.Gather.fst:482-486) and aten.index.Tensor.
+// kuiops/gather/Kuiops.Gather.fst:482-486), aten.scatter.src
+// (kuipy/kuiops.py:757-807) and aten.index.Tensor.
 #include "common.hpp"
 
 namespace kuiops {
@@ -39,6 +41,31 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherShape g, int64_t tota
             out[o] = E(0);
             if (err) *err = 1;
         }
+    }
+}
+
+// out[x with axis dim replaced by idx[x]] = src[x] for every x of idx's shape
+// (src has idx's shape); out already holds a copy of self.  Where indices
+// repeat along dim, which of the writers lands is unspecified, as in aten.
+template <typename E>
+__global__ __launch_bounds__(256) void scatter_kernel(GatherShape g, int64_t total, const E *src,
+                                                      const int64_t *idx, E *out, int *err) {
+    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < total; o += (int64_t)gridDim.x * 256) {
+        int64_t rem = o, off = 0;
+        bool ok = true;
+        const int64_t iv = idx[o];
+        for (int d = g.rank - 1; d >= 0; --d) {
+            const int64_t c = rem % g.idx[d];
+            rem /= g.idx[d];
+            int64_t cc = c;
+            if (d == g.dim) {
+                cc = iv;
+                if (iv < 0 || iv >= g.inp[d]) ok = false;
+            }
+            off += cc * g.inp_stride[d];
+        }
+        if (ok) out[off] = src[o];
+        else if (err) *err = 1;
     }
 }
 
@@ -95,6 +122,35 @@ extern "C" int kuiops_gather(int rank, const int64_t *inp_shape, const int64_t *
         case 2: hipLaunchKernelGGL(gather_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, g, total, (const uint16_t *)inp, idx, (uint16_t *)out, err_flag); break;
         case 4: hipLaunchKernelGGL(gather_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, g, total, (const uint32_t *)inp, idx, (uint32_t *)out, err_flag); break;
         case 8: hipLaunchKernelGGL(gather_kernel<uint64_t>, dim3(grid), dim3(256), 0, s, g, total, (const uint64_t *)inp, idx, (uint64_t *)out, err_flag); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
+extern "C" int kuiops_scatter(int rank, const int64_t *out_shape, const int64_t *idx_shape, int dim, int elem_bytes,
+                              const void *src, const int64_t *idx, void *out, int *err_flag, void *stream) {
+    if (rank < 1 || rank > kMaxRank || !out_shape || !idx_shape || dim < 0 || dim >= rank) return KUIOPS_E_INVALID;
+    GatherShape g{};
+    g.rank = rank; g.dim = dim;
+    int64_t total = 1;
+    for (int d = 0; d < rank; ++d) {
+        g.inp[d] = out_shape[d];
+        g.idx[d] = idx_shape[d];
+        if (g.idx[d] < 0 || g.inp[d] < 0) return KUIOPS_E_INVALID;
+        if (d != dim && g.idx[d] > g.inp[d]) return KUIOPS_E_INVALID;
+        total *= g.idx[d];
+    }
+    if (total == 0) return KUIOPS_OK;
+    if (!src || !idx || !out) return KUIOPS_E_INVALID;
+    int64_t st = 1;
+    for (int d = rank - 1; d >= 0; --d) { g.inp_stride[d] = st; st *= g.inp[d]; }
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = grid_for(total);
+    switch (elem_bytes) {
+        case 1: hipLaunchKernelGGL(scatter_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, g, total, (const uint8_t *)src, idx, (uint8_t *)out, err_flag); break;
+        case 2: hipLaunchKernelGGL(scatter_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, g, total, (const uint16_t *)src, idx, (uint16_t *)out, err_flag); break;
+        case 4: hipLaunchKernelGGL(scatter_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, g, total, (const uint32_t *)src, idx, (uint32_t *)out, err_flag); break;
+        case 8: hipLaunchKernelGGL(scatter_kernel<uint64_t>, dim3(grid), dim3(256), 0, s, g, total, (const uint64_t *)src, idx, (uint64_t *)out, err_flag); break;
         default: return KUIOPS_E_UNSUPPORTED;
     }
     return launch_status();

@@ -1,0 +1,523 @@
+// Sampling-tail ordering and prefix work for gfx950: row sort, row cumsum and
+// inverse-CDF multinomial sampling over the last dim (the top-p path of a
+// sampler: sort -> softmax -> cumsum -> mask -> scatter -> multinomial).
+//
+// sort: every element becomes a unique 64-bit key (an order-preserving 32-bit
+//   image of the value in the requested direction, then the element index),
+//   so sorting keys gives aten's stable sort exactly: ties keep index order,
+//   NaN sorts as the largest value.  Pass 1 bitonic-sorts chunks of 2048 keys
+//   in LDS (one 1024-thread work-group per chunk); pass 2 gives each key its
+//   final rank = its position in its own chunk + the number of smaller keys in
+//   every other chunk (a binary search of each other chunk, staged in LDS in
+//   turn) and writes value and index there.  Values are copied bit-exactly.
+// cumsum: one 1024-thread work-group per row, tiles of 4096 elements (four
+//   consecutive per thread, coalesced), block scans plus a running carry
+//   (fp32 accumulate for fp32, fp64 for fp64, exact for int64).
+// multinomial: with replacement, from caller-supplied uniforms u in [0, 1):
+//   sample = the first index whose running weight sum (fp64) exceeds u * total
+//   (inverse CDF), so zero-weight entries are never drawn.  One work-group per
+//   row.  Rows with a negative, NaN or infinite weight or a zero total set
+//   *err_flag and draw index 0.
+//
+// Semantics: aten.sort / aten.cumsum / aten.multinomial, the reference's
+// fallthrough results (no kuiops kernels exist for them: KERNELS.md rows
+// "aten.sort.default", "aten.cumsum.default", "aten.multinomial.default").
+#include "common.hpp"
+
+namespace kuiops {
+
+constexpr int kSortChunk = 2048;
+constexpr int kSortThreads = 1024;
+constexpr int kSortPer = kSortChunk / kSortThreads;      // keys per thread
+
+// Unsigned image of v whose order is the value order (NaN above +inf; -0 and
+// +0 compare equal, as in aten).
+__device__ __forceinline__ uint32_t value_key(float v) {
+    const uint32_t b = v == 0.f ? 0u : __float_as_uint(v);
+    if (v != v) return 0xffffffffu;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+template <typename T> __device__ __forceinline__ float sort_val(T v) { return to_f32(v); }
+
+// Bitonic sort of kSortChunk keys in LDS, ascending (each thread handles
+// kSortPer / 2 compare-exchanges per stage).
+__device__ __forceinline__ void bitonic_chunk(uint64_t *s) {
+    const int tid = threadIdx.x;
+    for (int size = 2; size <= kSortChunk; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+            for (int h = 0; h < kSortPer / 2; ++h) {
+                const int q = tid + h * kSortThreads;           // pair number
+                const int i = (q / stride) * 2 * stride + (q % stride);
+                const int j = i + stride;
+                const bool up = (i & size) == 0;
+                const uint64_t a = s[i], b = s[j];
+                if ((a > b) == up) { s[i] = b; s[j] = a; }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Pass 1: chunk `blockIdx.x` of row `blockIdx.y` -> sorted keys in ws.  With a
+// single chunk per row the outputs are written directly.
+template <typename T>
+__global__ __launch_bounds__(kSortThreads) void sort_chunk_kernel(int64_t n, int nchunks, const T *X, T *vals,
+                                                                   int64_t *inds, uint64_t *ws, int descending) {
+    __shared__ uint64_t s[kSortChunk];
+    const int tid = threadIdx.x, c = blockIdx.x;
+    const int64_t row = blockIdx.y;
+    const T *x = X + row * n;
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) {
+        const int p = tid + h * kSortThreads;
+        const int64_t i = (int64_t)c * kSortChunk + p;
+        uint64_t key = ~0ull;                        // padding sorts last
+        if (i < n) {
+            uint32_t k = value_key(sort_val<T>(x[i]));
+            if (descending) k = ~k;
+            key = ((uint64_t)k << 32) | (uint32_t)i;
+        }
+        s[p] = key;
+    }
+    __syncthreads();
+    bitonic_chunk(s);
+    if (nchunks == 1) {
+#pragma unroll
+        for (int h = 0; h < kSortPer; ++h) {
+            const int p = tid + h * kSortThreads;
+            if (p < n) {
+                const int64_t src = (int64_t)(uint32_t)s[p];
+                vals[row * n + p] = x[src];
+                inds[row * n + p] = src;
+            }
+        }
+        return;
+    }
+    uint64_t *w = ws + (row * nchunks + c) * kSortChunk;
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) w[tid + h * kSortThreads] = s[tid + h * kSortThreads];
+}
+
+// Pass 2: rank of each key of chunk blockIdx.x among all keys of the row.
+// The other chunks pass through two LDS buffers; the next one is loaded into
+// registers while the current one is searched.
+template <typename T>
+__global__ __launch_bounds__(kSortThreads) void sort_rank_kernel(int64_t n, int nchunks, const T *X, T *vals,
+                                                                  int64_t *inds, const uint64_t *ws) {
+    __shared__ uint64_t s[2][kSortChunk];
+    const int tid = threadIdx.x, c = blockIdx.x;
+    const int64_t row = blockIdx.y;
+    const uint64_t *base = ws + row * nchunks * (int64_t)kSortChunk;
+    uint64_t mine[kSortPer];
+    int64_t rank[kSortPer];
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) {
+        const int p = tid + h * kSortThreads;
+        mine[h] = base[(int64_t)c * kSortChunk + p];
+        rank[h] = p;                                 // keys of its own chunk below it
+    }
+    uint64_t nxt[kSortPer];
+    auto load = [&](int o) {
+#pragma unroll
+        for (int h = 0; h < kSortPer; ++h) nxt[h] = base[(int64_t)o * kSortChunk + tid + h * kSortThreads];
+    };
+    auto other = [&](int k) { return k < c ? k : k + 1; };   // k-th chunk other than c
+    const int nother = nchunks - 1;
+    load(other(0));
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) s[0][tid + h * kSortThreads] = nxt[h];
+    __syncthreads();
+    for (int k = 0; k < nother; ++k) {
+        const int cur = k & 1;
+        if (k + 1 < nother) load(other(k + 1));
+#pragma unroll
+        for (int h = 0; h < kSortPer; ++h) {
+            // number of keys in the chunk below mine[h] (keys are unique;
+            // padding ~0 is above every real key)
+            int lo = 0, hi = kSortChunk;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (s[cur][mid] < mine[h]) lo = mid + 1;
+                else hi = mid;
+            }
+            rank[h] += lo;
+        }
+        if (k + 1 < nother) {
+#pragma unroll
+            for (int h = 0; h < kSortPer; ++h) s[cur ^ 1][tid + h * kSortThreads] = nxt[h];
+        }
+        __syncthreads();
+    }
+    const T *x = X + row * n;
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) {
+        if (mine[h] == ~0ull) continue;              // padding
+        const int64_t src = (int64_t)(uint32_t)mine[h];
+        vals[row * n + rank[h]] = x[src];
+        inds[row * n + rank[h]] = src;
+    }
+}
+
+// ------------------------------------------------------------------ scans
+
+template <typename A>
+__device__ __forceinline__ A wave_incl_scan(A x, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const A y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    return x;
+}
+
+// Exclusive block scan of one value per thread (1024 threads), fixed order;
+// returns the exclusive prefix and the block total.
+template <typename A>
+__device__ __forceinline__ A block_scan_excl(A v, A *s_wave, A &total) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const A incl = wave_incl_scan(v, lane);
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        const A w = lane < kSortThreads / 64 ? s_wave[lane] : A(0);
+        const A ws = wave_incl_scan(w, lane);
+        if (lane < kSortThreads / 64) s_wave[lane] = ws - w;
+        if (lane == kSortThreads / 64 - 1) s_wave[kSortThreads / 64] = ws;
+    }
+    __syncthreads();
+    const A excl = s_wave[wave] + (incl - v);
+    total = s_wave[kSortThreads / 64];
+    __syncthreads();
+    return excl;
+}
+
+// Rows are scanned in tiles of 1024 x 4 consecutive elements: thread t loads
+// elements 4t..4t+3 of the tile (coalesced), scans them in registers, and a
+// block scan of the per-thread sums plus the carry of the earlier tiles
+// offsets them.
+constexpr int kScanVPT = 4;
+constexpr int kScanTile = kSortThreads * kScanVPT;
+
+// Loads the run x[b .. b + RP) into v (zeros past n): 16-byte loads when the
+// run is whole and aligned, else element by element.
+template <typename T, typename A, int RP>
+__device__ __forceinline__ void load_run(const T *x, int64_t b, int64_t n, A *v) {
+    constexpr int E = 16 / sizeof(T);           // elements per 16-byte load
+    if (RP % E == 0 && b + RP <= n && ((reinterpret_cast<uintptr_t>(x + b) & 15) == 0)) {
+#pragma unroll
+        for (int c = 0; c < RP / E; ++c) {
+            const u32x4 raw = *reinterpret_cast<const u32x4 *>(x + b + c * E);
+            typedef T tv __attribute__((ext_vector_type(E)));
+            const tv t = __builtin_bit_cast(tv, raw);
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[c * E + e] = (A)t[e];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < RP; ++j) v[j] = b + j < n ? (A)x[b + j] : A(0);
+    }
+}
+
+// Stores y[b + j] = v[j] + off for the run (16-byte stores when whole and aligned).
+template <typename T, typename A, int RP>
+__device__ __forceinline__ void store_run(T *y, int64_t b, int64_t n, const A *v, A off) {
+    constexpr int E = 16 / sizeof(T);
+    if (RP % E == 0 && b + RP <= n && ((reinterpret_cast<uintptr_t>(y + b) & 15) == 0)) {
+#pragma unroll
+        for (int c = 0; c < RP / E; ++c) {
+            typedef T tv __attribute__((ext_vector_type(E)));
+            tv t;
+#pragma unroll
+            for (int e = 0; e < E; ++e) t[e] = (T)(off + v[c * E + e]);
+            *reinterpret_cast<u32x4 *>(y + b + c * E) = __builtin_bit_cast(u32x4, t);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < RP; ++j)
+            if (b + j < n) y[b + j] = (T)(off + v[j]);
+    }
+}
+
+// Rows of at most 1024 x RP elements: thread t owns the contiguous run
+// [RP t, RP t + RP), loaded at once (every cache line is used whole by its
+// lane), scanned in registers, offset by one block scan.
+template <typename T, int RP>
+__global__ __launch_bounds__(kSortThreads) void cumsum_reg_kernel(int64_t n, const T *X, T *Y) {
+    typedef T A;
+    __shared__ A s_wave[kSortThreads / 64 + 1];
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const T *x = X + row * n;
+    T *y = Y + row * n;
+    const int64_t b = (int64_t)tid * RP;
+    A v[RP];
+    load_run<T, A, RP>(x, b, n, v);
+#pragma unroll
+    for (int j = 1; j < RP; ++j) v[j] += v[j - 1];
+    A total;
+    const A excl = block_scan_excl<A>(v[RP - 1], s_wave, total);
+    store_run<T, A, RP>(y, b, n, v, excl);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSortThreads) void cumsum_kernel(int64_t n, const T *X, T *Y) {
+    typedef T A;                                // fp32 accumulate for fp32, fp64 / int64 exact types
+    __shared__ A s_wave[kSortThreads / 64 + 1];
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const T *x = X + row * n;
+    T *y = Y + row * n;
+    A carry = A(0);
+    for (int64_t t0 = 0; t0 < n; t0 += kScanTile) {
+        const int64_t b = t0 + (int64_t)tid * kScanVPT;
+        A v[kScanVPT];
+#pragma unroll
+        for (int j = 0; j < kScanVPT; ++j) v[j] = b + j < n ? (A)x[b + j] : A(0);
+#pragma unroll
+        for (int j = 1; j < kScanVPT; ++j) v[j] += v[j - 1];
+        A total;
+        const A excl = block_scan_excl<A>(v[kScanVPT - 1], s_wave, total) + carry;
+#pragma unroll
+        for (int j = 0; j < kScanVPT; ++j)
+            if (b + j < n) y[b + j] = (T)(excl + v[j]);
+        carry += total;
+    }
+}
+
+// ------------------------------------------------------------ multinomial
+
+// Pass 1 sums the row (fp64) and validates it; pass 2 walks the tiles with a
+// running fp64 prefix per sample: the first element whose inclusive prefix
+// exceeds u * total (and whose weight is positive) is the draw, found as the
+// smallest such index of the tile (LDS atomic min).
+template <typename T>
+__global__ __launch_bounds__(kSortThreads) void multinomial_kernel(int64_t n, int64_t ns, const T *P, const float *U,
+                                                                    int64_t *out, int *err) {
+    __shared__ double s_wave[kSortThreads / 64 + 1];
+    __shared__ int s_bad;
+    __shared__ unsigned long long s_pick;
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const T *p = P + row * n;
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+    double sum = 0.0;
+    int64_t last_pos = -1;
+    bool bad = false;
+    for (int64_t t0 = 0; t0 < n; t0 += kScanTile) {
+        const int64_t b = t0 + (int64_t)tid * kScanVPT;
+#pragma unroll
+        for (int j = 0; j < kScanVPT; ++j) {
+            if (b + j >= n) continue;
+            const double v = (double)to_f32_or_self(p[b + j]);
+            if (!(v >= 0.0) || v == INFINITY) bad = true;      // negative, NaN, inf
+            if (v > 0.0) last_pos = b + j;
+            sum += v;
+        }
+    }
+    if (bad) s_bad = 1;
+    double total;
+    (void)block_scan_excl<double>(sum, s_wave, total);
+    if (tid == 0) s_pick = 0ull;
+    __syncthreads();
+    // the last positive weight of the row: draws whose target the rounded
+    // prefix sums never exceed (u rounding onto the total) take it
+    if (last_pos >= 0) atomicMax(&s_pick, (unsigned long long)last_pos);
+    __syncthreads();
+    const int64_t row_last = (int64_t)s_pick;
+    const bool row_bad = s_bad != 0 || !(total > 0.0);
+    for (int64_t sidx = 0; sidx < ns; ++sidx) {
+        if (row_bad) {
+            if (tid == 0) {
+                out[row * ns + sidx] = 0;
+                if (err) *err = 1;
+            }
+            continue;
+        }
+        const double target = (double)U[row * ns + sidx] * total;
+        double carry = 0.0;
+        int64_t pick = -1;
+        for (int64_t t0 = 0; t0 < n && pick < 0; t0 += kScanTile) {
+            const int64_t b = t0 + (int64_t)tid * kScanVPT;
+            double v[kScanVPT], c[kScanVPT];
+#pragma unroll
+            for (int j = 0; j < kScanVPT; ++j) v[j] = b + j < n ? (double)to_f32_or_self(p[b + j]) : 0.0;
+            c[0] = v[0];
+#pragma unroll
+            for (int j = 1; j < kScanVPT; ++j) c[j] = c[j - 1] + v[j];
+            double tile_total;
+            const double excl = block_scan_excl<double>(c[kScanVPT - 1], s_wave, tile_total) + carry;
+            if (tid == 0) s_pick = ~0ull;
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < kScanVPT; ++j)
+                if (b + j < n && v[j] > 0.0 && excl + c[j] > target) {
+                    atomicMin(&s_pick, (unsigned long long)(b + j));
+                    break;
+                }
+            __syncthreads();
+            if (s_pick != ~0ull) pick = (int64_t)s_pick;
+            carry += tile_total;
+            __syncthreads();
+        }
+        if (tid == 0) out[row * ns + sidx] = pick >= 0 ? pick : row_last;
+    }
+}
+
+// Rows of at most 1024 x RP weights: thread t holds the contiguous run
+// [RP t, RP t + RP) in registers; one block scan gives each run its fp64
+// prefix, and each draw is the smallest index (LDS atomic min) whose
+// inclusive prefix exceeds u * total with a positive weight.
+template <typename T, int RP>
+__global__ __launch_bounds__(kSortThreads) void multinomial_reg_kernel(int64_t n, int64_t ns, const T *P,
+                                                                        const float *U, int64_t *out, int *err) {
+    __shared__ double s_wave[kSortThreads / 64 + 1];
+    __shared__ int s_bad;
+    __shared__ unsigned long long s_pick, s_last;
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const T *p = P + row * n;
+    const int64_t b = (int64_t)tid * RP;
+    if (tid == 0) { s_bad = 0; s_last = 0ull; }
+    float v[RP];
+    load_run<T, float, RP>(p, b, n, v);
+    double sum = 0.0;
+    int64_t last_pos = -1;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < RP; ++j) {
+        if (!(v[j] >= 0.f) || v[j] == INFINITY) bad = true;     // negative, NaN, inf
+        if (v[j] > 0.f) last_pos = b + j;
+        sum += (double)v[j];
+    }
+    __syncthreads();
+    if (bad) s_bad = 1;
+    if (last_pos >= 0) atomicMax(&s_last, (unsigned long long)last_pos);
+    double total;
+    const double excl = block_scan_excl<double>(sum, s_wave, total);
+    const bool row_bad = s_bad != 0 || !(total > 0.0);
+    const int64_t row_last = (int64_t)s_last;
+    for (int64_t sidx = 0; sidx < ns; ++sidx) {
+        if (row_bad) {
+            if (tid == 0) {
+                out[row * ns + sidx] = 0;
+                if (err) *err = 1;
+            }
+            continue;
+        }
+        const double target = (double)U[row * ns + sidx] * total;
+        if (tid == 0) s_pick = ~0ull;
+        __syncthreads();
+        if (excl + sum > target) {
+            double run = excl;
+#pragma unroll
+            for (int j = 0; j < RP; ++j) {
+                run += (double)v[j];
+                if (run > target && v[j] > 0.f) {
+                    atomicMin(&s_pick, (unsigned long long)(b + j));
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid == 0) out[row * ns + sidx] = s_pick != ~0ull ? (int64_t)s_pick : row_last;
+        __syncthreads();
+    }
+}
+
+static int sort_nchunks(int64_t n) { return (int)cdiv(n, kSortChunk); }
+
+size_t sort_workspace_bytes(int64_t m, int64_t n) {
+    const int nc = sort_nchunks(n);
+    return nc > 1 ? (size_t)m * nc * kSortChunk * sizeof(uint64_t) : 0;
+}
+
+}  // namespace kuiops
+
+using namespace kuiops;
+
+extern "C" int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *X, void *values, int64_t *indices,
+                                   int descending, void *workspace, size_t workspace_bytes, void *stream) {
+    if (m < 0 || n < 0) return KUIOPS_E_INVALID;
+    if (m == 0 || n == 0) return KUIOPS_OK;
+    if (!X || !values || !indices) return KUIOPS_E_INVALID;
+    if (n >= (int64_t)UINT32_MAX || m > 65535) return KUIOPS_E_UNSUPPORTED;
+    const int nc = sort_nchunks(n);
+    if (nc > 65535) return KUIOPS_E_UNSUPPORTED;
+    const size_t need = sort_workspace_bytes(m, n);
+    if (need && (!workspace || workspace_bytes < need)) return KUIOPS_E_WORKSPACE;
+    uint64_t *ws = reinterpret_cast<uint64_t *>(workspace);
+    hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)nc, (unsigned)m);
+#define KUIOPS_SORT(T)                                                                                        \
+    do {                                                                                                      \
+        hipLaunchKernelGGL(sort_chunk_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,        \
+                           (T *)values, indices, ws, descending);                                              \
+        if (nc > 1)                                                                                           \
+            hipLaunchKernelGGL(sort_rank_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,     \
+                               (T *)values, indices, (const uint64_t *)ws);                                   \
+    } while (0)
+    switch (dtype) {
+        case KUIOPS_F32: KUIOPS_SORT(float); break;
+        case KUIOPS_BF16: KUIOPS_SORT(bf16_t); break;
+        case KUIOPS_F16: KUIOPS_SORT(f16_t); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+#undef KUIOPS_SORT
+    return launch_status();
+}
+
+extern "C" int kuiops_cumsum_lastdim(int64_t m, int64_t n, int dtype, const void *X, void *Y, void *stream) {
+    if (m < 0 || n < 0) return KUIOPS_E_INVALID;
+    if (m == 0 || n == 0) return KUIOPS_OK;
+    if (!X || !Y) return KUIOPS_E_INVALID;
+    if (m > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)m);
+#define KUIOPS_CUMSUM(T)                                                                                      \
+    do {                                                                                                      \
+        if (n <= kSortThreads * 8)                                                                            \
+            hipLaunchKernelGGL((cumsum_reg_kernel<T, 8>), grid, dim3(kSortThreads), 0, st, n, (const T *)X, (T *)Y); \
+        else if (n <= kSortThreads * 32)                                                                      \
+            hipLaunchKernelGGL((cumsum_reg_kernel<T, 32>), grid, dim3(kSortThreads), 0, st, n, (const T *)X, (T *)Y); \
+        else                                                                                                  \
+            hipLaunchKernelGGL(cumsum_kernel<T>, grid, dim3(kSortThreads), 0, st, n, (const T *)X, (T *)Y);   \
+    } while (0)
+    switch (dtype) {
+        case KUIOPS_F32: KUIOPS_CUMSUM(float); break;
+        case KUIOPS_F64: KUIOPS_CUMSUM(double); break;
+        case KUIOPS_I64: KUIOPS_CUMSUM(int64_t); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+#undef KUIOPS_CUMSUM
+    return launch_status();
+}
+
+extern "C" int kuiops_multinomial(int64_t m, int64_t n, int dtype, const void *probs, int64_t num_samples,
+                                  const float *uniforms, int64_t *out, int *err_flag, void *stream) {
+    if (m < 0 || n < 0 || num_samples < 0) return KUIOPS_E_INVALID;
+    if (m == 0 || num_samples == 0) return KUIOPS_OK;
+    if (n == 0 || !probs || !uniforms || !out) return KUIOPS_E_INVALID;
+    if (m > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)m);
+    if (n <= kSortThreads * 32 && dtype != KUIOPS_F64) {
+        switch (dtype) {
+            case KUIOPS_F32: hipLaunchKernelGGL((multinomial_reg_kernel<float, 32>), grid, dim3(kSortThreads), 0, st, n, num_samples, (const float *)probs, uniforms, out, err_flag); break;
+            case KUIOPS_BF16: hipLaunchKernelGGL((multinomial_reg_kernel<bf16_t, 32>), grid, dim3(kSortThreads), 0, st, n, num_samples, (const bf16_t *)probs, uniforms, out, err_flag); break;
+            case KUIOPS_F16: hipLaunchKernelGGL((multinomial_reg_kernel<f16_t, 32>), grid, dim3(kSortThreads), 0, st, n, num_samples, (const f16_t *)probs, uniforms, out, err_flag); break;
+            default: return KUIOPS_E_UNSUPPORTED;
+        }
+        return launch_status();
+    }
+    switch (dtype) {
+        case KUIOPS_F32: hipLaunchKernelGGL(multinomial_kernel<float>, grid, dim3(kSortThreads), 0, st, n, num_samples, (const float *)probs, uniforms, out, err_flag); break;
+        case KUIOPS_F64: hipLaunchKernelGGL(multinomial_kernel<double>, grid, dim3(kSortThreads), 0, st, n, num_samples, (const double *)probs, uniforms, out, err_flag); break;
+        case KUIOPS_BF16: hipLaunchKernelGGL(multinomial_kernel<bf16_t>, grid, dim3(kSortThreads), 0, st, n, num_samples, (const bf16_t *)probs, uniforms, out, err_flag); break;
+        case KUIOPS_F16: hipLaunchKernelGGL(multinomial_kernel<f16_t>, grid, dim3(kSortThreads), 0, st, n, num_samples, (const f16_t *)probs, uniforms, out, err_flag); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    return launch_status();
+}

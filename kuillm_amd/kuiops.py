@@ -329,6 +329,131 @@ class GatherImpl(_Family):
             return None
 
 
+class ScatterImpl(_Family):
+    """aten.scatter.src -> kuiops_scatter (reference ScatterImpl
+    kuipy/kuiops.py:757-807: same int64 index, dtype and rank gates; the
+    reference's src-shape == index-shape requirement is relaxed to aten's
+    src >= index).  Returns a scattered copy of self."""
+    tune_key = "SCATTER"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) < 4 or kwargs.get("reduce") is not None:
+            return None
+        Self, dim, Idx, Src = args[0], args[1], args[2], args[3]
+        if not all(isinstance(t, torch.Tensor) for t in (Self, Idx, Src)):
+            return None
+        if not (_is_dev(Self, Idx, Src) and Idx.dtype == torch.int64 and Src.dtype == Self.dtype):
+            return None
+        rank = Self.dim()
+        if rank < 1 or rank > 8 or Idx.dim() != rank or Src.dim() != rank:
+            return None
+        dim = _norm_dim(int(dim), rank)
+        if not (0 <= dim < rank) or Self.element_size() not in (1, 2, 4, 8):
+            return None
+        for d in range(rank):
+            if int(Idx.shape[d]) > int(Src.shape[d]) or (d != dim and int(Idx.shape[d]) > int(Self.shape[d])):
+                return None
+        if Self.numel() > _SIZE_LIMIT:
+            return None
+        return (dim, [Self, Idx, Src])
+
+    def run(self, spec, args, kwargs):
+        dim, (Self, Idx, Src) = spec
+        try:
+            return K.scatter(Self, dim, Idx, Src)
+        except _lib.Unsupported:
+            return None
+
+
+class SortImpl(_Family):
+    """aten.sort (default and stable overloads) -> kuiops_sort_lastdim: a
+    stable sort, a valid result for the unstable overload too.  No reference
+    kernel exists (KERNELS.md row aten.sort.default): aten.sort is the
+    reference's result."""
+    tune_key = "SORT"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if not args or not _is_dev(args[0]):
+            return None
+        X = args[0]
+        if func == aten.sort.stable:
+            dim, desc = kwargs.get("dim", -1), kwargs.get("descending", False)
+        else:
+            dim = args[1] if len(args) > 1 else kwargs.get("dim", -1)
+            desc = args[2] if len(args) > 2 else kwargs.get("descending", False)
+        if X.dtype not in (torch.float32, torch.bfloat16, torch.float16) or X.dim() < 1:
+            return None
+        dim = _norm_dim(int(dim), X.dim())
+        n = int(X.shape[dim])
+        if n >= 2 ** 32 - 1 or (n and X.numel() // n > 65535):
+            return None
+        return (X, dim, bool(desc))
+
+    def run(self, spec, args, kwargs):
+        X, dim, desc = spec
+        try:
+            return K.sort(X, dim, desc)
+        except _lib.Unsupported:
+            return None
+
+
+class CumsumImpl(_Family):
+    """aten.cumsum (same-dtype fp32 / fp64 / int64) -> kuiops_cumsum_lastdim.
+    No reference kernel (KERNELS.md rows aten.cumsum.default)."""
+    tune_key = "CUMSUM"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) < 2 or not _is_dev(args[0]):
+            return None
+        X, dim = args[0], args[1]
+        dt = kwargs.get("dtype")
+        if (dt is not None and dt != X.dtype) or X.dtype not in (torch.float32, torch.float64, torch.int64):
+            return None
+        if X.dim() < 1:
+            return None
+        return (X, _norm_dim(int(dim), X.dim()))
+
+    def run(self, spec, args, kwargs):
+        X, dim = spec
+        try:
+            return K.cumsum(X, dim)
+        except _lib.Unsupported:
+            return None
+
+
+class MultinomialImpl(_Family):
+    """aten.multinomial -> kuiops_multinomial: inverse-CDF draws from uniforms
+    that torch.rand takes from the call's generator (a different random
+    stream than aten's, the same distribution).  With replacement, or one
+    sample per row.  No reference kernel (KERNELS.md row
+    aten.multinomial.default)."""
+    tune_key = "MULTINOMIAL"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) < 2 or not _is_dev(args[0]):
+            return None
+        P, ns = args[0], int(args[1])
+        repl = args[2] if len(args) > 2 else kwargs.get("replacement", False)
+        if P.dtype not in (torch.float32, torch.float64, torch.bfloat16, torch.float16) or P.dim() not in (1, 2):
+            return None
+        if ns < 1 or (not repl and ns > 1) or P.shape[-1] == 0:
+            return None
+        return (P, ns, kwargs.get("generator"))
+
+    def run(self, spec, args, kwargs):
+        P, ns, gen = spec
+        rows = 1 if P.dim() == 1 else P.shape[0]
+        u = torch.rand((rows, ns), generator=gen, device=P.device, dtype=torch.float32)
+        try:
+            return K.multinomial(P, ns, u)
+        except _lib.Unsupported:
+            return None
+
+
 class IndexImpl(_Family):
     """aten.index.Tensor with exactly one int64 index tensor -> kuiops_index
     (embedding-row gathers; no reference kernel, kuiops/index/.gitkeep)."""

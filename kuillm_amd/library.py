@@ -34,6 +34,10 @@ _SCHEMAS = {
     "topk": "topk(Tensor x, int k, int dim=-1, bool largest=True, bool sorted=True) -> (Tensor, Tensor)",
     "gather": "gather(Tensor inp, int dim, Tensor idx) -> Tensor",
     "index": "index(Tensor inp, int dim, Tensor idx) -> Tensor",
+    "scatter": "scatter(Tensor inp, int dim, Tensor idx, Tensor src) -> Tensor",
+    "sort": "sort(Tensor x, int dim=-1, bool descending=False) -> (Tensor, Tensor)",
+    "cumsum": "cumsum(Tensor x, int dim) -> Tensor",
+    "multinomial": "multinomial(Tensor probs, int num_samples, Tensor uniforms) -> Tensor",
 }
 for _s in _SCHEMAS.values():
     _LIB.define(_s)
@@ -79,9 +83,27 @@ def _index(inp, dim, idx):
     return ops.index(inp, dim, idx)
 
 
+def _scatter(inp, dim, idx, src):
+    return ops.scatter(inp, dim, idx, src)
+
+
+def _sort(x, dim=-1, descending=False):
+    v, i = ops.sort(x, dim=dim, descending=descending)
+    return v.contiguous(), i.contiguous()
+
+
+def _cumsum(x, dim):
+    return ops.cumsum(x, dim).contiguous()
+
+
+def _multinomial(probs, num_samples, uniforms):
+    return ops.multinomial(probs, num_samples, replacement=True, uniforms=uniforms)
+
+
 for _name, _fn in (("mm", _mm), ("addmm", _addmm), ("bmm", _bmm), ("softmax", _softmax),
                    ("sdpa", _sdpa), ("sdpa_decode", _sdpa_decode), ("topk", _topk),
-                   ("gather", _gather), ("index", _index)):
+                   ("gather", _gather), ("index", _index), ("scatter", _scatter), ("sort", _sort),
+                   ("cumsum", _cumsum), ("multinomial", _multinomial)):
     _LIB.impl(_name, _fn, "CUDA")
 
 
@@ -139,3 +161,25 @@ def _gather_fake(inp, dim, idx):
 def _index_fake(inp, dim, idx):
     dim = dim % inp.dim()
     return inp.new_empty((*inp.shape[:dim], *idx.shape, *inp.shape[dim + 1:]))
+
+
+@_fake("scatter")
+def _scatter_fake(inp, dim, idx, src):
+    return torch.empty_like(inp, memory_format=torch.contiguous_format)
+
+
+@_fake("sort")
+def _sort_fake(x, dim=-1, descending=False):
+    return (torch.empty_like(x, memory_format=torch.contiguous_format),
+            torch.empty_like(x, dtype=torch.int64, memory_format=torch.contiguous_format))
+
+
+@_fake("cumsum")
+def _cumsum_fake(x, dim):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+@_fake("multinomial")
+def _multinomial_fake(probs, num_samples, uniforms):
+    shape = (num_samples,) if probs.dim() == 1 else (probs.shape[0], num_samples)
+    return probs.new_empty(shape, dtype=torch.int64)

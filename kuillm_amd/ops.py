@@ -409,6 +409,126 @@ def index(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = N
     return out
 
 
+def scatter(inp: torch.Tensor, dim: int, idx: torch.Tensor, src: torch.Tensor, check: bool | None = None):
+    """torch.scatter(inp, dim, idx, src) (aten.scatter.src): a copy of inp with
+    out[x with dim <- idx[x]] = src[x] for every x of idx's shape (src sliced
+    to idx's shape); int64 indices; bit-exact."""
+    if idx.dtype != torch.int64 or idx.dim() != inp.dim() or src.dim() != inp.dim() or src.dtype != inp.dtype \
+            or inp.dim() < 1 or inp.dim() > 8:
+        raise _lib.Unsupported("scatter", _lib.E_UNSUPPORTED)
+    dim = dim % inp.dim()
+    for d in range(inp.dim()):
+        if idx.shape[d] > src.shape[d] or (d != dim and idx.shape[d] > inp.shape[d]):
+            raise _lib.KuiopsError("scatter", _lib.E_INVALID)
+    out = inp.contiguous().clone()
+    if idx.numel() == 0:
+        return out
+    xc = idx.contiguous()
+    sc = src[tuple(slice(0, n) for n in idx.shape)].contiguous()
+    flag = torch.zeros(1, dtype=torch.int32, device=inp.device) if (check or (check is None and CHECK_INDEX)) else None
+    lib = _lib_handle()
+    _lib.check("kuiops_scatter", lib.kuiops_scatter(
+        inp.dim(), _lib.i64_array(out.shape), _lib.i64_array(xc.shape), dim, out.element_size(),
+        sc.data_ptr(), xc.data_ptr(), out.data_ptr(), _ptr(flag), _stream(inp.device)))
+    _raise_if_flagged(flag, "scatter")
+    return out
+
+
+def sort(x: torch.Tensor, dim: int = -1, descending: bool = False):
+    """(values, int64 indices) of a stable sort along ``dim`` (aten.sort with
+    stable=True): NaN counts as the largest value, -0 equals +0, equal values
+    keep index order."""
+    if x.dim() == 0:
+        raise _lib.Unsupported("sort", _lib.E_UNSUPPORTED)
+    dim = dim % x.dim()
+    moved = dim != x.dim() - 1
+    xc = (x.movedim(dim, -1) if moved else x).contiguous()
+    n = xc.shape[-1]
+    m = xc.numel() // n if n else 0
+    vals = torch.empty_like(xc)
+    inds = torch.empty(xc.shape, dtype=torch.int64, device=x.device)
+    if vals.numel():
+        lib = _lib_handle()
+        ws_bytes = lib.kuiops_query_workspace(_lib.OP_SORT, m, n, 0)
+        ws = workspace(x.device, ws_bytes) if ws_bytes else None
+        _lib.check("kuiops_sort_lastdim", lib.kuiops_sort_lastdim(
+            m, n, _dt(x.dtype), xc.data_ptr(), vals.data_ptr(), inds.data_ptr(), 1 if descending else 0,
+            _ptr(ws), ws.numel() if ws is not None else 0, _stream(x.device)))
+    if moved:
+        vals, inds = vals.movedim(-1, dim), inds.movedim(-1, dim)
+    return vals, inds
+
+
+def cumsum(x: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    """Inclusive prefix sum along ``dim`` (aten.cumsum) for fp32 / fp64 / int64."""
+    if x.dim() == 0:
+        raise _lib.Unsupported("cumsum", _lib.E_UNSUPPORTED)
+    dim = dim % x.dim()
+    moved = dim != x.dim() - 1
+    xc = (x.movedim(dim, -1) if moved else x).contiguous()
+    n = xc.shape[-1]
+    m = xc.numel() // n if n else 0
+    out = torch.empty_like(xc)
+    if out.numel():
+        lib = _lib_handle()
+        _lib.check("kuiops_cumsum_lastdim", lib.kuiops_cumsum_lastdim(
+            m, n, _dt(x.dtype), xc.data_ptr(), out.data_ptr(), _stream(x.device)))
+    return out.movedim(-1, dim) if moved else out
+
+
+def multinomial(probs: torch.Tensor, num_samples: int, replacement: bool = False, generator=None,
+                uniforms: torch.Tensor | None = None, check: bool = True) -> torch.Tensor:
+    """Draws from the rows of ``probs`` ([n] or [m, n] non-negative weights) by
+    inverse CDF: sample = first index whose running weight sum exceeds u *
+    total, u from ``uniforms`` ([m, num_samples] fp32 on the device) or
+    torch.rand(generator).  With replacement, or one sample per row (then
+    replacement does not matter), as the sampling tail uses it."""
+    if probs.dim() not in (1, 2) or num_samples < 1:
+        raise _lib.Unsupported("multinomial", _lib.E_UNSUPPORTED)
+    if not replacement and num_samples > 1:
+        raise _lib.Unsupported("multinomial", _lib.E_UNSUPPORTED)
+    p2 = probs.reshape(-1, probs.shape[-1]).contiguous()
+    m, n = p2.shape
+    if uniforms is None:
+        uniforms = torch.rand((m, num_samples), generator=generator, device=probs.device, dtype=torch.float32)
+    u = uniforms.reshape(m, num_samples).to(torch.float32).contiguous()
+    out = torch.empty((m, num_samples), dtype=torch.int64, device=probs.device)
+    flag = torch.zeros(1, dtype=torch.int32, device=probs.device) if check else None
+    lib = _lib_handle()
+    _lib.check("kuiops_multinomial", lib.kuiops_multinomial(
+        m, n, _dt(probs.dtype), p2.data_ptr(), num_samples, u.data_ptr(), out.data_ptr(), _ptr(flag),
+        _stream(probs.device)))
+    if flag is not None and int(flag.item()) != 0:
+        raise RuntimeError("multinomial: probability rows must be finite, non-negative and sum above 0")
+    return out.view(num_samples) if probs.dim() == 1 else out
+
+
+def top_p_filter(scores: torch.Tensor, top_p: float, filter_value: float = -float("inf"),
+                 min_tokens_to_keep: int = 1) -> torch.Tensor:
+    """transformers' TopPLogitsWarper on [m, vocab] scores: ascending sort,
+    softmax, cumsum, drop the sorted prefix whose cumulative probability is
+    <= 1 - top_p (keeping the last min_tokens_to_keep), scatter the mask back
+    and fill the dropped scores with filter_value."""
+    sorted_logits, sorted_idx = sort(scores, -1, descending=False)
+    cum = cumsum(softmax(sorted_logits), -1)
+    remove = cum <= (1 - top_p)
+    remove[..., -min_tokens_to_keep:] = False
+    mask = scatter(remove, 1, sorted_idx, remove)
+    return scores.masked_fill(mask, filter_value)
+
+
+def sample_top_p(scores: torch.Tensor, top_p: float, temperature: float = 1.0, generator=None,
+                 uniforms: torch.Tensor | None = None, check: bool = False) -> torch.Tensor:
+    """One sampled token per row of [m, vocab] fp32 scores: temperature, top-p
+    filter, softmax, multinomial (the HF sampling tail) -> int64 [m].  With
+    check=False nothing synchronises with the host (the call can be recorded
+    in a HIP graph); the softmax rows it samples from are always valid."""
+    if temperature != 1.0:
+        scores = scores / temperature
+    probs = softmax(top_p_filter(scores, top_p))
+    return multinomial(probs, 1, generator=generator, uniforms=uniforms, check=check).view(-1)
+
+
 # ------------------------------------------------------ decoder-layer glue
 
 def _rows(x: torch.Tensor) -> torch.Tensor:

@@ -12,8 +12,8 @@ from __future__ import annotations
 import json
 
 from . import config as C
-from .kuiops import (AddmmImpl, BmmImpl, GatherImpl, IndexImpl, MmImpl, SdpaImpl, SoftmaxImpl,
-                     TopkImpl)
+from .kuiops import (AddmmImpl, BmmImpl, CumsumImpl, GatherImpl, IndexImpl, MmImpl, MultinomialImpl,
+                     ScatterImpl, SdpaImpl, SoftmaxImpl, SortImpl, TopkImpl)
 
 _REGISTRY = None
 _TUNE_PARAMS = None
@@ -42,6 +42,8 @@ def _build_registry(tune_params):
     mm, bmm, addmm = MmImpl(tune_params), BmmImpl(tune_params), AddmmImpl(tune_params)
     softmax, sdpa = SoftmaxImpl(tune_params), SdpaImpl(tune_params)
     topk, gather, index = TopkImpl(tune_params), GatherImpl(tune_params), IndexImpl(tune_params)
+    scatter, sort = ScatterImpl(tune_params), SortImpl(tune_params)
+    cumsum, multinomial = CumsumImpl(tune_params), MultinomialImpl(tune_params)
     return {
         aten.mm.default: mm,
         aten.bmm.default: bmm,
@@ -52,6 +54,11 @@ def _build_registry(tune_params):
         aten.topk.default: topk,
         aten.gather.default: gather,
         aten.index.Tensor: index,
+        aten.scatter.src: scatter,
+        aten.sort.default: sort,
+        aten.sort.stable: sort,
+        aten.cumsum.default: cumsum,
+        aten.multinomial.default: multinomial,
     }
 
 

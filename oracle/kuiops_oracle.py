@@ -17,6 +17,12 @@ therefore restates aten semantics, op by op, citing the reference's family:
   gather             kuipy/kuiops.py:717-754, kuiops/gather/Kuiops.Gather.fst:482-486
   topk / index       no reference kernel (kuiops/topk/.gitkeep,
                      kuiops/index/.gitkeep): aten.topk / aten.index.Tensor
+  scatter            kuipy/kuiops.py:757-807 (aten.scatter.src)
+  sort / cumsum /    no reference kernel (KERNELS.md rows aten.sort.default,
+  multinomial        aten.cumsum.default, aten.multinomial.default): aten
+                     semantics; multinomial as the inverse CDF of given
+                     uniforms; top_p_filter restates transformers'
+                     TopPLogitsWarper (the sampling tail these serve)
   verify metric      kuipy/__init__.py:193-225
   decoder glue       RMSNorm / SwiGLU / rotary + KV cache and a whole
                      Llama-style decoder: the stock
@@ -33,7 +39,9 @@ How each function is pinned (tests/test_oracle.py):
     wrong sign / index or a transposed operand fails (identity and one-hot
     operands, integer-valued products that are exact in fp32, softmax of a
     constant row, attention with constant V, single-key attention, causal
-    row 0, brute-force sorting for topk, explicit loops for gather / index);
+    row 0, brute-force sorting for topk and sort, explicit loops for
+    gather / index / scatter, integer prefix sums, a CDF table lookup for
+    multinomial);
   * the decoder pieces against the transformers Llama modules run on the
     CPU (RMSNorm, rotary embedding, MLP, the whole causal LM), plus closed
     forms (constant-row RMSNorm, position-0 rotation = identity, rotation
@@ -250,6 +258,90 @@ def index(inp, dim: int, idx) -> np.ndarray:
         raise IndexError("index: index out of range")
     idx = np.where(idx < 0, idx + size, idx)
     return np.take(inp, idx, axis=dim)
+
+
+def scatter(inp, dim: int, idx, src) -> np.ndarray:
+    """Copy of inp with out[x with axis `dim` replaced by idx[x]] = src[x] for
+    every x of idx's shape (kuipy/kuiops.py:757-807; aten.scatter.src)."""
+    out = np.array(inp, copy=True)
+    idx = np.asarray(idx, dtype=np.int64)
+    src = np.asarray(src)
+    if np.any(idx < 0) or np.any(idx >= out.shape[dim]):
+        raise IndexError("scatter: index out of range")
+    for x in np.ndindex(*idx.shape):
+        y = list(x)
+        y[dim] = idx[x]
+        out[tuple(y)] = src[x]
+    return out
+
+
+# ------------------------------------------------------- sort / cumsum / sampling
+
+
+def sort(x, descending=False):
+    """(values, int64 indices) of a stable sort of the last axis (aten.sort
+    with stable=True): NaN ranks above every number, -0 equals +0, equal
+    values keep ascending index order."""
+    x = np.asarray(x)
+    flat = x.reshape(-1, x.shape[-1])
+    vals = np.empty_like(flat)
+    inds = np.empty(flat.shape, dtype=np.int64)
+    for r in range(flat.shape[0]):
+        row = flat[r]
+        key, isnan = _order_key(row)
+        key = np.where(key == 0, 0.0, key)          # -0 == +0
+        idx = np.arange(row.shape[0])
+        if descending:
+            order = np.lexsort((idx, -key, ~isnan))
+        else:
+            order = np.lexsort((idx, key, isnan))
+        vals[r] = row[order]
+        inds[r] = order
+    return vals.reshape(x.shape), inds.reshape(x.shape)
+
+
+def cumsum(x, acc="f64") -> np.ndarray:
+    """Inclusive prefix sum of the last axis (aten.cumsum); floating input is
+    accumulated in fp64 (the reference value), integers exactly."""
+    x = np.asarray(x)
+    if np.issubdtype(x.dtype, np.integer):
+        return np.cumsum(x, axis=-1, dtype=np.int64)
+    return np.cumsum(x.astype(np.float64), axis=-1)
+
+
+def multinomial(p, u) -> np.ndarray:
+    """Inverse-CDF draws: for row r and uniform u[r, s], the first index i
+    whose running weight sum (fp64) exceeds u * total, never a zero weight
+    (a u rounding onto the total takes the last positive weight)."""
+    p = np.asarray(p, dtype=np.float64)
+    p2 = p.reshape(-1, p.shape[-1])
+    u2 = np.asarray(u, dtype=np.float64).reshape(p2.shape[0], -1)
+    out = np.empty(u2.shape, dtype=np.int64)
+    for r in range(p2.shape[0]):
+        row = p2[r]
+        if np.any(~np.isfinite(row)) or np.any(row < 0) or not row.sum() > 0:
+            raise ValueError("multinomial: invalid probability row")
+        cdf = np.cumsum(row)
+        pos = np.nonzero(row > 0)[0]
+        for s_ in range(u2.shape[1]):
+            t = u2[r, s_] * cdf[-1]
+            cand = pos[cdf[pos] > t]
+            out[r, s_] = cand[0] if cand.size else pos[-1]
+    return out
+
+
+def top_p_filter(scores, top_p: float, filter_value=-np.inf, min_tokens_to_keep: int = 1) -> np.ndarray:
+    """transformers' TopPLogitsWarper on [m, vocab] fp32 scores: ascending
+    stable sort, softmax, cumulative sum, drop the sorted prefix with
+    cumulative probability <= 1 - top_p (keeping the last min_tokens_to_keep),
+    mask the dropped scores with filter_value."""
+    scores = np.asarray(scores, dtype=np.float32)
+    vals, idx = sort(scores, descending=False)
+    cum = cumsum(softmax(vals), acc="f64")
+    remove = cum <= (1 - top_p)
+    remove[..., -min_tokens_to_keep:] = False
+    mask = scatter(np.zeros_like(remove), 1, idx, remove)
+    return np.where(mask, np.float32(filter_value), scores)
 
 
 # ------------------------------------------------------------ verify metric

@@ -96,6 +96,29 @@ def main():
     g["index_emb"], g["index_ids"], g["index_out"] = Emb.numpy(), ids.numpy(), Emb[ids].numpy()
     T3 = torch.randn(2, 9, 4); ids2 = torch.tensor([[-1, 0, 3], [8, -9, 2]])
     g["index3_inp"], g["index3_ids"], g["index3_out"] = T3.numpy(), ids2.numpy(), T3[:, ids2].numpy()
+    # sort (stable): ties, NaN, -0 / +0, both directions; a row wider than one sort chunk
+    X = torch.randint(-20, 20, (3, 257)).float() / 4.0
+    X[0, 5] = float("nan"); X[2, 100] = float("nan"); X[1, 7] = -0.0; X[1, 9] = 0.0; X[1, 11] = -0.0
+    g["sort_X"] = X.numpy()
+    for tag, desc in (("asc", False), ("desc", True)):
+        v, i = torch.sort(X, descending=desc, stable=True)
+        g[f"sort_{tag}_v"], g[f"sort_{tag}_i"] = v.numpy(), i.numpy()
+    Xw = torch.randn(2, 5000)
+    g["sortw_X"] = Xw.numpy()
+    v, i = torch.sort(Xw, descending=True, stable=True)
+    g["sortw_v"], g["sortw_i"] = v.numpy(), i.numpy()
+    # cumsum: fp32 and int64 rows
+    Xc = torch.randn(4, 3000)
+    g["cumsum_X"], g["cumsum_Y"] = Xc.numpy(), torch.cumsum(Xc, -1).numpy()
+    Xi = torch.randint(-1000, 1000, (3, 777))
+    g["cumsum_i64_X"], g["cumsum_i64_Y"] = Xi.numpy(), torch.cumsum(Xi, -1).numpy()
+    # scatter.src (ScatterImpl, kuipy/kuiops.py:757-807): permutation indices
+    # (no repeated targets) in fp32 and bool, as the top-p filter uses it
+    S = torch.randn(4, 9); perm = torch.stack([torch.randperm(9) for _ in range(4)]); src = torch.randn(4, 9)
+    g["scatter_self"], g["scatter_idx"], g["scatter_src"] = S.numpy(), perm.numpy(), src.numpy()
+    g["scatter_out"] = S.scatter(1, perm, src).numpy()
+    mb = torch.rand(4, 9) > 0.5
+    g["scatter_bool_src"], g["scatter_bool_out"] = mb.numpy(), mb.scatter(1, perm, mb).numpy()
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(g)} arrays)")
 

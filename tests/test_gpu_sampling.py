@@ -160,3 +160,120 @@ def test_index_vs_oracle(cuda, golden):
     assert torch.equal(ops.index(emb, 0, tok), emb[tok])
     with pytest.raises(IndexError):
         ops.index(emb, 0, torch.tensor([32000], device=cuda), check=True)
+
+
+# ------------------------------------------- sort / cumsum / scatter / sampling
+
+def test_sort_golden(cuda, golden):
+    """Stable sort with ties, NaN and signed zeros, both directions; a row
+    wider than one 2048-key chunk (bit-exact values and indices)."""
+    X = torch.from_numpy(golden["sort_X"]).to(cuda)
+    for tag, desc in (("asc", False), ("desc", True)):
+        v, i = ops.sort(X, descending=desc)
+        np.testing.assert_array_equal(v.cpu().numpy(), golden[f"sort_{tag}_v"])
+        np.testing.assert_array_equal(i.cpu().numpy(), golden[f"sort_{tag}_i"])
+    v, i = ops.sort(torch.from_numpy(golden["sortw_X"]).to(cuda), descending=True)
+    np.testing.assert_array_equal(i.cpu().numpy(), golden["sortw_i"])
+    np.testing.assert_array_equal(v.cpu().numpy(), golden["sortw_v"])
+
+
+@pytest.mark.parametrize("m,n,dtype", [(1, 32000, torch.float32), (3, 2048, torch.float32), (2, 2049, torch.float32), (1, 4097, torch.float32),
+                                       (5, 1, torch.float32), (4, 7000, torch.bfloat16), (2, 513, torch.float16),
+                                       (1, 131072, torch.float32)])
+def test_sort_vs_oracle(cuda, m, n, dtype):
+    g = torch.Generator().manual_seed(n)
+    x = (torch.randn(m, n, generator=g) * 4).to(dtype)
+    for desc in (False, True):
+        v, i = ops.sort(x.to(cuda), descending=desc)
+        rv, ri = O.sort(npy(x), descending=desc)
+        np.testing.assert_array_equal(i.cpu().numpy(), ri)
+        assert torch.equal(v.cpu(), x.gather(1, torch.from_numpy(ri)))
+        # against aten's stable sort too
+        tv, ti = torch.sort(x, descending=desc, stable=True)
+        assert torch.equal(i.cpu(), ti)
+
+
+def test_sort_dim_and_empty(cuda):
+    x = torch.randn(6, 5, 4)
+    v, i = ops.sort(x.to(cuda), dim=1)
+    tv, ti = torch.sort(x, dim=1, stable=True)
+    assert torch.equal(v.cpu(), tv) and torch.equal(i.cpu(), ti)
+    v, i = ops.sort(torch.empty(3, 0, device=cuda))
+    assert v.shape == (3, 0) and i.shape == (3, 0)
+
+
+def test_cumsum_golden_and_vs_oracle(cuda, golden):
+    y = ops.cumsum(torch.from_numpy(golden["cumsum_X"]).to(cuda))
+    np.testing.assert_allclose(y.cpu().numpy(), golden["cumsum_Y"], rtol=1e-4, atol=1e-3)
+    yi = ops.cumsum(torch.from_numpy(golden["cumsum_i64_X"]).to(cuda))
+    np.testing.assert_array_equal(yi.cpu().numpy(), golden["cumsum_i64_Y"])
+    x = torch.randn(3, 50000, dtype=torch.float64)
+    np.testing.assert_allclose(ops.cumsum(x.to(cuda)).cpu().numpy(), O.cumsum(x.numpy()), rtol=1e-10, atol=1e-9)
+    x = torch.rand(2, 32000)                  # probabilities: the top-p cumulative sums
+    np.testing.assert_allclose(ops.cumsum(x.to(cuda)).cpu().numpy(), O.cumsum(x.numpy()), rtol=1e-5, atol=1e-3)
+    # along another dim
+    x = torch.randint(-5, 5, (4, 7, 3))
+    assert torch.equal(ops.cumsum(x.to(cuda), dim=1).cpu(), torch.cumsum(x, 1))
+
+
+def test_scatter_golden(cuda, golden):
+    S = torch.from_numpy(golden["scatter_self"]).to(cuda)
+    idx = torch.from_numpy(golden["scatter_idx"]).to(cuda)
+    out = ops.scatter(S, 1, idx, torch.from_numpy(golden["scatter_src"]).to(cuda))
+    np.testing.assert_array_equal(out.cpu().numpy(), golden["scatter_out"])
+    mb = torch.from_numpy(golden["scatter_bool_src"]).to(cuda)
+    np.testing.assert_array_equal(ops.scatter(mb, 1, idx, mb).cpu().numpy(), golden["scatter_bool_out"])
+    # partial index along dim 0, self untouched elsewhere; out-of-range flagged
+    base = torch.arange(12.0).view(3, 4)
+    out = ops.scatter(base.to(cuda), 0, torch.tensor([[2, 0]], device=cuda), torch.tensor([[-1.0, -2.0]], device=cuda))
+    assert torch.equal(out.cpu(), base.scatter(0, torch.tensor([[2, 0]]), torch.tensor([[-1.0, -2.0]])))
+    with pytest.raises(IndexError):
+        ops.scatter(base.to(cuda), 0, torch.tensor([[3, 0]], device=cuda), torch.ones(1, 2, device=cuda), check=True)
+
+
+@pytest.mark.parametrize("m,n,ns", [(1, 32000, 1), (4, 1000, 16), (3, 7, 50), (2, 40000, 3)])
+def test_multinomial_vs_oracle(cuda, m, n, ns):
+    """Draws are the inverse CDF of the given uniforms: equal to the oracle's
+    (fp64 CDF) for the same uniforms; zero weights are never drawn."""
+    g = torch.Generator().manual_seed(m * n)
+    p = torch.rand(m, n, generator=g) * (torch.rand(m, n, generator=g) > 0.3)
+    p[:, 0] = 0.0
+    u = torch.rand(m, ns, generator=g)
+    d = ops.multinomial(p.to(cuda), ns, replacement=True, uniforms=u.to(cuda))
+    np.testing.assert_array_equal(d.cpu().numpy(), O.multinomial(p.numpy(), u.numpy()))
+    assert (p.gather(1, d.cpu()) > 0).all()
+
+
+def test_multinomial_distribution_and_errors(cuda):
+    p = torch.tensor([0.1, 0.0, 0.6, 0.3], device=cuda)
+    d = ops.multinomial(p.expand(20000, 4).contiguous(), 1, generator=torch.Generator(device=cuda).manual_seed(1))
+    freq = torch.bincount(d.view(-1).cpu(), minlength=4).float() / 20000
+    assert freq[1] == 0
+    assert torch.allclose(freq, p.cpu(), atol=0.015)
+    with pytest.raises(RuntimeError):
+        ops.multinomial(torch.tensor([[1.0, -0.5]], device=cuda), 1)
+    with pytest.raises(RuntimeError):
+        ops.multinomial(torch.zeros(2, 5, device=cuda), 1)
+
+
+def test_top_p_filter_and_sampler_vs_oracle(cuda):
+    """The HF top-p tail on the GPU (sort, softmax, cumsum, scatter, masked
+    fill) keeps exactly the oracle's tokens (rows with a cumulative value
+    within 1e-5 of the threshold are skipped: fp32 vs fp64 sums), and the
+    sampler's draws equal the oracle's for the same uniforms."""
+    g = torch.Generator().manual_seed(3)
+    scores = torch.randn(4, 32000, generator=g) * 3
+    for top_p in (0.5, 0.9):
+        got = ops.top_p_filter(scores.to(cuda), top_p).cpu().numpy()
+        exp = O.top_p_filter(scores.numpy(), top_p)
+        vals, _ = O.sort(scores.numpy())
+        cum = O.cumsum(O.softmax(vals))
+        for r in range(4):
+            if np.min(np.abs(cum[r] - (1 - top_p))) < 1e-5:
+                continue
+            np.testing.assert_array_equal(np.isinf(got[r]), np.isinf(exp[r]))
+            np.testing.assert_array_equal(got[r][~np.isinf(got[r])], exp[r][~np.isinf(exp[r])])
+    u = torch.rand(4, 1, generator=g)
+    tok = ops.sample_top_p(scores.to(cuda), 0.9, uniforms=u.to(cuda)).cpu().numpy()
+    probs = O.softmax(O.top_p_filter(scores.numpy(), 0.9))
+    np.testing.assert_array_equal(tok, O.multinomial(probs, u.numpy())[:, 0])

@@ -236,3 +236,89 @@ def test_verify_metric_ignores_nonfinite():
     a[0] = np.nan; b[0] = 0.0
     assert O.rel_frobenius(a, b) == 0.0
     assert O.rel_frobenius(a + 1.0, b) > 0.1
+
+
+# ------------------------------------------- sort / cumsum / scatter / sampling
+
+def test_sort_golden_ties_nan_zero(golden):
+    X = golden["sort_X"]
+    for tag, desc in (("asc", False), ("desc", True)):
+        v, i = O.sort(X, descending=desc)
+        np.testing.assert_array_equal(v, golden[f"sort_{tag}_v"])       # NaN == NaN positionally
+        np.testing.assert_array_equal(i, golden[f"sort_{tag}_i"])
+    v, i = O.sort(golden["sortw_X"], descending=True)
+    np.testing.assert_array_equal(i, golden["sortw_i"])
+    np.testing.assert_array_equal(v, golden["sortw_v"])
+
+
+def test_sort_brute_force_stable():
+    # python's sorted() is stable: ties keep index order; NaN last (ascending)
+    x = rng.integers(-3, 4, size=40).astype(np.float32)
+    x[[3, 17]] = np.nan
+    x[5], x[6] = -0.0, 0.0
+    key = lambda j: (1, 0.0) if np.isnan(x[j]) else (0, float(x[j]) + 0.0)  # noqa: E731
+    order = sorted(range(40), key=key)
+    v, i = O.sort(x)
+    np.testing.assert_array_equal(i, order)
+    rev = sorted(range(40), key=lambda j: (0, 0.0) if np.isnan(x[j]) else (1, -float(x[j]) + 0.0))
+    np.testing.assert_array_equal(O.sort(x, descending=True)[1], rev)
+
+
+def test_cumsum_golden_and_closed_forms(golden):
+    np.testing.assert_allclose(O.cumsum(golden["cumsum_X"]), golden["cumsum_Y"], rtol=1e-4, atol=1e-3)
+    np.testing.assert_array_equal(O.cumsum(golden["cumsum_i64_X"]), golden["cumsum_i64_Y"])
+    np.testing.assert_array_equal(O.cumsum(np.ones((2, 9), np.int64)), np.tile(np.arange(1, 10), (2, 1)))
+    x = rng.standard_normal((3, 50))
+    c = O.cumsum(x)
+    np.testing.assert_allclose(np.diff(c, axis=-1), x[:, 1:], atol=1e-12)   # differences give back x
+    assert np.allclose(c[:, 0], x[:, 0])
+
+
+def test_scatter_golden_and_loop(golden):
+    out = O.scatter(golden["scatter_self"], 1, golden["scatter_idx"], golden["scatter_src"])
+    np.testing.assert_array_equal(out, golden["scatter_out"])
+    outb = O.scatter(golden["scatter_bool_src"], 1, golden["scatter_idx"], golden["scatter_bool_src"])
+    np.testing.assert_array_equal(outb, golden["scatter_bool_out"])
+    # scatter inverts gather along a permutation
+    perm = golden["scatter_idx"]
+    src = golden["scatter_src"]
+    np.testing.assert_array_equal(O.gather(O.scatter(np.zeros_like(src), 1, perm, src), 1, perm), src)
+    # a partial index only touches its targets
+    base = np.arange(12, dtype=np.float32).reshape(3, 4)
+    out = O.scatter(base, 0, np.array([[2, 0]]), np.array([[-1.0, -2.0]], np.float32))
+    assert out[2, 0] == -1 and out[0, 1] == -2 and out[1, 1] == 5 and out[0, 0] == 0
+
+
+def test_multinomial_inverse_cdf_closed_forms():
+    # one-hot rows always draw their hot index
+    p = np.zeros((3, 10)); p[0, 4] = 1; p[1, 0] = 0.3; p[2, 9] = 5
+    u = rng.random((3, 6))
+    np.testing.assert_array_equal(O.multinomial(p, u), np.array([[4] * 6, [0] * 6, [9] * 6]))
+    # uniform weights: u in the middle of bucket k draws k
+    n = 16
+    u = (np.arange(n) + 0.5) / n
+    np.testing.assert_array_equal(O.multinomial(np.ones((1, n)), u.reshape(1, -1))[0], np.arange(n))
+    # zero weights are never drawn, also at the edges u = 0 and u -> 1
+    p = np.array([[0, 0, 2, 0, 1, 0, 0]], dtype=np.float64)
+    d = O.multinomial(p, np.array([[0.0, 0.5, 0.6666, 0.6667, 0.999999999]]))
+    np.testing.assert_array_equal(d[0], [2, 2, 2, 4, 4])
+    # against numpy's searchsorted on the CDF
+    p = rng.random((4, 50)) * (rng.random((4, 50)) > 0.3)
+    u = rng.random((4, 20))
+    cdf = np.cumsum(p, axis=1)
+    exp = np.stack([np.searchsorted(cdf[r], u[r] * cdf[r, -1], side="right") for r in range(4)])
+    np.testing.assert_array_equal(O.multinomial(p, u), exp)
+    with pytest.raises(ValueError):
+        O.multinomial(np.array([[1.0, -1.0]]), np.array([[0.5]]))
+
+
+def test_top_p_filter_matches_transformers():
+    torch = pytest.importorskip("torch")
+    tr = pytest.importorskip("transformers.generation.logits_process")
+    scores = (rng.standard_normal((3, 300)) * 3).astype(np.float32)
+    for top_p in (0.5, 0.9, 0.95):
+        warp = tr.TopPLogitsWarper(top_p=top_p)
+        exp = warp(None, torch.from_numpy(scores.copy())).numpy()
+        got = O.top_p_filter(scores, top_p)
+        np.testing.assert_array_equal(np.isinf(got), np.isinf(exp))
+        np.testing.assert_array_equal(got[~np.isinf(got)], exp[~np.isinf(exp)])

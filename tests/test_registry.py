@@ -157,3 +157,33 @@ def test_strictness_levels(monkeypatch):
     monkeypatch.setattr(kuipy.C, "JIT_STRICTNESS", 2)
     with pytest.raises(kuipy.NotOffloaded):
         kuipy._jit_try(aten.mm.default, (), {})
+
+
+def test_sampling_tail_gates(fake):
+    sc = K.ScatterImpl({})
+    s32 = cu(4, 9, dtype=torch.float32)
+    i64 = cu(4, 9, dtype=torch.int64)
+    assert sc.supported(aten.scatter.src, (s32, 1, i64, s32), {}) is not None
+    assert sc.supported(aten.scatter.src, (cu(4, 9, dtype=torch.bool), 1, i64, cu(4, 9, dtype=torch.bool)), {}) \
+        is not None
+    assert sc.supported(aten.scatter.src, (s32, 1, cu(4, 9, dtype=torch.int32), s32), {}) is None     # int32 index
+    assert sc.supported(aten.scatter.src, (s32, 1, i64, cu(4, 9, dtype=torch.float16)), {}) is None  # src dtype
+    assert sc.supported(aten.scatter.src, (s32, 1, cu(5, 9, dtype=torch.int64), s32), {}) is None    # idx > self
+    so = K.SortImpl({})
+    assert so.supported(aten.sort.default, (cu(4, 32000, dtype=torch.float32),), {}) is not None
+    spec = so.supported(aten.sort.stable, (cu(4, 7),), {"stable": True, "dim": 0, "descending": True})
+    assert spec is not None and spec[1:] == (0, True)
+    assert so.supported(aten.sort.default, (cu(4, 7, dtype=torch.int64),), {}) is None
+    cs = K.CumsumImpl({})
+    assert cs.supported(aten.cumsum.default, (cu(4, 7, dtype=torch.float32), 1), {}) is not None
+    assert cs.supported(aten.cumsum.default, (cu(4, 7, dtype=torch.int64), -1), {}) is not None
+    assert cs.supported(aten.cumsum.default, (cu(4, 7, dtype=torch.float32), 1), {"dtype": torch.float64}) is None
+    assert cs.supported(aten.cumsum.default, (cu(4, 7, dtype=torch.bool), 1), {}) is None
+    mn = K.MultinomialImpl({})
+    assert mn.supported(aten.multinomial.default, (cu(4, 100, dtype=torch.float32), 1), {}) is not None
+    assert mn.supported(aten.multinomial.default, (cu(4, 100, dtype=torch.float32), 5, True), {}) is not None
+    assert mn.supported(aten.multinomial.default, (cu(4, 100, dtype=torch.float32), 5), {}) is None  # no replacement
+    assert mn.supported(aten.multinomial.default, (cu(2, 4, 100, dtype=torch.float32), 1), {}) is None
+    reg = registry.registry()
+    for op in (aten.scatter.src, aten.sort.default, aten.sort.stable, aten.cumsum.default, aten.multinomial.default):
+        assert op in reg
