@@ -59,6 +59,12 @@ def _is_dev(*ts):
     return all(isinstance(t, torch.Tensor) and t.is_cuda for t in ts)
 
 
+def _gemv_max_m(params) -> int:
+    """The tuned decode-GEMM row limit (0 .. 64) of a GEMM family."""
+    m = params.get("gemv_max_m", ops.GEMV_MAX_M) if isinstance(params, dict) else ops.GEMV_MAX_M
+    return max(0, min(ops.GEMV_MAX_M, int(m)))
+
+
 class _Family:
     tune_key = ""
     tune_params = ()
@@ -98,9 +104,21 @@ class MmImpl(_Family):
     def run(self, spec, args, kwargs):
         _, _, _, _, (A, B) = spec
         try:
-            return K.mm(A, B)
+            return K.mm(A, B, _gemv_max_m(self.tune_params))
         except _lib.Unsupported:
             return None
+
+    def tune(self, all_tune_params):
+        """Measure the decode-GEMM / MFMA crossover on this GPU (when there is
+        one) and keep it as ``gemv_max_m`` (the reference's tune() hook,
+        kuipy/kuiops.py:38-40, which only stores the parameters)."""
+        from . import tune as _tune
+        params = dict(self.tune_params) if isinstance(self.tune_params, dict) else {}
+        if torch.cuda.is_available():
+            params["gemv_max_m"] = _tune.sweep_gemv_max_m()
+        self.tune_params = params
+        all_tune_params[self.tune_key] = params
+        return all_tune_params
 
 
 class AddmmImpl(_Family):
@@ -133,7 +151,7 @@ class AddmmImpl(_Family):
     def run(self, spec, args, kwargs):
         _, _, _, _, (Cin, A, B), alpha, beta = spec
         try:
-            return K.addmm(Cin, A, B, beta, alpha)
+            return K.addmm(Cin, A, B, beta, alpha, _gemv_max_m(self.tune_params))
         except _lib.Unsupported:
             return None
 
@@ -244,6 +262,17 @@ class SdpaImpl(_Family):
         if scale is None:
             scale = 1.0 / math.sqrt(e)
         return (func, float(scale), causal, need_lse, [q, k, v])
+
+    def tune(self, all_tune_params):
+        """Measure, on this GPU, up to how many query rows per KV head the
+        split-KV decode kernel beats the flash kernel, as ``decode_max_rows``."""
+        from . import tune as _tune
+        params = dict(self.tune_params) if isinstance(self.tune_params, dict) else {}
+        if torch.cuda.is_available():
+            params["decode_max_rows"] = _tune.sweep_decode_max_rows()
+        self.tune_params = params
+        all_tune_params[self.tune_key] = params
+        return all_tune_params
 
     def run(self, spec, args, kwargs):
         func, scale, causal, need_lse, (q, k, v) = spec

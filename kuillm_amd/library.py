@@ -24,8 +24,8 @@ from . import ops
 _LIB = torch.library.Library("kuiops", "DEF")
 
 _SCHEMAS = {
-    "mm": "mm(Tensor A, Tensor B) -> Tensor",
-    "addmm": "addmm(Tensor C, Tensor A, Tensor B, float beta=1.0, float alpha=1.0) -> Tensor",
+    "mm": "mm(Tensor A, Tensor B, int gemv_max_m=64) -> Tensor",
+    "addmm": "addmm(Tensor C, Tensor A, Tensor B, float beta=1.0, float alpha=1.0, int gemv_max_m=64) -> Tensor",
     "bmm": "bmm(Tensor A, Tensor B) -> Tensor",
     "softmax": "softmax(Tensor x) -> Tensor",
     "sdpa": "sdpa(Tensor q, Tensor k, Tensor v, bool is_causal=False, float? scale=None, "
@@ -45,12 +45,12 @@ for _s in _SCHEMAS.values():
 
 # ------------------------------------------------------------ HIP kernels
 
-def _mm(A, B):
-    return ops.mm(A, B)
+def _mm(A, B, gemv_max_m=64):
+    return ops.mm(A, B, gemv_max_m=gemv_max_m)
 
 
-def _addmm(C, A, B, beta=1.0, alpha=1.0):
-    return ops.addmm(C, A, B, beta=beta, alpha=alpha)
+def _addmm(C, A, B, beta=1.0, alpha=1.0, gemv_max_m=64):
+    return ops.addmm(C, A, B, beta=beta, alpha=alpha, gemv_max_m=gemv_max_m)
 
 
 def _bmm(A, B):
@@ -114,12 +114,12 @@ def _fake(name):
 
 
 @_fake("mm")
-def _mm_fake(A, B):
+def _mm_fake(A, B, gemv_max_m=64):
     return A.new_empty((A.shape[0], B.shape[1]))
 
 
 @_fake("addmm")
-def _addmm_fake(C, A, B, beta=1.0, alpha=1.0):
+def _addmm_fake(C, A, B, beta=1.0, alpha=1.0, gemv_max_m=64):
     return A.new_empty((A.shape[0], B.shape[1]))
 
 

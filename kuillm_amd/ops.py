@@ -104,8 +104,9 @@ def _gemv(x, B, ldb, layout, bias, out):
     return out
 
 
-def mm(A: torch.Tensor, B: torch.Tensor, out_dtype=None) -> torch.Tensor:
-    """A[M, K] @ B[K, N] with fp32 accumulation (aten.mm semantics)."""
+def mm(A: torch.Tensor, B: torch.Tensor, out_dtype=None, gemv_max_m: int | None = None) -> torch.Tensor:
+    """A[M, K] @ B[K, N] with fp32 accumulation (aten.mm semantics); rows
+    M <= gemv_max_m (default GEMV_MAX_M, at most 64) take the decode GEMM."""
     if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0] or A.dtype != B.dtype:
         raise _lib.KuiopsError("mm", _lib.E_INVALID)
     A = _rowmajor(A)
@@ -117,7 +118,7 @@ def mm(A: torch.Tensor, B: torch.Tensor, out_dtype=None) -> torch.Tensor:
         return out
     if K == 0:
         return out.zero_()
-    if A.dtype in HALF and M <= GEMV_MAX_M:
+    if A.dtype in HALF and M <= min(GEMV_MAX_M, GEMV_MAX_M if gemv_max_m is None else gemv_max_m):
         try:
             return _gemv(A, B, ldb, layout, None, out)
         except _lib.Unsupported:
@@ -129,8 +130,10 @@ def mm(A: torch.Tensor, B: torch.Tensor, out_dtype=None) -> torch.Tensor:
     return out
 
 
-def addmm(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, beta=1.0, alpha=1.0) -> torch.Tensor:
-    """beta * C + alpha * (A @ B) with C broadcast to [M, N] (aten.addmm)."""
+def addmm(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, beta=1.0, alpha=1.0,
+          gemv_max_m: int | None = None) -> torch.Tensor:
+    """beta * C + alpha * (A @ B) with C broadcast to [M, N] (aten.addmm); rows
+    M <= gemv_max_m (default GEMV_MAX_M) take the decode GEMM."""
     if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0]:
         raise _lib.KuiopsError("addmm", _lib.E_INVALID)
     if not (A.dtype == B.dtype == C.dtype):
@@ -152,7 +155,8 @@ def addmm(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, beta=1.0, alpha=1.0
     out = torch.empty((M, N), dtype=A.dtype, device=A.device)
     if M == 0 or N == 0:
         return out
-    if (A.dtype in HALF and M <= GEMV_MAX_M and alpha == 1.0 and K > 0
+    if (A.dtype in HALF and M <= min(GEMV_MAX_M, GEMV_MAX_M if gemv_max_m is None else gemv_max_m)
+            and alpha == 1.0 and K > 0
             and (c_kind == _lib.C_NONE or (c_kind == _lib.C_ROW and beta == 1.0))):
         try:
             return _gemv(A, B, ldb, layout, Cin, out)

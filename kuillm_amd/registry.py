@@ -10,6 +10,7 @@ kuipy/registry.py:71,76); ``KUIPY_RE_TUNE=1`` re-runs every family's
 from __future__ import annotations
 
 import json
+from pathlib import Path
 
 from . import config as C
 from .kuiops import (AddmmImpl, BmmImpl, CumsumImpl, GatherImpl, IndexImpl, MmImpl, MultinomialImpl,
@@ -30,7 +31,7 @@ def load_tune_params(path=None) -> dict:
 
 
 def save_tune_params(params: dict, path=None) -> None:
-    p = path or C.TUNE_FILE
+    p = Path(path) if path else C.TUNE_FILE
     p.parent.mkdir(parents=True, exist_ok=True)
     with open(p, "w") as f:
         json.dump(params, f, indent=2, sort_keys=True, default=list)

@@ -187,3 +187,12 @@ def test_sampling_tail_gates(fake):
     reg = registry.registry()
     for op in (aten.scatter.src, aten.sort.default, aten.sort.stable, aten.cumsum.default, aten.multinomial.default):
         assert op in reg
+
+
+def test_tune_crossover_logic():
+    from kuillm_amd import tune
+    assert tune.pick_crossover([1, 2, 4, 8], lambda c: c <= 4) == 4
+    assert tune.pick_crossover([1, 2, 4, 8], lambda c: c != 2) == 1          # first failure stops the sweep
+    assert tune.pick_crossover([1, 2, 4], lambda c: False) == 0
+    assert K._gemv_max_m({"gemv_max_m": 500}) == 64 and K._gemv_max_m({"gemv_max_m": -3}) == 0
+    assert K._gemv_max_m(()) == 64
