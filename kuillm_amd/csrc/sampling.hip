@@ -434,6 +434,84 @@ size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
     return 0;
 }
 
+// ------------------------------------------------- greedy decode tail
+
+// softmax + top-1 of one row per work-group, for rows of at most 32 K
+// elements (the register-cached path of softmax_row_kernel, with the same
+// arithmetic, so the probabilities are bitwise those of the softmax kernel),
+// followed by the arg-max with topk's ordering (NaN largest, lowest index on
+// ties).  Thread 0 writes the index (and the probability), then advances the
+// row's decode state: pos[row] += 1, kv_len[row] += 1 when given.
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int off) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, off, 64), hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSmThreads) void softmax_top1_kernel(int64_t n, const T *X, float *prob, int64_t *index,
+                                                                   int32_t *pos, int32_t *kv_len) {
+    typedef float A;
+    const int64_t row = blockIdx.x;
+    const T *x = X + row * n;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ A s_a[kSmThreads / 64], s_b[kSmThreads / 64];
+    __shared__ unsigned long long s_k[kSmThreads / 64];
+    A v[kSmCache];
+    A m = -(A)INFINITY, s = 0;
+#pragma unroll
+    for (int j = 0; j < kSmCache; ++j) {
+        const int64_t i = tid + (int64_t)kSmThreads * j;
+        v[j] = i < n ? (A)to_f32_or_self(x[i]) : -(A)INFINITY;
+        m = (v[j] > m || v[j] != v[j]) ? v[j] : m;
+    }
+    m = wave_max(m);
+    if (lane == 0) s_a[wave] = m;
+    __syncthreads();
+    m = s_a[0];
+#pragma unroll
+    for (int w = 1; w < kSmThreads / 64; ++w) m = (s_a[w] > m || s_a[w] != s_a[w]) ? s_a[w] : m;
+#pragma unroll
+    for (int j = 0; j < kSmCache; ++j) {
+        v[j] = acc_exp(v[j] - m);
+        if (tid + (int64_t)kSmThreads * j < n) s += v[j];
+    }
+    s = wave_sum(s);
+    if (lane == 0) s_b[wave] = s;
+    __syncthreads();
+    s = 0;
+#pragma unroll
+    for (int w = 0; w < kSmThreads / 64; ++w) s += s_b[w];
+    const A inv = (A)1 / s;
+    // (order key of the probability, complement of the index): the maximum
+    // is the largest probability at the lowest index
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int j = 0; j < kSmCache; ++j) {
+        const int64_t i = tid + (int64_t)kSmThreads * j;
+        if (i >= n) continue;
+        const unsigned long long k = ((unsigned long long)order_key(v[j] * inv, true) << 32) |
+                                     (0xffffffffu - (uint32_t)i);
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = shfl_xor_u64(best, off);
+        best = o > best ? o : best;
+    }
+    if (lane == 0) s_k[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        best = s_k[0];
+#pragma unroll
+        for (int w = 1; w < kSmThreads / 64; ++w) best = s_k[w] > best ? s_k[w] : best;
+        const int64_t i = (int64_t)(0xffffffffu - (uint32_t)best);
+        index[row] = i;
+        if (prob) prob[row] = acc_exp((A)to_f32_or_self(x[i]) - m) * inv;
+        if (pos) pos[row] += 1;
+        if (kv_len) kv_len[row] += 1;
+    }
+}
+
 }  // namespace kuiops
 
 using namespace kuiops;
@@ -478,6 +556,23 @@ extern "C" int kuiops_topk_lastdim(int64_t m, int64_t n, int64_t k, int dtype, c
         case KUIOPS_F32: hipLaunchKernelGGL(topk_kernel<float>, grid, block, 0, st, n, (int)k, (const float *)X, (float *)values, indices, largest); break;
         case KUIOPS_BF16: hipLaunchKernelGGL(topk_kernel<bf16_t>, grid, block, 0, st, n, (int)k, (const bf16_t *)X, (bf16_t *)values, indices, largest); break;
         case KUIOPS_F16: hipLaunchKernelGGL(topk_kernel<f16_t>, grid, block, 0, st, n, (int)k, (const f16_t *)X, (f16_t *)values, indices, largest); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
+extern "C" int kuiops_softmax_top1(int64_t m, int64_t n, int dtype, const void *X, float *prob, int64_t *index,
+                                   int32_t *pos, int32_t *kv_len, void *stream) {
+    if (m < 0 || n < 0) return KUIOPS_E_INVALID;
+    if (m == 0) return KUIOPS_OK;
+    if (n == 0 || !X || !index) return KUIOPS_E_INVALID;
+    if (n > (int64_t)kSmThreads * kSmCache || m > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)m);
+    switch (dtype) {
+        case KUIOPS_F32: hipLaunchKernelGGL(softmax_top1_kernel<float>, grid, dim3(kSmThreads), 0, st, n, (const float *)X, prob, index, pos, kv_len); break;
+        case KUIOPS_BF16: hipLaunchKernelGGL(softmax_top1_kernel<bf16_t>, grid, dim3(kSmThreads), 0, st, n, (const bf16_t *)X, prob, index, pos, kv_len); break;
+        case KUIOPS_F16: hipLaunchKernelGGL(softmax_top1_kernel<f16_t>, grid, dim3(kSmThreads), 0, st, n, (const f16_t *)X, prob, index, pos, kv_len); break;
         default: return KUIOPS_E_UNSUPPORTED;
     }
     return launch_status();

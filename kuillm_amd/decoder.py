@@ -203,7 +203,8 @@ class LlamaDecoder:
 
     def _decode_step_fused(self):
         """One batch-1 decode step, same arithmetic as ``_layers`` + ``_head``
-        (every rounding point kept), in 5 launches per layer: qkv (embedding
+        (every rounding point kept), in 5 launches per layer plus LM head and
+        a fused softmax / top-1 / state-advance launch: qkv (embedding
         lookup / RMSNorm stage, rotary + cache append epilogue) -> attention
         -> o -> gate|up (RMSNorm stage, SwiGLU epilogue) -> down."""
         s = self.s
@@ -227,9 +228,11 @@ class LlamaDecoder:
             down = self.down1
         ops.decode_linear(hb[cur], self.head, "rmsnorm", in_add=down, norm_w=self.norm, eps=s.eps,
                           out=self.logits1)
-        probs = ops.softmax(self.logits1.view(1, -1).float())
-        ops.topk(probs, 1, out=(self.top_v, self.tok.view(1, 1)))
-        self.step_state.add_(1)
+        # softmax(logits.float()) + top-1 and the position / key-count
+        # advance, in one launch (same probabilities and order as the
+        # softmax + topk pair of _head)
+        ops.softmax_top1(self.logits1.view(1, -1), index_out=self.tok, prob_out=self.top_v.view(1),
+                         pos=self.pos, kv_len=self.kv_len)
         return self.logits1.view(1, -1)
 
     def capture(self):

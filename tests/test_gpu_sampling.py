@@ -277,3 +277,35 @@ def test_top_p_filter_and_sampler_vs_oracle(cuda):
     tok = ops.sample_top_p(scores.to(cuda), 0.9, uniforms=u.to(cuda)).cpu().numpy()
     probs = O.softmax(O.top_p_filter(scores.numpy(), 0.9))
     np.testing.assert_array_equal(tok, O.multinomial(probs, u.numpy())[:, 0])
+
+
+@pytest.mark.parametrize("m,n,dtype", [(1, 32000, torch.bfloat16), (3, 32000, torch.float32), (2, 1000, torch.float16),
+                                       (1, 32768, torch.float32), (4, 7, torch.float32)])
+def test_softmax_top1_matches_softmax_topk(cuda, m, n, dtype):
+    """The fused greedy tail returns exactly topk(softmax(x.float()), 1):
+    same probability bits, same index (lowest on ties), and advances the
+    decode state by one."""
+    g = torch.Generator().manual_seed(n + m)
+    x = (torch.randn(m, n, generator=g) * 4).to(dtype).to(cuda)
+    x[0, n // 2] = x[0].max()                      # a tie at the top: the lower index wins
+    pos = torch.arange(m, dtype=torch.int32, device=cuda)
+    kvl = pos + 10
+    prob = torch.empty(m, dtype=torch.float32, device=cuda)
+    _, idx = ops.softmax_top1(x, prob_out=prob, pos=pos, kv_len=kvl)
+    pv, pi = ops.topk(ops.softmax(x.float()), 1)
+    assert torch.equal(idx, pi.view(-1))
+    if n > 1024:
+        assert torch.equal(prob, pv.view(-1))
+    else:   # rows of <= 1024 take the one-wave softmax kernel (another summation order)
+        torch.testing.assert_close(prob, pv.view(-1), rtol=1e-6, atol=0)
+    tv, ti = torch.topk(torch.softmax(x.float(), -1), 1)
+    assert torch.equal(idx.cpu(), ti.view(-1).cpu())
+    assert torch.equal(pos.cpu(), torch.arange(m, dtype=torch.int32) + 1)
+    assert torch.equal(kvl.cpu(), torch.arange(m, dtype=torch.int32) + 11)
+
+
+def test_softmax_top1_nan_row(cuda):
+    x = torch.tensor([[0.5, float("nan"), 2.0, 2.0]], device=cuda)
+    _, idx = ops.softmax_top1(x)
+    _, ref = ops.topk(ops.softmax(x), 1)
+    assert torch.equal(idx, ref.view(-1))
