@@ -229,14 +229,17 @@ KUIOPS_API int kuiops_topk_lastdim(int64_t m, int64_t n, int64_t k, int dtype,
  * probability prob[row] -- with the probabilities bitwise equal to
  * kuiops_softmax_lastdim's on the fp32 row when n > 1024 (shorter rows take
  * its one-wave kernel, which sums in another order) and topk's ordering (NaN largest,
- * lowest index on ties); then pos[row] += 1 and kv_len[row] += 1 when those
- * device int32 arrays are given (a graph-replayed decode step advancing its
- * own position and key count).  dtype F32, BF16, F16 (converted exactly to
+ * lowest index on ties); then, when given, history[row * hist_len + pos[row]]
+ * = index (positions outside [0, hist_len) are skipped), pos[row] += 1 and
+ * kv_len[row] += 1 (device int32 arrays: a graph-replayed decode step
+ * recording its token and advancing its own position and key count).
+ * history needs pos.  dtype F32, BF16, F16 (converted exactly to
  * fp32 first).  No reference counterpart: it fuses the _softmax launch
  * (kuiops/softmax/wrapper_softmax.cu.j2:14-16), aten.topk(k = 1) and the
  * position updates of one greedy step.                                       */
 KUIOPS_API int kuiops_softmax_top1(int64_t m, int64_t n, int dtype, const void *X, float *prob,
-                        int64_t *index, int32_t *pos, int32_t *kv_len, void *stream);
+                        int64_t *index, int32_t *pos, int32_t *kv_len, int64_t *history,
+                        int64_t hist_len, void *stream);
 
 /* out[x] = inp[x with axis `dim` replaced by idx[x]]  (torch.gather).
  * Contiguous row-major tensors of rank 1..8; idx int64 with idx_shape

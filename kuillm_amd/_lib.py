@@ -58,7 +58,7 @@ SIGNATURES = {
                                   _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp, _vp, _sz, _vp]),
     "kuiops_softmax_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp]),
     "kuiops_topk_lastdim": (_int, [_i64, _i64, _i64, _int, _vp, _vp, _vp, _int, _int, _vp, _sz, _vp]),
-    "kuiops_softmax_top1": (_int, [_i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "kuiops_softmax_top1": (_int, [_i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "kuiops_gather": (_int, [_int, _i64p, _i64p, _int, _int, _vp, _vp, _vp, _vp, _vp]),
     "kuiops_scatter": (_int, [_int, _i64p, _i64p, _int, _int, _vp, _vp, _vp, _vp, _vp]),
     "kuiops_sort_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp, _int, _vp, _sz, _vp]),

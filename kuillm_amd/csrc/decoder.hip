@@ -328,8 +328,8 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
         }
         accs[g] = wave_sum(acc);
     }
-    if (lane != 0) return;
     if constexpr (OK == kOutPlain) {
+        if (lane != 0) return;
 #pragma unroll
         for (int g = 0; g < RG; ++g) {
             const int64_t r = r0 + g;
@@ -340,10 +340,12 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
             }
         }
     } else {
+        // every lane holds every row's sum (wave_sum is a butterfly): lane
+        // g / 2 finishes pair g / 2, so the pairs' epilogues run side by side
 #pragma unroll
         for (int g = 0; g < RG; g += 2) {
             const int64_t r = r0 + g;                    // even: rows r, r + 1 form pair r / 2
-            if (r + 1 >= r1) continue;
+            if (lane != g / 2 || r + 1 >= r1) continue;
             const int64_t p = r >> 1;
             const float x1 = rnd<T>(accs[g]), x2 = rnd<T>(accs[g + 1]);
             if constexpr (OK == kOutSwiGlu) {

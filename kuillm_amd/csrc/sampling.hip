@@ -440,8 +440,9 @@ size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
 // elements (the register-cached path of softmax_row_kernel, with the same
 // arithmetic, so the probabilities are bitwise those of the softmax kernel),
 // followed by the arg-max with topk's ordering (NaN largest, lowest index on
-// ties).  Thread 0 writes the index (and the probability), then advances the
-// row's decode state: pos[row] += 1, kv_len[row] += 1 when given.
+// ties).  Thread 0 writes the index (and the probability), records it at
+// history[row][pos[row]] when given, then advances the row's decode state:
+// pos[row] += 1, kv_len[row] += 1 when given.
 __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int off) {
     const uint32_t lo = __shfl_xor((uint32_t)v, off, 64), hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
     return ((unsigned long long)hi << 32) | lo;
@@ -449,7 +450,8 @@ __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v,
 
 template <typename T>
 __global__ __launch_bounds__(kSmThreads) void softmax_top1_kernel(int64_t n, const T *X, float *prob, int64_t *index,
-                                                                   int32_t *pos, int32_t *kv_len) {
+                                                                   int32_t *pos, int32_t *kv_len, int64_t *history,
+                                                                   int64_t hist_len) {
     typedef float A;
     const int64_t row = blockIdx.x;
     const T *x = X + row * n;
@@ -507,6 +509,7 @@ __global__ __launch_bounds__(kSmThreads) void softmax_top1_kernel(int64_t n, con
         const int64_t i = (int64_t)(0xffffffffu - (uint32_t)best);
         index[row] = i;
         if (prob) prob[row] = acc_exp((A)to_f32_or_self(x[i]) - m) * inv;
+        if (history && pos && pos[row] >= 0 && pos[row] < hist_len) history[row * hist_len + pos[row]] = i;
         if (pos) pos[row] += 1;
         if (kv_len) kv_len[row] += 1;
     }
@@ -562,7 +565,8 @@ extern "C" int kuiops_topk_lastdim(int64_t m, int64_t n, int64_t k, int dtype, c
 }
 
 extern "C" int kuiops_softmax_top1(int64_t m, int64_t n, int dtype, const void *X, float *prob, int64_t *index,
-                                   int32_t *pos, int32_t *kv_len, void *stream) {
+                                   int32_t *pos, int32_t *kv_len, int64_t *history, int64_t hist_len, void *stream) {
+    if (history && (hist_len <= 0 || !pos)) return KUIOPS_E_INVALID;
     if (m < 0 || n < 0) return KUIOPS_E_INVALID;
     if (m == 0) return KUIOPS_OK;
     if (n == 0 || !X || !index) return KUIOPS_E_INVALID;
@@ -570,9 +574,9 @@ extern "C" int kuiops_softmax_top1(int64_t m, int64_t n, int dtype, const void *
     hipStream_t st = as_stream(stream);
     const dim3 grid((unsigned)m);
     switch (dtype) {
-        case KUIOPS_F32: hipLaunchKernelGGL(softmax_top1_kernel<float>, grid, dim3(kSmThreads), 0, st, n, (const float *)X, prob, index, pos, kv_len); break;
-        case KUIOPS_BF16: hipLaunchKernelGGL(softmax_top1_kernel<bf16_t>, grid, dim3(kSmThreads), 0, st, n, (const bf16_t *)X, prob, index, pos, kv_len); break;
-        case KUIOPS_F16: hipLaunchKernelGGL(softmax_top1_kernel<f16_t>, grid, dim3(kSmThreads), 0, st, n, (const f16_t *)X, prob, index, pos, kv_len); break;
+        case KUIOPS_F32: hipLaunchKernelGGL(softmax_top1_kernel<float>, grid, dim3(kSmThreads), 0, st, n, (const float *)X, prob, index, pos, kv_len, history, hist_len); break;
+        case KUIOPS_BF16: hipLaunchKernelGGL(softmax_top1_kernel<bf16_t>, grid, dim3(kSmThreads), 0, st, n, (const bf16_t *)X, prob, index, pos, kv_len, history, hist_len); break;
+        case KUIOPS_F16: hipLaunchKernelGGL(softmax_top1_kernel<f16_t>, grid, dim3(kSmThreads), 0, st, n, (const f16_t *)X, prob, index, pos, kv_len, history, hist_len); break;
         default: return KUIOPS_E_UNSUPPORTED;
     }
     return launch_status();

@@ -129,6 +129,9 @@ class LlamaDecoder:
         self.down1 = torch.empty(s.d, **bf)
         self.logits1 = torch.empty(s.vocab, **bf)
         self.top_v = torch.empty(1, 1, dtype=torch.float32, device=dev)
+        # token chosen at each position (written by the step itself, so a
+        # replayed step needs no copy out)
+        self.history = torch.zeros(1, self.cap + 1, dtype=torch.int64, device=dev)
 
     @classmethod
     def from_hf(cls, model, capacity: int, batch: int = 1, device="cuda"):
@@ -232,7 +235,7 @@ class LlamaDecoder:
         # advance, in one launch (same probabilities and order as the
         # softmax + topk pair of _head)
         ops.softmax_top1(self.logits1.view(1, -1), index_out=self.tok, prob_out=self.top_v.view(1),
-                         pos=self.pos, kv_len=self.kv_len)
+                         pos=self.pos, kv_len=self.kv_len, history=self.history)
         return self.logits1.view(1, -1)
 
     def capture(self):
@@ -267,12 +270,17 @@ class LlamaDecoder:
         if use_graph and self.graph is None:
             self.capture()
         out[0].copy_(self.tok)
+        p0 = int(self.pos[0])
         for i in range(1, n_new):
             if use_graph:
                 self.graph.replay()
             else:
                 self._decode_step()
-            out[i].copy_(self.tok)
+            if not self.fused:
+                out[i].copy_(self.tok)
+        if self.fused and n_new > 1:
+            # the fused step recorded the token of position p at history[p]
+            out[1:].copy_(self.history[:, p0:p0 + n_new - 1].t())
         return out.t()
 
     def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True) -> torch.Tensor:

@@ -357,11 +357,13 @@ def topk(x: torch.Tensor, k: int, dim: int = -1, largest: bool = True, sorted: b
 
 
 def softmax_top1(x: torch.Tensor, index_out: torch.Tensor | None = None, prob_out: torch.Tensor | None = None,
-                 pos: torch.Tensor | None = None, kv_len: torch.Tensor | None = None):
+                 pos: torch.Tensor | None = None, kv_len: torch.Tensor | None = None,
+                 history: torch.Tensor | None = None):
     """Greedy tail in one launch: (probability, int64 index) of the top-1 of
     softmax(x.float()) per row of x [m, n] (n <= 32768), equal to
-    ``topk(softmax(x.float()), 1)``; optionally advances the device int32
-    ``pos`` / ``kv_len`` [m] by one (see kuiops_softmax_top1)."""
+    ``topk(softmax(x.float()), 1)``; optionally records the index in
+    ``history`` [m, L] (int64) at column pos[row] and advances the device
+    int32 ``pos`` / ``kv_len`` [m] by one (see kuiops_softmax_top1)."""
     x2 = x.reshape(-1, x.shape[-1]).contiguous()
     m, n = x2.shape
     if index_out is None:
@@ -374,10 +376,13 @@ def softmax_top1(x: torch.Tensor, index_out: torch.Tensor | None = None, prob_ou
     if (prob_out is not None and prob_out.dtype != torch.float32) or \
             any(t is not None and t.dtype != torch.int32 for t in (pos, kv_len)):
         raise _lib.KuiopsError("softmax_top1", _lib.E_INVALID)
+    if history is not None and (pos is None or history.dim() != 2 or history.shape[0] != m
+                                or history.dtype != torch.int64 or not history.is_contiguous()):
+        raise _lib.KuiopsError("softmax_top1", _lib.E_INVALID)
     lib = _lib_handle()
     _lib.check("kuiops_softmax_top1", lib.kuiops_softmax_top1(
         m, n, _dt(x.dtype), x2.data_ptr(), _ptr(prob_out), index_out.data_ptr(), _ptr(pos), _ptr(kv_len),
-        _stream(x.device)))
+        _ptr(history), history.shape[1] if history is not None else 0, _stream(x.device)))
     return prob_out, index_out
 
 
