@@ -39,6 +39,7 @@ struct AttnArgs {
     float scale_log2;   // softmax scale * log2(e)
     int causal;
     int nqb;            // query blocks per (batch, head)
+    int pair;           // causal prefill: a work-group runs query blocks p and nqb-1-p
     // decode
     int splits;
     int64_t chunk;      // keys per split
@@ -114,9 +115,12 @@ void fa_fwd_kernel(AttnArgs a) {
     const int nblocks = gridDim.x, bid = blockIdx.x;
     int w = bid;
     if ((nblocks & 7) == 0) w = (bid & 7) * (nblocks >> 3) + (bid >> 3);
-    const int hb = w / a.nqb;
-    int qb = w - hb * a.nqb;
-    if (CAUSAL) qb = a.nqb - 1 - qb;
+    // Work units per (batch, head): one query block each, or (causal, paired)
+    // the pair of blocks p and nqb - 1 - p, which together cost nqb + 1 key
+    // blocks whatever p is, so every work-group has the same work.
+    const int upb = a.pair ? a.nqb >> 1 : a.nqb;
+    const int hb = w / upb;
+    const int unit = w - hb * upb;
     const int64_t b = hb / a.hq, h = hb - b * a.hq;
     const int64_t hk = h / (a.hq / a.hkv);
 
@@ -129,6 +133,10 @@ void fa_fwd_kernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t rsK = make_rsrc(Kb, a.s > 0 ? kbytes : 0);
     const __amdgpu_buffer_rsrc_t rsV = make_rsrc(Vb, a.s > 0 ? vbytes : 0);
 
+    for (int pass = 0; pass < (a.pair ? 2 : 1); ++pass) {
+    // heaviest block first: the last (causal) block of the pair, or of the head
+    const int qb = CAUSAL ? (pass == 0 ? a.nqb - 1 - unit : unit) : unit;
+    if (pass) __syncthreads();      // every wave is done with the LDS slots
     const int64_t q0 = (int64_t)qb * BQ;
     const int64_t qw = q0 + wave * 32;
     const int64_t myq = qw + lq;
@@ -289,6 +297,9 @@ void fa_fwd_kernel(AttnArgs a) {
         };
 #pragma unroll
         for (int i = 0; i < VPF - 1; ++i) load_v(i, vr[i]);
+        // The MFMA-only phase runs at raised wave priority, so the other
+        // wave of the SIMD fills the gaps with its VALU work.
+        __builtin_amdgcn_s_setprio(1);
         frag pf;
 #pragma unroll
         for (int idx = 0; idx < NV; ++idx) {
@@ -303,6 +314,7 @@ void fa_fwd_kernel(AttnArgs a) {
             if (idx + VPF - 1 < NV) load_v(idx + VPF - 1, vr[(idx + VPF - 1) % VPF]);
             o[dt] = Mfma<T>::m32(vr[idx % VPF], pf, o[dt]);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     // Software pipeline over KV blocks: step j runs the softmax of block j
@@ -355,6 +367,7 @@ void fa_fwd_kernel(AttnArgs a) {
         if (a.lse && lh == 0)
             a.lse[(b * a.hq + h) * a.l + myq] = l_tot > 0.f ? (m_used + __log2f(l_tot)) * kLn2 : -INFINITY;
     }
+    }   // pass
 }
 
 // ------------------------------------------------------------------ decode
@@ -766,11 +779,19 @@ size_t decode_workspace_bytes(int64_t rows, int64_t kv_len, int64_t ev) {
 
 template <typename T, int HD>
 static int launch_fwd(AttnArgs a, hipStream_t st) {
-    // 4 waves, 128 queries per work-group; 8-wave (256-query) blocks halve
-    // the L2 -> LDS traffic but measured no faster (causal: slower, from the
-    // coarser load balance).
+    // 4 waves, 128 queries per work-group, two work-groups per CU.  (256
+    // queries per work-group as 4 waves of 64 would halve the LDS reads per
+    // MFMA, but needs more than 256 registers per wave; the compiler then
+    // keeps the scores in accumulation registers and copies them for every
+    // softmax step: 1.5x slower, measured.)
     a.nqb = (int)cdiv(a.l, 128);
-    const int64_t blocks = (int64_t)a.nqb * a.n * a.hq;
+    // Causal: pair the query blocks of a head (equal work per work-group)
+    // when the pairs still fill both work-group slots of every CU (causal
+    // S=4096, 32 heads: 512 pairs).  Fewer pairs would leave CUs half idle;
+    // then the blocks run singly, heaviest first.
+    const int64_t singles = (int64_t)a.nqb * a.n * a.hq;
+    a.pair = (a.causal && (a.nqb & 1) == 0 && singles / 2 >= 2 * (int64_t)num_cus()) ? 1 : 0;
+    const int64_t blocks = a.pair ? singles / 2 : singles;
     if (blocks > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
