@@ -398,16 +398,23 @@ __device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, flo
     m1 = M;
 }
 
-template <typename T, int HD, int R, int NWV = 4>
+template <typename T, int HD, int R, int NWV = 4, int NB = 4>
 __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
+    // NB: keys per lane group per step; all K / V loads of a step are issued
+    // before any is used, so a step is one memory round trip.
     constexpr int NT = NWV * 64;
     constexpr int LPK = HD / 8;       // lanes per key (8 d values each)
     constexpr int KPW = 64 / LPK;     // keys per wave step
-    constexpr int NB = 4;             // keys per lane group per step
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kg = lane / LPK, dl = lane % LPK;
     const int split = blockIdx.x;
-    const int hk = blockIdx.y / a.row_groups, rg = blockIdx.y % a.row_groups;
+    // One split, many row groups: work-groups are dispatched round-robin
+    // over the 8 XCDs, so consecutive (KV head, row group) units are spread
+    // to give all row groups of a KV head one XCD (its K / V then come from
+    // that XCD's L2 after the first read).
+    int unit = blockIdx.y;
+    if (gridDim.x == 1 && (gridDim.y & 7) == 0) unit = (unit & 7) * (gridDim.y >> 3) + (unit >> 3);
+    const int hk = unit / a.row_groups, rg = unit % a.row_groups;
     const int64_t b = blockIdx.z;
     const int G = (int)(a.hq / a.hkv);
     const int rows_kv = G * (int)a.l;            // query rows sharing this KV head
@@ -519,18 +526,31 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
         }
     }
 
-    // Merge the key slots (KPW per wave, lanes with equal dl) of all waves
-    // through LDS, in slot order; a single split writes the normalised
-    // output, otherwise the split's state goes to the workspace.
-    constexpr int NSL = NWV * KPW;
-    __shared__ float sm[NSL][R], sl[NSL][R], so[NSL][R][HD];
-    {
-        const int slot = wave * KPW + kg;
+    // Merge the KPW key slots of a wave (lanes with equal dl) by a butterfly
+    // over the lane bits above dl: partners compute the same commutative
+    // merge, so every lane ends with the wave's bitwise-same state.  Then the
+    // waves' states merge through LDS in wave order; a single split writes
+    // the normalised output, otherwise the split's state goes to the
+    // workspace.
+#pragma unroll
+    for (int sh = LPK; sh < 64; sh <<= 1) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (dl == 0) { sm[slot][r] = m[r]; sl[slot][r] = lsum[r]; }
+            const float m2 = __shfl_xor(m[r], sh, 64), l2 = __shfl_xor(lsum[r], sh, 64);
+            float o2[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) so[slot][r][dl * 8 + e] = o[r][e];
+            for (int e = 0; e < 8; ++e) o2[e] = __shfl_xor(o[r][e], sh, 64);
+            merge_state<8>(m[r], lsum[r], o[r], m2, l2, o2);
+        }
+    }
+    constexpr int NSL = NWV;
+    __shared__ float sm[NSL][R], sl[NSL][R], so[NSL][R][HD];
+    if (kg == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (dl == 0) { sm[wave][r] = m[r]; sl[wave][r] = lsum[r]; }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) so[wave][r][dl * 8 + e] = o[r][e];
         }
     }
     __syncthreads();
@@ -768,6 +788,16 @@ static bool decode_single_split(int64_t s, int64_t ev, int R) {
     return s <= per_step;
 }
 
+// Caches of at most kDecodeWideWaves x (keys per wave step) x kDecodeWideNB
+// keys (768 at head dim 64, 384 at 128) take the one-step row-wide kernel.
+// Measured on the Llama-1B decode step (32 q / 8 kv heads, 640-key cache):
+// 8 waves x 12 keys 6.2 us, 16 x 6 6.6 us, 4 x 20 6.7 us; 2 rows per
+// work-group 8.6 us, 4 rows 16.2 us; split-KV with in-kernel merge 10.6 us.
+constexpr int kDecodeWideWaves = 8, kDecodeWideNB = 12;
+static bool decode_row_wide(int64_t s, int64_t hd) {
+    return s <= kDecodeWideWaves * (64 / (hd / 8)) * kDecodeWideNB;
+}
+
 // Workspace: split arrival counters (one per work-group row group, at most
 // one per query row; zero between calls), then the split states.
 static size_t decode_counter_bytes(int64_t rows) { return (size_t)cdiv(rows * 4, 256) * 256; }
@@ -802,6 +832,17 @@ template <typename T, int HD>
 static int launch_decode(AttnArgs a, hipStream_t st) {
     const int G = (int)(a.hq / a.hkv);
     const int rows_kv = G * (int)a.l;
+    if (decode_row_wide(a.s, HD) && a.hkv * rows_kv <= 65535) {
+        // short caches: one 16-wave work-group per query row loads every key
+        // in one step (one memory round trip, no split merge); the rows of a
+        // KV head share its K / V through L2
+        a.rows_per_group = 1;
+        a.row_groups = rows_kv;
+        dim3 grid(1u, (unsigned)(a.hkv * rows_kv), (unsigned)a.n);
+        hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1, kDecodeWideWaves, kDecodeWideNB>), grid,
+                           dim3(kDecodeWideWaves * 64), 0, st, a);
+        return launch_status();
+    }
     const int R = decode_rows_per_group(rows_kv);
     a.rows_per_group = R;
     a.row_groups = (int)cdiv(rows_kv, R);
@@ -872,7 +913,8 @@ extern "C" int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l,
     a.kv_len = kv_len;
     const int64_t ss = s > 0 ? s : 1;
     a.chunk = decode_chunk(ss);
-    if (decode_single_split(ss, ev, decode_rows_per_group((int)((hq / hkv) * l)))) a.chunk = ss;
+    if (decode_row_wide(ss, ev) || decode_single_split(ss, ev, decode_rows_per_group((int)((hq / hkv) * l))))
+        a.chunk = ss;
     a.splits = (int)cdiv(ss, a.chunk);
     const int64_t rows = n * hq * l;
     const size_t need = decode_workspace_bytes(rows, s, ev);

@@ -243,6 +243,18 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
     const T *W = reinterpret_cast<const T *>(a.W);
     const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * a.rpw;
     const int64_t r1 = min(a.N, r0 + a.rpw);
+    // Rotary epilogue operands (the token position and the pair's inverse
+    // frequency), loaded first so that their latency hides under the W loads
+    // instead of following the dot products.
+    int64_t rope_pos = 0;
+    float rope_freq = 0.f;
+    if constexpr (OK == kOutRope) {
+        rope_pos = a.pos ? (int64_t)a.pos[0] : 0;
+        if (lane < RG / 2) {
+            const int64_t p = (r0 + 2 * lane) >> 1, half = a.pair_off, head = p / half;
+            if (head < a.hq + a.hkv && r0 + 2 * lane + 1 < r1) rope_freq = a.inv_freq[p - head * half];
+        }
+    }
     u32x4 wv[RG][KC];
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
@@ -352,10 +364,10 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
                 reinterpret_cast<T *>(a.out)[p] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
             } else {
                 const int64_t half = a.pair_off, head = p / half, i = p - head * half;
-                const int64_t pos = a.pos ? (int64_t)a.pos[0] : 0;
+                const int64_t pos = rope_pos;
                 const bool store_kv = pos >= 0 && pos < a.cap;
                 if (head < a.hq + a.hkv) {
-                    const float ang = (float)pos * a.inv_freq[i];
+                    const float ang = (float)pos * rope_freq;
                     const float c = rnd<T>(cosf(ang)), sn = rnd<T>(sinf(ang));
                     const T o1 = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * sn));
                     const T o2 = from_f32<T>(rnd<T>(x2 * c) + rnd<T>(x1 * sn));

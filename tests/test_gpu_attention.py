@@ -99,6 +99,10 @@ def test_sdpa_full_size_one_head(cuda, S):
 DECODE = [  # n, hq, hkv, l, s, d
     (1, 32, 32, 1, 4096, 128),
     (1, 32, 8, 1, 600, 64),
+    (1, 32, 8, 1, 768, 64),     # longest cache of the one-step row-wide kernel
+    (1, 32, 8, 1, 769, 64),     # one key more: split-KV
+    (1, 12, 4, 2, 300, 64),     # row-wide, 24 rows (no XCD regrouping)
+    (1, 16, 4, 1, 384, 128),    # row-wide at head dim 128 (longest)
     (2, 8, 2, 1, 77, 128),
     (1, 4, 4, 1, 1, 64),
 ]
