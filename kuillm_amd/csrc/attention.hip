@@ -250,10 +250,6 @@ void fa_fwd_kernel(AttnArgs a) {
             m_used = m_new;
         }
         const float mref = (m_used == -INFINITY) ? 0.f : m_used;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) nxt[t][e] = 0.f;
         float rs = 0.f;
         constexpr int KS = HD / 16;                 // MFMA k-steps of one score block
         constexpr int EPK = 32 / KS;                // exps per k-step
@@ -272,7 +268,8 @@ void fa_fwd_kernel(AttnArgs a) {
         for (int kk = 0; kk < KS; ++kk) {
             if (kk + KPF - 1 < KS) load_k(kk + KPF - 1, kr[(kk + KPF - 1) % KPF]);
 #pragma unroll
-            for (int t = 0; t < 2; ++t) nxt[t] = Mfma<T>::m32(kr[kk % KPF][t], qf[kk], nxt[t]);
+            for (int t = 0; t < 2; ++t)      // (the first k-step starts from a zero accumulator operand)
+                nxt[t] = Mfma<T>::m32(kr[kk % KPF][t], qf[kk], kk == 0 ? f32x16{} : nxt[t]);
 #pragma unroll
             for (int i = 0; i < EPK; ++i) {
                 const int idx = kk * EPK + i, t = idx >> 4, e = idx & 15;

@@ -511,7 +511,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
         }
     }
 
-    if constexpr (sizeof(Tout) == 2 && WM == 2 && TM * 32 == WTM) {
+    if constexpr (sizeof(Tout) == 2 && WM == 2 && WN == 4 && TM * 32 == WTM && 32 * (BN * 2 + 16) <= SBYTES) {
         if (a.vec_store) {
             // Staged epilogue: the tile goes out as whole 512-byte row segments
             // (16 bytes per lane) instead of the accumulator layout's 64-byte

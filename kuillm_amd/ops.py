@@ -124,6 +124,17 @@ def mm(A: torch.Tensor, B: torch.Tensor, out_dtype=None, gemv_max_m: int | None 
         except _lib.Unsupported:
             pass
     lib = _lib_handle()
+    ws_bytes = lib.kuiops_query_workspace(_lib.OP_ADDMM, M, N, K) if A.dtype in HALF else 0
+    if ws_bytes:
+        # Too few output tiles to fill the GPU: the same kernels with split-K,
+        # whose fp32 partials need a workspace (kuiops_mm takes none), through
+        # the addmm entry point with no addend.
+        ws = workspace(A.device, ws_bytes)
+        _lib.check("kuiops_addmm", lib.kuiops_addmm(
+            M, K, N, 1.0, 0.0, _dt(A.dtype), A.data_ptr(), A.stride(0), B.data_ptr(), ldb, layout,
+            None, _lib.C_NONE, 0, _dt(out.dtype), out.data_ptr(), out.stride(0),
+            0, ws.data_ptr(), ws.numel(), _stream(A.device)))
+        return out
     _lib.check("kuiops_mm", lib.kuiops_mm(
         M, N, K, _dt(A.dtype), A.data_ptr(), A.stride(0), B.data_ptr(), ldb, layout,
         _dt(out.dtype), out.data_ptr(), out.stride(0), _stream(A.device)))

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from kuillm_amd import ops
+from kuillm_amd import _lib, ops
 from oracle import kuiops_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -49,6 +49,20 @@ def test_mm_vs_oracle(cuda, dtype, layout, M, N, K):
     out = ops.mm(A.to(cuda), Bd)
     assert out.dtype == dtype and out.shape == (M, N)
     assert_tol(out, ref, dtype)
+
+
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("M,N,K", [(256, 512, 2048), (130, 384, 4096)])
+def test_mm_few_tiles_splitk(cuda, layout, M, N, K):
+    """Few output tiles and a long K: ops.mm takes split-K through the addmm
+    entry point (workspace partials, fixed-order sum)."""
+    A, B = gen((M, K), torch.bfloat16, seed=21), gen((K, N), torch.bfloat16, 0.02, seed=22)
+    lib = _lib.load()
+    assert lib.kuiops_query_workspace(_lib.OP_ADDMM, M, N, K) > 0      # the split path is taken
+    Bd = B.to(cuda) if layout == "row" else B.t().contiguous().to(cuda).t()
+    out = ops.mm(A.to(cuda), Bd)
+    assert torch.equal(out, ops.mm(A.to(cuda), Bd))
+    assert_tol(out, O.mm(npy(A), npy(B)), torch.bfloat16)
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (17, 9, 13), (64, 64, 64)])
