@@ -324,11 +324,20 @@ void fa_fwd_kernel(AttnArgs a) {
     // Waves whose queries are all masked in a block still run it (their
     // probabilities are 0).
     const bool live = qw < a.l;
+    // Key-block order: the second block of a causal pair walks its keys
+    // backwards.  At step t of a work-group, pair p is at key block t during
+    // its first block (2(nqb - p) steps) and at 2p + 1 - (t - 2(nqb - p)) =
+    // 2 nqb + 1 - t during its second: whatever p, every work-group of the
+    // launch is at one of just two key blocks, so the K / V blocks they
+    // stream stay shared in L2.  The online softmax is order-independent up
+    // to rounding.
+    const bool rev = CAUSAL && a.pair && pass == 1;
+    auto kvb = [&](int j) { return rev ? nkv - 1 - j : j; };
     f32x16 scA[2], scB[2];
     if (nkv > 0) {
-        issue_k(0, sK0);
-        issue_v(0, sV0);
-        if (nkv > 1) issue_k(1, sK1);
+        issue_k(kvb(0), sK0);
+        issue_v(kvb(0), sV0);
+        if (nkv > 1) issue_k(kvb(1), sK1);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (live) qk(sK0, scA);
@@ -340,9 +349,9 @@ void fa_fwd_kernel(AttnArgs a) {
             if (j >= nkv) break;
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (j + 2 < nkv) issue_k(j + 2, hs ? sK1 : sK0);
-            if (j + 1 < nkv) issue_v(j + 1, hs ? sV0 : sV1);
-            if (live) step(hs ? scB : scA, hs ? scA : scB, hs ? sK0 : sK1, hs ? sV1 : sV0, (int64_t)j * BKV);
+            if (j + 2 < nkv) issue_k(kvb(j + 2), hs ? sK1 : sK0);
+            if (j + 1 < nkv) issue_v(kvb(j + 1), hs ? sV0 : sV1);
+            if (live) step(hs ? scB : scA, hs ? scA : scB, hs ? sK0 : sK1, hs ? sV1 : sV0, (int64_t)kvb(j) * BKV);
         }
     }
 
