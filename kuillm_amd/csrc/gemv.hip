@@ -461,10 +461,12 @@ static int gemv_dispatch(const GemvArgs &a, bool wcol, hipStream_t st) {
 }
 
 constexpr int kStripW = 64;      // 128-byte row segments: narrower ones halve HBM efficiency
-// Work-group shape: up to 32 rows of x, 16 waves x 2 stages x 4 KB = 128 KB
-// LDS (one work-group per CU, 128 VGPRs per lane); 33..64 rows need more
-// accumulators, so 8 waves x 4 stages (256 VGPRs).  Both keep 32 stages of
-// 4 KB in flight per CU.
+// Work-group shape (128 KB of LDS, one work-group per CU): up to 16 rows of
+// x and 33..64 rows take 8 waves x 4 stages of 4 KB, so three stages per wave
+// stay in flight while it computes on the fourth (4096 x 11008, M = 1 / 4 /
+// 16: 15.3 / 15.5 / 16.1 us, against 15.7 / 15.9 / 16.4 us for 16 waves x 2
+// stages; 2 or 3 K splits per strip were slower, 17.8-21 us); 17..32 rows
+// keep 16 waves x 2 stages (128 VGPRs per lane).
 constexpr int kStripWaves = 16, kStripStages = 2;
 constexpr int kStripWavesWide = 8, kStripStagesWide = 4;
 
@@ -502,7 +504,7 @@ static void strip_launch(GemvArgs a, hipStream_t st) {
 template <typename T, typename Tout>
 static int strip_dispatch(const GemvArgs &a, hipStream_t st) {
     switch (cdiv(a.M, 16)) {
-        case 1: strip_launch<T, Tout, 1, kStripWaves, kStripStages>(a, st); break;
+        case 1: strip_launch<T, Tout, 1, kStripWavesWide, kStripStagesWide>(a, st); break;
         case 2: strip_launch<T, Tout, 2, kStripWaves, kStripStages>(a, st); break;
         case 3: strip_launch<T, Tout, 3, kStripWavesWide, kStripStagesWide>(a, st); break;
         case 4: strip_launch<T, Tout, 4, kStripWavesWide, kStripStagesWide>(a, st); break;
