@@ -212,9 +212,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
     static_assert(DPS >= 1 && CPR >= 2, "strip width");
     typedef typename Mfma<T>::frag frag;
     // one array per stage (distinct objects: see the GEMM kernels)
+    static_assert(NS >= 2 && NS <= 8, "stages");
     __shared__ __attribute__((aligned(1024))) char st0[NW * STG], st1[NW * STG];
     __shared__ __attribute__((aligned(1024))) char st2[NS > 2 ? NW * STG : 16], st3[NS > 3 ? NW * STG : 16];
-    char *const ST[4] = {st0, st1, st2, st3};
+    __shared__ __attribute__((aligned(1024))) char st4[NS > 4 ? NW * STG : 16], st5[NS > 5 ? NW * STG : 16];
+    __shared__ __attribute__((aligned(1024))) char st6[NS > 6 ? NW * STG : 16], st7[NS > 7 ? NW * STG : 16];
+    char *const ST[8] = {st0, st1, st2, st3, st4, st5, st6, st7};
 
     const int tid = threadIdx.x, lane = tid & 63;
     // wave-uniform by construction; readfirstlane lets the compiler keep the
@@ -339,9 +342,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
     compute(nst - NS, ST[0], xr[0]);
 #pragma unroll
     for (int s = 1; s < NS; ++s) {
-        if (s == 1) wait_vmcnt_g<(NS - 2) * PER>();
-        else if (s == 2) wait_vmcnt_g<(NS > 3 ? (NS - 3) * PER : 0)>();
-        else wait_vmcnt_g<0>();
+        // stages issued after this one: NS - 1 - s
+        switch (NS - 1 - s) {
+            case 6: wait_vmcnt_g<(NS > 7 ? 6 * PER : 0)>(); break;
+            case 5: wait_vmcnt_g<(NS > 6 ? 5 * PER : 0)>(); break;
+            case 4: wait_vmcnt_g<(NS > 5 ? 4 * PER : 0)>(); break;
+            case 3: wait_vmcnt_g<(NS > 4 ? 3 * PER : 0)>(); break;
+            case 2: wait_vmcnt_g<(NS > 3 ? 2 * PER : 0)>(); break;
+            case 1: wait_vmcnt_g<(NS > 2 ? 1 * PER : 0)>(); break;
+            default: wait_vmcnt_g<0>(); break;
+        }
         compute(nst - NS + s, ST[s], xr[s]);
     }
 
@@ -465,7 +475,8 @@ constexpr int kStripW = 64;      // 128-byte row segments: narrower ones halve H
 // x and 33..64 rows take 8 waves x 4 stages of 4 KB, so three stages per wave
 // stay in flight while it computes on the fourth (4096 x 11008, M = 1 / 4 /
 // 16: 15.3 / 15.5 / 16.1 us, against 15.7 / 15.9 / 16.4 us for 16 waves x 2
-// stages; 2 or 3 K splits per strip were slower, 17.8-21 us); 17..32 rows
+// stages and 15.6 / 15.7 / 16.2 us for 4 waves x 8 stages; 2 or 3 K splits
+// per strip were slower, 17.8-21 us); 17..32 rows
 // keep 16 waves x 2 stages (128 VGPRs per lane).
 constexpr int kStripWaves = 16, kStripStages = 2;
 constexpr int kStripWavesWide = 8, kStripStagesWide = 4;
