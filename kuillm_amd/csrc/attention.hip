@@ -870,8 +870,10 @@ static int launch_decode(AttnArgs a, hipStream_t st) {
     const bool fused = a.splits <= kFusedMergeMaxSplits;
     if (!fused) a.counters = nullptr;
     switch (R) {
-        case 1: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1>), grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 2>), grid, dim3(256), 0, st, a); break;
+        // one or two rows: 8 keys per lane group, so a split of up to 128
+        // (head dim 128) or 256 (64) keys is a single load round trip
+        case 1: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1, 4, 8>), grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 2, 4, 8>), grid, dim3(256), 0, st, a); break;
         case 4: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 4>), grid, dim3(256), 0, st, a); break;
         default: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 8>), grid, dim3(256), 0, st, a); break;
     }
