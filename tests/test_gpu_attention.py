@@ -127,3 +127,27 @@ def test_sdpa_decode_bottom_right_causal(cuda, l):
     ref, lref = O.sdpa(npy(q), npy(k), npy(v), causal=True, align="bottom_right")
     close(out, ref)
     np.testing.assert_allclose(npy(lse), lref, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("n,hq,hkv,l,s,d", [(2, 32, 8, 2048, 2048, 64), (1, 64, 64, 2048, 2304, 128)])
+def test_sdpa_causal_paired_blocks(cuda, n, hq, hkv, l, s, d):
+    """Grids large enough for paired causal query blocks (block p with block
+    nqb-1-p, the second walked backwards over its keys): GQA, head dim 64,
+    and more keys than queries (top-left causal alignment).  Sampled heads
+    against the oracle, plus the same call on one head (a small grid that
+    runs single blocks) must agree to rounding."""
+    torch.manual_seed(l + s + d)
+    q = torch.randn(n, hq, l, d, device=cuda).to(torch.bfloat16)
+    k = torch.randn(n, hkv, s, d, device=cuda).to(torch.bfloat16)
+    v = torch.randn(n, hkv, s, d, device=cuda).to(torch.bfloat16)
+    out, lse = ops.sdpa(q, k, v, is_causal=True)
+    g = hq // hkv
+    for b, h in ((0, 0), (n - 1, hq - 1), (n - 1, hq // 2 + 1)):
+        kh = h // g
+        ref, lref = O.sdpa(npy(q[b:b + 1, h:h + 1]), npy(k[b:b + 1, kh:kh + 1]), npy(v[b:b + 1, kh:kh + 1]),
+                           causal=True)
+        close(out[b:b + 1, h:h + 1], ref)
+        np.testing.assert_allclose(npy(lse[b:b + 1, h:h + 1]), lref, atol=1e-3, rtol=1e-4)
+        single, _ = ops.sdpa(q[b:b + 1, h:h + 1].contiguous(), k[b:b + 1, kh:kh + 1].contiguous(),
+                             v[b:b + 1, kh:kh + 1].contiguous(), is_causal=True)
+        assert (single.float() - out[b:b + 1, h:h + 1].float()).abs().max().item() < 2e-2
