@@ -562,7 +562,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
                     const int64_t gcol = n0 + ch * 8;
                     const u32x4 v = *reinterpret_cast<const u32x4 *>((bnd ? sB0 : sA0) + row * RS + ch * 16);
                     if (grow < a.M && gcol < a.N)
-                        *reinterpret_cast<u32x4 *>(reinterpret_cast<Tout *>(a.out) + grow * a.ldo + gcol) = v;
+                        // streaming store: the output is not read again here
+                        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(reinterpret_cast<Tout *>(a.out) + grow * a.ldo + gcol));
                 }
             }
             return;
