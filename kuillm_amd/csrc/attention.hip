@@ -822,11 +822,12 @@ static int launch_fwd(AttnArgs a, hipStream_t st) {
     // softmax step: 1.5x slower, measured.)
     a.nqb = (int)cdiv(a.l, 128);
     // Causal: pair the query blocks of a head (equal work per work-group)
-    // when the pairs still fill both work-group slots of every CU (causal
-    // S=4096, 32 heads: 512 pairs).  Fewer pairs would leave CUs half idle;
-    // then the blocks run singly, heaviest first.
+    // when the pairs still give every CU a work-group.  Single blocks, even
+    // heaviest first, end with the longest block alone: at S=2048 (32 heads,
+    // 256 pairs, one per CU) pairing is 9% faster than 512 single blocks at
+    // two per CU (64.5 -> 59.2 us); at S=4096 the 512 pairs fill both slots.
     const int64_t singles = (int64_t)a.nqb * a.n * a.hq;
-    a.pair = (a.causal && (a.nqb & 1) == 0 && singles / 2 >= 2 * (int64_t)num_cus()) ? 1 : 0;
+    a.pair = (a.causal && (a.nqb & 1) == 0 && singles / 2 >= (int64_t)num_cus()) ? 1 : 0;
     const int64_t blocks = a.pair ? singles / 2 : singles;
     if (blocks > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
