@@ -13,9 +13,11 @@
 //   V is transposed into LDS in that same order ([d][key], 4-key groups
 //   permuted 0,2,1,3 inside each 16) and one ds_read_b128 yields an operand.
 //   Softmax runs in the log2 domain (exp2 on the hardware exp unit) in fp32.
-//   Causal work-groups are dispatched heaviest-first and fully masked waves
-//   skip their MFMAs; all q-blocks of one head are mapped to one XCD so its
-//   K / V stay in that XCD's L2.
+//   Causal grids that give every CU a work-group pair query blocks p and
+//   nqb-1-p in one work-group (equal work everywhere; the second block walks
+//   its keys backwards so all work-groups stream the same key blocks);
+//   smaller ones run single blocks heaviest-first.  All q-blocks of one head
+//   are mapped to one XCD so its K / V stay in that XCD's L2.
 //
 // fa_decode_kernel -- decode (few queries per head) over a long KV cache:
 //   HBM-bound, so the keys are split over work-groups (split-KV); each
