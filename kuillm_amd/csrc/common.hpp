@@ -153,7 +153,7 @@ inline int num_cus() {
     return cache[dev];
 }
 
-inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+__host__ __device__ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 inline int dtype_bytes(int dt) {
     switch (dt) {

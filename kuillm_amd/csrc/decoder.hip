@@ -265,6 +265,18 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
             wv[g][j] = ch < nch ? *reinterpret_cast<const u32x4 *>(W + r * a.ldw + ch * 8) : u32x4{0, 0, 0, 0};
         }
     }
+    // Rotary cos / sin of this lane's pair, computed while the W rows are in
+    // flight (their loads were issued after the two operands above, so only
+    // those are waited for); computed in the epilogue they would lengthen
+    // the kernel's final dependency chain by ~0.7 us.
+    float rope_c = 0.f, rope_s = 0.f;
+    if constexpr (OK == kOutRope) {
+        if (lane < RG / 2) {
+            const float ang = (float)rope_pos * rope_freq;
+            rope_c = rnd<T>(cosf(ang));
+            rope_s = rnd<T>(sinf(ang));
+        }
+    }
     // ---- input stage
     float h[XCH][8];
     float ss = 0.f;
@@ -353,37 +365,64 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
         }
     } else {
         // every lane holds every row's sum (wave_sum is a butterfly): lane
-        // g / 2 finishes pair g / 2, so the pairs' epilogues run side by side
+        // g / 2 finishes pair g / 2, so the pairs' epilogues run side by side.
+        // The results go through LDS: the work-group's pairs are consecutive
+        // (pg0 ..), so each output half is one contiguous run, stored with a
+        // single 16-byte write (2-byte stores from every wave of every
+        // work-group cost the qkv kernel ~1.5 us).
+        constexpr int PW = RG / 2, PG = 4 * PW;       // pairs per wave / work-group
+        __shared__ __attribute__((aligned(16))) T s_o[2][PG];
+        const int64_t pg0 = (int64_t)blockIdx.x * PG;
+        const int np = (int)min((int64_t)PG, a.N / 2 - pg0);
+        const int64_t pos = rope_pos;
+        const bool store_kv = pos >= 0 && pos < a.cap;
 #pragma unroll
         for (int g = 0; g < RG; g += 2) {
             const int64_t r = r0 + g;                    // even: rows r, r + 1 form pair r / 2
             if (lane != g / 2 || r + 1 >= r1) continue;
             const int64_t p = r >> 1;
+            const int slot = wave * PW + g / 2;
             const float x1 = rnd<T>(accs[g]), x2 = rnd<T>(accs[g + 1]);
             if constexpr (OK == kOutSwiGlu) {
-                reinterpret_cast<T *>(a.out)[p] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
+                s_o[0][slot] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
             } else {
-                const int64_t half = a.pair_off, head = p / half, i = p - head * half;
-                const int64_t pos = rope_pos;
-                const bool store_kv = pos >= 0 && pos < a.cap;
+                const int64_t head = p / a.pair_off;
                 if (head < a.hq + a.hkv) {
-                    const float ang = (float)pos * rope_freq;
-                    const float c = rnd<T>(cosf(ang)), sn = rnd<T>(sinf(ang));
-                    const T o1 = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * sn));
-                    const T o2 = from_f32<T>(rnd<T>(x2 * c) + rnd<T>(x1 * sn));
-                    T *dst;
-                    if (head < a.hq) {
-                        dst = reinterpret_cast<T *>(a.out) + head * a.hd;
-                    } else {
-                        if (!store_kv) continue;
-                        dst = reinterpret_cast<T *>(a.kc) + (head - a.hq) * a.sk1 + pos * a.sk2;
-                    }
-                    dst[i] = o1;
-                    dst[i + half] = o2;
-                } else if (store_kv) {
-                    T *dst = reinterpret_cast<T *>(a.vc) + (head - a.hq - a.hkv) * a.sv1 + pos * a.sv2;
-                    dst[i] = from_f32<T>(x1);
-                    dst[i + half] = from_f32<T>(x2);
+                    const float c = rope_c, sn = rope_s;
+                    s_o[0][slot] = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * sn));
+                    s_o[1][slot] = from_f32<T>(rnd<T>(x2 * c) + rnd<T>(x1 * sn));
+                } else {
+                    s_o[0][slot] = from_f32<T>(x1);
+                    s_o[1][slot] = from_f32<T>(x2);
+                }
+            }
+        }
+        __syncthreads();
+        // destination of pair p's half e: SwiGLU out[p]; rotary q -> out,
+        // k -> k cache, v -> v cache at position pos (element i, or i + hd/2)
+        auto dst_of = [&](int64_t p, int e) -> T * {
+            if constexpr (OK == kOutSwiGlu) {
+                return reinterpret_cast<T *>(a.out) + p;
+            } else {
+                const int64_t half = a.pair_off, head = p / half, i = p - head * half + e * half;
+                if (head < a.hq) return reinterpret_cast<T *>(a.out) + head * a.hd + i;
+                if (!store_kv) return nullptr;
+                if (head < a.hq + a.hkv) return reinterpret_cast<T *>(a.kc) + (head - a.hq) * a.sk1 + pos * a.sk2 + i;
+                return reinterpret_cast<T *>(a.vc) + (head - a.hq - a.hkv) * a.sv1 + pos * a.sv2 + i;
+            }
+        };
+        constexpr int NE = OK == kOutSwiGlu ? 1 : 2;
+        if (tid < NE && np > 0) {
+            const int e = tid;
+            T *d0 = dst_of(pg0, e);
+            // one run when all pairs are present and share the first pair's head
+            const bool one_run = np == PG && (OK == kOutSwiGlu || (pg0 % a.pair_off) + PG <= a.pair_off);
+            if (PG * sizeof(T) == 16 && one_run && d0 && aligned16(d0)) {
+                *reinterpret_cast<u32x4 *>(d0) = *reinterpret_cast<const u32x4 *>(s_o[e]);
+            } else {
+                for (int k = 0; k < np; ++k) {
+                    T *d = dst_of(pg0 + k, e);
+                    if (d) *d = s_o[e][k];
                 }
             }
         }
