@@ -188,6 +188,7 @@ struct DecLinArgs {
     const int64_t *in_row; int64_t ld_in, in_rows;
     // paired epilogues: logical row 2p + e is W row base(p) + e * pair_off
     int64_t pair_off;
+    int pair_shift;                    // log2(pair_off) when a power of two, else -1
     // rotary epilogue (kOutRope): rows are [q heads | k heads | v heads] of hd
     int64_t hq, hkv, hd;
     const float *inv_freq;
@@ -200,12 +201,18 @@ struct DecLinArgs {
 // W row of logical row j: identity, or the pair mapping of the paired
 // epilogues (SwiGLU: rows p and p + ffn; rotary: rows i and i + hd/2 of a
 // head, so that one wave holds both halves of each rotated pair).
+// p / pair_off (a shift for the power-of-two head halves of real models: a
+// 64-bit division would sit on the W loads' address path)
+__device__ __forceinline__ int64_t pair_div(const DecLinArgs &a, int64_t p) {
+    return a.pair_shift >= 0 ? p >> a.pair_shift : p / a.pair_off;
+}
+
 template <int OK>
 __device__ __forceinline__ int64_t dec_row(const DecLinArgs &a, int64_t j) {
     if constexpr (OK == kOutPlain) return j;
     const int64_t p = j >> 1, e = j & 1;
     if constexpr (OK == kOutSwiGlu) return p + e * a.pair_off;
-    const int64_t half = a.pair_off, head = p / half;
+    const int64_t half = a.pair_off, head = pair_div(a, p);
     return head * a.hd + (p - head * half) + e * half;
 }
 
@@ -251,7 +258,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
     if constexpr (OK == kOutRope) {
         rope_pos = a.pos ? (int64_t)a.pos[0] : 0;
         if (lane < RG / 2) {
-            const int64_t p = (r0 + 2 * lane) >> 1, half = a.pair_off, head = p / half;
+            const int64_t p = (r0 + 2 * lane) >> 1, half = a.pair_off, head = pair_div(a, p);
             if (head < a.hq + a.hkv && r0 + 2 * lane + 1 < r1) rope_freq = a.inv_freq[p - head * half];
         }
     }
@@ -386,7 +393,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
             if constexpr (OK == kOutSwiGlu) {
                 s_o[0][slot] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
             } else {
-                const int64_t head = p / a.pair_off;
+                const int64_t head = pair_div(a, p);
                 if (head < a.hq + a.hkv) {
                     const float c = rope_c, sn = rope_s;
                     s_o[0][slot] = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * sn));
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
             if constexpr (OK == kOutSwiGlu) {
                 return reinterpret_cast<T *>(a.out) + p;
             } else {
-                const int64_t half = a.pair_off, head = p / half, i = p - head * half + e * half;
+                const int64_t half = a.pair_off, head = pair_div(a, p), i = p - head * half + e * half;
                 if (head < a.hq) return reinterpret_cast<T *>(a.out) + head * a.hd + i;
                 if (!store_kv) return nullptr;
                 if (head < a.hq + a.hkv) return reinterpret_cast<T *>(a.kc) + (head - a.hq) * a.sk1 + pos * a.sk2 + i;
@@ -416,7 +423,7 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
             const int e = tid;
             T *d0 = dst_of(pg0, e);
             // one run when all pairs are present and share the first pair's head
-            const bool one_run = np == PG && (OK == kOutSwiGlu || (pg0 % a.pair_off) + PG <= a.pair_off);
+            const bool one_run = np == PG && (OK == kOutSwiGlu || (pg0 - pair_div(a, pg0) * a.pair_off) + PG <= a.pair_off);
             if (PG * sizeof(T) == 16 && one_run && d0 && aligned16(d0)) {
                 *reinterpret_cast<u32x4 *>(d0) = *reinterpret_cast<const u32x4 *>(s_o[e]);
             } else {
@@ -445,6 +452,14 @@ static void decode_rows_dispatch(const DecLinArgs &a, int x_kind, unsigned grid,
     if (x_kind == kXPlain) decode_rows_launch<T, kXPlain, OK>(a, grid, st);
     else if (x_kind == kXRmsNorm) decode_rows_launch<T, kXRmsNorm, OK>(a, grid, st);
     else decode_rows_launch<T, kXSwiGlu, OK>(a, grid, st);
+}
+
+// log2(v) when v is a power of two, else -1.
+static int log2_exact(int64_t v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int k = 0;
+    while ((int64_t(1) << k) < v) ++k;
+    return k;
 }
 
 // Shared host path of the decode projections: argument checks, rows per
@@ -561,7 +576,7 @@ extern "C" int kuiops_decode_gate_up(int64_t ffn, int64_t K, int dtype, int x_ki
     if (ffn < 0) return KUIOPS_E_INVALID;
     DecLinArgs a{};
     a.N = 2 * ffn; a.K = K; a.in = in; a.in_add = in_add; a.norm_w = norm_w; a.eps = eps; a.h_out = h_out;
-    a.W = W; a.ldw = ldw; a.out = out; a.pair_off = ffn;
+    a.W = W; a.ldw = ldw; a.out = out; a.pair_off = ffn; a.pair_shift = log2_exact(ffn);
     return decode_linear_run<kOutSwiGlu>(a, dtype, x_kind, stream);
 }
 
@@ -577,7 +592,7 @@ extern "C" int kuiops_decode_qkv_rope(int64_t hq, int64_t hkv, int64_t hd, int64
     a.N = (hq + 2 * hkv) * hd; a.K = K; a.in = in; a.in_add = in_add; a.norm_w = norm_w; a.eps = eps;
     a.h_out = h_out; a.W = W; a.ldw = ldw; a.out = q_out;
     a.in_row = in_row; a.ld_in = ld_in; a.in_rows = in_rows;
-    a.pair_off = hd / 2; a.hq = hq; a.hkv = hkv; a.hd = hd; a.inv_freq = inv_freq; a.pos = pos;
+    a.pair_off = hd / 2; a.pair_shift = log2_exact(hd / 2); a.hq = hq; a.hkv = hkv; a.hd = hd; a.inv_freq = inv_freq; a.pos = pos;
     a.kc = k_cache; a.sk1 = sk_head; a.sk2 = sk_pos; a.vc = v_cache; a.sv1 = sv_head; a.sv2 = sv_pos;
     a.cap = cache_cap;
     return decode_linear_run<kOutRope>(a, dtype, x_kind, stream);
