@@ -424,7 +424,10 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     if (gridDim.x == 1 && (gridDim.y & 7) == 0) unit = (unit & 7) * (gridDim.y >> 3) + (unit >> 3);
     const int hk = unit / a.row_groups, rg = unit % a.row_groups;
     const int64_t b = blockIdx.z;
-    const int G = (int)(a.hq / a.hkv);
+    // head / query index arithmetic in 32 bits (a 64-bit division is a long
+    // instruction sequence ahead of the Q loads); decode row counts are small
+    const int G = (int)a.hq / (int)a.hkv;
+    const int LQ = (int)a.l;
     const int rows_kv = G * (int)a.l;            // query rows sharing this KV head
     const int r0 = rg * a.rows_per_group;
 
@@ -443,8 +446,8 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     for (int r = 0; r < R; ++r) {
         const int rr = r0 + r;
         const bool ok = rr < rows_kv && r < a.rows_per_group;
-        const int64_t head = hk * G + (ok ? rr / a.l : 0);
-        const int64_t qi = ok ? rr % a.l : 0;
+        const int64_t head = hk * G + (ok ? rr / LQ : 0);
+        const int64_t qi = ok ? rr % LQ : 0;
         const T *Qp = reinterpret_cast<const T *>(a.Q) + b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8;
         u32x4 raw = ok ? *reinterpret_cast<const u32x4 *>(Qp) : u32x4{0, 0, 0, 0};
         typedef T t8 __attribute__((ext_vector_type(8)));
@@ -578,7 +581,7 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
             oo = __builtin_fmaf(so[sv][r][d], wgt, oo);
         }
         const int rr = r0 + r;
-        const int64_t head = hk * G + rr / a.l, qi = rr % a.l;
+        const int64_t head = hk * G + rr / LQ, qi = rr % LQ;
         const int64_t grow = (b * a.hq + head) * a.l + qi;
         if (a.splits == 1) {
             T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
@@ -634,7 +637,7 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     constexpr int kSc1 = 16;                    // cache policy: system-coherent level 1 (agent scope)
     auto grow_of = [&](int r) {
         const int rr = r0 + r;
-        return (b * a.hq + hk * G + rr / a.l) * a.l + rr % a.l;
+        return (b * a.hq + hk * G + rr / LQ) * a.l + rr % LQ;
     };
     // Thread (r, d) = tid issues its o loads (at most 32 splits) before the
     // weights are known, so both arrive in one memory round trip.
@@ -691,7 +694,7 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
         const float L = s_L[r];
         const float inv = L > 0.f ? 1.f / L : 0.f;
         const int rr = r0 + r;
-        const int64_t head = hk * G + rr / a.l, qi = rr % a.l;
+        const int64_t head = hk * G + rr / LQ, qi = rr % LQ;
         T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
         Op[d] = from_f32<T>(acc * inv);
         if (a.lse && d == 0) a.lse[grow] = L > 0.f ? (s_M[r] + __log2f(L)) * kLn2 : -INFINITY;
