@@ -422,6 +422,176 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
     }
 }
 
+// Row-streaming decode GEMM for row-major W and at most 4 rows of x
+// (VALU, no MFMA): lane l of a wave owns 8 adjacent output columns, so one
+// 16-byte load per lane covers 512 columns (1 KB) of a W row, and a
+// work-group of 8 waves walks a K range of its 512-column block in groups of
+// 8 rows (wave w takes groups w, w + 8, ...; two groups, 16 loads per lane,
+// in flight).  Cold W (not in the MALL) streams from HBM far better in
+// these 1 KB row segments than in the 128-byte segments of the strip kernel.
+// The waves' sums meet in LDS in wave order; the K splits of one column
+// block are summed in split order by the last work-group of that block to
+// arrive (agent-coherent partials and counter, as in the strip kernel), so
+// the result is bitwise repeatable.
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4 &v, float *f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(T) == 2 && __is_same(T, bf16_t)) {
+            f[2 * i] = __uint_as_float(v[i] << 16);
+            f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+        } else {
+            const uint32_t u = v[i];
+            f[2 * i] = (float)__builtin_bit_cast(f16_t, (uint16_t)(u & 0xffffu));
+            f[2 * i + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(u >> 16));
+        }
+    }
+}
+
+template <typename T, typename Tout, int MR, int P>
+__global__ __launch_bounds__(512) void gemv_rows_kernel(GemvArgs a) {
+    constexpr int NW = 8, CB = 512;                 // waves, columns per block; P groups in flight
+    __shared__ float red[NW * CB];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cb = blockIdx.x, split = blockIdx.y;
+    const int64_t n0 = (int64_t)cb * CB;
+    // columns past N read a valid neighbouring 16 bytes (not stored)
+    const int64_t colc = min(n0 + 8 * lane, a.N - 8);
+    const int64_t kbeg = (int64_t)split * a.k_part;
+    const int64_t kend = min(a.K, kbeg + a.k_part);
+    const int ngroups = kend > kbeg ? (int)((kend - kbeg) / 8) : 0;   // k_part, K multiples of 8
+    const T *W = reinterpret_cast<const T *>(a.W);
+    const T *x = reinterpret_cast<const T *>(a.x);
+
+    float acc[MR][8];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[m][c] = 0.f;
+
+    u32x4 wr[P][8];
+    auto load = [&](int g, u32x4 *w) __attribute__((always_inline)) {
+        const T *p = W + (kbeg + 8 * (int64_t)g) * a.ldw + colc;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p + j * a.ldw));
+    };
+    auto fma8 = [&](int g, const u32x4 *w) __attribute__((always_inline)) {
+        const int64_t k = kbeg + 8 * (int64_t)g;
+        float xf[MR][8];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            // rows past M repeat row M - 1 (not stored)
+            const u32x4 xv = *reinterpret_cast<const u32x4 *>(x + (int64_t)min(m, (int)a.M - 1) * a.ldx + k);
+            unpack8<T>(xv, xf[m]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float wf[8];
+            unpack8<T>(w[j], wf);
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[m][c] = __builtin_fmaf(xf[m][j], wf[c], acc[m][c]);
+        }
+    };
+    // wave w: groups w, w + NW, ...; P groups in flight
+    int g = wave;
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+        if (g + p * NW < ngroups) load(g + p * NW, wr[p]);
+    for (; g < ngroups; g += P * NW) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int gg = g + p * NW;
+            if (gg < ngroups) {
+                fma8(gg, wr[p]);
+                if (gg + P * NW < ngroups) load(gg + P * NW, wr[p]);
+            }
+        }
+    }
+
+    // waves summed in wave order; thread t then owns column n0 + t
+    const int64_t col = n0 + tid;
+    float res[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        if (m) __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 8; ++c) red[wave * CB + 8 * lane + c] = acc[m][c];
+        __syncthreads();
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w * CB + tid];
+        res[m] = v;
+    }
+    if (a.splits == 1) {
+        if (col < a.N) {
+            const float b = a.bias ? to_f32(reinterpret_cast<const T *>(a.bias)[col]) : 0.f;
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < a.M) reinterpret_cast<Tout *>(a.out)[m * a.ldo + col] = from_f32<Tout>(res[m] + b);
+        }
+        return;
+    }
+    if (col < a.N) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < a.M)
+                __hip_atomic_store(&a.partial[((int64_t)split * a.M + m) * a.N + col], res[m], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&a.counters[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(a.splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+    if (col < a.N) {
+        const float b = a.bias ? to_f32(reinterpret_cast<const T *>(a.bias)[col]) : 0.f;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            if (m >= a.M) break;
+            float v = 0.f;
+            int z = 0;
+            for (; z + 8 <= a.splits; z += 8) {
+                float t[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    t[i] = __hip_atomic_load(&a.partial[((int64_t)(z + i) * a.M + m) * a.N + col], __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v += t[i];
+            }
+            for (; z < a.splits; ++z)
+                v += __hip_atomic_load(&a.partial[((int64_t)z * a.M + m) * a.N + col], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            reinterpret_cast<Tout *>(a.out)[m * a.ldo + col] = from_f32<Tout>(v + b);
+        }
+    }
+    if (tid == 0) __hip_atomic_store(&a.counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kRowsCB = 512;        // columns per work-group of the row-streaming kernel
+constexpr int kRowsMaxM = 2;
+
+// K splits of the row-streaming kernel: at most ~192 work-groups (one per
+// CU).  Every split adds the merge tail (write-through partials, counter,
+// re-read) to its column block, so fewer, longer K ranges win: 4096 x 11008,
+// M = 1, cold W: 8 splits 17.5 us, 11 18.0, 16 19.9, 32 19.8, 64 24.0.
+static int rows_splits(int64_t N, int64_t K) {
+    const int64_t cbs = cdiv(N, kRowsCB);
+    int64_t s = 192 / cbs;
+    const int64_t maxs = cdiv(K, 64);                // at least one group per wave
+    if (s > maxs) s = maxs;
+    if (s > 64) s = 64;
+    return s < 1 ? 1 : (int)s;
+}
+
 static int gemv_choose_splits(int64_t M, int64_t N, int64_t K) {
     (void)M;
     const int64_t strips = cdiv(N, kGemvStrip);
@@ -442,7 +612,8 @@ constexpr size_t kGemvCounterBytes = 16384;       // 4096 strips: N <= 262144
 size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     const int s = gemv_choose_splits(M, N, K);
     const int s2 = strip_splits(N, K);
-    const int mx = s > s2 ? s : s2;
+    const int s3 = M <= kRowsMaxM ? rows_splits(N, K) : 1;
+    const int mx = max(max(s, s2), s3);
     return kGemvCounterBytes + (mx > 1 ? (size_t)mx * M * N * sizeof(float) : 0);
 }
 
@@ -524,6 +695,24 @@ static int strip_dispatch(const GemvArgs &a, hipStream_t st) {
     return launch_status();
 }
 
+static bool rows_eligible(const GemvArgs &a, bool wcol) {
+    if (wcol || a.M > kRowsMaxM || a.N % 8 || a.ldw % 8 || a.K % 8 || a.N < kRowsCB) return false;
+    if (cdiv(a.N, kRowsCB) * 4 > (int64_t)kGemvCounterBytes) return false;
+    if (getenv("KUIOPS_GEMV_NO_ROWS")) return false;
+    return true;
+}
+
+template <typename T, typename Tout>
+static int rows_dispatch(const GemvArgs &a, hipStream_t st) {
+    dim3 grid((unsigned)cdiv(a.N, kRowsCB), (unsigned)a.splits);
+    switch (a.M) {
+        case 1: hipLaunchKernelGGL((gemv_rows_kernel<T, Tout, 1, 2>), grid, dim3(512), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((gemv_rows_kernel<T, Tout, 2, 2>), grid, dim3(512), 0, st, a); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
 }  // namespace kuiops
 
 using namespace kuiops;
@@ -549,6 +738,20 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
     a.x = x; a.ldx = ldx; a.W = W; a.ldw = ldw; a.bias = bias;
     a.out = out; a.ldo = ldo;
     hipStream_t st0 = as_stream(stream);
+    if (splits <= 0 && rows_eligible(a, wcol)) {
+        a.splits = rows_splits(N, K);
+        a.k_part = cdiv(cdiv(K, a.splits), 8) * 8;
+        a.splits = (int)cdiv(K, a.k_part);
+        if (a.splits > 1) {
+            const size_t need = kGemvCounterBytes + (size_t)a.splits * M * N * sizeof(float);
+            if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
+            a.counters = reinterpret_cast<unsigned *>(workspace);
+            a.partial = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + kGemvCounterBytes);
+        }
+        if (in_dtype == KUIOPS_BF16)
+            return out_dtype == KUIOPS_F32 ? rows_dispatch<bf16_t, float>(a, st0) : rows_dispatch<bf16_t, bf16_t>(a, st0);
+        return out_dtype == KUIOPS_F32 ? rows_dispatch<f16_t, float>(a, st0) : rows_dispatch<f16_t, f16_t>(a, st0);
+    }
     if (splits <= 0 && strip_eligible(a, wcol)) {
         a.splits = strip_splits(N, K);
         if (a.splits > 1) {

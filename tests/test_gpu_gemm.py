@@ -237,6 +237,29 @@ def test_decode_gemm_split_sequence_keeps_counters_zero(cuda):
     assert not ws[:16384].any()
 
 
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("N,K", [(512, 8), (1000, 4104), (11008, 4096), (4104, 520), (2048, 8192)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_gemm_row_stream(cuda, M, N, K, dtype):
+    """Row-streaming decode GEMM (M <= 2, row-major W, N >= 512): a ragged last
+    512-column block, one 8-row group (K = 8), one or several K splits merged
+    in split order, a strided W view, bias, fp32 output; bitwise repeatable."""
+    x = gen((M, K), dtype, seed=21)
+    Wbig = gen((K, N + 16), dtype, 0.02, seed=22)
+    b = gen((N,), dtype, seed=23)
+    ref = O.mm(npy(x), npy(Wbig[:, 8:8 + N]))
+    Wd = Wbig.to(cuda)[:, 8:8 + N]
+    out = ops.mm(x.to(cuda), Wd)
+    assert torch.equal(out, ops.mm(x.to(cuda), Wd))
+    assert_tol(out, ref, dtype)
+    o32 = ops.mm(x.to(cuda), Wd, out_dtype=torch.float32)
+    np.testing.assert_allclose(npy(o32), ref, rtol=1e-4, atol=1e-4)
+    ob = ops.addmm(b.to(cuda), x.to(cuda), Wd)
+    assert_tol(ob, O.addmm(npy(b), npy(x), npy(Wbig[:, 8:8 + N])), dtype)
+    torch.cuda.synchronize()
+    assert not ops._WS[(cuda.index or 0, "gemv")][:16384].any()
+
+
 def test_decode_gemm_bias_odd_shapes(cuda):
     for (M, N, K) in [(3, 1000, 520), (1, 8, 8), (7, 4104, 4096)]:
         x, W = gen((M, K), torch.bfloat16, seed=13), gen((K, N), torch.bfloat16, 0.1, seed=14)
