@@ -1,24 +1,21 @@
 // Skinny decode GEMM with deterministic split-K:  out[M, N] = x[M, K] @ W[K, N] (+ bias[N]),
-// 1 <= M <= 64, bf16 / f16 in, fp32 accumulate.
+// 1 <= M <= 64, bf16 / f16 in, fp32 accumulate.  HBM-bound on W (K*N*2 bytes,
+// read exactly once), so each kernel is built around how W streams from HBM.
 //
-// The kernel is HBM-bound on W (K*N*2 bytes, read exactly once), so the design
-// goal is many bytes in flight and no re-reads:
-//   * A wave owns a 128-column strip and consumes W in 32(k) x 128(n) steps
-//     with 16x16x32 MFMAs; x (at most 64 rows) is the MFMA A operand, padded to
-//     16-row blocks with zeros.
-//   * Row-major W ([K, N], N contiguous): lane l loads an 8(k) x 8(n) block
-//     (8 x 16 bytes, rows k0 + 8*(l/16) .. +7, columns 8*(l%16) .. +7) and
-//     transposes it in registers; MFMA number c then covers columns
-//     {8*i + c}, so each lane ends with 8 adjacent output columns.
-//     K-contiguous W ([N, K] storage): the same operand is one 16-byte load.
-//   * A work-group is 4 waves on one strip, interleaving their K steps; the
-//     four partial tiles are summed through LDS in wave order.
-//   * `splits` work-groups share a strip.  Each writes its fp32 partial tile to
-//     the workspace and a second kernel sums the partials in split order
-//     0..splits-1, adds the bias and converts, so the result is bitwise
-//     repeatable.  (Reducing in the last-arriving work-group instead would
-//     need device-scope fences, which on a chip with one L2 per XCD write
-//     back that L2.)
+//   * gemv_rows_kernel (row-major W, M <= 2): VALU dot products; a wave reads
+//     1 KB row segments (512 columns, 8 per lane), a work-group walks a K
+//     range of one 512-column block; K splits merged in-kernel.
+//   * gemv_strip_kernel (row-major W, 3 <= M <= 64): a work-group owns a
+//     64-column strip, streams its rows through LDS by buffer DMA and feeds
+//     16x16x32 MFMAs with x as the A operand (transposing LDS reads give the
+//     W operand); the waves' K ranges are summed in LDS in wave order.
+//   * gemv_splitk_kernel (K-contiguous W, i.e. an nn.Linear weight seen
+//     through .t(), or shapes the others refuse): one 16-byte load per lane is
+//     already an MFMA operand; `splits` work-groups share a strip and
+//     gemv_reduce_kernel sums their partials in split order.
+//
+// Wherever K is split over work-groups the partials are summed in split
+// order 0..splits-1, so results are bitwise repeatable.
 #include <stdlib.h>
 
 #include "common.hpp"
