@@ -419,8 +419,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
     }
 }
 
-// Row-streaming decode GEMM for row-major W and at most 4 rows of x
-// (VALU, no MFMA): lane l of a wave owns 8 adjacent output columns, so one
+// Row-streaming decode GEMM for row-major W and at most 2 rows of x
+// (VALU v_dot2, no MFMA; beyond 2 rows the VALU work bounds it): lane l of a wave owns 8 adjacent output columns, so one
 // 16-byte load per lane covers 512 columns (1 KB) of a W row, and a
 // work-group of 8 waves walks a K range of its 512-column block in groups of
 // 8 rows (wave w takes groups w, w + 8, ...; two groups, 16 loads per lane,
@@ -430,18 +430,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
 // block are summed in split order by the last work-group of that block to
 // arrive (agent-coherent partials and counter, as in the strip kernel), so
 // the result is bitwise repeatable.
+//
+// a.x * b.x + a.y * b.y + c for packed pairs (fp32 accumulate)
 template <typename T>
-__device__ __forceinline__ void unpack8(const u32x4 &v, float *f) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if constexpr (sizeof(T) == 2 && __is_same(T, bf16_t)) {
-            f[2 * i] = __uint_as_float(v[i] << 16);
-            f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
-        } else {
-            const uint32_t u = v[i];
-            f[2 * i] = (float)__builtin_bit_cast(f16_t, (uint16_t)(u & 0xffffu));
-            f[2 * i + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(u >> 16));
-        }
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (__is_same(T, bf16_t)) {
+        typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c, false);
+    } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
     }
 }
 
@@ -475,23 +473,26 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvArgs a) {
         for (int j = 0; j < 8; ++j)
             w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p + j * a.ldw));
     };
-    auto fma8 = [&](int g, const u32x4 *w) __attribute__((always_inline)) {
+    // rows 2p and 2p + 1 of a group pair up for v_dot2 (two products and the
+    // accumulator per instruction): one v_perm_b32 gathers a column's two W
+    // values, and x's consecutive k pair is already one 32-bit word.
+    auto dot8 = [&](int g, const u32x4 *w) __attribute__((always_inline)) {
         const int64_t k = kbeg + 8 * (int64_t)g;
-        float xf[MR][8];
+        u32x4 xv[MR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            // rows past M repeat row M - 1 (not stored)
-            const u32x4 xv = *reinterpret_cast<const u32x4 *>(x + (int64_t)min(m, (int)a.M - 1) * a.ldx + k);
-            unpack8<T>(xv, xf[m]);
-        }
+        for (int m = 0; m < MR; ++m)   // rows past M repeat row M - 1 (not stored)
+            xv[m] = *reinterpret_cast<const u32x4 *>(x + (int64_t)min(m, (int)a.M - 1) * a.ldx + k);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float wf[8];
-            unpack8<T>(w[j], wf);
+        for (int pp = 0; pp < 4; ++pp) {
 #pragma unroll
-            for (int m = 0; m < MR; ++m)
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
-                for (int c = 0; c < 8; ++c) acc[m][c] = __builtin_fmaf(xf[m][j], wf[c], acc[m][c]);
+                for (int e = 0; e < 2; ++e) {
+                    const uint32_t wp = __builtin_amdgcn_perm(w[2 * pp + 1][i], w[2 * pp][i], e ? 0x07060302u : 0x05040100u);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) acc[m][2 * i + e] = dot2<T>(xv[m][pp], wp, acc[m][2 * i + e]);
+                }
+            }
         }
     };
     // wave w: groups w, w + NW, ...; P groups in flight
@@ -504,7 +505,7 @@ __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvArgs a) {
         for (int p = 0; p < P; ++p) {
             const int gg = g + p * NW;
             if (gg < ngroups) {
-                fma8(gg, wr[p]);
+                dot8(gg, wr[p]);
                 if (gg + P * NW < ngroups) load(gg + P * NW, wr[p]);
             }
         }
