@@ -227,12 +227,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
     const int xcd = bid & 7, q8 = nb >> 3, r8 = nb & 7;
     const int strip = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
     const int64_t n0 = (int64_t)strip * SW;
-    // K is cut into splits * NW parts of k_part rows: wave w of split s owns
-    // part s * NW + w.  The last parts may be short or empty; their rows past
-    // K lie outside the buffer range below and load as zeros.
+    // Rows past the split's end (or K) lie outside the buffer range below and
+    // load as zeros.
     const int split = blockIdx.y;
-    const int64_t kbeg = ((int64_t)split * NW + wave) * a.k_part;
-    const int64_t kend = min(a.K, kbeg + a.k_part);
+    // A split covers NW * k_part rows; its waves take the 32-row stages in
+    // turn (wave w: rows kbeg + 32 * (NW * kt + w)), so the waves of a
+    // work-group read neighbouring rows at any moment (cold W streams ~5%
+    // faster than with one contiguous K range per wave).
+    const int64_t kbeg = (int64_t)split * NW * a.k_part + 32 * wave;
+    const int64_t kend = min(a.K, ((int64_t)split + 1) * NW * a.k_part);
+    constexpr int64_t rowstep = 32 * NW;
     const int nst = (int)(a.k_part / 32);
     const T *x = reinterpret_cast<const T *>(a.x);
 
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
         // columns past N read the next row (or zeros past the end); not stored
         goff[j] = (uint32_t)(((int64_t)r * a.ldw + c * 8) * 2);
     }
-    const uint32_t step = (uint32_t)(32 * a.ldw * 2);
+    const uint32_t step = (uint32_t)(rowstep * a.ldw * 2);
     const int lc = lane & 15, G = lane >> 4;
     // x fragments (A operand) travel with their stage's DMA: vmcnt counts in
     // issue order, so a later, separate x load would make every wait drain
@@ -270,7 +274,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rsW, (__attribute__((address_space(3))) void *)to_lds_g(st + wave * STG + j * 1024), 16,
                 (int)(goff[j] + kt * step), 0, 0, 0);
-        const int64_t kl = min(kbeg + (int64_t)kt * 32 + 8 * G, a.K - 8);
+        const int64_t kl = min(kbeg + (int64_t)kt * rowstep + 8 * G, a.K - 8);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
             // unconditional load from a clamped row (no branch around the
@@ -300,7 +304,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
     auto compute = [&](int kt, const char *stg, const u32x4 *xs) __attribute__((always_inline)) {
         // x columns of rows outside [kbeg, kend) meet zero W rows but are
         // zeroed too, so an Inf or NaN there cannot leak into the sum
-        const bool kin = kbeg + (int64_t)kt * 32 + 8 * G < kend;
+        const bool kin = kbeg + (int64_t)kt * rowstep + 8 * G < kend;
         const char *sw = stg + wave * STG;
         frag fb[CG];
 #pragma unroll
