@@ -117,15 +117,20 @@ def profile_kernels(torch, ops, dev):
     for _ in range(3):
         ops.addmm(bias, A, B)
     W = (torch.randn(4096, 11008, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    x = torch.randn(4, 4096, device=dev, generator=g).to(torch.bfloat16)
-    for _ in range(3):
-        ops.mm(x, W)
+    for M in (1, 4, 16):
+        x = torch.randn(M, 4096, device=dev, generator=g).to(torch.bfloat16)
+        for _ in range(3):
+            ops.mm(x, W)
     q, k, v = (torch.randn(1, 32, 4096, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
     for _ in range(3):
         ops.sdpa(q, k, v, is_causal=True)
     qd = torch.randn(1, 32, 1, 128, device=dev, generator=g).to(torch.bfloat16)
     for _ in range(3):
         ops.sdpa(qd, k, v)
+    A3 = torch.randn(32, 2048, 128, device=dev, generator=g).to(torch.bfloat16)
+    B3 = torch.randn(32, 128, 2048, device=dev, generator=g).to(torch.bfloat16)
+    for _ in range(3):
+        ops.bmm(A3, B3)
     src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -171,8 +176,7 @@ def extra_workloads(torch, ops, steps, warmup, dev):
         nbytes = 4096 * 11008 * 2 + M * 4096 * 2 + M * 11008 * 2
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"decode_gemm_M{M}"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 5),
-                                    "roofline": roofline("hbm", gbs, "GB/s",
-                                                         traffic_bytes("decode_gemm_M4") if M == 4 else None),
+                                    "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes(f"decode_gemm_M{M}")),
                                     "warm_same_W_GBs": round(nbytes / (ms_warm * 1e-3) / 1e9, 1)}
     del Ws
     # config 2b: bmm 32 x [2048,128] @ [128,2048]
@@ -182,7 +186,7 @@ def extra_workloads(torch, ops, steps, warmup, dev):
     tf = 2 * 32 * 2048 * 2048 * 128 / (ms * 1e-3) / 1e12
     gbs = (2 * 32 * 2048 * 128 * 2 + 32 * 2048 * 2048 * 2) / (ms * 1e-3) / 1e9
     out["bmm_32x2048x128x2048"] = {"value": round(tf, 1), "unit": "TFLOP/s", "ms": round(ms, 5),
-                                   "roofline": roofline("hbm", gbs, "GB/s"),
+                                   "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes("bmm_32x2048x128x2048")),
                                    "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4)}
     del A3, B3
     # config 3: causal SDPA B=1, H=32, D=128
