@@ -715,6 +715,13 @@ __global__ __launch_bounds__(128) void fa_decode_combine_kernel(AttnArgs a) {
     __shared__ float s_w[64];
     __shared__ float s_M, s_L;
     const float *ml = a.ws_ml + grow * a.splits * 2;
+    // The partial outputs do not depend on the weights: load (up to 32 of)
+    // them together with the split maxima, so the kernel is one round trip.
+    constexpr int PRE = 32;
+    const float *o = a.ws_o + grow * a.splits * HD + min(tid, HD - 1);
+    float op[PRE];
+#pragma unroll
+    for (int z = 0; z < PRE; ++z) op[z] = z < a.splits ? o[z * HD] : 0.f;
     if (tid < 64) {
         const float mz = tid < a.splits ? ml[2 * tid] : -INFINITY;
         const float lz = tid < a.splits ? ml[2 * tid + 1] : 0.f;
@@ -729,10 +736,11 @@ __global__ __launch_bounds__(128) void fa_decode_combine_kernel(AttnArgs a) {
     const float L = s_L, M = s_M;
     const float inv = L > 0.f ? 1.f / L : 0.f;
     if (tid < HD) {
-        const float *o = a.ws_o + grow * a.splits * HD + tid;
         float acc = 0.f;
-#pragma unroll 8
-        for (int z = 0; z < a.splits; ++z) acc += s_w[z] * o[z * HD];
+#pragma unroll
+        for (int z = 0; z < PRE; ++z)
+            if (z < a.splits) acc += s_w[z] * op[z];
+        for (int z = PRE; z < a.splits; ++z) acc += s_w[z] * o[z * HD];
         T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
         Op[tid] = from_f32<T>(acc * inv);
     }
