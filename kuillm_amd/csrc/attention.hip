@@ -834,7 +834,10 @@ static int launch_fwd(AttnArgs a, hipStream_t st) {
     // keeps the scores in accumulation registers and copies them for every
     // softmax step: 1.5x slower, measured.  8 waves of 32 queries, pairs of
     // 256-query blocks one per CU, halve the L2 -> LDS traffic but were 9%
-    // slower at causal S=4096.)
+    // slower at causal S=4096.  At S=2048 (one work-group per CU) an 8-wave
+    // form in which two 4-wave groups split a pair's key blocks evenly, each
+    // in its own LDS half, and merge the shared block's softmax state through
+    // LDS was 5% slower (62.9 against 59.9 us): 256 VGPRs with spills.)
     a.nqb = (int)cdiv(a.l, 128);
     // Causal: pair the query blocks of a head (equal work per work-group)
     // when the pairs still give every CU a work-group.  Single blocks, even
