@@ -69,12 +69,16 @@ def test_hip_graph_replay_matches_eager(cuda):
     k = torch.randn(1, 32, 700, 128, device=cuda, dtype=torch.bfloat16)
     logits = torch.randn(1, 32000, device=cuda)
 
+    bias = torch.randn(11008, device=cuda, dtype=torch.bfloat16)
+
     def step():
         y = ops.mm(x, W)
+        y1 = ops.mm(x[:1], W)                # row-streaming kernel, K split merged in-kernel
+        y2 = ops.addmm(bias, x[:2], W)
         o, _ = ops.sdpa(q, k, k)
         p = ops.softmax(logits)
         t = ops.topk(p, 1)[1]
-        return y, o, p, t
+        return y, y1, y2, o, p, t
 
     eager = step()                   # also allocates the workspaces outside capture
     s = torch.cuda.Stream()
