@@ -458,6 +458,12 @@ __global__ __launch_bounds__(kSmThreads) void softmax_top1_kernel(int64_t n, con
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ A s_a[kSmThreads / 64], s_b[kSmThreads / 64];
     __shared__ unsigned long long s_k[kSmThreads / 64];
+    // the decode state is read up front, so the final writes wait on nothing
+    int32_t pos0 = 0, kv0 = 0;
+    if (tid == 0) {
+        if (pos) pos0 = pos[row];
+        if (kv_len) kv0 = kv_len[row];
+    }
     A v[kSmCache];
     A m = -(A)INFINITY, s = 0;
 #pragma unroll
@@ -508,10 +514,13 @@ __global__ __launch_bounds__(kSmThreads) void softmax_top1_kernel(int64_t n, con
         for (int w = 1; w < kSmThreads / 64; ++w) best = s_k[w] > best ? s_k[w] : best;
         const int64_t i = (int64_t)(0xffffffffu - (uint32_t)best);
         index[row] = i;
-        if (prob) prob[row] = acc_exp((A)to_f32_or_self(x[i]) - m) * inv;
-        if (history && pos && pos[row] >= 0 && pos[row] < hist_len) history[row * hist_len + pos[row]] = i;
-        if (pos) pos[row] += 1;
-        if (kv_len) kv_len[row] += 1;
+        // the winner's probability is in the key: order_key of a value >= 0
+        // is its bit pattern with the top bit set (NaN: all ones)
+        const uint32_t pk = (uint32_t)(best >> 32);
+        if (prob) prob[row] = pk == 0xffffffffu ? __builtin_nanf("") : __uint_as_float(pk & 0x7fffffffu);
+        if (history && pos && pos0 >= 0 && pos0 < hist_len) history[row * hist_len + pos0] = i;
+        if (pos) pos[row] = pos0 + 1;
+        if (kv_len) kv_len[row] = kv0 + 1;
     }
 }
 
