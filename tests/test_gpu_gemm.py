@@ -260,6 +260,25 @@ def test_decode_gemm_row_stream(cuda, M, N, K, dtype):
     assert not ops._WS[(cuda.index or 0, "gemv")][:16384].any()
 
 
+@pytest.mark.parametrize("M", [1, 2])
+def test_decode_gemm_row_stream_strided_x_and_nan(cuda, M):
+    """Row-streaming decode GEMM with x a view whose row stride exceeds K, and
+    a NaN in one x element: the NaN reaches every output of its row (as in
+    aten) and nothing else."""
+    K, N = 2048, 4096
+    xb = gen((M, K + 24), torch.bfloat16, seed=31)
+    W = gen((K, N), torch.bfloat16, 0.02, seed=32)
+    x = xb.to(cuda)[:, 8:8 + K]
+    out = ops.mm(x, W.to(cuda))
+    assert_tol(out, O.mm(npy(xb[:, 8:8 + K]), npy(W)), torch.bfloat16)
+    xn = xb.clone()
+    xn[M - 1, 8 + 1000] = float("nan")
+    outn = ops.mm(xn.to(cuda)[:, 8:8 + K], W.to(cuda))
+    assert torch.isnan(outn[M - 1]).all()
+    if M > 1:
+        assert torch.equal(outn[:M - 1], out[:M - 1])
+
+
 def test_decode_gemm_bias_odd_shapes(cuda):
     for (M, N, K) in [(3, 1000, 520), (1, 8, 8), (7, 4104, 4096)]:
         x, W = gen((M, K), torch.bfloat16, seed=13), gen((K, N), torch.bfloat16, 0.1, seed=14)
