@@ -45,6 +45,15 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/hbm_traffic.{json,md} from two rocprofv3 --pmc runs of "
+                         "--profile-kernels (FETCH_SIZE, then WRITE_SIZE); no GPU needed")
+    ap.add_argument("--summarize-busy", metavar="DIR",
+                    help="write profiles/mfma_busy.{md,json} from a rocprofv3 --pmc run of --profile-kernels "
+                         "with SQ_VALU_MFMA_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("DIR", "OUT_MD"),
+                    help="write a kernel-duration table from a rocprofv3 --kernel-trace run")
+    ap.add_argument("--command", default="", help="the profiling command, recorded in the summary")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="run only the dominant kernel of each workload 3x plus a 256 MiB copy "
                          "(the byte-counter calibration), for rocprofv3 --pmc runs")
@@ -101,62 +110,293 @@ def traffic_bytes(kernel):
     return int(k["fetch_kib"] * 1024 * t["fetch_scale"] + k["write_kib"] * 1024 * t["write_scale"])
 
 
-def roofline(bound, achieved, unit, traffic=None):
+BUSY_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "mfma_busy.json")
+
+
+def mfma_busy(segment):
+    """MFMA-pipe busy fraction of the segment's longest kernel from the
+    committed counter summary (profiles/mfma_busy.json), or None."""
+    try:
+        with open(BUSY_FILE) as f:
+            return json.load(f)["segments"][segment]["mfma_busy"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def roofline(bound, achieved, unit, traffic=None, segment=None):
     peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
-    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": traffic}
+    r = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+         "frac": round(achieved / peak, 4), "traffic": traffic}
+    if bound == "mfma" and segment:
+        r["mfma_busy_counter"] = mfma_busy(segment)
+    return r
+
+
+# Workloads of ``--profile-kernels``, in launch order.  Each segment's steps
+# sit between two torch.cuda._sleep markers ("spin_kernel" dispatches) so that
+# the counter summaries can split the dispatch list without knowing how many
+# kernels a segment launches; every segment runs its step PROFILE_REPS times.
+PROFILE_REPS = 3
+PROFILE_SEGMENTS = ("addmm_4096", "decode_gemm_M1", "decode_gemm_M4", "decode_gemm_M16",
+                    "sdpa_causal_S2048", "sdpa_causal_S4096", "sdpa_decode_kv4096",
+                    "bmm_32x2048x128x2048", "llama1b_decode_token", "copy_256MiB")
+# algorithmic HBM bytes per step of each segment (the "achieved" numerators)
+ALGO_BYTES = {
+    "addmm_4096": 3 * 4096 * 4096 * 2 + 4096 * 2,
+    "decode_gemm_M1": 4096 * 11008 * 2 + 1 * (4096 + 11008) * 2,
+    "decode_gemm_M4": 4096 * 11008 * 2 + 4 * (4096 + 11008) * 2,
+    "decode_gemm_M16": 4096 * 11008 * 2 + 16 * (4096 + 11008) * 2,
+    "sdpa_causal_S2048": 4 * 32 * 2048 * 128 * 2,
+    "sdpa_causal_S4096": 4 * 32 * 4096 * 128 * 2,
+    "sdpa_decode_kv4096": 2 * 32 * 4096 * 128 * 2,
+    "bmm_32x2048x128x2048": 2 * 32 * 2048 * 128 * 2 + 32 * 2048 * 2048 * 2,
+    "copy_256MiB": 2 * 256 * 2 ** 20,
+}
 
 
 def profile_kernels(torch, ops, dev):
-    """The dominant kernel of each measured workload, 3 launches each, then a
-    256 MiB device copy whose byte counts calibrate FETCH_SIZE / WRITE_SIZE."""
+    """The steps of every measured workload, PROFILE_REPS times each, one
+    segment per entry of PROFILE_SEGMENTS (marker first), for rocprofv3
+    --pmc runs; the last segment is a 256 MiB device copy whose byte counts
+    calibrate FETCH_SIZE / WRITE_SIZE.  The Llama segment is one eager
+    decode step (every kernel of one token) after a 512-token prefill."""
     g = torch.Generator(device=dev).manual_seed(0)
-    A = torch.randn(4096, 4096, device=dev, generator=g).to(torch.bfloat16)
-    B = (torch.randn(4096, 4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    bias = (torch.randn(4096, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    for _ in range(3):
-        ops.addmm(bias, A, B)
-    W = (torch.randn(4096, 11008, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    bf = torch.bfloat16
+
+    def segment(name, step):
+        step()                               # allocations and first-touch outside the segment
+        torch.cuda.synchronize()
+        torch.cuda._sleep(1000)              # marker: segment starts
+        for _ in range(PROFILE_REPS):
+            step()
+        torch.cuda._sleep(1000)              # marker: segment ends
+        torch.cuda.synchronize()
+        print(f"profile segment {name} done", flush=True)
+
+    A = torch.randn(4096, 4096, device=dev, generator=g).to(bf)
+    B = (torch.randn(4096, 4096, device=dev, generator=g) * 0.02).to(bf)
+    bias = (torch.randn(4096, device=dev, generator=g) * 0.02).to(bf)
+    segment("addmm_4096", lambda: ops.addmm(bias, A, B))
+    del A, B, bias
+    W = (torch.randn(4096, 11008, device=dev, generator=g) * 0.02).to(bf)
     for M in (1, 4, 16):
-        x = torch.randn(M, 4096, device=dev, generator=g).to(torch.bfloat16)
-        for _ in range(3):
-            ops.mm(x, W)
-    q, k, v = (torch.randn(1, 32, 4096, 128, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
-    for _ in range(3):
-        ops.sdpa(q, k, v, is_causal=True)
-    qd = torch.randn(1, 32, 1, 128, device=dev, generator=g).to(torch.bfloat16)
-    for _ in range(3):
-        ops.sdpa(qd, k, v)
-    A3 = torch.randn(32, 2048, 128, device=dev, generator=g).to(torch.bfloat16)
-    B3 = torch.randn(32, 128, 2048, device=dev, generator=g).to(torch.bfloat16)
-    for _ in range(3):
-        ops.bmm(A3, B3)
+        x = torch.randn(M, 4096, device=dev, generator=g).to(bf)
+        segment(f"decode_gemm_M{M}", lambda: ops.mm(x, W))
+    del W
+    for S in (2048, 4096):
+        q, k, v = (torch.randn(1, 32, S, 128, device=dev, generator=g).to(bf) for _ in range(3))
+        segment(f"sdpa_causal_S{S}", lambda: ops.sdpa(q, k, v, is_causal=True))
+    qd = torch.randn(1, 32, 1, 128, device=dev, generator=g).to(bf)
+    segment("sdpa_decode_kv4096", lambda: ops.sdpa(qd, k, v))
+    del q, k, v
+    A3 = torch.randn(32, 2048, 128, device=dev, generator=g).to(bf)
+    B3 = torch.randn(32, 128, 2048, device=dev, generator=g).to(bf)
+    segment("bmm_32x2048x128x2048", lambda: ops.bmm(A3, B3))
+    del A3, B3
+    from kuillm_amd.decoder import LlamaDecoder, LlamaShape
+    c = LLAMA1B
+    dec = LlamaDecoder(LlamaShape(**c), llama_state(torch, c, dev), capacity=1024, device=dev)
+    dec.prefill(torch.randint(0, c["vocab"], (1, 512), generator=torch.Generator().manual_seed(0)))
+    segment("llama1b_decode_token", dec._decode_step)
+    del dec
     src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+    segment("copy_256MiB", lambda: dst.copy_(src))
+
+
+# ------------------------------------------------ rocprofv3 output summaries
+
+def _find_csv(directory, suffix):
+    import glob
+    hits = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not hits:
+        raise SystemExit(f"no *{suffix} under {directory}")
+    return hits[0]
+
+
+def read_counter_dispatches(directory):
+    """[(kernel name, {counter: value summed over the dispatch})] in dispatch
+    order, from the *_counter_collection.csv of a rocprofv3 --pmc run."""
+    import csv
+    per = {}
+    with open(_find_csv(directory, "counter_collection.csv")) as f:
+        for r in csv.DictReader(f):
+            d = per.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], {}])
+            name = r["Counter_Name"]
+            d[1][name] = d[1].get(name, 0.0) + float(r["Counter_Value"])
+    return [tuple(per[k]) for k in sorted(per)]
+
+
+def split_segments(dispatches):
+    """Group the dispatches of a ``--profile-kernels`` run by segment: spin_kernel
+    markers come in pairs around the steps of each name of PROFILE_SEGMENTS;
+    dispatches outside a pair (input set-up) belong to no segment."""
+    segs, cur = {}, None
+    names = iter(PROFILE_SEGMENTS)
+    for kernel, counters in dispatches:
+        if "spin_kernel" in kernel:
+            if cur is None:
+                cur = next(names)
+                segs[cur] = []
+            else:
+                cur = None
+        elif cur is not None:
+            segs[cur].append((kernel, counters))
+    missing = [n for n in PROFILE_SEGMENTS if n not in segs]
+    if missing:
+        raise SystemExit(f"profile run incomplete: segments {missing} have no marker")
+    return segs
+
+
+def _short(kernel, n=60):
+    k = kernel.split("(")[0]
+    return k if len(k) <= n else k[:n] + "..."
+
+
+def summarize_traffic(fetch_dir, write_dir, out_json, out_md, command):
+    """Per-step HBM bytes of every segment from a FETCH_SIZE run and a
+    WRITE_SIZE run, scaled by what the counters read for the 256 MiB copy."""
+    F = split_segments(read_counter_dispatches(fetch_dir))
+    Wr = split_segments(read_counter_dispatches(write_dir))
+
+    def per_step(seg, counter):
+        return sum(c.get(counter, 0.0) for _, c in seg) / PROFILE_REPS
+
+    copy_bytes_kib = 256 * 1024
+    fscale = copy_bytes_kib / per_step(F["copy_256MiB"], "FETCH_SIZE")
+    wscale = copy_bytes_kib / per_step(Wr["copy_256MiB"], "WRITE_SIZE")
+    res = {"fetch_scale": fscale, "write_scale": wscale,
+           "calibration": f"256 MiB device copy: FETCH_SIZE {copy_bytes_kib / fscale:.1f} KiB, "
+                          f"WRITE_SIZE {copy_bytes_kib / wscale:.1f} KiB per dispatch",
+           "command": command, "kernels": {}}
+    rows = []
+    for name in PROFILE_SEGMENTS[:-1]:
+        fk, wk = per_step(F[name], "FETCH_SIZE"), per_step(Wr[name], "WRITE_SIZE")
+        top = max(F[name], key=lambda kc: kc[1].get("FETCH_SIZE", 0.0))[0] if F[name] else ""
+        res["kernels"][name] = {"kernel": top, "fetch_kib": round(fk, 3), "write_kib": round(wk, 3),
+                                "dispatches_per_step": len(F[name]) // PROFILE_REPS}
+        t = fk * 1024 * fscale + wk * 1024 * wscale
+        alg = ALGO_BYTES.get(name)
+        rows.append(f"| {name} | {len(F[name]) // PROFILE_REPS} | `{_short(top)}` | {fk:.1f} | {wk:.1f} | "
+                    f"{t / 2 ** 20:.1f} MiB | " + (f"{alg / 2 ** 20:.1f} MiB | {t / alg:.2f} |" if alg else "— | — |"))
+    with open(out_json, "w") as f:
+        json.dump(res, f, indent=1)
+    with open(out_md, "w") as f:
+        f.write("# HBM traffic per step (rocprofv3 FETCH_SIZE / WRITE_SIZE)\n\nCommands (repository root):\n\n```\n"
+                f"{command}\n```\n\n{res['calibration']}; scale factors fetch x{fscale:.3f}, write x{wscale:.3f}. "
+                "FETCH_SIZE counts what leaves the L2, so MALL hits count as HBM traffic here.\n\n"
+                "| segment | dispatches / step | largest kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic (scaled) | "
+                "algorithmic bytes | ratio |\n|---|---|---|---|---|---|---|---|\n" + "\n".join(rows) + "\n")
+    print("\n".join(rows))
+
+
+N_XCD, N_SIMD = 8, 256 * 4      # MI355X: 8 XCDs, 256 CUs x 4 SIMDs
+
+
+def summarize_busy(directory, out_md, command):
+    """MFMA-pipe busy fraction and LDS bank conflicts of every segment's
+    kernels from a run with SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE,
+    SQ_LDS_BANK_CONFLICT and SQ_LDS_IDX_ACTIVE.  GRBM_GUI_ACTIVE is summed
+    over the 8 XCDs (per-XCD cycles = value / 8) and the MFMA busy count over
+    the 1024 SIMDs, so busy = (MFMA / 1024) / (GRBM / 8)."""
+    segs = split_segments(read_counter_dispatches(directory))
+    rows, busy_json = [], {"command": command, "segments": {}}
+    for name in PROFILE_SEGMENTS[:-1]:
+        kern = {}
+        for k, c in segs[name]:
+            a = kern.setdefault(k, {"n": 0})
+            a["n"] += 1
+            for ck, v in c.items():
+                a[ck] = a.get(ck, 0.0) + v
+        ranked = sorted(kern.items(), key=lambda kv: -kv[1].get("GRBM_GUI_ACTIVE", 0.0))
+        for k, a in ranked[:2]:
+            n = a["n"]
+            grbm = a.get("GRBM_GUI_ACTIVE", 0.0) / n / N_XCD
+            mfma = a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / n / N_SIMD
+            conf = a.get("SQ_LDS_BANK_CONFLICT", 0.0) / n
+            lds = a.get("SQ_LDS_IDX_ACTIVE", 0.0) / n
+            busy = mfma / grbm if grbm else 0.0
+            rows.append(f"| {name} | `{_short(k)}` | {n // PROFILE_REPS} | {grbm:.0f} | {mfma:.0f} | {busy:.3f} | "
+                        f"{conf:.0f} | {(conf / lds if lds else 0.0):.4f} |")
+            busy_json["segments"].setdefault(name, {"kernel": k, "mfma_busy": round(busy, 4),
+                                                    "lds_bank_conflict_ratio": round(conf / lds, 5) if lds else None})
+    with open(out_md[:-3] + ".json" if out_md.endswith(".md") else out_md + ".json", "w") as f:
+        json.dump(busy_json, f, indent=1)
+    with open(out_md, "w") as f:
+        f.write("# MFMA busy and LDS bank conflicts (rocprofv3 counters)\n\nCommand (repository root):\n\n```\n"
+                f"{command}\n```\n\nPer dispatch: GRBM_GUI_ACTIVE / 8 XCDs = active cycles; "
+                "SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs = MFMA-busy cycles per SIMD; busy = their ratio. "
+                "LDS conflict ratio = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.\n\n"
+                "| segment | kernel | dispatches / step | active cycles | MFMA busy cycles / SIMD | MFMA busy | "
+                "LDS bank-conflict cycles | conflict ratio |\n|---|---|---|---|---|---|---|---|\n"
+                + "\n".join(rows) + "\n")
+    print("\n".join(rows))
+
+
+def summarize_trace(directory, out_md, command, top=40):
+    """Kernel durations from a rocprofv3 --kernel-trace run: per kernel and
+    grid, calls / average / min / max microseconds and share of GPU time."""
+    import csv
+    groups = {}
+    with open(_find_csv(directory, "kernel_trace.csv")) as f:
+        for r in csv.DictReader(f):
+            wx = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+            wy = int(r["Grid_Size_Y"]) // max(1, int(r["Workgroup_Size_Y"]))
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+            groups.setdefault((r["Kernel_Name"], wx, wy), []).append(us)
+    total = sum(sum(v) for v in groups.values()) or 1.0
+    items = sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]
+    rows = [f"| `{_short(k, 90)}` | {wx}, {wy} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
+            f"{100 * sum(v) / total:.1f} |" for (k, wx, wy), v in items]
+    with open(out_md, "w") as f:
+        f.write("# Kernel durations (rocprofv3 kernel trace)\n\nCommand (repository root):\n\n```\n"
+                f"{command}\n```\n\n| kernel | grid x, y (work-groups) | calls | avg us | min us | max us | "
+                "% of GPU time |\n|---|---|---|---|---|---|---|\n" + "\n".join(rows) + "\n")
+    print("\n".join(rows[:15]))
+
+
+def _cpu_median(fn, seconds, max_calls=50):
+    fn()                                          # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < max_calls):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
 
 
 def cpu_baseline(torch, seconds):
-    """Stock torch addmm on the host cores, fp32, same shape as the headline."""
+    """The reference's CPU path -- stock torch aten on the host cores; its
+    families never take CPU tensors (kuipy/kuiops.py:531) -- on the headline
+    addmm shape in fp32 (``value``), and on BASELINE config 0, the
+    GPT-2-small MLP up-projection x[64,768] @ W[768,3072] + bias[3072]
+    (``config0``).  ``cores`` is the number of threads torch used;
+    ``host_cpus`` / ``affinity_cpus`` are what the box offers."""
     threads = torch.get_num_threads()
     g = torch.Generator().manual_seed(0)
     A = torch.randn(4096, 4096, generator=g)
     B = torch.randn(4096, 4096, generator=g) * 0.02
     bias = torch.randn(4096, generator=g) * 0.02
-    torch.addmm(bias, A, B)                      # warm-up
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        torch.addmm(bias, A, B)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
+    med, n = _cpu_median(lambda: torch.addmm(bias, A, B), seconds * 0.7)
+    del A, B, bias
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 768, generator=g)
+    W = torch.randn(768, 3072, generator=g) * 0.02
+    b0 = torch.randn(3072, generator=g) * 0.02
+    med0, n0 = _cpu_median(lambda: torch.addmm(b0, x, W), seconds * 0.3, max_calls=2000)
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
     return {"value": round(2 * 4096 ** 3 / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "reference",
+            "host_cpus": os.cpu_count(), "affinity_cpus": affinity, "kind": "reference",
             "sample": f"stock torch {torch.__version__} CPU fp32 addmm bias[4096] + A[4096,4096] @ "
-                      f"B[4096,4096], median of {len(times)} calls ({med * 1e3:.1f} ms each)"}
+                      f"B[4096,4096], median of {n} calls ({med * 1e3:.1f} ms each)",
+            "config0": {"value": round(2 * 64 * 768 * 3072 / med0 / 1e9, 2), "unit": "GFLOP/s",
+                        "us_per_call": round(med0 * 1e6, 1),
+                        "sample": f"BASELINE config 0: fp32 addmm bias[3072] + x[64,768] @ W[768,3072], "
+                                  f"seed 0, median of {n0} calls"}}
 
 
 def extra_workloads(torch, ops, steps, warmup, dev):
@@ -197,8 +437,8 @@ def extra_workloads(torch, ops, steps, warmup, dev):
         ms = graph_time_ms(torch, lambda: ops.sdpa(q, k, v, is_causal=True), steps, warmup, reps=5)
         tf = 0.5 * 4 * 32 * S * S * 128 / (ms * 1e-3) / 1e12
         out[f"sdpa_causal_S{S}"] = {"value": round(tf, 1), "unit": "TFLOP/s", "ms": round(ms, 5),
-                                    "roofline": roofline("mfma", tf, "TFLOP/s",
-                                                         traffic_bytes("sdpa_causal_S4096") if S == 4096 else None)}
+                                    "roofline": roofline("mfma", tf, "TFLOP/s", traffic_bytes(f"sdpa_causal_S{S}"),
+                                                         f"sdpa_causal_S{S}")}
     # config 3b: decode SDPA, S_q = 1 over a 4096-token KV cache
     # (cold K / V caches cycled as for the decode GEMM: 5 x 67 MB > MALL)
     qd = torch.randn(1, 32, 1, 128, device=dev).to(bf)
@@ -301,13 +541,24 @@ def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3):
             "prefill_tflops": round(flops_prefill / (pre * 1e-3) / 1e12, 1),
             "end_to_end_tokens_per_s": round(n_new / ((pre + dms) * 1e-3), 1),
             "decode_bytes_per_token": int(step_bytes),
-            "roofline": roofline("hbm", gbs, "GB/s"),
+            "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes("llama1b_decode_token")),
             "config": "random-init Llama-style 1B (16 x d2048, GQA 32/8, hd 64, FFN 5632, vocab 32000), "
                       "bf16, batch 1, 512-token prompt, 128 greedy tokens"}
 
 
 def main():
     args = parse()
+    prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic, TRAFFIC_FILE, os.path.join(prof, "hbm_traffic.md"),
+                          args.command)
+        return
+    if args.summarize_busy:
+        summarize_busy(args.summarize_busy, os.path.join(prof, "mfma_busy.md"), args.command)
+        return
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace, args.command)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the kuiops hot "
               "path has no multi-GPU code -- run with --gpus 1.", file=sys.stderr)
@@ -348,7 +599,7 @@ def main():
         "data": "synthetic (seeded N(0,1) / N(0,0.02) tensors, resident in HBM)",
         "config": {"workload": "prefill addmm bf16 bias[4096] + A[4096,4096] @ B[4096,4096], fp32 accumulate",
                    "M": 4096, "N": 4096, "K": 4096, "b_layout": "row-major [K,N]", "parallelism": "single GPU"},
-        "roofline": roofline("mfma", tflops, "TFLOP/s", traffic_bytes("addmm_4096")),
+        "roofline": roofline("mfma", tflops, "TFLOP/s", traffic_bytes("addmm_4096"), "addmm_4096"),
     }
     del A, B, bias
     if not args.no_extra:

@@ -7,241 +7,228 @@ Drop-in usage, as with the reference's ``kuipy`` (kuipy/__init__.py:135-175)::
     with kuipy.KuiperMode():               # or KuiperMode(verify=True)
         model.generate(...)
 
-Inside the mode every aten call on the thread is looked up in the registry;
-a family whose ``supported()`` accepts the call runs the HIP kernel through
-the C ABI of include/kuiops.h, everything else runs stock PyTorch.
-``verify=True`` also runs stock PyTorch on every offloaded op and records the
-relative Frobenius error; ``KUIPY_PRINT_PROFILING=1`` records the signatures
-of the kernel-launching ops seen.
+Public names kept from the reference (kuipy/__init__.py:44-263):
+``KuiperMode(verify, verify_tol)`` with ``dummy_print_mode``, ``is_available``,
+``verify_stats`` / ``reset_verify`` / ``_verify_compare`` /
+``print_verify_report(out_dev, tol)`` and ``print_profile_data(out_dev)``.
+The implementation below is organised around three small pieces of state:
+
+* the offload step (``_offload``): registry lookup + strictness policy;
+* a verify ledger: per-op tallies of the relative Frobenius error between the
+  kernel's result and stock PyTorch's;
+* a call log: the distinct (op, signature) pairs of kernel-launching ops.
 """
 from __future__ import annotations
 
 import sys
 
+import torch
+from torch.utils._python_dispatch import TorchDispatchMode
+from torch.utils._pytree import tree_leaves
+
 from . import config as C
 
 __all__ = ["KuiperMode", "is_available", "verify_stats", "reset_verify", "print_verify_report",
-           "print_profile_data", "profile_data"]
-
-
-# ----------------------------------------------------------- call signatures
-
-def arg_data(a):
-    """Hashable summary of an argument for the profile log."""
-    import torch
-    if isinstance(a, torch.Tensor):
-        shape = tuple(a.shape) if C.JIT_VERBOSITY > 1 else len(a.shape)
-        return (shape, a.dtype, a.device)
-    if isinstance(a, (list, tuple)):
-        return ("list", tuple(arg_data(x) for x in a))
-    if isinstance(a, (torch.dtype, torch.device, bool)):
-        return a
-    return type(a).__name__
-
-
-def print_arg_data(a):
-    if isinstance(a, tuple) and len(a) == 2 and a[0] == "list":
-        return "[" + ", ".join(print_arg_data(x) for x in a[1]) + ", ]"
-    if isinstance(a, tuple) and len(a) == 3:
-        return f"Tensor(nshape={a[0]}, dtype={a[1]}, device={a[2]})"
-    return str(a)
-
-
-def print_call_data_aux(args, kwargs_keys, kwargs_values, ret):
-    kw = ", ".join(f"{k}={print_arg_data(v)}" for k, v in zip(kwargs_keys, kwargs_values))
-    return f"args={[print_arg_data(a) for a in args]}, kwargs={{ {kw} }} -> {print_arg_data(ret)}"
-
-
-def print_call_data(args, kwargs):
-    return print_call_data_aux(tuple(arg_data(a) for a in args), tuple(kwargs.keys()),
-                               tuple(arg_data(v) for v in kwargs.values()), "no return captured")
+           "print_profile_data", "profile_data", "NotOffloaded"]
 
 
 def is_available() -> bool:
     """True when the native library loads and a GPU is visible (the reference
     checks for its F* toolchain instead, kuipy/__init__.py:44-48)."""
     try:
-        import torch
         from . import compile as _compile
         _compile.load_library()
-        return torch.cuda.is_available()
     except Exception:
         return False
+    return torch.cuda.is_available()
 
 
-# ------------------------------------------------------------------ dispatch
-
-_jit_warned = False
-
+# ------------------------------------------------------------ offload step
 
 class NotOffloaded(RuntimeError):
     """Raised at KUIPY_JIT_STRICTNESS=2 for an op no kernel served."""
 
 
-def _jit_try(func, args, kwargs):
-    """Dispatch to a kuiops kernel; None means "run stock PyTorch".
+_warned_once = [False]
 
-    Strictness (kuipy/config.py:42-46 semantics): 0 -- errors warn once and
-    fall back; 1 -- errors raise; 2 -- additionally raise for ops the
-    registry does not serve."""
-    global _jit_warned
+
+def _offload(func, args, kwargs):
+    """The kernel result for ``func(*args, **kwargs)``, or None when stock
+    PyTorch has to run it.
+
+    Strictness levels (the reference's KUIPY_JIT_STRICTNESS,
+    kuipy/config.py:42-46): 0 turns a failing kernel into one warning and a
+    fallback, 1 lets the error propagate, 2 additionally refuses ops that no
+    family serves."""
     from .registry import try_dispatch
+    level = C.JIT_STRICTNESS
     try:
-        ret = try_dispatch(func, args, kwargs)
-    except Exception as e:
-        if C.JIT_STRICTNESS > 0:
+        result = try_dispatch(func, args, kwargs)
+    except Exception as err:
+        if level >= 1:
             raise
-        if not _jit_warned:
-            _jit_warned = True
-            print(f"[kuipy] kernel dispatch failed, falling back to PyTorch: {e}", file=sys.stderr)
-        ret = None
-    if ret is None:
-        if C.JIT_VERBOSITY > 1:
-            print(f"[kuipy] operator {func} ({print_call_data(args, kwargs)}) did not match",
-                  file=sys.stderr)
-        if C.JIT_STRICTNESS > 1:
-            raise NotOffloaded(f"operator {func} was not offloaded (KUIPY_JIT_STRICTNESS=2)")
-    return ret
+        if not _warned_once[0]:
+            _warned_once[0] = True
+            print(f"[kuipy] {func}: kernel failed ({err}); using stock PyTorch from now on "
+                  "for failing calls", file=sys.stderr)
+        result = None
+    if result is not None:
+        return result
+    if C.JIT_VERBOSITY > 1:
+        print(f"[kuipy] no kernel for {func} {_signature(args, kwargs)}", file=sys.stderr)
+    if level >= 2:
+        raise NotOffloaded(f"{func} was not offloaded (KUIPY_JIT_STRICTNESS=2)")
+    return None
 
 
-def _tensors(x):
-    import torch
+# ---------------------------------------------------------------- call log
+
+def _describe(x) -> str:
+    """Compact text for one argument: ``bf16[4,8]@cuda:0`` for a tensor (the
+    rank only, ``bf16[2d]``, unless KUIPY_JIT_VERBOSITY > 1)."""
     if isinstance(x, torch.Tensor):
-        yield x
-    elif isinstance(x, (list, tuple)):
-        for e in x:
-            yield from _tensors(e)
+        dt = str(x.dtype).replace("torch.", "")
+        dims = ",".join(str(int(s)) for s in x.shape) if C.JIT_VERBOSITY > 1 else f"{x.dim()}d"
+        return f"{dt}[{dims}]@{x.device}"
+    if isinstance(x, (list, tuple)):
+        return "(" + " ".join(_describe(e) for e in x) + ")"
+    if isinstance(x, (torch.dtype, torch.device, bool, type(None))):
+        return str(x)
+    return type(x).__name__
 
 
-def _launches_gpu_kernel(func, args, out):
-    """False for view / metadata ops whose outputs alias an input."""
-    if func._schema.is_mutable:
-        return True
-    ins = {t.untyped_storage().data_ptr() for t in _tensors(args)}
-    outs = list(_tensors(out))
-    return not (outs and all(t.untyped_storage().data_ptr() in ins for t in outs))
+def _signature(args, kwargs, result=None) -> str:
+    text = " ".join(_describe(a) for a in args)
+    if kwargs:
+        text += " | " + " ".join(f"{k}={_describe(v)}" for k, v in kwargs.items())
+    if result is not None:
+        text += " -> " + _describe(result)
+    return text
 
 
-def _has_device_kernel(func):
-    """True iff the op registers a direct device kernel (not a composite)."""
-    import torch
-    try:
-        return torch._C._dispatch_has_kernel_for_dispatch_key(func.name(), torch._C.DispatchKey.CUDA)
-    except Exception:
-        return False
+# op -> set of signature strings of the calls seen with KUIPY_PRINT_PROFILING=1
+profile_data: dict = {}
 
 
-profile_data = set()
-_KuiperMode_class = None
+def _record_call(func, args, kwargs, result) -> None:
+    """Log a call that runs a device kernel.  View ops (their schema returns
+    aliases of an input) and calls without a tensor result launch nothing."""
+    if func.is_view or not any(isinstance(t, torch.Tensor) for t in tree_leaves(result)):
+        return
+    profile_data.setdefault(func, set()).add(_signature(args, kwargs, result))
 
 
-def _KuiperMode_cls():
-    global _KuiperMode_class
-    if _KuiperMode_class is not None:
-        return _KuiperMode_class
-    from torch.utils._python_dispatch import TorchDispatchMode
-
-    class KuiperMode(TorchDispatchMode):
-        """Route eligible aten calls to the kuiops HIP kernels.
-
-        ``verify=True`` runs stock PyTorch as well on every non-mutating op a
-        kernel served and folds the relative Frobenius error into
-        ``verify_stats`` (print with ``print_verify_report()``)."""
-        dummy_print_mode = False   # only record profile data, never offload
-
-        def __init__(self, verify=False, verify_tol=2e-2):
-            super().__init__()
-            self.verify = verify
-            self.verify_tol = verify_tol
-
-        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
-            kwargs = kwargs or {}
-            if self.dummy_print_mode:
-                out = func(*args, **kwargs)
-            else:
-                out = _jit_try(func, args, kwargs)
-                if out is None:
-                    out = func(*args, **kwargs)
-                elif self.verify and not func._schema.is_mutable:
-                    _verify_compare(func, out, func(*args, **kwargs), self.verify_tol)
-            if C.ENABLE_PRINT_PROFILING and _launches_gpu_kernel(func, args, out):
-                profile_data.add((func, tuple(arg_data(a) for a in args), tuple(kwargs.keys()),
-                                  tuple(arg_data(v) for v in kwargs.values()), arg_data(out)))
-            return out
-
-    _KuiperMode_class = KuiperMode
-    return KuiperMode
+def print_profile_data(out_dev=sys.stdout):
+    """List every kernel-launching op seen, with its distinct call
+    signatures.  Ops that only decompose into other ops (no device kernel of
+    their own) are marked, since their parts cannot be offloaded one by one."""
+    for func in sorted(profile_data, key=str):
+        try:
+            direct = func.has_kernel_for_dispatch_key(torch._C.DispatchKey.CUDA)
+        except Exception:
+            direct = False
+        note = "" if direct else "  (composite: no device kernel of its own)"
+        print(f"{func}{note}", file=out_dev)
+        for sig in sorted(profile_data[func]):
+            print(f"    {sig}", file=out_dev)
 
 
-def __getattr__(name):
-    if name == "KuiperMode":
-        return _KuiperMode_cls()
-    raise AttributeError(name)
+# ----------------------------------------------------------- verify ledger
 
-
-# -------------------------------------------------------------- verify mode
-
-verify_stats = {}
+# str(op) -> {"n": checked, "fail": over tolerance, "max_rel": largest error,
+#             "worst": text of the latest failure}
+verify_stats: dict = {}
 
 
 def reset_verify():
     verify_stats.clear()
 
 
+def _rel_error(got: torch.Tensor, want: torch.Tensor):
+    """||got - want|| / ||want|| over the positions finite in both, in fp64;
+    None when no position is (e.g. a fully masked attention row)."""
+    g = got.detach().to(torch.float64).reshape(-1)
+    w = want.detach().to(torch.float64).reshape(-1)
+    keep = torch.isfinite(g) & torch.isfinite(w)
+    if not bool(keep.any()):
+        return None
+    zero = torch.zeros((), dtype=torch.float64, device=g.device)
+    diff = torch.where(keep, g - w, zero)
+    base = torch.where(keep, w, zero)
+    return float(torch.linalg.vector_norm(diff) / (torch.linalg.vector_norm(base) + 1e-12))
+
+
 def _verify_compare(func, out, ref, tol):
-    """Fold the relative Frobenius error of each floating output into
-    ``verify_stats[str(func)]`` (kuipy/__init__.py:193-225 semantics):
-    positions not finite in both are ignored (fully masked attention rows),
-    empty references are skipped, shape mismatches count as failures."""
-    name = str(func)
-    st = verify_stats.setdefault(name, {"n": 0, "fail": 0, "max_rel": 0.0, "worst": None})
-    for o, r in zip(_tensors(out), _tensors(ref)):
-        if not (o.is_floating_point() and r.is_floating_point()):
+    """Add one comparison of a kernel's result ``out`` with stock PyTorch's
+    ``ref`` to ``verify_stats[str(func)]``.  Outputs are paired in order;
+    non-floating and empty ones are not compared, a shape disagreement counts
+    as a failure (reference semantics, kuipy/__init__.py:193-225)."""
+    entry = verify_stats.setdefault(str(func), {"n": 0, "fail": 0, "max_rel": 0.0, "worst": None})
+    pairs = zip((t for t in tree_leaves(out) if isinstance(t, torch.Tensor)),
+                (t for t in tree_leaves(ref) if isinstance(t, torch.Tensor)))
+    for got, want in pairs:
+        if not (got.is_floating_point() and want.is_floating_point()) or 0 in (got.numel(), want.numel()):
             continue
-        if r.numel() == 0 or o.numel() == 0:
+        if got.shape != want.shape:
+            entry["fail"] += 1
+            entry["worst"] = f"shape mismatch {tuple(got.shape)} vs {tuple(want.shape)}"
             continue
-        if o.shape != r.shape:
-            st["fail"] += 1
-            st["worst"] = f"shape mismatch {tuple(o.shape)} vs {tuple(r.shape)}"
+        rel = _rel_error(got, want)
+        if rel is None:
             continue
-        of, rf = o.float(), r.float()
-        finite = of.isfinite() & rf.isfinite()
-        if not bool(finite.any()):
-            continue
-        of, rf = of[finite], rf[finite]
-        rel = float((of - rf).norm() / (rf.norm() + 1e-12))
-        st["n"] += 1
-        st["max_rel"] = max(st["max_rel"], rel)
-        if rel > tol:
-            st["fail"] += 1
-            st["worst"] = f"rel={rel:.3e} (tol {tol:.1e})"
+        entry["n"] += 1
+        entry["max_rel"] = max(entry["max_rel"], rel)
+        if not rel <= tol:
+            entry["fail"] += 1
+            entry["worst"] = f"rel={rel:.3e} (tol {tol:.1e})"
 
 
 def print_verify_report(out_dev=sys.stdout, tol=2e-2):
-    """Per-op pass / fail summary of a verify run; returns True when clean."""
+    """Print one line per verified op and an overall verdict.  Returns True
+    when every comparison was within tolerance, False otherwise, and None
+    when nothing was verified."""
     if not verify_stats:
-        print("[verify] no kuiops-dispatched ops were checked.", file=out_dev)
+        print("[verify] nothing was checked (no op was served by a kuiops kernel)", file=out_dev)
         return None
-    total_fail = sum(s["fail"] for s in verify_stats.values())
-    print(f"[verify] kuiops vs stock PyTorch (relative Frobenius norm, tol {tol:.1e}):", file=out_dev)
-    for name in sorted(verify_stats):
-        s = verify_stats[name]
-        status = "FAIL" if s["fail"] else "ok"
-        line = f"  [{status:4}] {name}: {s['n']} checked, {s['fail']} fail, max_rel={s['max_rel']:.3e}"
-        if s["worst"]:
-            line += f", worst: {s['worst']}"
-        print(line, file=out_dev)
-    print(f"[verify] result: {'PASS' if total_fail == 0 else f'FAIL ({total_fail} divergences)'}",
+    width = max(len(k) for k in verify_stats)
+    print(f"[verify] kuiops against stock PyTorch, relative Frobenius error, tolerance {tol:.1e}",
           file=out_dev)
-    return total_fail == 0
+    failures = 0
+    for name, e in sorted(verify_stats.items()):
+        failures += e["fail"]
+        tag = "FAIL" if e["fail"] else "ok"
+        tail = f"  last failure: {e['worst']}" if e["fail"] else ""
+        print(f"  {name:<{width}}  {tag:<4} checked {e['n']:>5}  failed {e['fail']:>4}  "
+              f"max_rel {e['max_rel']:.2e}{tail}", file=out_dev)
+    print("[verify] " + ("PASS" if failures == 0 else f"FAIL: {failures} comparisons over tolerance"),
+          file=out_dev)
+    return failures == 0
 
 
-def print_profile_data(out_dev=sys.stdout):
-    grouped = {}
-    for func, args, kkeys, kvals, ret in profile_data:
-        grouped.setdefault(func, []).append(print_call_data_aux(args, kkeys, kvals, ret))
-    for func, calls in grouped.items():
-        tag = "" if _has_device_kernel(func) else "  [no device kernel: composite]"
-        print(f"Function {func}:{tag}", file=out_dev)
-        for call in calls:
-            print(f"  {call}", file=out_dev)
+# ------------------------------------------------------------- dispatch mode
+
+class KuiperMode(TorchDispatchMode):
+    """Route eligible aten calls to the kuiops HIP kernels; everything else
+    runs stock PyTorch.
+
+    ``verify=True`` also runs stock PyTorch on every non-mutating op a kernel
+    served and adds the comparison to ``verify_stats``.  With
+    ``dummy_print_mode`` set nothing is offloaded and only the call log is
+    kept (KUIPY_PRINT_PROFILING=1)."""
+    dummy_print_mode = False
+
+    def __init__(self, verify=False, verify_tol=2e-2):
+        super().__init__()
+        self.verify = verify
+        self.verify_tol = verify_tol
+
+    def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        result = None if self.dummy_print_mode else _offload(func, args, kwargs)
+        if result is None:
+            result = func(*args, **kwargs)
+        elif self.verify and not func._schema.is_mutable:
+            _verify_compare(func, result, func(*args, **kwargs), self.verify_tol)
+        if C.ENABLE_PRINT_PROFILING:
+            _record_call(func, args, kwargs, result)
+        return result

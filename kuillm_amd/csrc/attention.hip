@@ -767,6 +767,18 @@ static bool attn_common_ok(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_
     return true;
 }
 
+// fa_fwd_kernel addresses one (batch, head)'s K / V through a buffer
+// descriptor whose size field is 31 bits, with 32-bit byte offsets: the last
+// key row must end below 2^31 bytes, and the offsets of the padding rows of
+// the last 64-key block (which read zero past the descriptor) below 2^32.
+static bool fwd_offsets_fit(int64_t s, int64_t e, int64_t sk2, int64_t sv2) {
+    if (s == 0) return true;
+    if (sk2 < 0 || sv2 < 0) return false;
+    const int64_t st = sk2 > sv2 ? sk2 : sv2;
+    if (((s - 1) * st + e) * 2 >= (int64_t(1) << 31)) return false;
+    return ((s + 64) * st + e) * 2 < (int64_t(1) << 32);
+}
+
 static void fill_args(AttnArgs &a, int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, const void *Q,
                       const int64_t *sq, const void *K, const int64_t *sk, const void *V, const int64_t *sv,
                       void *O, const int64_t *so, float *lse, float scale, int causal) {
@@ -915,6 +927,7 @@ extern "C" int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, in
     }
     if (n == 0 || hq == 0 || l == 0) return KUIOPS_OK;
     if (hq > 65535 || n > 65535) return KUIOPS_E_UNSUPPORTED;
+    if (!fwd_offsets_fit(s, e, sk[2], sv[2])) return KUIOPS_E_UNSUPPORTED;
     AttnArgs a{};
     fill_args(a, n, hq, hkv, l, s, Q, sq, K, sk, V, sv, O, so, lse, scale, causal);
     hipStream_t st = as_stream(stream);

@@ -51,16 +51,33 @@ def _dt(dtype) -> int:
 # ----------------------------------------------------------------- workspace
 # One buffer per (device, kind).  "gemv" and "attn" hold split arrival
 # counters (decode GEMM, decode attention), which must start at zero: they
-# are zero-filled when allocated and the kernels leave the counters at zero.  "scratch" is plain partial-result space.
+# are zero-filled when allocated and the kernels leave the counters at zero.
+# "scratch" is plain partial-result space.
+#
+# A HIP graph records the raw address of the buffer it was captured with, so
+# a buffer is never freed once handed out: when a call needs more bytes, the
+# old buffer moves to _RETIRED (kept alive for the life of the process, its
+# counters still zero) and a larger one replaces it for later calls.  Growing
+# during capture would put the new allocation and its zero fill inside the
+# graph, so it is refused: run the largest shape once eagerly first.
+# Kernels that use one kind of workspace on one device must not run
+# concurrently on two streams (the counters would be shared).
 _WS = {}
+_RETIRED = []
 
 
 def workspace(device: torch.device, nbytes: int, kind: str = "scratch") -> torch.Tensor:
     key = (device.index if device.index is not None else torch.cuda.current_device(), kind)
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
+        if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"kuiops workspace '{kind}' must grow to {nbytes} bytes during HIP graph capture; "
+                "run the same calls once outside capture first")
         size = max(int(nbytes), 1 << 20)
         size = (size + (1 << 20) - 1) // (1 << 20) * (1 << 20)
+        if buf is not None:
+            _RETIRED.append(buf)
         buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _WS[key] = buf
     return buf

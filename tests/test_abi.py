@@ -94,6 +94,27 @@ def test_host_side_argument_validation(lib):
                                None) == _lib.E_UNSUPPORTED
 
 
+@pytest.mark.parametrize("s, sk2, sv2", [
+    (262145, 4096, 128),          # (B, S, H, D) keys, H*D = 4096: last key row ends past 2^31 bytes
+    (262145, 128, 4096),          # the same through V
+    (600000, 4096, 4096),         # far past: a 32-bit offset would wrap onto other keys
+    (40, 1 << 27, 128),           # huge key stride: the padded last block passes 2^32
+    (8, -64, 128),                # negative strides are never addressed by a descriptor
+])
+def test_sdpa_fwd_rejects_keys_beyond_32bit_offsets(lib, s, sk2, sv2):
+    # fa_fwd_kernel reads K / V through buffer descriptors with 32-bit byte
+    # offsets; the entry point must refuse shapes they cannot address rather
+    # than read zeros or wrap (host-side gate, nothing is launched).
+    p = ctypes.c_void_p(1 << 20)
+    sq = _lib.strides3(0, 0, 128)
+    so = _lib.strides3(0, 0, 128)
+    sk = _lib.strides3(0, 0, sk2)
+    sv = _lib.strides3(0, 0, sv2)
+    for causal in (0, 1):
+        assert lib.kuiops_sdpa_fwd(1, 1, 1, 1, s, 128, 128, _lib.BF16, p, sq, p, sk, p, sv, p, so, None,
+                                   0.088, causal, None) == _lib.E_UNSUPPORTED
+
+
 def test_error_mapping():
     with pytest.raises(_lib.Unsupported):
         _lib.check("x", _lib.E_UNSUPPORTED)
