@@ -159,6 +159,25 @@ KUIOPS_API int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
                        int splits, void *workspace, size_t workspace_bytes,
                        void *stream);
 
+/* kuiops_gemv_splitk without a workspace argument: it allocates nothing
+ * (no hipMalloc / hipFree, no torch, no allocating library call), so it can
+ * be called by code that may not allocate -- under HIP graph capture, in
+ * tight serving loops, from harnesses that forbid allocation.  No
+ * counterpart in the reference.  Split partials and arrival counters live in
+ * a file-scope device array of kuiops_gemv_splitk_noalloc_max_bytes() bytes
+ * per GPU (8 MiB), held until the process ends; a shape whose workspace
+ * (kuiops_query_workspace) exceeds it returns KUIOPS_E_WORKSPACE.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU race.
+ * The counters it uses are cleared by a fill kernel at the start of each
+ * call.  Same kernels and results as kuiops_gemv_splitk.                 */
+KUIOPS_API int kuiops_gemv_splitk_noalloc(int64_t M, int64_t N, int64_t K, int in_dtype,
+                       const void *x, int64_t ldx,
+                       const void *W, int64_t ldw, int w_layout,
+                       const void *bias,
+                       int out_dtype, void *out, int64_t ldo,
+                       int splits, void *stream);
+KUIOPS_API size_t kuiops_gemv_splitk_noalloc_max_bytes(void);
+
 /* ---------------------------------------------------------------- SDPA --
  * Flash-attention forward: O = softmax(scale * Q K^T [+ causal mask]) V,
  * LSE = logsumexp over keys (natural log, fp32, optional: pass NULL).

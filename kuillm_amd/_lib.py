@@ -52,6 +52,9 @@ SIGNATURES = {
                           _int, _vp, _i64, _i64, _vp]),
     "kuiops_gemv_splitk": (_int, [_i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _int, _vp, _int,
                                   _vp, _i64, _int, _vp, _sz, _vp]),
+    "kuiops_gemv_splitk_noalloc": (_int, [_i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _int, _vp, _int,
+                                          _vp, _i64, _int, _vp]),
+    "kuiops_gemv_splitk_noalloc_max_bytes": (_sz, []),
     "kuiops_sdpa_fwd": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
                                _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp]),
     "kuiops_sdpa_decode": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,

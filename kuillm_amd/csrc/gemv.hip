@@ -20,6 +20,8 @@
 
 #include "common.hpp"
 
+#include <mutex>
+
 namespace kuiops {
 
 struct GemvArgs {
@@ -731,10 +733,77 @@ static int rows_dispatch(const GemvArgs &a, hipStream_t st) {
 
 using namespace kuiops;
 
+static void clear_counters_on(unsigned *counters, int64_t n, hipStream_t st);
+
+static int gemv_run(int64_t M, int64_t N, int64_t K, int in_dtype, const void *x, int64_t ldx, const void *W,
+                    int64_t ldw, int w_layout, const void *bias, int out_dtype, void *out, int64_t ldo, int splits,
+                    void *workspace, size_t workspace_bytes, bool clear_counters, void *stream);
+
 extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype, const void *x, int64_t ldx,
                                   const void *W, int64_t ldw, int w_layout, const void *bias, int out_dtype,
                                   void *out, int64_t ldo, int splits, void *workspace, size_t workspace_bytes,
                                   void *stream) {
+    return gemv_run(M, N, K, in_dtype, x, ldx, W, ldw, w_layout, bias, out_dtype, out, ldo, splits, workspace,
+                    workspace_bytes, false, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the same kernels with their workspace in a
+// file-scope device array instead of caller / torch memory.  Each GPU holds
+// its own copy of `scratch` (at its own address, found once per device with
+// hipGetSymbolAddress) for the life of the process.  Calls that overlap on
+// one GPU share it and race.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+__global__ void clear_u32_kernel(unsigned *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+static int scratch_for_current_device(void **ptr) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return KUIOPS_E_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return KUIOPS_E_HIP;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return KUIOPS_OK;
+}
+
+// The arrival counters must be zero when a split kernel starts.  The kernels
+// leave them at zero, but the shared array keeps whatever the previous call
+// on this GPU left, so every allocation-free call clears the counters it
+// uses first (a fill kernel, not a memset, so the call can be captured).
+static void clear_counters_on(unsigned *counters, int64_t n, hipStream_t st) {
+    hipLaunchKernelGGL(clear_u32_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, counters, (int)n);
+}
+
+extern "C" size_t kuiops_gemv_splitk_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int kuiops_gemv_splitk_noalloc(int64_t M, int64_t N, int64_t K, int in_dtype, const void *x,
+                                          int64_t ldx, const void *W, int64_t ldw, int w_layout, const void *bias,
+                                          int out_dtype, void *out, int64_t ldo, int splits, void *stream) {
+    if (M < 0 || N < 0 || K < 0) return KUIOPS_E_INVALID;
+    if (M == 0 || N == 0) return KUIOPS_OK;
+    if (M <= 64 && gemv_workspace_bytes(M, N, K) > kNoAllocScratchBytes) return KUIOPS_E_WORKSPACE;
+    void *ws = nullptr;
+    const int st = scratch_for_current_device(&ws);
+    if (st != KUIOPS_OK) return st;
+    return gemv_run(M, N, K, in_dtype, x, ldx, W, ldw, w_layout, bias, out_dtype, out, ldo, splits, ws,
+                    kNoAllocScratchBytes, true, stream);
+}
+
+static int gemv_run(int64_t M, int64_t N, int64_t K, int in_dtype, const void *x, int64_t ldx, const void *W,
+                    int64_t ldw, int w_layout, const void *bias, int out_dtype, void *out, int64_t ldo, int splits,
+                    void *workspace, size_t workspace_bytes, bool clear_counters, void *stream) {
     if (M < 0 || N < 0 || K < 0) return KUIOPS_E_INVALID;
     if (w_layout != KUIOPS_B_ROW && w_layout != KUIOPS_B_COL) return KUIOPS_E_INVALID;
     if (M == 0 || N == 0) return KUIOPS_OK;
@@ -761,6 +830,7 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
             if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
             a.counters = reinterpret_cast<unsigned *>(workspace);
             a.partial = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + kGemvCounterBytes);
+            if (clear_counters) clear_counters_on(a.counters, cdiv(N, kRowsCB), st0);
         }
         if (in_dtype == KUIOPS_BF16)
             return out_dtype == KUIOPS_F32 ? rows_dispatch<bf16_t, float>(a, st0) : rows_dispatch<bf16_t, bf16_t>(a, st0);
@@ -773,6 +843,7 @@ extern "C" int kuiops_gemv_splitk(int64_t M, int64_t N, int64_t K, int in_dtype,
             if (!workspace || workspace_bytes < need || !aligned16(workspace)) return KUIOPS_E_WORKSPACE;
             a.counters = reinterpret_cast<unsigned *>(workspace);
             a.partial = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) + kGemvCounterBytes);
+            if (clear_counters) clear_counters_on(a.counters, cdiv(N, kStripW), st0);
         }
         if (in_dtype == KUIOPS_BF16)
             return out_dtype == KUIOPS_F32 ? strip_dispatch<bf16_t, float>(a, st0) : strip_dispatch<bf16_t, bf16_t>(a, st0);
