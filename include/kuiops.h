@@ -408,6 +408,64 @@ KUIOPS_API int kuiops_decode_qkv_rope(int64_t hq, int64_t hkv, int64_t hd, int64
                            void *v_cache, int64_t sv_head, int64_t sv_pos, int64_t cache_cap,
                            void *stream);
 
+/* ----------------------------------------------- elementwise / mean / cat --
+ * The reference's generic glue families: ElementwiseImpl
+ * (kuipy/kuiops.py:150-320, its 21 aten overloads registered at
+ * kuipy/registry.py:33-53), MeanImpl (kuipy/kuiops.py:860-921) and CatImpl
+ * (kuipy/kuiops.py:810-857); each replaces the per-instantiation launcher of
+ * kuiops/{elementwise,mean,cat}/wrapper_*.cu.j2.                            */
+
+/* Elementwise op codes.  Values are part of the ABI. */
+typedef enum kuiops_ew_op {
+    KUIOPS_EW_ADD = 0,          /* a + s0 * b           (aten.add, alpha = s0)   */
+    KUIOPS_EW_SUB = 1,          /* a - s0 * b           (aten.sub, alpha = s0)   */
+    KUIOPS_EW_MUL = 2,
+    KUIOPS_EW_DIV = 3,          /* true division                                 */
+    KUIOPS_EW_NEG = 4,
+    KUIOPS_EW_SILU = 5,         /* a / (1 + exp(-a))                             */
+    KUIOPS_EW_RSQRT = 6,
+    KUIOPS_EW_COS = 7,
+    KUIOPS_EW_SIN = 8,
+    KUIOPS_EW_EXP = 9,
+    KUIOPS_EW_SQRT = 10,
+    KUIOPS_EW_POW_SCALAR = 11,  /* a ^ s0 (aten.pow.Tensor_Scalar)               */
+    KUIOPS_EW_EQ = 12,          /* comparisons: bool output                      */
+    KUIOPS_EW_NE = 13,
+    KUIOPS_EW_LE = 14,
+    KUIOPS_EW_LT = 15,
+    KUIOPS_EW_GE = 16,
+    KUIOPS_EW_GT = 17,
+    KUIOPS_EW_WHERE = 18,       /* a ? b : c (aten.where.self)                   */
+    KUIOPS_EW_BITWISE_NOT = 19, /* integer / bool operands                       */
+    KUIOPS_EW_BITWISE_AND = 20,
+    KUIOPS_EW_BITWISE_OR = 21
+} kuiops_ew_op;
+
+/* out = op(in[0], in[1], in[2]) over `shape` (rank <= 8), with
+ * broadcasting: operand k's element at index (i0..) is at
+ * in_ptrs[k] + sum_d i_d * in_strides[k * rank + d] elements (stride 0 =
+ * broadcast).  `out` is contiguous of `shape`.  n_in = the op's arity, or 1
+ * for a binary op whose second operand is the scalar s1.  s0 is add / sub's
+ * alpha or pow's exponent.  compute_dtype is F32 (for 16/32-bit float
+ * results, aten's opmath), F64 or I64 (integers, bool, bitwise ops); every
+ * operand is converted to it, and the result is rounded once to out_dtype.  */
+KUIOPS_API int kuiops_elementwise(int op, int rank, const int64_t *shape, int n_in, const int *in_dtypes,
+                       const void *const *in_ptrs, const int64_t *in_strides, double s0, double s1,
+                       int compute_dtype, int out_dtype, void *out, void *stream);
+
+/* out[r] = mean(x[r, 0:n]) for r < m; rows at stride ldx (elements), unit
+ * stride within a row; out has x's dtype (F32, BF16, F16, F64); fp32 (fp64)
+ * accumulation, the sum scaled by m / (m*n) as aten's mean.dim scales it.  */
+KUIOPS_API int kuiops_mean_lastdim(int64_t m, int64_t n, int dtype, const void *x, int64_t ldx, void *out,
+                        void *stream);
+
+/* Concatenation viewed as `outer` rows: input i contributes widths[i]
+ * elements to every output row, read from inputs[i] + o * outer_strides[i];
+ * output rows are contiguous of sum(widths) elements, inputs in order.
+ * n_inputs <= 32; elem_bytes 1, 2, 4 or 8 (a byte copy: any dtype).         */
+KUIOPS_API int kuiops_cat(int n_inputs, const void *const *inputs, const int64_t *widths,
+               const int64_t *outer_strides, int64_t outer, int elem_bytes, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,9 @@ F32, F16, BF16, F64, I64, I32, I16, I8, U8, BOOL = range(10)
 B_ROW, B_COL = 0, 1
 # kuiops_c_kind
 C_NONE, C_FULL, C_ROW = 0, 1, 2
+# kuiops_ew_op
+EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_NEG, EW_SILU, EW_RSQRT, EW_COS, EW_SIN, EW_EXP, EW_SQRT, EW_POW_SCALAR, \
+    EW_EQ, EW_NE, EW_LE, EW_LT, EW_GE, EW_GT, EW_WHERE, EW_BITWISE_NOT, EW_BITWISE_AND, EW_BITWISE_OR = range(22)
 # kuiops_op
 OP_ADDMM, OP_GEMV_SPLITK, OP_SDPA_DECODE, OP_TOPK, OP_SORT = 1, 2, 3, 4, 5
 
@@ -55,6 +58,10 @@ SIGNATURES = {
     "kuiops_gemv_splitk_noalloc": (_int, [_i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _int, _vp, _int,
                                           _vp, _i64, _int, _vp]),
     "kuiops_gemv_splitk_noalloc_max_bytes": (_sz, []),
+    "kuiops_elementwise": (_int, [_int, _int, _i64p, _int, ctypes.POINTER(_int), ctypes.POINTER(_vp), _i64p,
+                                  _dbl, _dbl, _int, _int, _vp, _vp]),
+    "kuiops_mean_lastdim": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _vp]),
+    "kuiops_cat": (_int, [_int, ctypes.POINTER(_vp), _i64p, _i64p, _i64, _int, _vp, _vp]),
     "kuiops_sdpa_fwd": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
                                _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp]),
     "kuiops_sdpa_decode": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,

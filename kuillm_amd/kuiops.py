@@ -514,5 +514,207 @@ class IndexImpl(_Family):
             return None
 
 
-ALL_FAMILIES = (MmImpl, AddmmImpl, BmmImpl, SoftmaxImpl, SdpaImpl, TopkImpl, GatherImpl, IndexImpl)
+# ------------------------------------------- elementwise / mean / cat
+
+def _operand(x, device):
+    """A tensor operand on ``device``, a python scalar (numbers and 0-d CPU
+    tensors, which aten treats as wrapped scalars), or None when neither."""
+    if isinstance(x, torch.Tensor):
+        if x.is_complex():
+            return None
+        if x.device == device:
+            return x
+        if x.dim() == 0 and x.device.type == "cpu" and not x.is_meta:
+            return x.item()
+        return None
+    if isinstance(x, (bool, int, float)):
+        return x
+    return None
+
+
+def _compute_dtype(dtype):
+    if dtype == torch.float64:
+        return torch.float64
+    if dtype.is_floating_point:
+        return torch.float32
+    return torch.int64
+
+
+class ElementwiseImpl(_Family):
+    """The reference's ElementwiseImpl (kuipy/kuiops.py:150-320): unary maps,
+    binary maps with a tensor or scalar second operand, scalar comparisons,
+    where and bitwise ops, over the aten overloads of kuipy/registry.py:33-53
+    -> kuiops_elementwise.
+
+    Wider than the reference's gate: operands may broadcast and be strided,
+    dtypes promote as aten promotes them (bf16 * fp32 -> fp32), the Tensor
+    forms of the comparisons are served, and exp / sqrt / ne / ge / gt are
+    added.  Arithmetic is aten's: 16-bit floats compute in fp32, python
+    scalars enter unrounded."""
+    tune_key = "ELEM"
+    tune_params = ()
+
+    _UNARY = {aten.silu.default: _lib.EW_SILU, aten.neg.default: _lib.EW_NEG, aten.rsqrt.default: _lib.EW_RSQRT,
+              aten.cos.default: _lib.EW_COS, aten.sin.default: _lib.EW_SIN, aten.exp.default: _lib.EW_EXP,
+              aten.sqrt.default: _lib.EW_SQRT}
+    _BINARY = {aten.add.Tensor: _lib.EW_ADD, aten.add.Scalar: _lib.EW_ADD, aten.sub.Tensor: _lib.EW_SUB,
+               aten.sub.Scalar: _lib.EW_SUB, aten.mul.Tensor: _lib.EW_MUL, aten.mul.Scalar: _lib.EW_MUL,
+               aten.div.Tensor: _lib.EW_DIV, aten.div.Scalar: _lib.EW_DIV}
+    _COMPARE = {aten.eq.Scalar: _lib.EW_EQ, aten.eq.Tensor: _lib.EW_EQ, aten.ne.Scalar: _lib.EW_NE,
+                aten.ne.Tensor: _lib.EW_NE, aten.le.Scalar: _lib.EW_LE, aten.le.Tensor: _lib.EW_LE,
+                aten.lt.Scalar: _lib.EW_LT, aten.lt.Tensor: _lib.EW_LT, aten.ge.Scalar: _lib.EW_GE,
+                aten.ge.Tensor: _lib.EW_GE, aten.gt.Scalar: _lib.EW_GT, aten.gt.Tensor: _lib.EW_GT}
+    _BITWISE = {aten.bitwise_not.default: _lib.EW_BITWISE_NOT, aten.bitwise_and.Tensor: _lib.EW_BITWISE_AND,
+                aten.bitwise_or.Tensor: _lib.EW_BITWISE_OR}
+    OPS = (tuple(_UNARY) + tuple(_BINARY) + tuple(_COMPARE) + tuple(_BITWISE)
+           + (aten.pow.Tensor_Scalar, aten.where.self))
+
+    def supported(self, func, args, kwargs):
+        if not args or not _is_dev(args[0]) or args[0].is_complex():
+            return None
+        A = args[0]
+        dev = A.device
+        if func in self._UNARY:
+            if len(args) != 1 or kwargs:
+                return None
+            if not (A.dtype.is_floating_point or (func == aten.neg.default and A.dtype != torch.bool)):
+                return None
+            return (self._UNARY[func], [A], A.dtype, _compute_dtype(A.dtype), 1.0, 0.0)
+        if func == aten.pow.Tensor_Scalar:
+            e = args[1] if len(args) > 1 else None
+            if not A.dtype.is_floating_point or isinstance(e, bool) or not isinstance(e, (int, float)):
+                return None
+            return (_lib.EW_POW_SCALAR, [A], A.dtype, _compute_dtype(A.dtype), float(e), 0.0)
+        if func == aten.where.self:
+            if len(args) != 3 or A.dtype != torch.bool:
+                return None
+            x, y = (_operand(t, dev) for t in args[1:])
+            if x is None or y is None:
+                return None
+            out = torch.result_type(args[1], args[2])
+            return (_lib.EW_WHERE, [A, x, y], out, _compute_dtype(out), 1.0, 0.0)
+        if func in self._BITWISE:
+            return None if kwargs else self._bitwise(func, args)
+        if len(args) != 2:
+            return None
+        other = _operand(args[1], dev)
+        if other is None:
+            return None
+        out = torch.result_type(A, args[1] if isinstance(args[1], torch.Tensor) else other)
+        if func in self._COMPARE:
+            if kwargs:
+                return None
+            return self._binary_spec(self._COMPARE[func], A, other, torch.bool, _compute_dtype(out), 1.0)
+        op = self._BINARY.get(func)
+        if op is None:
+            return None
+        alpha = 1.0
+        if op in (_lib.EW_ADD, _lib.EW_SUB):
+            a = kwargs.get("alpha", 1)
+            if isinstance(a, bool) or not isinstance(a, (int, float)):
+                return None
+            alpha = float(a)
+            if op == _lib.EW_SUB and out == torch.bool:
+                return None
+        elif kwargs.get("rounding_mode") is not None or set(kwargs) - {"rounding_mode"}:
+            return None
+        if op == _lib.EW_DIV and not out.is_floating_point:
+            out = torch.get_default_dtype()
+        return self._binary_spec(op, A, other, out, _compute_dtype(out), alpha)
+
+    @staticmethod
+    def _binary_spec(op, A, other, out, compute, alpha):
+        if isinstance(other, torch.Tensor):
+            return (op, [A, other], out, compute, alpha, 0.0)
+        return (op, [A], out, compute, alpha, float(other))
+
+    def _bitwise(self, func, args):
+        A = args[0]
+        if A.dtype.is_floating_point:
+            return None
+        if func == aten.bitwise_not.default:
+            return (_lib.EW_BITWISE_NOT, [A], A.dtype, torch.int64, 1.0, 0.0) if len(args) == 1 else None
+        if len(args) != 2 or not _is_dev(args[1]) or args[1].device != A.device or args[1].dtype.is_floating_point:
+            return None
+        out = torch.promote_types(A.dtype, args[1].dtype)
+        return (self._BITWISE[func], [A, args[1]], out, torch.int64, 1.0, 0.0)
+
+    def run(self, spec, args, kwargs):
+        op, inputs, out, compute, s0, s1 = spec
+        dev = inputs[0].device
+        # where's scalar branches become 0-d device tensors (a fill kernel)
+        inputs = [t if isinstance(t, torch.Tensor) else torch.full((), t, dtype=out, device=dev) for t in inputs]
+        try:
+            return K.elementwise(op, inputs, out, compute, s0, s1)
+        except _lib.Unsupported:
+            return None
+
+
+class MeanImpl(_Family):
+    """aten.mean.dim over the last axis -> kuiops_mean_lastdim (reference
+    MeanImpl kuipy/kuiops.py:860-921, which takes keepdim=True only; both
+    keepdim forms are served here)."""
+    tune_key = "MEAN"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if len(args) < 2 or not _is_dev(args[0]):
+            return None
+        X, dim = args[0], args[1]
+        keepdim = args[2] if len(args) > 2 else kwargs.get("keepdim", False)
+        dt = kwargs.get("dtype")
+        if (dt is not None and dt != X.dtype) or X.dtype not in _FLOAT_DTYPES or X.dim() < 1:
+            return None
+        if isinstance(dim, (list, tuple)):
+            if len(dim) != 1:
+                return None
+            dim = dim[0]
+        if dim is None or _norm_dim(int(dim), X.dim()) != X.dim() - 1 or X.shape[-1] == 0:
+            return None
+        return (X, bool(keepdim))
+
+    def run(self, spec, args, kwargs):
+        X, keepdim = spec
+        try:
+            return K.mean_lastdim(X, keepdim)
+        except _lib.Unsupported:
+            return None
+
+
+class CatImpl(_Family):
+    """aten.cat.default -> kuiops_cat (reference CatImpl kuipy/kuiops.py:810-857,
+    two inputs only; here up to 32 inputs of one dtype and rank, strided
+    inputs read in place when each row of the concatenated dims is one run)."""
+    tune_key = "CAT"
+    tune_params = ()
+
+    def supported(self, func, args, kwargs):
+        if not args:
+            return None
+        tensors = args[0]
+        dim = args[1] if len(args) > 1 else kwargs.get("dim", 0)
+        if not isinstance(tensors, (list, tuple)) or not 1 <= len(tensors) <= 32:
+            return None
+        A = tensors[0]
+        if not _is_dev(*tensors) or A.dim() < 1:
+            return None
+        if any(t.dtype != A.dtype or t.device != A.device or t.dim() != A.dim() for t in tensors):
+            return None
+        d = _norm_dim(int(dim), A.dim())
+        if not 0 <= d < A.dim():
+            return None
+        if any(t.shape[i] != A.shape[i] for t in tensors for i in range(A.dim()) if i != d):
+            return None
+        return (list(tensors), d)
+
+    def run(self, spec, args, kwargs):
+        tensors, d = spec
+        try:
+            return K.cat(tensors, d)
+        except _lib.Unsupported:
+            return None
+
+
+ALL_FAMILIES = (MmImpl, AddmmImpl, BmmImpl, SoftmaxImpl, SdpaImpl, TopkImpl, GatherImpl, IndexImpl, ScatterImpl,
+                SortImpl, CumsumImpl, MultinomialImpl, ElementwiseImpl, MeanImpl, CatImpl)
 log(f"kuiops families: {[f.__name__ for f in ALL_FAMILIES]}")

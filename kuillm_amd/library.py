@@ -12,7 +12,7 @@ back silently.
 
 Schemas follow the aten ops they replace (mm, addmm, bmm, _softmax over the
 last dim, scaled-dot-product attention returning (out, lse), topk, gather,
-single-tensor index) with the reference's argument meaning
+index, the elementwise maps, last-axis mean, cat) with the reference's argument meaning
 (kuipy/kuiops.py:403-754).
 """
 from __future__ import annotations
@@ -38,6 +38,10 @@ _SCHEMAS = {
     "sort": "sort(Tensor x, int dim=-1, bool descending=False) -> (Tensor, Tensor)",
     "cumsum": "cumsum(Tensor x, int dim) -> Tensor",
     "multinomial": "multinomial(Tensor probs, int num_samples, Tensor uniforms) -> Tensor",
+    "elementwise": "elementwise(int op, Tensor[] inputs, ScalarType out_dtype, ScalarType compute_dtype, "
+                   "float s0=1.0, float s1=0.0) -> Tensor",
+    "mean_lastdim": "mean_lastdim(Tensor x, bool keepdim=False) -> Tensor",
+    "cat": "cat(Tensor[] tensors, int dim=0) -> Tensor",
 }
 for _s in _SCHEMAS.values():
     _LIB.define(_s)
@@ -100,10 +104,23 @@ def _multinomial(probs, num_samples, uniforms):
     return ops.multinomial(probs, num_samples, replacement=True, uniforms=uniforms)
 
 
+def _elementwise(op, inputs, out_dtype, compute_dtype, s0=1.0, s1=0.0):
+    return ops.elementwise(op, list(inputs), out_dtype, compute_dtype, s0=s0, s1=s1)
+
+
+def _mean_lastdim(x, keepdim=False):
+    return ops.mean_lastdim(x, keepdim)
+
+
+def _cat(tensors, dim=0):
+    return ops.cat(list(tensors), dim)
+
+
 for _name, _fn in (("mm", _mm), ("addmm", _addmm), ("bmm", _bmm), ("softmax", _softmax),
                    ("sdpa", _sdpa), ("sdpa_decode", _sdpa_decode), ("topk", _topk),
                    ("gather", _gather), ("index", _index), ("scatter", _scatter), ("sort", _sort),
-                   ("cumsum", _cumsum), ("multinomial", _multinomial)):
+                   ("cumsum", _cumsum), ("multinomial", _multinomial), ("elementwise", _elementwise),
+                   ("mean_lastdim", _mean_lastdim), ("cat", _cat)):
     _LIB.impl(_name, _fn, "CUDA")
 
 
@@ -183,3 +200,22 @@ def _cumsum_fake(x, dim):
 def _multinomial_fake(probs, num_samples, uniforms):
     shape = (num_samples,) if probs.dim() == 1 else (probs.shape[0], num_samples)
     return probs.new_empty(shape, dtype=torch.int64)
+
+
+@_fake("elementwise")
+def _elementwise_fake(op, inputs, out_dtype, compute_dtype, s0=1.0, s1=0.0):
+    shape = torch.broadcast_shapes(*[tuple(t.shape) for t in inputs])
+    return inputs[0].new_empty(shape, dtype=out_dtype)
+
+
+@_fake("mean_lastdim")
+def _mean_lastdim_fake(x, keepdim=False):
+    return x.new_empty((*x.shape[:-1], 1) if keepdim else tuple(x.shape[:-1]))
+
+
+@_fake("cat")
+def _cat_fake(tensors, dim=0):
+    shape = list(tensors[0].shape)
+    d = dim % len(shape)
+    shape[d] = sum(int(t.shape[d]) for t in tensors)
+    return tensors[0].new_empty(shape)

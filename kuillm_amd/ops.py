@@ -12,6 +12,7 @@ stock PyTorch (the reference's dispatch contract, kuipy/__init__.py:53-75).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 
@@ -754,3 +755,156 @@ def decode_qkv_rope(x, W, hq, hkv, hd, inv_freq, pos, q_out, k_cache, v_cache, x
         q_out.data_ptr(), k_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), v_cache.data_ptr(),
         v_cache.stride(0), v_cache.stride(1), k_cache.shape[1], _stream(x.device)))
     return q_out
+
+
+# ----------------------------------------------- elementwise / mean / cat
+
+def _compute_code(dtype) -> int:
+    """Arithmetic type of an elementwise op whose operands promote to
+    ``dtype``: fp64 stays fp64, other floats compute in fp32 (aten's opmath
+    type), integers and bool in int64."""
+    if dtype == torch.float64:
+        return _lib.F64
+    if dtype.is_floating_point:
+        return _lib.F32
+    if dtype.is_complex:
+        raise _lib.Unsupported("elementwise", _lib.E_UNSUPPORTED)
+    return _lib.I64
+
+
+def _collapse(shape, stride_sets):
+    """Drop size-1 dims and merge neighbours that every operand walks as one
+    (stride[d] == stride[d+1] * shape[d+1]); returns (shape, [strides])."""
+    dims = [d for d in range(len(shape)) if shape[d] != 1]
+    out_shape = [shape[d] for d in dims]
+    outs = [[st[d] for d in dims] for st in stride_sets]
+    i = len(out_shape) - 2
+    while i >= 0:
+        if all(st[i] == st[i + 1] * out_shape[i + 1] for st in outs):
+            out_shape[i] *= out_shape[i + 1]
+            del out_shape[i + 1]
+            for st in outs:
+                st[i] = st[i + 1]
+                del st[i + 1]
+        i -= 1
+    return out_shape, outs
+
+
+def elementwise(op: int, inputs, out_dtype, compute_dtype=None, s0: float = 1.0, s1: float = 0.0):
+    """out = op(inputs...) with broadcasting; ``op`` is a KUIOPS_EW_* code.
+    Binary ops given one tensor take the python scalar ``s1`` as their second
+    operand; ``s0`` is add / sub's alpha or pow's exponent.  ``compute_dtype``
+    (default: promoted from the inputs) selects fp32 / fp64 / int64
+    arithmetic.  Returns a new contiguous tensor of ``out_dtype``."""
+    if not inputs:
+        raise _lib.KuiopsError("kuiops_elementwise", _lib.E_INVALID)
+    dev = inputs[0].device
+    shape = list(torch.broadcast_shapes(*[tuple(t.shape) for t in inputs]))
+    out = torch.empty(shape, dtype=out_dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    if compute_dtype is None:
+        compute_dtype = inputs[0].dtype
+        for t in inputs[1:]:
+            compute_dtype = torch.promote_types(compute_dtype, t.dtype)
+    strides = [list(t.expand(shape).stride()) for t in inputs]
+    cshape, cstrides = _collapse(shape, strides)
+    if len(cshape) > 8:
+        raise _lib.Unsupported("kuiops_elementwise", _lib.E_UNSUPPORTED)
+    n = len(inputs)
+    rank = len(cshape)
+    flat = [s for st in cstrides for s in st]
+    lib = _lib_handle()
+    _lib.check("kuiops_elementwise", lib.kuiops_elementwise(
+        int(op), rank, _lib.i64_array(cshape), n, (ctypes.c_int * n)(*[_dt(t.dtype) for t in inputs]),
+        (ctypes.c_void_p * n)(*[t.data_ptr() for t in inputs]), _lib.i64_array(flat), float(s0), float(s1),
+        _compute_code(compute_dtype), _dt(out_dtype), out.data_ptr(), _stream(dev)))
+    return out
+
+
+def mean_lastdim(x: torch.Tensor, keepdim: bool = False) -> torch.Tensor:
+    """x.mean(-1, keepdim) with fp32 accumulation (fp64 for fp64), scaled as
+    aten scales its sums (by output numel / input numel)."""
+    if x.dim() == 0 or x.dtype not in (torch.float32, torch.float16, torch.bfloat16, torch.float64):
+        raise _lib.Unsupported("kuiops_mean_lastdim", _lib.E_UNSUPPORTED)
+    n = x.shape[-1]
+    rows = x.reshape(-1, n) if x.dim() != 2 else x
+    if n > 0 and (rows.stride(-1) != 1 or (rows.shape[0] > 1 and rows.stride(0) < n)):
+        rows = rows.contiguous()
+    m = rows.shape[0]
+    out_shape = (*x.shape[:-1], 1) if keepdim else tuple(x.shape[:-1])
+    out = torch.empty(out_shape, dtype=x.dtype, device=x.device)
+    if m == 0:
+        return out
+    lib = _lib_handle()
+    _lib.check("kuiops_mean_lastdim", lib.kuiops_mean_lastdim(
+        m, n, _dt(x.dtype), rows.data_ptr(), rows.stride(0) if m > 1 else n, out.data_ptr(), _stream(x.device)))
+    return out
+
+
+def _outer_stride(t: torch.Tensor, dim: int):
+    """(outer rows, stride between rows) when t's dims from ``dim`` on form
+    one contiguous run per row and its leading dims walk rows at one stride;
+    None otherwise."""
+    inner = 1
+    for d in range(t.dim() - 1, dim - 1, -1):
+        if t.shape[d] != 1 and t.stride(d) != inner:
+            return None
+        inner *= t.shape[d]
+    lead = [(t.shape[d], t.stride(d)) for d in range(dim) if t.shape[d] != 1]
+    if not lead:
+        return 1, max(inner, 1)
+    for (s0, st0), (s1, st1) in zip(lead, lead[1:]):
+        if st0 != st1 * s1:
+            return None
+    rows = 1
+    for s, _ in lead:
+        rows *= s
+    return rows, lead[-1][1]
+
+
+def cat(tensors, dim: int = 0) -> torch.Tensor:
+    """torch.cat of same-dtype, same-rank tensors along ``dim``.  Inputs whose
+    rows are not single strided runs are made contiguous first."""
+    if not tensors:
+        raise _lib.KuiopsError("kuiops_cat", _lib.E_INVALID)
+    ref = tensors[0]
+    rank = ref.dim()
+    if rank == 0 or any(t.dim() != rank or t.dtype != ref.dtype or t.device != ref.device for t in tensors):
+        raise _lib.Unsupported("kuiops_cat", _lib.E_UNSUPPORTED)
+    dim = dim % rank
+    for t in tensors:
+        if any(t.shape[d] != ref.shape[d] for d in range(rank) if d != dim):
+            raise _lib.KuiopsError("kuiops_cat", _lib.E_INVALID)
+    if len(tensors) > 32:
+        raise _lib.Unsupported("kuiops_cat", _lib.E_UNSUPPORTED)
+    shape = list(ref.shape)
+    shape[dim] = sum(int(t.shape[dim]) for t in tensors)
+    out = torch.empty(shape, dtype=ref.dtype, device=ref.device)
+    if out.numel() == 0:
+        return out
+    outer = 1
+    for d in range(dim):
+        outer *= shape[d]
+    inner = 1
+    for d in range(dim + 1, rank):
+        inner *= shape[d]
+    ptrs, widths, strides, keep = [], [], [], []
+    for t in tensors:
+        w = int(t.shape[dim]) * inner
+        if w == 0:
+            continue
+        rs = _outer_stride(t, dim)
+        if rs is None:
+            t = t.contiguous()
+            rs = _outer_stride(t, dim)
+        keep.append(t)
+        ptrs.append(t.data_ptr())
+        widths.append(w)
+        strides.append(rs[1])
+    n = len(ptrs)
+    lib = _lib_handle()
+    _lib.check("kuiops_cat", lib.kuiops_cat(
+        n, (ctypes.c_void_p * max(n, 1))(*ptrs), _lib.i64_array(widths), _lib.i64_array(strides), outer,
+        ref.element_size(), out.data_ptr(), _stream(ref.device)))
+    return out

@@ -13,8 +13,8 @@ import json
 from pathlib import Path
 
 from . import config as C
-from .kuiops import (AddmmImpl, BmmImpl, CumsumImpl, GatherImpl, IndexImpl, MmImpl, MultinomialImpl,
-                     ScatterImpl, SdpaImpl, SoftmaxImpl, SortImpl, TopkImpl)
+from .kuiops import (AddmmImpl, BmmImpl, CatImpl, CumsumImpl, ElementwiseImpl, GatherImpl, IndexImpl, MeanImpl,
+                     MmImpl, MultinomialImpl, ScatterImpl, SdpaImpl, SoftmaxImpl, SortImpl, TopkImpl)
 
 _REGISTRY = None
 _TUNE_PARAMS = None
@@ -45,7 +45,11 @@ def _build_registry(tune_params):
     topk, gather, index = TopkImpl(tune_params), GatherImpl(tune_params), IndexImpl(tune_params)
     scatter, sort = ScatterImpl(tune_params), SortImpl(tune_params)
     cumsum, multinomial = CumsumImpl(tune_params), MultinomialImpl(tune_params)
-    return {
+    elem, mean, cat = ElementwiseImpl(tune_params), MeanImpl(tune_params), CatImpl(tune_params)
+    table = {op: elem for op in ElementwiseImpl.OPS}
+    table.update({
+        aten.mean.dim: mean,
+        aten.cat.default: cat,
         aten.mm.default: mm,
         aten.bmm.default: bmm,
         aten.addmm.default: addmm,
@@ -60,7 +64,8 @@ def _build_registry(tune_params):
         aten.sort.stable: sort,
         aten.cumsum.default: cumsum,
         aten.multinomial.default: multinomial,
-    }
+    })
+    return table
 
 
 def _tune_impls(tune_params):

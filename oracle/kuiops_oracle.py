@@ -18,6 +18,8 @@ therefore restates aten semantics, op by op, citing the reference's family:
   topk / index       no reference kernel (kuiops/topk/.gitkeep,
                      kuiops/index/.gitkeep): aten.topk / aten.index.Tensor
   scatter            kuipy/kuiops.py:757-807 (aten.scatter.src)
+  elementwise /      ElementwiseImpl / MeanImpl / CatImpl, kuipy/kuiops.py:150-320,
+  mean / cat         810-921 (aten semantics: opmath compute type, broadcasting)
   sort / cumsum /    no reference kernel (KERNELS.md rows aten.sort.default,
   multinomial        aten.cumsum.default, aten.multinomial.default): aten
                      semantics; multinomial as the inverse CDF of given
@@ -87,6 +89,113 @@ def round_dtype(x, dtype: str) -> np.ndarray:
     if dtype == "f32":
         return np.asarray(x, dtype=np.float32)
     return np.asarray(x, dtype=np.float64)
+
+
+# ----------------------------------------------- elementwise / mean / cat
+# ElementwiseImpl / MeanImpl / CatImpl (kuipy/kuiops.py:150-320, 810-921,
+# registered for the aten overloads of kuipy/registry.py:33-57).  Restated
+# from aten: operands broadcast, are converted to the compute type (fp32 for
+# 16/32-bit floats -- aten's "opmath" type -- fp64 for fp64, int64 for
+# integers and bool), scalars enter unrounded in that type, and the result is
+# rounded once to the output dtype by the caller (``round_dtype``).
+
+_UNARY_F = {
+    "neg": lambda a: -a,
+    "silu": lambda a: a / (a.dtype.type(1) + np.exp(-a)),
+    "rsqrt": lambda a: a.dtype.type(1) / np.sqrt(a),
+    "cos": np.cos,
+    "sin": np.sin,
+    "exp": np.exp,
+    "sqrt": np.sqrt,
+}
+
+
+def _pow_scalar(a, e, store=None):
+    # aten's special cases of pow(Tensor, Scalar); for 16-bit storage types
+    # the integer powers multiply in the storage type, so the square is
+    # rounded to it before the third factor / the reciprocal
+    one = a.dtype.type(1)
+    sq = a * a
+    if store in ("bf16", "f16"):
+        sq = round_dtype(sq, store).astype(a.dtype)
+    if e == 2:
+        return a * a
+    if e == 3:
+        return sq * a
+    if e == 1:
+        return a.copy()
+    if e == 0.5:
+        return np.sqrt(a)
+    if e == -0.5:
+        return one / np.sqrt(a)
+    if e == -1:
+        return one / a
+    if e == -2:
+        return one / sq
+    return np.power(a, a.dtype.type(e))
+
+
+def elementwise(op: str, *operands, alpha=1.0, exponent=None, compute="f32", store=None) -> np.ndarray:
+    """op over broadcast operands in the compute type ('f32', 'f64' or
+    'i64'); python scalars are operands too.  ``store`` is the output
+    storage dtype where it changes an intermediate rounding (pow).  Ops: neg silu rsqrt cos sin
+    exp sqrt pow add sub mul div eq ne le lt ge gt where bitwise_not
+    bitwise_and bitwise_or.  Comparisons return bool, the rest the compute
+    type (unrounded)."""
+    ct = {"f32": np.float32, "f64": np.float64, "i64": np.int64}[compute]
+    with np.errstate(all="ignore"):
+        xs = [np.asarray(x).astype(ct) if not np.isscalar(x) else ct(x) for x in operands]
+        xs = [np.asarray(x) for x in xs]
+        if op in _UNARY_F:
+            return _UNARY_F[op](xs[0])
+        if op == "pow":
+            return _pow_scalar(xs[0], exponent, store)
+        if op == "where":
+            c = np.asarray(operands[0]).astype(bool)
+            return np.where(c, xs[1], xs[2])
+        if op == "bitwise_not":
+            b = np.asarray(operands[0])
+            return ~b if b.dtype == bool else ~b.astype(np.int64)
+        if op in ("bitwise_and", "bitwise_or"):
+            a, b = (np.asarray(x) for x in operands[:2])
+            return (a & b) if op == "bitwise_and" else (a | b)
+        a, b = xs[0], xs[1]
+        if op in ("add", "sub"):
+            if alpha == 1:
+                return a + b if op == "add" else a - b
+            # aten's alpha kernels: one fused multiply-add, a + (+-alpha) * b
+            al = alpha if op == "add" else -alpha
+            if ct is np.int64:
+                return a + np.int64(al) * b
+            wide = np.float64 if ct is np.float32 else np.longdouble
+            return (wide(al) * b.astype(wide) + a.astype(wide)).astype(ct)
+        if op == "mul":
+            return a * b
+        if op == "div":
+            return a / b
+        cmp = {"eq": np.equal, "ne": np.not_equal, "le": np.less_equal, "lt": np.less,
+               "ge": np.greater_equal, "gt": np.greater}
+        if op in cmp:
+            return cmp[op](a, b)
+    raise ValueError(f"elementwise: unknown op {op}")
+
+
+def mean_lastdim(x, keepdim=False) -> np.ndarray:
+    """Mean over the last axis with a wide (fp64) sum, scaled by
+    m / (m * n) as aten's mean.dim scales it (MeanImpl kuipy/kuiops.py:860-921).
+    Unrounded: callers round to the storage dtype."""
+    x = np.asarray(x, dtype=np.float64)
+    n = x.shape[-1]
+    m = x.size // n if n else 0
+    factor = np.float64(m) / np.float64(m * n)
+    out = x.sum(-1) * factor
+    return out[..., None] if keepdim else out
+
+
+def cat(tensors, dim=0) -> np.ndarray:
+    """Concatenation along ``dim`` (CatImpl kuipy/kuiops.py:810-857); a copy,
+    bit-exact in any dtype."""
+    return np.concatenate([np.asarray(t) for t in tensors], axis=dim)
 
 
 # ------------------------------------------------------------------- GEMM

@@ -119,6 +119,49 @@ def main():
     g["scatter_out"] = S.scatter(1, perm, src).numpy()
     mb = torch.rand(4, 9) > 0.5
     g["scatter_bool_src"], g["scatter_bool_out"] = mb.numpy(), mb.scatter(1, perm, mb).numpy()
+    # elementwise / mean / cat (ElementwiseImpl / MeanImpl / CatImpl,
+    # kuipy/kuiops.py:150-320, 810-921): bf16 and fp32 operands, a broadcast
+    # column, python scalars, mixed bf16 * fp32 promotion
+    ex = torch.randn(4, 33) * 2
+    ey = torch.randn(4, 33) + 3.0                          # away from 0 for div
+    ecol = torch.randn(4, 1)
+    for dt in ("f32", "bf16"):
+        tdt = torch.float32 if dt == "f32" else torch.bfloat16
+        x, y, col = ex.to(tdt), ey.to(tdt), ecol.to(tdt)
+        g[f"ew_{dt}_x"], g[f"ew_{dt}_y"], g[f"ew_{dt}_col"] = bits(x), bits(y), bits(col)
+        for name, fn in (("neg", torch.neg), ("silu", F.silu), ("cos", torch.cos), ("sin", torch.sin),
+                         ("exp", torch.exp), ("sq", lambda t: t.pow(2)), ("p3", lambda t: t.pow(3)),
+                         ("p15", lambda t: t.abs().pow(1.5))):
+            g[f"ew_{dt}_{name}"] = bits(fn(x))
+        g[f"ew_{dt}_rsqrt"] = bits(torch.rsqrt(y))
+        g[f"ew_{dt}_sqrt"] = bits(torch.sqrt(y))
+        g[f"ew_{dt}_add"] = bits(x + y)
+        g[f"ew_{dt}_add_a"] = bits(torch.add(x, y, alpha=0.5))
+        g[f"ew_{dt}_sub"] = bits(x - y)
+        g[f"ew_{dt}_mul"] = bits(x * y)
+        g[f"ew_{dt}_div"] = bits(x / y)
+        g[f"ew_{dt}_mulcol"] = bits(x * col)
+        g[f"ew_{dt}_adds"] = bits(x + 1e-6)
+        g[f"ew_{dt}_muls"] = bits(x * 0.125)
+        g[f"ew_{dt}_lt"] = (x < 0.5).numpy()
+        g[f"ew_{dt}_le"] = (x <= y).numpy()
+        g[f"ew_{dt}_eq"] = (x == 0.0).numpy()
+        g[f"ew_{dt}_where"] = bits(torch.where(x > 0, x, y))
+    xb, yf = ex.bfloat16(), ey
+    g["ew_mixed_out"] = (xb * yf).numpy()                  # bf16 * fp32 -> fp32
+    bm1, bm2 = torch.rand(5, 9) > 0.5, torch.rand(5, 9) > 0.3
+    g["ew_b1"], g["ew_b2"] = bm1.numpy(), bm2.numpy()
+    g["ew_band"], g["ew_bor"], g["ew_bnot"] = (bm1 & bm2).numpy(), (bm1 | bm2).numpy(), (~bm1).numpy()
+    ei = torch.randint(-50, 50, (6, 7))
+    g["ew_i64"], g["ew_i64_add"], g["ew_i64_mul"] = ei.numpy(), (ei + 3).numpy(), (ei * ei).numpy()
+    mx = torch.randn(6, 100).bfloat16()
+    g["mean_bf16_x"], g["mean_bf16_out"] = bits(mx), bits(mx.mean(-1, keepdim=True))
+    mxf = torch.randn(3, 5000)
+    g["mean_f32_x"], g["mean_f32_out"] = mxf.numpy(), mxf.mean(-1).numpy()
+    c1, c2 = torch.randn(2, 3, 5, 8).bfloat16(), torch.randn(2, 3, 7, 8).bfloat16()
+    g["cat_a"], g["cat_b"], g["cat_out"] = bits(c1), bits(c2), bits(torch.cat([c1, c2], dim=2))
+    q = torch.randn(2, 4, 6, 16)
+    g["cat_q"], g["cat_rot"] = q.numpy(), torch.cat((-q[..., 8:], q[..., :8]), dim=-1).numpy()
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(g)} arrays)")
 
