@@ -198,6 +198,26 @@ KUIOPS_API int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, in
                     void *O, const int64_t so[3],
                     float *lse, float scale, int causal, void *stream);
 
+/* kuiops_sdpa_fwd with an additive attention bias -- the reference family's
+ * own form (kuipy/kuiops.py:627-681: a full (N, H, L, S) bias, which it
+ * pre-divides by the scale, :673-676) and the call its app issues,
+ * _scaled_dot_product_efficient_attention with a bf16 bias from left-padded
+ * batched generation (KERNELS.md:64, infer.py:22-24,102):
+ *   O = softmax(scale * Q K^T + bias [+ causal mask]) V.
+ * Bias element (b, h, i, j) is at bias + b*sb[0] + h*sb[1] + i*sb[2] + j
+ * (stride 0 broadcasts, e.g. one padding mask for every head), in `dtype`;
+ * sb[] multiples of 4 and bias 8-byte aligned.  -inf entries mask keys;
+ * rows with no visible key output 0 and LSE = -inf.  bias == NULL is
+ * kuiops_sdpa_fwd.  scale > 0.                                              */
+KUIOPS_API int kuiops_sdpa_fwd_bias(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s,
+                         int64_t e, int64_t ev, int dtype,
+                         const void *Q, const int64_t sq[3],
+                         const void *K, const int64_t sk[3],
+                         const void *V, const int64_t sv[3],
+                         void *O, const int64_t so[3],
+                         float *lse, float scale, int causal,
+                         const void *bias, const int64_t sb[3], void *stream);
+
 /* Decode attention (l small, typically 1) over a KV cache, split over the
  * key axis; same tensor conventions as kuiops_sdpa_fwd.  Causal masking with
  * l > 1 aligns the queries to the END of the keys (query i sees keys

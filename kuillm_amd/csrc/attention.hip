@@ -51,6 +51,12 @@ struct AttnArgs {
     float *ws_o;        // [rows_total][splits][ev]
     unsigned *counters; // [n][hkv][row_groups] split arrival counters (zero between calls)
     const int32_t *kv_len;  // decode: per-batch key count in device memory (<= s), or null
+    // additive attention bias (fa_fwd_kernel BIAS): element (b, h, q, key) at
+    // bias + b*sb0 + h*sb1 + q*sb2 + key, in the dtype of Q; added to the raw
+    // scores pre-divided by the scale (softmax(scale * (QK^T + bias / scale)))
+    const void *bias;
+    int64_t sb0, sb1, sb2;
+    float inv_scale;
 };
 
 constexpr float kLn2 = 0.69314718055994530942f;
@@ -88,7 +94,7 @@ __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t vof
 // are rescaled: probabilities stay below 2^8 meanwhile.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename T, int HD, bool CAUSAL, int NWV>
+template <typename T, int HD, bool CAUSAL, int NWV, bool BIAS = false>
 __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(AttnArgs a) {
     constexpr int BQ = 32 * NWV, BKV = 64;          // 32 queries per wave
@@ -200,6 +206,44 @@ void fa_fwd_kernel(AttnArgs a) {
         for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
     float m_used = -INFINITY, l_run = 0.f;
 
+    // Bias of this lane's query for the 32 score slots of a key block: slot
+    // (t, e) is key kv0 + 32t + 8(e/4) + 4lh + e%4, so each (t, e/4) is 4
+    // consecutive keys, one 8-byte load.  Loaded one block ahead (br), added
+    // (times 1/scale) to the raw scores at the start of the block's step.
+    typedef T t4v __attribute__((ext_vector_type(4)));
+    t4v br[8];
+    const T *brow = nullptr;
+    if constexpr (BIAS) {
+        const int64_t qrow = myq < a.l ? myq : a.l - 1;
+        brow = reinterpret_cast<const T *>(a.bias) + b * a.sb0 + h * a.sb1 + qrow * a.sb2;
+    }
+    auto load_bias = [&](int64_t kv0) __attribute__((always_inline)) {
+        if constexpr (BIAS) {
+            if (kv0 + BKV <= a.s) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    br[i] = *reinterpret_cast<const t4v *>(brow + kv0 + 32 * (i >> 2) + 8 * (i & 3) + 4 * lh);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int64_t key = kv0 + 32 * (i >> 2) + 8 * (i & 3) + 4 * lh + c;
+                        br[i][c] = key < a.s ? brow[key] : (T)0.f;
+                    }
+            }
+        }
+    };
+    auto add_bias = [&](f32x16 *sc) __attribute__((always_inline)) {
+        if constexpr (BIAS) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    sc[t][e] = __builtin_fmaf(to_f32(br[4 * t + (e >> 2)][e & 3]), a.inv_scale, sc[t][e]);
+        }
+    };
+
     // S^T block = K_blk Q^T: sc[t][e] = score of key kv0 + 32t + 8(e/4) + 4lh + e%4, query myq.
     auto qk = [&](const char *pk, f32x16 *sc) __attribute__((always_inline)) {
 #pragma unroll
@@ -219,8 +263,12 @@ void fa_fwd_kernel(AttnArgs a) {
     // One pipeline step on score block `cur` (keys kv0 ..): mask and row
     // max, lazy rescale, then exp(cur) interleaved with the MFMAs of the next
     // block's scores (K slot `pk`, into `nxt`), then O^T += V^T P^T.
-    auto step = [&](f32x16 *cur, f32x16 *nxt, const char *pk, const char *pv, int64_t kv0)
+    auto step = [&](f32x16 *cur, f32x16 *nxt, const char *pk, const char *pv, int64_t kv0, int64_t kv_next)
         __attribute__((always_inline)) {
+        if constexpr (BIAS) {
+            add_bias(cur);
+            if (kv_next >= 0) load_bias(kv_next);
+        }
         const bool need_mask = (kv0 + BKV > a.s) || (CAUSAL && kv0 + BKV - 1 > qw);
         if (need_mask) {
             // key offset within the block of lane-slot (t, e) is 32t + 8(e/4) + 4lh + e%4
@@ -337,6 +385,7 @@ void fa_fwd_kernel(AttnArgs a) {
     auto kvb = [&](int j) { return rev ? nkv - 1 - j : j; };
     f32x16 scA[2], scB[2];
     if (nkv > 0) {
+        if (live) load_bias((int64_t)kvb(0) * BKV);
         issue_k(kvb(0), sK0);
         issue_v(kvb(0), sV0);
         if (nkv > 1) issue_k(kvb(1), sK1);
@@ -353,7 +402,8 @@ void fa_fwd_kernel(AttnArgs a) {
             __syncthreads();
             if (j + 2 < nkv) issue_k(kvb(j + 2), hs ? sK1 : sK0);
             if (j + 1 < nkv) issue_v(kvb(j + 1), hs ? sV0 : sV1);
-            if (live) step(hs ? scB : scA, hs ? scA : scB, hs ? sK0 : sK1, hs ? sV1 : sV0, (int64_t)kvb(j) * BKV);
+            if (live) step(hs ? scB : scA, hs ? scA : scB, hs ? sK0 : sK1, hs ? sV1 : sV0, (int64_t)kvb(j) * BKV,
+                           j + 1 < nkv ? (int64_t)kvb(j + 1) * BKV : -1);
         }
     }
 
@@ -860,8 +910,14 @@ static int launch_fwd(AttnArgs a, hipStream_t st) {
     a.pair = (a.causal && (a.nqb & 1) == 0 && singles / 2 >= (int64_t)num_cus()) ? 1 : 0;
     const int64_t blocks = a.pair ? singles / 2 : singles;
     if (blocks > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
-    if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    if (a.bias) {
+        if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false, 4, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    } else if (a.causal) {
+        hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    }
     return launch_status();
 }
 
@@ -930,6 +986,35 @@ extern "C" int kuiops_sdpa_fwd(int64_t n, int64_t hq, int64_t hkv, int64_t l, in
     if (!fwd_offsets_fit(s, e, sk[2], sv[2])) return KUIOPS_E_UNSUPPORTED;
     AttnArgs a{};
     fill_args(a, n, hq, hkv, l, s, Q, sq, K, sk, V, sv, O, so, lse, scale, causal);
+    hipStream_t st = as_stream(stream);
+    if (dtype == KUIOPS_BF16) return e == 128 ? launch_fwd<bf16_t, 128>(a, st) : launch_fwd<bf16_t, 64>(a, st);
+    return e == 128 ? launch_fwd<f16_t, 128>(a, st) : launch_fwd<f16_t, 64>(a, st);
+}
+
+extern "C" int kuiops_sdpa_fwd_bias(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, int64_t e,
+                                    int64_t ev, int dtype, const void *Q, const int64_t sq[3], const void *K,
+                                    const int64_t sk[3], const void *V, const int64_t sv[3], void *O,
+                                    const int64_t so[3], float *lse, float scale, int causal, const void *bias,
+                                    const int64_t sb[3], void *stream) {
+    if (!bias) return kuiops_sdpa_fwd(n, hq, hkv, l, s, e, ev, dtype, Q, sq, K, sk, V, sv, O, so, lse, scale,
+                                      causal, stream);
+    if (!sb) return KUIOPS_E_INVALID;
+    int status;
+    if (!attn_common_ok(n, hq, hkv, l, s, e, ev, dtype, Q, sq, K, sk, V, sv, O, so, status)) {
+        if (status == KUIOPS_E_INVALID || n * hq * l != 0) return status;
+    }
+    if (n == 0 || hq == 0 || l == 0) return KUIOPS_OK;
+    if (hq > 65535 || n > 65535) return KUIOPS_E_UNSUPPORTED;
+    if (!fwd_offsets_fit(s, e, sk[2], sv[2])) return KUIOPS_E_UNSUPPORTED;
+    if (!(scale > 0.f)) return KUIOPS_E_UNSUPPORTED;
+    // 8-byte loads of 4 consecutive keys: row starts 8-byte aligned
+    if ((reinterpret_cast<uintptr_t>(bias) & 7) || sb[0] % 4 || sb[1] % 4 || sb[2] % 4) return KUIOPS_E_UNSUPPORTED;
+    if (sb[0] < 0 || sb[1] < 0 || sb[2] < 0) return KUIOPS_E_UNSUPPORTED;
+    AttnArgs a{};
+    fill_args(a, n, hq, hkv, l, s, Q, sq, K, sk, V, sv, O, so, lse, scale, causal);
+    a.bias = bias;
+    a.sb0 = sb[0]; a.sb1 = sb[1]; a.sb2 = sb[2];
+    a.inv_scale = 1.f / scale;
     hipStream_t st = as_stream(stream);
     if (dtype == KUIOPS_BF16) return e == 128 ? launch_fwd<bf16_t, 128>(a, st) : launch_fwd<bf16_t, 64>(a, st);
     return e == 128 ? launch_fwd<f16_t, 128>(a, st) : launch_fwd<f16_t, 64>(a, st);

@@ -70,7 +70,7 @@ def _rewrite(graph, node, spec):
         return K.softmax.default, (node.args[0],), {}
     if t in (aten._scaled_dot_product_flash_attention.default,
              aten._scaled_dot_product_efficient_attention.default):
-        _, scale, causal, _, _ = spec
+        _, scale, causal, _, _, bias = spec
         users = _getitem_users(node)
         # outputs 0 (attention) and 1 (log-sum-exp, fp32 [N, H, L]) map
         # onto kuiops.sdpa; the efficient kernel pads its LSE, so there
@@ -78,7 +78,10 @@ def _rewrite(graph, node, spec):
         allowed = {0, 1} if t is aten._scaled_dot_product_flash_attention.default else {0}
         if users is None or not set(users) <= allowed:
             return None
-        return K.sdpa.default, tuple(node.args[:3]), {"is_causal": causal, "scale": scale}
+        kw = {"is_causal": causal, "scale": scale}
+        if bias is not None:
+            kw["bias"] = node.args[3] if len(node.args) > 3 else node.kwargs["attn_bias"]
+        return K.sdpa.default, tuple(node.args[:3]), kw
     if t is aten.topk.default:
         _, k, dim, largest, srt = spec
         return K.topk.default, (node.args[0], k, dim, largest, srt), {}

@@ -219,9 +219,11 @@ class SdpaImpl(_Family):
 
     The reference family (kuipy/kuiops.py:621-681, disconnected at
     kuipy/registry.py:27-28,59) needs a full additive bias and rejects
-    is_causal; here the bias must be absent (no masks beyond causal), and
-    causal, GQA head counts and decode shapes are served.  Returns the aten
-    output tuple with an fp32 (N, H, L) log-sum-exp."""
+    is_causal; here an additive bias (any layout broadcastable to
+    (N, H, L, S), in the query dtype -- the padding mask of batched
+    generation) is served, and so are causal masking, GQA head counts and
+    decode shapes.  Returns the aten output tuple with an fp32 (N, H, L)
+    log-sum-exp."""
     tune_key = "SDPA"
     tune_params = {"decode_max_rows": 8}
 
@@ -245,7 +247,7 @@ class SdpaImpl(_Family):
         if len(args) < 3:
             return None
         q, k, v, bias, need_lse, dropout, causal, debug = self._parse(func, args, kwargs)
-        if bias is not None or dropout != 0.0 or debug:
+        if dropout != 0.0 or debug:
             return None
         if not (_is_dev(q, k, v) and q.dim() == 4 and k.dim() == 4 and v.dim() == 4):
             return None
@@ -256,12 +258,21 @@ class SdpaImpl(_Family):
         n3, hkv3, s3, ev = (int(x) for x in v.shape)
         if (n, e) != (n2, e2) or (n, hkv, s) != (n3, hkv3, s3) or hkv == 0 or hq % hkv:
             return None
-        if e != ev or e not in (64, 128) or n > 65535 or hq > 65535:
+        if e != ev or not 0 < e <= 128 or n > 65535 or hq > 65535:
             return None
+        if bias is not None:
+            if not (_is_dev(bias) and bias.device == q.device and bias.dtype == q.dtype and bias.dim() <= 4):
+                return None
+            try:
+                torch.broadcast_shapes(tuple(bias.shape), (n, hq, l, s))
+            except RuntimeError:
+                return None
         scale = kwargs.get("scale", None)
         if scale is None:
             scale = 1.0 / math.sqrt(e)
-        return (func, float(scale), causal, need_lse, [q, k, v])
+        if not scale > 0:
+            return None
+        return (func, float(scale), causal, need_lse, [q, k, v], bias)
 
     def tune(self, all_tune_params):
         """Measure, on this GPU, up to how many query rows per KV head the
@@ -275,10 +286,10 @@ class SdpaImpl(_Family):
         return all_tune_params
 
     def run(self, spec, args, kwargs):
-        func, scale, causal, need_lse, (q, k, v) = spec
+        func, scale, causal, need_lse, (q, k, v), bias = spec
         try:
             rows = self.tune_params.get("decode_max_rows", 8) if isinstance(self.tune_params, dict) else 8
-            out, lse = K.sdpa(q, k, v, causal, scale, int(rows))
+            out, lse = K.sdpa(q, k, v, causal, scale, int(rows), bias)
         except _lib.Unsupported:
             return None
         n, hq, l = out.shape[0], out.shape[1], out.shape[2]

@@ -29,7 +29,7 @@ _SCHEMAS = {
     "bmm": "bmm(Tensor A, Tensor B) -> Tensor",
     "softmax": "softmax(Tensor x) -> Tensor",
     "sdpa": "sdpa(Tensor q, Tensor k, Tensor v, bool is_causal=False, float? scale=None, "
-            "int decode_max_rows=8) -> (Tensor, Tensor)",
+            "int decode_max_rows=8, Tensor? bias=None) -> (Tensor, Tensor)",
     "sdpa_decode": "sdpa_decode(Tensor q, Tensor k, Tensor v, bool causal=True, float? scale=None) -> Tensor",
     "topk": "topk(Tensor x, int k, int dim=-1, bool largest=True, bool sorted=True) -> (Tensor, Tensor)",
     "gather": "gather(Tensor inp, int dim, Tensor idx) -> Tensor",
@@ -65,9 +65,9 @@ def _softmax(x):
     return ops.softmax(x)
 
 
-def _sdpa(q, k, v, is_causal=False, scale=None, decode_max_rows=8):
+def _sdpa(q, k, v, is_causal=False, scale=None, decode_max_rows=8, bias=None):
     return ops.sdpa(q, k, v, is_causal=is_causal, scale=scale, return_lse=True,
-                    decode_max_rows=decode_max_rows)
+                    decode_max_rows=decode_max_rows, bias=bias)
 
 
 def _sdpa_decode(q, k, v, causal=True, scale=None):
@@ -151,7 +151,7 @@ def _softmax_fake(x):
 
 
 @_fake("sdpa")
-def _sdpa_fake(q, k, v, is_causal=False, scale=None, decode_max_rows=8):
+def _sdpa_fake(q, k, v, is_causal=False, scale=None, decode_max_rows=8, bias=None):
     n, hq, l, _ = q.shape
     return (q.new_empty((n, hq, l, v.shape[-1])),
             q.new_empty((n, hq, l), dtype=torch.float32))

@@ -262,18 +262,54 @@ def _attn_prep(q, k, v):
     return q, k, v, (n, hq, hkv, l, s, e, ev)
 
 
-def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=8, out=None):
-    """softmax(scale * q k^T [causal]) v  ->  (out, lse)   (aten SDPA semantics).
+def _bias_view(bias, n, hq, l, s, dtype):
+    """The additive bias as an (n, hq, l, s) view with a unit key stride,
+    strides that are multiples of 4 and an 8-byte aligned base (broadcast
+    dims keep stride 0).  A misaligned bias is copied with its key axis padded
+    to a multiple of 4 before it is broadcast, never after."""
+    if bias.dtype != dtype or bias.dim() > 4:
+        raise _lib.Unsupported("sdpa_fwd_bias", _lib.E_UNSUPPORTED)
+    b = bias.reshape((1,) * (4 - bias.dim()) + tuple(bias.shape)) if bias.dim() < 4 else bias
+    if b.shape[-1] == 1 and s > 1:
+        b = b.expand(*b.shape[:-1], s)
+    if s > 1 and b.stride(-1) != 1:
+        b = b.contiguous()
+    if any(st % 4 for sz, st in zip(b.shape[:3], b.stride()[:3]) if sz > 1) or b.data_ptr() % 8:
+        b = torch.nn.functional.pad(b, (0, (-b.shape[-1]) % 4))[..., :b.shape[-1]]
+    return b.expand(n, hq, l, s)
+
+
+def _pad_head(t, e_pad):
+    e = t.shape[-1]
+    return t if e == e_pad else torch.nn.functional.pad(t, (0, e_pad - e))
+
+
+def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=8, out=None, bias=None):
+    """softmax(scale * q k^T [+ bias] [causal]) v  ->  (out, lse)   (aten SDPA
+    semantics).
 
     q (n, hq, l, e), k / v (n, hkv, s, e) with hq % hkv == 0; causal masking is
-    aten's top-left alignment (query i sees keys j <= i).  Non-causal calls
-    with few query rows per KV head use the split-KV decode kernel.  ``out``
-    ([n, hq, l, ev] with a unit last stride, e.g. a transposed view of an
-    [n, l, hq, ev] buffer) receives the result in place.
+    aten's top-left alignment (query i sees keys j <= i).  ``bias`` is an
+    additive mask broadcastable to (n, hq, l, s) in q's dtype (-inf masks a
+    key), as aten's efficient-attention attn_bias.  Non-causal calls without
+    a bias and with few query rows per KV head use the split-KV decode kernel.
+    ``out`` ([n, hq, l, ev] with a unit last stride, e.g. a transposed view of
+    an [n, l, hq, ev] buffer) receives the result in place.
     """
     q, k, v, (n, hq, hkv, l, s, e, ev) = _attn_prep(q, k, v)
     if scale is None:
         scale = 1.0 / math.sqrt(e)
+    if e == ev and e < 128 and e not in (64,) and q.dtype in HALF:
+        # other head dims: zero-pad to the kernels' 64 / 128 (q k^T and the
+        # kept output columns are unchanged; the scale is the caller's)
+        e_pad = 64 if e < 64 else 128
+        o, lse = sdpa(_pad_head(q, e_pad), _pad_head(k, e_pad), _pad_head(v, e_pad), is_causal, scale,
+                      return_lse, decode_max_rows, None, bias)
+        o = o[..., :e]
+        if out is not None:
+            out.copy_(o)
+            o = out
+        return o, lse
     if out is None:
         out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
     elif tuple(out.shape) != (n, hq, l, ev) or out.stride(-1) != 1 or out.dtype != q.dtype:
@@ -286,6 +322,13 @@ def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=
     sk = _lib.strides3(*k.stride()[:3])
     sv = _lib.strides3(*v.stride()[:3])
     so = _lib.strides3(*out.stride()[:3])
+    if bias is not None:
+        b = _bias_view(bias, n, hq, l, s, q.dtype)
+        _lib.check("kuiops_sdpa_fwd_bias", lib.kuiops_sdpa_fwd_bias(
+            n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), sq, k.data_ptr(), sk,
+            v.data_ptr(), sv, out.data_ptr(), so, _ptr(lse), float(scale), 1 if is_causal else 0,
+            b.data_ptr(), _lib.strides3(*b.stride()[:3]), _stream(q.device)))
+        return out, lse
     if not is_causal and (hq // hkv) * l <= decode_max_rows and s > 0:
         ws_bytes = lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, n * hq * l, s, ev)
         ws = workspace(q.device, ws_bytes, "attn")

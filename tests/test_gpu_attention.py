@@ -55,10 +55,90 @@ def test_sdpa_golden(cuda, golden):
         return torch.from_numpy(golden[name].view(np.int16)).view(torch.bfloat16).to(cuda)
     out, _ = ops.sdpa(tb("sdpa_bf16_Q"), tb("sdpa_bf16_K"), tb("sdpa_bf16_V"), is_causal=True)
     close(out, golden["sdpa_bf16_out_causal"])
-    Q, K, V = (torch.from_numpy(golden[k]).to(cuda).to(torch.bfloat16) for k in ("sdpa_Q", "sdpa_K", "sdpa_V"))
-    # the golden head dim is 16: outside the kernels (head dim 64 / 128)
-    with pytest.raises(Exception):
-        ops.sdpa(Q, K, V)
+
+
+def bf16_np(a):
+    return O.round_bf16(np.asarray(a, np.float32))
+
+
+def test_sdpa_bias_golden(cuda, golden):
+    """The reference family's own form: a full (N, H, L, S) additive bias
+    with scale 0.3 (tests/test_jit_ops.py:173-193 shape, head dim 16, zero-
+    padded to the kernel's 64 on the host).  Against the oracle on the
+    bf16-rounded inputs, and against aten's fp32 result within the bf16
+    input rounding."""
+    Qf, Kf, Vf, Bf = (golden[k] for k in ("sdpa_Q", "sdpa_K", "sdpa_V", "sdpa_bias"))
+    Q, K, V, B = (torch.from_numpy(a).to(cuda).to(torch.bfloat16) for a in (Qf, Kf, Vf, Bf))
+    out, lse = ops.sdpa(Q, K, V, scale=0.3, bias=B)
+    ref, lref = O.sdpa(bf16_np(Qf), bf16_np(Kf), bf16_np(Vf), scale=0.3, bias=bf16_np(Bf))
+    close(out, ref)
+    np.testing.assert_allclose(npy(lse), lref, atol=2e-3, rtol=1e-3)
+    close(out, golden["sdpa_out_bias"], rtol=3e-2, atol=3e-2)
+    np.testing.assert_allclose(npy(lse), golden["sdpa_lse_bias"], atol=5e-2)
+    # the other golden cases at head dim 16 (padded the same way)
+    out, _ = ops.sdpa(Q, K, V, is_causal=True)
+    ref, _ = O.sdpa(bf16_np(Qf), bf16_np(Kf), bf16_np(Vf), causal=True)
+    close(out, ref)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_full_bias_vs_oracle(cuda, d, causal):
+    n, hq, hkv, l, s = 2, 4, 2, 150, 150
+    q, k, v = gen((n, hq, l, d), seed=21), gen((n, hkv, s, d), seed=22), gen((n, hkv, s, d), seed=23)
+    bias = gen((n, hq, l, s), seed=24)
+    out, lse = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda), is_causal=causal, bias=bias.to(cuda))
+    ref, lref = O.sdpa(npy(q), npy(k), npy(v), causal=causal, bias=npy(bias))
+    close(out, ref)
+    np.testing.assert_allclose(npy(lse), lref, atol=2e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_sdpa_left_padded_batch(cuda, d):
+    """Batched generation with left padding (the reference app's call,
+    KERNELS.md:64, infer.py:22-24): one additive mask (N, 1, 1, S) for every
+    head and query, -inf on each sequence's padding, causal on top; rows
+    whose every key is masked are left out, as verify mode leaves them out."""
+    n, hq, hkv, s = 3, 8, 2, 257
+    pads = [0, 13, 100]
+    q, k, v = gen((n, hq, s, d), seed=31), gen((n, hkv, s, d), seed=32), gen((n, hkv, s, d), seed=33)
+    mask = torch.zeros(n, 1, 1, s)
+    for b, p in enumerate(pads):
+        mask[b, ..., :p] = float("-inf")
+    out, lse = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda), is_causal=True, bias=mask.to(torch.bfloat16).to(cuda))
+    ref, lref = O.sdpa(npy(q), npy(k), npy(v), causal=True, bias=npy(mask))
+    for b, p in enumerate(pads):
+        close(out[b:b + 1, :, p:], ref[b:b + 1, :, p:])
+        np.testing.assert_allclose(npy(lse)[b, :, p:], lref[b, :, p:], atol=2e-3, rtol=1e-3)
+    # decode step of the same batch: one query per sequence over the cache
+    qd = gen((n, hq, 1, d), seed=34)
+    out, _ = ops.sdpa(qd.to(cuda), k.to(cuda), v.to(cuda), bias=mask.to(torch.bfloat16).to(cuda))
+    ref, _ = O.sdpa(npy(qd), npy(k), npy(v), bias=npy(mask))
+    close(out, ref)
+
+
+@pytest.mark.parametrize("e", [16, 80, 96])
+def test_sdpa_other_head_dims(cuda, e):
+    q, k, v = gen((1, 4, 100, e), seed=41), gen((1, 2, 100, e), seed=42), gen((1, 2, 100, e), seed=43)
+    out, lse = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda), is_causal=True)
+    ref, lref = O.sdpa(npy(q), npy(k), npy(v), causal=True)
+    assert out.shape == (1, 4, 100, e)
+    close(out, ref)
+    np.testing.assert_allclose(npy(lse), lref, atol=2e-3, rtol=1e-3)
+
+
+def test_efficient_attention_with_bias_under_kuiper_mode(cuda):
+    import kuillm_amd as kuipy
+    aten = torch.ops.aten
+    q, k, v = (gen((2, 4, 64, 128), seed=51 + i).to(cuda) for i in range(3))
+    bias = gen((2, 4, 64, 64), seed=54).to(cuda)
+    kuipy.reset_verify()
+    with kuipy.KuiperMode(verify=True):
+        out, lse, _, _ = aten._scaled_dot_product_efficient_attention(q, k, v, bias, True, 0.0, False)
+    assert kuipy.print_verify_report() is True
+    assert "aten._scaled_dot_product_efficient_attention.default" in kuipy.verify_stats
+    ref, _ = O.sdpa(npy(q), npy(k), npy(v), bias=npy(bias))
+    close(out, ref)
 
 
 def test_sdpa_strided_views(cuda):

@@ -74,11 +74,16 @@ def test_sdpa_gate(fake):
     spec = impl.supported(fl, (q, k, v, 0.0, True), {})
     assert spec is not None and spec[2] is True and abs(spec[1] - 128 ** -0.5) < 1e-12
     assert impl.supported(eff, (q, k, v, None, True, 0.0, True), {"scale": 0.3})[1] == 0.3
-    assert impl.supported(eff, (q, k, v, cu(1, 8, 64, 64), True), {}) is None            # explicit bias
+    spec = impl.supported(eff, (q, k, v, cu(1, 8, 64, 64), True), {})                    # explicit bias
+    assert spec is not None and spec[-1].shape == (1, 8, 64, 64)
+    assert impl.supported(eff, (q, k, v, cu(1, 1, 1, 64), True), {}) is not None         # broadcast mask
+    assert impl.supported(eff, (q, k, v, cu(1, 8, 64, 63), True), {}) is None            # wrong key count
+    assert impl.supported(eff, (q, k, v, cu(1, 8, 64, 64, dtype=torch.float32), True), {}) is None
     assert impl.supported(fl, (q, k, v, 0.1, False), {}) is None                         # dropout
     assert impl.supported(fl, (q, k, v, 0.0, False, True), {}) is None                   # debug mask
     assert impl.supported(fl, (cu(1, 3, 64, 128), k, v), {}) is None                     # 3 % 2 heads
-    assert impl.supported(fl, (cu(1, 2, 8, 96), cu(1, 2, 8, 96), cu(1, 2, 8, 96)), {}) is None
+    assert impl.supported(fl, (cu(1, 2, 8, 96), cu(1, 2, 8, 96), cu(1, 2, 8, 96)), {}) is not None  # padded
+    assert impl.supported(fl, (cu(1, 2, 8, 160), cu(1, 2, 8, 160), cu(1, 2, 8, 160)), {}) is None
     f32 = torch.float32
     assert impl.supported(fl, (cu(1, 2, 8, 64, dtype=f32), cu(1, 2, 8, 64, dtype=f32),
                                cu(1, 2, 8, 64, dtype=f32)), {}) is None
