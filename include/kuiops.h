@@ -341,6 +341,18 @@ KUIOPS_API int kuiops_index(int64_t outer, int64_t size, int64_t inner, int64_t 
                  int elem_bytes, const void *inp, const int64_t *idx,
                  void *out, int *err_flag, void *stream);
 
+/* aten.index.Tensor with k (1..8) int64 index tensors on adjacent axes --
+ * the reference app's mask[T(4,int64), T(4,int64)] (KERNELS.md:67) among
+ * them: inp is viewed as (outer, sizes[0], .., sizes[k-1], inner), contiguous;
+ * idx[d] points to n_pos int64 indices (the index tensors broadcast to one
+ * shape, contiguous); out[o, j, i] = inp[o, idx[0][j], .., idx[k-1][j], i],
+ * contiguous (outer, n_pos, inner).  Negative indices wrap; out-of-range
+ * ones write 0 and set *err_flag.  Any element type (a byte copy of
+ * elem_bytes 1, 2, 4 or 8).  No reference kernel (kuiops/index/.gitkeep).  */
+KUIOPS_API int kuiops_index_multi(int64_t outer, int k, const int64_t *sizes, int64_t inner, int64_t n_pos,
+                       const int64_t *const *idx, int elem_bytes, const void *inp, void *out,
+                       int *err_flag, void *stream);
+
 /* ---- decoder-layer glue (the elementwise / norm / cat work around the hot
  * path; bf16 or f16, rows 16-byte aligned, n % 8 == 0) ------------------- */
 

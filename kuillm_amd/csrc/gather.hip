@@ -88,6 +88,40 @@ __global__ __launch_bounds__(256) void index_kernel(int64_t outer, int64_t size,
     }
 }
 
+// aten.index.Tensor with k <= 8 index tensors on adjacent axes: inp viewed
+// as (outer, size[0..k), inner), the k index tensors broadcast to n_pos
+// positions (contiguous int64 each); out (outer, n_pos, inner).
+constexpr int kMaxIdx = 8;
+struct MultiIndex {
+    const int64_t *idx[kMaxIdx];
+    int64_t size[kMaxIdx];
+    int k;
+};
+
+template <typename V>
+__global__ __launch_bounds__(256) void index_multi_kernel(int64_t outer, int64_t span, int64_t inner_v, int64_t n_pos,
+                                                          MultiIndex mi, const V *inp, V *out, int *err) {
+    const int64_t total = outer * n_pos * inner_v;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+        const int64_t i = t % inner_v;
+        const int64_t r = t / inner_v;
+        const int64_t j = r % n_pos, o = r / n_pos;
+        int64_t lin = 0;
+        bool ok = true;
+        for (int d = 0; d < mi.k; ++d) {
+            int64_t v = mi.idx[d][j];
+            if (v < 0) v += mi.size[d];
+            ok = ok && v >= 0 && v < mi.size[d];
+            lin = lin * mi.size[d] + v;
+        }
+        if (ok) out[t] = inp[(o * span + lin) * inner_v + i];
+        else {
+            out[t] = V{};
+            if (err) *err = 1;
+        }
+    }
+}
+
 static unsigned grid_for(int64_t total) {
     int64_t b = cdiv(total, 256);
     if (b > 65536) b = 65536;
@@ -175,6 +209,43 @@ extern "C" int kuiops_index(int64_t outer, int64_t size, int64_t inner, int64_t 
         case 2: hipLaunchKernelGGL(index_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, outer, size, inner, n_idx, (const uint16_t *)inp, idx, (uint16_t *)out, err_flag); break;
         case 4: hipLaunchKernelGGL(index_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, outer, size, inner, n_idx, (const uint32_t *)inp, idx, (uint32_t *)out, err_flag); break;
         case 8: hipLaunchKernelGGL(index_kernel<uint64_t>, dim3(grid), dim3(256), 0, s, outer, size, inner, n_idx, (const uint64_t *)inp, idx, (uint64_t *)out, err_flag); break;
+        default: return KUIOPS_E_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
+extern "C" int kuiops_index_multi(int64_t outer, int k, const int64_t *sizes, int64_t inner, int64_t n_pos,
+                                  const int64_t *const *idx, int elem_bytes, const void *inp, void *out,
+                                  int *err_flag, void *stream) {
+    if (outer < 0 || inner < 0 || n_pos < 0 || k < 1 || !sizes || !idx) return KUIOPS_E_INVALID;
+    if (k > kMaxIdx) return KUIOPS_E_UNSUPPORTED;
+    MultiIndex mi{};
+    mi.k = k;
+    int64_t span = 1;
+    for (int d = 0; d < k; ++d) {
+        if (sizes[d] < 0) return KUIOPS_E_INVALID;
+        mi.size[d] = sizes[d];
+        mi.idx[d] = idx[d];
+        span *= sizes[d];
+    }
+    if (outer * n_pos * inner == 0) return KUIOPS_OK;
+    if (!inp || !out) return KUIOPS_E_INVALID;
+    for (int d = 0; d < k; ++d)
+        if (!idx[d]) return KUIOPS_E_INVALID;
+    hipStream_t s = as_stream(stream);
+    const int64_t row_bytes = inner * elem_bytes;
+    if (row_bytes % 16 == 0 && aligned16(inp) && aligned16(out)) {
+        const int64_t iv = row_bytes / 16;
+        hipLaunchKernelGGL(index_multi_kernel<u32x4>, dim3(grid_for(outer * n_pos * iv)), dim3(256), 0, s, outer, span,
+                           iv, n_pos, mi, (const u32x4 *)inp, (u32x4 *)out, err_flag);
+        return launch_status();
+    }
+    const unsigned grid = grid_for(outer * n_pos * inner);
+    switch (elem_bytes) {
+        case 1: hipLaunchKernelGGL(index_multi_kernel<uint8_t>, dim3(grid), dim3(256), 0, s, outer, span, inner, n_pos, mi, (const uint8_t *)inp, (uint8_t *)out, err_flag); break;
+        case 2: hipLaunchKernelGGL(index_multi_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, outer, span, inner, n_pos, mi, (const uint16_t *)inp, (uint16_t *)out, err_flag); break;
+        case 4: hipLaunchKernelGGL(index_multi_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, outer, span, inner, n_pos, mi, (const uint32_t *)inp, (uint32_t *)out, err_flag); break;
+        case 8: hipLaunchKernelGGL(index_multi_kernel<uint64_t>, dim3(grid), dim3(256), 0, s, outer, span, inner, n_pos, mi, (const uint64_t *)inp, (uint64_t *)out, err_flag); break;
         default: return KUIOPS_E_UNSUPPORTED;
     }
     return launch_status();

@@ -89,8 +89,11 @@ def _rewrite(graph, node, spec):
         dim, _ = spec
         return K.gather.default, (node.args[0], dim, node.args[2]), {}
     if t is aten.index.Tensor:
-        d, _ = spec
-        return K.index.default, (node.args[0], d, node.args[1][d]), {}
+        d, tensors = spec
+        k = len(tensors) - 1
+        if k == 1:
+            return K.index.default, (node.args[0], d, node.args[1][d]), {}
+        return K.index_multi.default, (node.args[0], d, list(node.args[1][d:d + k])), {}
     return None
 
 

@@ -495,8 +495,13 @@ class MultinomialImpl(_Family):
 
 
 class IndexImpl(_Family):
-    """aten.index.Tensor with exactly one int64 index tensor -> kuiops_index
-    (embedding-row gathers; no reference kernel, kuiops/index/.gitkeep)."""
+    """aten.index.Tensor with int64 index tensors on adjacent axes (any
+    number; the reference app's call is a bool mask indexed by two int64
+    tensors, KERNELS.md:67) -> kuiops_index (one index tensor, e.g. an
+    embedding-row gather) or kuiops_index_multi (several, broadcast
+    together).  Bool index tensors (a data-dependent result size) and
+    non-adjacent index axes fall through.  No reference kernel
+    (kuiops/index/.gitkeep)."""
     tune_key = "INDEX"
     tune_params = ()
 
@@ -507,20 +512,22 @@ class IndexImpl(_Family):
         if not _is_dev(X) or X.element_size() not in (1, 2, 4, 8):
             return None
         pos = [i for i, t in enumerate(indices) if t is not None]
-        if len(pos) != 1:
+        if not pos or pos != list(range(pos[0], pos[0] + len(pos))) or pos[-1] >= X.dim() or len(pos) > 8:
             return None
-        d = pos[0]
-        idx = indices[d]
-        if not (isinstance(idx, torch.Tensor) and idx.dtype == torch.int64 and idx.is_cuda):
+        idx = [indices[d] for d in pos]
+        if not all(isinstance(t, torch.Tensor) and t.dtype == torch.int64 and t.is_cuda and t.device == X.device
+                   for t in idx):
             return None
-        if d >= X.dim():
+        try:
+            torch.broadcast_shapes(*[tuple(t.shape) for t in idx])
+        except RuntimeError:
             return None
-        return (d, [X, idx])
+        return (pos[0], [X] + idx)
 
     def run(self, spec, args, kwargs):
-        d, (X, idx) = spec
+        d, (X, *idx) = spec
         try:
-            return K.index(X, d, idx)
+            return K.index(X, d, idx[0]) if len(idx) == 1 else K.index_multi(X, d, idx)
         except _lib.Unsupported:
             return None
 

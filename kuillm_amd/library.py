@@ -34,6 +34,7 @@ _SCHEMAS = {
     "topk": "topk(Tensor x, int k, int dim=-1, bool largest=True, bool sorted=True) -> (Tensor, Tensor)",
     "gather": "gather(Tensor inp, int dim, Tensor idx) -> Tensor",
     "index": "index(Tensor inp, int dim, Tensor idx) -> Tensor",
+    "index_multi": "index_multi(Tensor inp, int first, Tensor[] idxs) -> Tensor",
     "scatter": "scatter(Tensor inp, int dim, Tensor idx, Tensor src) -> Tensor",
     "sort": "sort(Tensor x, int dim=-1, bool descending=False) -> (Tensor, Tensor)",
     "cumsum": "cumsum(Tensor x, int dim) -> Tensor",
@@ -87,6 +88,10 @@ def _index(inp, dim, idx):
     return ops.index(inp, dim, idx)
 
 
+def _index_multi(inp, first, idxs):
+    return ops.index_multi(inp, first, list(idxs))
+
+
 def _scatter(inp, dim, idx, src):
     return ops.scatter(inp, dim, idx, src)
 
@@ -118,7 +123,7 @@ def _cat(tensors, dim=0):
 
 for _name, _fn in (("mm", _mm), ("addmm", _addmm), ("bmm", _bmm), ("softmax", _softmax),
                    ("sdpa", _sdpa), ("sdpa_decode", _sdpa_decode), ("topk", _topk),
-                   ("gather", _gather), ("index", _index), ("scatter", _scatter), ("sort", _sort),
+                   ("gather", _gather), ("index", _index), ("index_multi", _index_multi), ("scatter", _scatter), ("sort", _sort),
                    ("cumsum", _cumsum), ("multinomial", _multinomial), ("elementwise", _elementwise),
                    ("mean_lastdim", _mean_lastdim), ("cat", _cat)):
     _LIB.impl(_name, _fn, "CUDA")
@@ -219,3 +224,9 @@ def _cat_fake(tensors, dim=0):
     d = dim % len(shape)
     shape[d] = sum(int(t.shape[d]) for t in tensors)
     return tensors[0].new_empty(shape)
+
+
+@_fake("index_multi")
+def _index_multi_fake(inp, first, idxs):
+    bshape = torch.broadcast_shapes(*[tuple(t.shape) for t in idxs])
+    return inp.new_empty((*inp.shape[:first], *bshape, *inp.shape[first + len(idxs):]))

@@ -515,6 +515,34 @@ def index(inp: torch.Tensor, dim: int, idx: torch.Tensor, check: bool | None = N
     return out
 
 
+def index_multi(inp: torch.Tensor, first: int, idxs, check: bool | None = None) -> torch.Tensor:
+    """inp[(slice(None),) * first + tuple(idxs)] for k >= 1 int64 index tensors
+    on the adjacent axes first .. first + k - 1 (aten.index.Tensor advanced
+    indexing): the index tensors broadcast together, and the result is
+    inp.shape[:first] + broadcast shape + inp.shape[first + k:]."""
+    k = len(idxs)
+    if k < 1 or k > 8 or any(t.dtype != torch.int64 for t in idxs) or first < 0 or first + k > inp.dim():
+        raise _lib.Unsupported("index_multi", _lib.E_UNSUPPORTED)
+    if inp.element_size() not in (1, 2, 4, 8):
+        raise _lib.Unsupported("index_multi", _lib.E_UNSUPPORTED)
+    bidx = [t.contiguous() for t in torch.broadcast_tensors(*idxs)]
+    bshape = tuple(bidx[0].shape)
+    ic = inp.contiguous()
+    outer = math.prod(ic.shape[:first])
+    sizes = ic.shape[first:first + k]
+    inner = math.prod(ic.shape[first + k:])
+    out = torch.empty((*ic.shape[:first], *bshape, *ic.shape[first + k:]), dtype=inp.dtype, device=inp.device)
+    if out.numel() == 0:
+        return out
+    flag = torch.zeros(1, dtype=torch.int32, device=inp.device) if (check or (check is None and CHECK_INDEX)) else None
+    lib = _lib_handle()
+    _lib.check("kuiops_index_multi", lib.kuiops_index_multi(
+        outer, k, _lib.i64_array(sizes), inner, bidx[0].numel(), (ctypes.c_void_p * k)(*[t.data_ptr() for t in bidx]),
+        ic.element_size(), ic.data_ptr(), out.data_ptr(), _ptr(flag), _stream(inp.device)))
+    _raise_if_flagged(flag, "index")
+    return out
+
+
 def scatter(inp: torch.Tensor, dim: int, idx: torch.Tensor, src: torch.Tensor, check: bool | None = None):
     """torch.scatter(inp, dim, idx, src) (aten.scatter.src): a copy of inp with
     out[x with dim <- idx[x]] = src[x] for every x of idx's shape (src sliced

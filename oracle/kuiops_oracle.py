@@ -369,6 +369,24 @@ def index(inp, dim: int, idx) -> np.ndarray:
     return np.take(inp, idx, axis=dim)
 
 
+def index_multi(inp, first: int, idxs) -> np.ndarray:
+    """inp[:, .., :, idxs[0], .., idxs[k-1], ...] with the k int64 index
+    tensors on adjacent axes first .. first+k-1, broadcast together (aten
+    advanced indexing, the reference app's mask[T(4,int64), T(4,int64)],
+    KERNELS.md:67); negative indices wrap.  Written as an explicit loop over
+    the broadcast index positions."""
+    inp = np.asarray(inp)
+    idxs = np.broadcast_arrays(*[np.asarray(t, dtype=np.int64) for t in idxs])
+    k = len(idxs)
+    bshape = idxs[0].shape
+    lead, trail = inp.shape[:first], inp.shape[first + k:]
+    out = np.empty(lead + bshape + trail, dtype=inp.dtype)
+    for pos in np.ndindex(*bshape):
+        sel = tuple(int(t[pos]) % inp.shape[first + d] for d, t in enumerate(idxs))
+        out[(slice(None),) * first + pos] = inp[(slice(None),) * first + sel]
+    return out
+
+
 def scatter(inp, dim: int, idx, src) -> np.ndarray:
     """Copy of inp with out[x with axis `dim` replaced by idx[x]] = src[x] for
     every x of idx's shape (kuipy/kuiops.py:757-807; aten.scatter.src)."""

@@ -162,6 +162,14 @@ def main():
     g["cat_a"], g["cat_b"], g["cat_out"] = bits(c1), bits(c2), bits(torch.cat([c1, c2], dim=2))
     q = torch.randn(2, 4, 6, 16)
     g["cat_q"], g["cat_rot"] = q.numpy(), torch.cat((-q[..., 8:], q[..., :8]), dim=-1).numpy()
+    # index.Tensor with two int64 index tensors on a bool matrix: the
+    # reference app's call T(2,bool)[T(4,int64),T(4,int64)] (KERNELS.md:67)
+    bm = torch.rand(24, 30) > 0.5
+    i0 = torch.randint(-24, 24, (2, 1, 3, 4)); i1 = torch.randint(0, 30, (1, 5, 3, 4))
+    g["index2_mask"], g["index2_i0"], g["index2_i1"], g["index2_out"] = bm.numpy(), i0.numpy(), i1.numpy(), bm[i0, i1].numpy()
+    t4 = torch.randn(3, 6, 7, 5)
+    j0, j1 = torch.randint(0, 6, (4,)), torch.randint(-7, 7, (4,))
+    g["index3d_inp"], g["index3d_j0"], g["index3d_j1"], g["index3d_out"] = t4.numpy(), j0.numpy(), j1.numpy(), t4[:, j0, j1].numpy()
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(g)} arrays)")
 

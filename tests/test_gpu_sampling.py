@@ -162,6 +162,33 @@ def test_index_vs_oracle(cuda, golden):
         ops.index(emb, 0, torch.tensor([32000], device=cuda), check=True)
 
 
+def test_index_multi_vs_oracle(cuda, golden):
+    """Several int64 index tensors on adjacent axes: the reference app's
+    bool-mask call (KERNELS.md:67), a middle-axis pair with negative indices,
+    broadcast index shapes, bit-exact against the aten golden and the oracle."""
+    import kuillm_amd as kuipy
+    m = torch.from_numpy(golden["index2_mask"]).to(cuda)
+    i0, i1 = (torch.from_numpy(golden[k]).to(cuda) for k in ("index2_i0", "index2_i1"))
+    out = ops.index_multi(m, 0, [i0, i1])
+    assert out.dtype == torch.bool and np.array_equal(out.cpu().numpy(), golden["index2_out"])
+    t = torch.from_numpy(golden["index3d_inp"]).to(cuda)
+    j0, j1 = (torch.from_numpy(golden[k]).to(cuda) for k in ("index3d_j0", "index3d_j1"))
+    assert np.array_equal(npy(ops.index_multi(t, 1, [j0, j1])), golden["index3d_out"])
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(3, 40, 50, 16, generator=g).to(torch.bfloat16)
+    a, b = torch.randint(-40, 40, (6, 1), generator=g), torch.randint(0, 50, (1, 9), generator=g)
+    got = ops.index_multi(x.to(cuda), 1, [a.to(cuda), b.to(cuda)])
+    assert np.array_equal(got.view(torch.int16).cpu().numpy(),
+                          O.index_multi(x.view(torch.int16).numpy(), 1, [a.numpy(), b.numpy()]))
+    kuipy.reset_verify()
+    with kuipy.KuiperMode(verify=True):
+        r = m[i0, i1]                       # dispatched as aten.index.Tensor with two indices
+        f = t[:, j0, j1]
+    assert torch.equal(r, out) and np.array_equal(npy(f), golden["index3d_out"])
+    with pytest.raises(IndexError):
+        ops.index_multi(t, 1, [j0, torch.tensor([7, 0, 0, 0], device=cuda)], check=True)
+
+
 # ------------------------------------------- sort / cumsum / scatter / sampling
 
 def test_sort_golden(cuda, golden):

@@ -65,7 +65,7 @@ def test_unsupported_nodes_stay():
         y = aten.mm(x, w)                                         # int32: not served
         a = aten._scaled_dot_product_flash_attention(q, k, v, 0.0, False)   # head dim 160
         s = aten._softmax(q, 2, False)                            # not the last dim
-        e = aten.index(x, [idx, idx])                             # two index tensors
+        e = aten.index(q, [idx, None, idx])                       # index axes not adjacent
         return y, a[0], s, e
     with FakeTensorMode():
         args = (cu(4, 4, dtype=torch.int32), cu(4, 4, dtype=torch.int32), cu(1, 2, 8, 160), cu(1, 2, 8, 160),

@@ -322,3 +322,19 @@ def test_top_p_filter_matches_transformers():
         got = O.top_p_filter(scores, top_p)
         np.testing.assert_array_equal(np.isinf(got), np.isinf(exp))
         np.testing.assert_array_equal(got[~np.isinf(got)], exp[~np.isinf(exp)])
+
+
+# ------------------------------------------------- multi-tensor index
+
+def test_index_multi_against_aten_golden_and_numpy(golden):
+    out = O.index_multi(golden["index2_mask"], 0, [golden["index2_i0"], golden["index2_i1"]])
+    assert out.dtype == np.bool_ and np.array_equal(out, golden["index2_out"])
+    out3 = O.index_multi(golden["index3d_inp"], 1, [golden["index3d_j0"], golden["index3d_j1"]])
+    assert np.array_equal(out3, golden["index3d_out"])
+    # numpy's own fancy indexing (the textbook routine) on a random case
+    x = rng.standard_normal((4, 5, 6, 3))
+    a, b = rng.integers(-5, 5, (2, 3)), rng.integers(0, 6, (1, 3))
+    assert np.array_equal(O.index_multi(x, 1, [a, b]), x[:, a, b])
+    # one index tensor reduces to the single-axis index
+    ids = rng.integers(0, 5, (7,))
+    assert np.array_equal(O.index_multi(x, 1, [ids]), O.index(x, 1, ids))

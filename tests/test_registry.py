@@ -114,7 +114,9 @@ def test_index_gate(fake):
     ids = cu(1, 7, dtype=torch.int64)
     assert impl.supported(aten.index.Tensor, (E, [ids]), {}) == (0, [E, ids])
     assert impl.supported(aten.index.Tensor, (cu(2, 9, 4), [None, ids]), {})[0] == 1
-    assert impl.supported(aten.index.Tensor, (E, [ids, ids]), {}) is None                 # two indices
+    spec = impl.supported(aten.index.Tensor, (E, [ids, ids]), {})                          # two indices
+    assert spec[0] == 0 and len(spec[1]) == 3
+    assert impl.supported(aten.index.Tensor, (cu(2, 9, 4), [ids, None, ids]), {}) is None  # not adjacent
     assert impl.supported(aten.index.Tensor, (E, [cu(32000, dtype=torch.bool)]), {}) is None
 
 
