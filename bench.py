@@ -152,6 +152,8 @@ ALGO_BYTES = {
     "bmm_32x2048x128x2048": 2 * 32 * 2048 * 128 * 2 + 32 * 2048 * 2048 * 2,
     "copy_256MiB": 2 * 256 * 2 ** 20,
 }
+# the profiled decode step runs after a 512-token prefill: 513 cached keys
+ALGO_BYTES["llama1b_decode_token"] = None     # filled in below, after llama_decode_bytes
 
 
 def profile_kernels(torch, ops, dev):
@@ -501,6 +503,9 @@ def llama_decode_bytes(c, kv_tokens):
     per_layer = c["d"] * (c["hq"] + 2 * c["hkv"]) * hd + c["hq"] * hd * c["d"] + 3 * c["d"] * c["ffn"]
     weights = (c["layers"] * per_layer + c["d"] * c["vocab"]) * 2
     return weights + c["layers"] * 2 * c["hkv"] * hd * 2 * kv_tokens
+
+
+ALGO_BYTES["llama1b_decode_token"] = llama_decode_bytes(LLAMA1B, 513)
 
 
 def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3):
