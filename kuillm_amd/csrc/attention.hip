@@ -662,10 +662,16 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     if (a.splits == 1 || !a.counters) return;
 
     // The last of the group's split work-groups to arrive merges the splits
-    // in split order (bitwise repeatable whatever the arrival order).  Each
-    // thread waits for its agent-coherent stores to complete before the
-    // barrier that precedes the counter increment, so no device-scope fence
-    // (an L2 write-back per XCD) is needed.
+    // in split order (bitwise repeatable whatever the arrival order).
+    // Ordering (as in the decode GEMM's merge): the split states are
+    // agent-scope relaxed atomic stores (`global_store sc1`, written through
+    // the per-XCD L2); each thread waits for their acknowledgements
+    // (s_waitcnt(0)) before the barrier that precedes tid 0's agent-scope
+    // counter RMW, and the merging work-group reads them with sc1 buffer
+    // loads, which miss the non-coherent caches.  This relies on the hardware
+    // rule that an acknowledged sc1 store is visible at the agent's coherence
+    // point before a later RMW of the same agent, not on a release / acquire
+    // pair (which would add an L2 write-back per XCD to every work-group).
     __shared__ int s_last;
     __shared__ float s_w[R][64];
     __shared__ float s_M[R], s_L[R];

@@ -396,11 +396,19 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
     }
     if (a.splits > 1) {
         // The last work-group of the strip to arrive sums the partials in
-        // split order (bitwise repeatable whatever the arrival order).  The
-        // partials and the counter use agent-coherent accesses, so no
-        // device-scope fence (an L2 write-back per XCD) is needed: each
-        // thread waits for its stores to complete before the barrier that
-        // precedes the counter increment.
+        // split order (bitwise repeatable whatever the arrival order).
+        // Ordering: the partials are agent-scope relaxed atomic stores, which
+        // the gfx942 / gfx950 memory model lowers to `global_store sc1`
+        // (written through the per-XCD L2 to the agent's coherence point);
+        // s_waitcnt(0) waits for their acknowledgements, the barrier orders
+        // every wave's acknowledged stores before tid 0's relaxed agent-scope
+        // counter RMW (performed at the coherence point), and the summing
+        // work-group reads with agent-scope relaxed atomic loads (`sc1`, which
+        // miss the non-coherent caches).  Relaxed atomics alone do not order
+        // two locations in the formal model; this relies on the hardware rule
+        // that an acknowledged sc1 store is visible at the coherence point
+        // before a later RMW of the same agent.  A release / acquire pair would
+        // add an L2 write-back per XCD to every work-group.
         __shared__ int s_last;
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);
