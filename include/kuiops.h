@@ -498,6 +498,36 @@ KUIOPS_API int kuiops_mean_lastdim(int64_t m, int64_t n, int dtype, const void *
 KUIOPS_API int kuiops_cat(int n_inputs, const void *const *inputs, const int64_t *widths,
                const int64_t *outer_strides, int64_t outer, int elem_bytes, void *out, void *stream);
 
+/* Batched decode projection for 1 <= M <= 16 sequences: the fused input
+ * stage and epilogue of kuiops_decode_linear / kuiops_decode_gate_up /
+ * kuiops_decode_qkv_rope, per row, over one nn.Linear weight W [N, K]
+ * (K contiguous, row stride ldw).  Row m of x comes from `in` at row
+ * in_row[m] (device int64, clamped to [0, in_rows)) when in_row is
+ * non-null (an embedding lookup), else at row m, rows ld_in apart; x_kind:
+ *   KUIOPS_X_PLAIN    x = in
+ *   KUIOPS_X_RMSNORM  h = round(in + in_add[m]); x = round(w * round(h *
+ *                     rsqrt(mean(h^2) + eps))); h stored to h_out[m] if set
+ *   KUIOPS_X_SWIGLU   x = round(round(silu(in[:K])) * in[K:2K])
+ * out_kind 0 (plain): out[m, r] = round(x_m . W[r]);
+ * out_kind 1 (SwiGLU pair): rows p and p + pair_off of W -> out[m, p];
+ * out_kind 2 (rotary + KV append): W = [q; k; v] heads of hd = 2 * pair_off,
+ *   rows i and i + hd/2 of a head rotated at position pos[m]; q -> out[m],
+ *   k / v -> caches at (m, head, pos[m]) with strides sk / sv {batch, head,
+ *   position} when pos[m] < cache_cap.
+ * Rounding points as the batch-1 entry points (h bit-identical; the dot
+ * products differ from them only in fp32 summation order).
+ * M * K * 2 <= 140 KiB, else KUIOPS_E_UNSUPPORTED.  No reference
+ * counterpart: it fuses the mm launcher with the RMSNorm / SwiGLU / rotary /
+ * KV-cache cat launches of a batched decode step (infer.py:57-89 generates
+ * in batches).                                                              */
+KUIOPS_API int kuiops_decode_rows_batched(int64_t M, int64_t N, int64_t K, int dtype, int x_kind, int out_kind,
+                               const void *in, int64_t ld_in, const int64_t *in_row, int64_t in_rows,
+                               const void *in_add, int64_t ld_add, const void *norm_w, float eps,
+                               void *h_out, int64_t ld_h, const void *W, int64_t ldw, void *out, int64_t ld_out,
+                               int64_t pair_off, int64_t hq, int64_t hkv, int64_t hd, const float *inv_freq,
+                               const int32_t *pos, void *k_cache, const int64_t sk[3], void *v_cache,
+                               const int64_t sv[3], int64_t cache_cap, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

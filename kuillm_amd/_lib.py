@@ -78,6 +78,9 @@ SIGNATURES = {
     "kuiops_multinomial": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
     "kuiops_index": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "kuiops_index_multi": (_int, [_i64, _int, _i64p, _i64, _i64, ctypes.POINTER(_vp), _int, _vp, _vp, _vp, _vp]),
+    "kuiops_decode_rows_batched": (_int, [_i64, _i64, _i64, _int, _int, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
+                                          _flt, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp,
+                                          _vp, _vp, _i64p, _vp, _i64p, _i64, _vp]),
     "kuiops_rmsnorm": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _flt, _vp, _i64, _vp]),
     "kuiops_silu_mul": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp]),
     "kuiops_rope_kv_append": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _vp, _vp,

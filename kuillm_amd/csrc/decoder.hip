@@ -493,9 +493,344 @@ static int decode_linear_run(DecLinArgs a, int dtype, int x_kind, void *stream) 
     return launch_status();
 }
 
+// ---------------------------------- batched decode projection (2..16 rows)
+
+// The decode projection for a batch of M <= 16 sequences: the same fused
+// input stage (plain / residual add + RMSNorm / SwiGLU) and epilogues (plain,
+// SwiGLU pair, rotary + KV append) as decode_rows_kernel, per row, with the
+// dot products on 16x16x32 MFMAs: an nn.Linear weight row is K-contiguous,
+// so a 16-byte load of it is already the B operand (8 k of one output), and
+// the normalised rows of x, staged in LDS, are the A operand (rows past M
+// are zero).  A work-group owns 16 outputs (8 pairs for the paired
+// epilogues); its NW waves split K and are summed in wave order.  In a 64-k
+// step the 4 lanes of a row read its 128 bytes as two 64-byte runs (one per
+// MFMA: k = 8 * cq and 32 + 8 * cq); PF steps are in flight.
+struct DecMArgs {
+    int64_t M, N, K;
+    const void *in; int64_t ld_in;
+    const int64_t *in_row; int64_t in_rows;  // optional per-row index into `in` (embedding lookup)
+    const void *in_add; int64_t ld_add;
+    const void *norm_w; float eps;
+    void *h_out; int64_t ld_h;
+    const void *W; int64_t ldw;
+    void *out; int64_t ld_out;
+    int64_t pair_off; int pair_shift;
+    int64_t hq, hkv, hd;
+    const float *inv_freq;
+    const int32_t *pos;                      // [M] device positions (rotary epilogue)
+    void *kc; int64_t sk0, sk1, sk2;         // k cache: batch, head, position strides
+    void *vc; int64_t sv0, sv1, sv2;
+    int64_t cap;
+    int64_t kq;                              // k per wave, a multiple of 64
+};
+
+__device__ __forceinline__ int64_t pair_div_m(const DecMArgs &a, int64_t p) {
+    return a.pair_shift >= 0 ? p >> a.pair_shift : p / a.pair_off;
+}
+
+// Epilogue of decode_mrows_kernel for x row m, output o of group g (the
+// group's 16 sums in vals[m][0..15]).
+template <typename T, int OK>
+__device__ __forceinline__ void decode_mrows_epilogue(const DecMArgs &a, int64_t g, int m, int o,
+                                                      const float (*vals)[17]) {
+    if constexpr (OK == kOutPlain) {
+        const int64_t r = g * 16 + o;
+        if (r < a.N) reinterpret_cast<T *>(a.out)[m * a.ld_out + r] = from_f32<T>(vals[m][o]);
+    } else if constexpr (OK == kOutSwiGlu) {
+        const int64_t p = g * 8 + o;
+        if (o < 8 && p < a.N / 2) {
+            const float x1 = rnd<T>(vals[m][o]), x2 = rnd<T>(vals[m][o + 8]);
+            reinterpret_cast<T *>(a.out)[m * a.ld_out + p] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
+        }
+    } else {
+        const int64_t p = g * 8 + (o & 7), e = o >> 3;
+        if (p >= a.N / 2) return;
+        const int64_t half = a.pair_off, head = pair_div_m(a, p), i = p - head * half + e * half;
+        const float x1 = rnd<T>(vals[m][o & 7]), x2 = rnd<T>(vals[m][(o & 7) + 8]);
+        const int64_t pos = a.pos ? (int64_t)a.pos[m] : 0;
+        float res;
+        if (head < a.hq + a.hkv) {
+            const float ang = (float)pos * a.inv_freq[p - head * half];
+            const float c = rnd<T>(cosf(ang)), sn = rnd<T>(sinf(ang));
+            res = e == 0 ? rnd<T>(x1 * c) + rnd<T>(-x2 * sn) : rnd<T>(x2 * c) + rnd<T>(x1 * sn);
+        } else {
+            res = e == 0 ? x1 : x2;
+        }
+        T *dst;
+        if (head < a.hq) {
+            dst = reinterpret_cast<T *>(a.out) + m * a.ld_out + head * a.hd + i;
+        } else {
+            if (pos < 0 || pos >= a.cap) return;
+            dst = head < a.hq + a.hkv
+                      ? reinterpret_cast<T *>(a.kc) + m * a.sk0 + (head - a.hq) * a.sk1 + pos * a.sk2 + i
+                      : reinterpret_cast<T *>(a.vc) + m * a.sv0 + (head - a.hq - a.hkv) * a.sv1 + pos * a.sv2 + i;
+        }
+        *dst = from_f32<T>(res);
+    }
+}
+
+template <typename T, int XK, int OK, int NW>
+__global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
+    typedef typename Mfma<T>::frag frag;
+    constexpr int PF = 32 / NW;                       // 64-k steps in flight per wave (64 KB per work-group)
+    extern __shared__ __attribute__((aligned(16))) char dsm[];
+    T *sx = reinterpret_cast<T *>(dsm);               // [M][K] normalised rows of x
+    __shared__ float red[NW][4][64];
+    __shared__ float vals[16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, cq = lane >> 4;
+    const int M = (int)a.M;
+
+    // ---- output groups: a work-group owns groups blockIdx.x + i * gridDim.x
+    // (16 outputs, or 8 pairs, each) and stages x once for all of them
+    const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
+    // W row of this lane's logical output n in group g (row 0, never
+    // stored, for outputs past N)
+    auto w_row = [&](int64_t g) __attribute__((always_inline)) -> const T * {
+        int64_t wrow;
+        bool wvalid;
+        if constexpr (OK == kOutPlain) {
+            wrow = g * 16 + n;
+            wvalid = wrow < a.N;
+        } else {
+            const int64_t p = g * 8 + (n & 7), e = n >> 3;
+            wvalid = p < a.N / 2;
+            if constexpr (OK == kOutSwiGlu) {
+                wrow = p + e * a.pair_off;
+            } else {
+                const int64_t half = a.pair_off, head = pair_div_m(a, p);
+                wrow = head * a.hd + (p - head * half) + e * half;
+            }
+        }
+        return reinterpret_cast<const T *>(a.W) + (wvalid ? wrow : 0) * a.ldw;
+    };
+    // every wave runs the same padded step count (steps past its K range
+    // load nothing), so group boundaries line up for the barriers
+    const int64_t kbeg = (int64_t)wave * a.kq;
+    const int64_t kend = min(a.K, kbeg + a.kq);
+    const int nsp = (int)(((a.kq / 64) + PF - 1) / PF) * PF;
+    // ---- input stage: wave w normalises rows w, w + NW, ... into LDS.  A
+    // lane issues XB chunk loads (and their residual / up halves) before it
+    // uses any, so a row costs one memory round trip per 64 * XB chunks.
+    constexpr int XB = 4;
+    const int nch = (int)(a.K / 8);
+    const T *addp = reinterpret_cast<const T *>(a.in_add);
+    for (int m = wave; m < M; m += NW) {
+        const T *in = reinterpret_cast<const T *>(a.in) +
+                      (a.in_row ? max((int64_t)0, min(a.in_row[m], a.in_rows - 1)) : (int64_t)m) * a.ld_in;
+        T *srow = sx + (int64_t)m * a.K;
+        float ss = 0.f;
+        for (int c0 = lane; c0 < nch; c0 += 64 * XB) {
+            u32x4 v0[XB], v1[XB];
+#pragma unroll
+            for (int j = 0; j < XB; ++j) {
+                const int c = c0 + 64 * j;
+                v0[j] = v1[j] = u32x4{0, 0, 0, 0};
+                if (c < nch) {
+                    v0[j] = *reinterpret_cast<const u32x4 *>(in + c * 8);
+                    if constexpr (XK == kXSwiGlu) v1[j] = *reinterpret_cast<const u32x4 *>(in + a.K + c * 8);
+                    if constexpr (XK == kXRmsNorm)
+                        if (addp) v1[j] = *reinterpret_cast<const u32x4 *>(addp + m * a.ld_add + c * 8);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < XB; ++j) {
+                const int c = c0 + 64 * j;
+                if (c >= nch) continue;
+                float h[8], o[8];
+                unpack8<T>(v0[j], h);
+                if constexpr (XK == kXRmsNorm) {
+                    if (addp) {
+                        unpack8<T>(v1[j], o);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) h[e] = rnd<T>(h[e] + o[e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss += h[e] * h[e];
+                    // the summed row goes to LDS first (rounded: exact), normalised below
+                    *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(h);
+                    if (a.h_out && blockIdx.x == 0)
+                        *reinterpret_cast<u32x4 *>(reinterpret_cast<T *>(a.h_out) + m * a.ld_h + c * 8) = pack8f<T>(h);
+                } else if constexpr (XK == kXSwiGlu) {
+                    unpack8<T>(v1[j], o);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) h[e] = rnd<T>(h[e] / (1.f + expf(-h[e]))) * o[e];
+                    *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(h);
+                } else {
+                    *reinterpret_cast<u32x4 *>(srow + c * 8) = v0[j];
+                }
+            }
+        }
+        if constexpr (XK == kXRmsNorm) {
+            ss = wave_sum(ss);
+            const float inv = rsqrtf(ss / (float)a.K + a.eps);
+            for (int c = lane; c < nch; c += 64) {
+                float h[8], w8[8], xo[8];
+                unpack8<T>(*reinterpret_cast<const u32x4 *>(srow + c * 8), h);
+                unpack8<T>(*reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.norm_w) + c * 8), w8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xo[e] = w8[e] * rnd<T>(h[e] * inv);
+                *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(xo);
+            }
+        }
+    }
+    u32x4 wr[PF][2];
+    auto load_w = [&](const T *Wr, int st, u32x4 *dst) __attribute__((always_inline)) {
+        const int64_t k = kbeg + (int64_t)st * 64 + 8 * cq;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            dst[h] = k + 32 * h < kend ? *reinterpret_cast<const u32x4 *>(Wr + k + 32 * h) : u32x4{0, 0, 0, 0};
+    };
+    const int64_t G = gridDim.x;
+    int64_t g = blockIdx.x;
+    const T *Wc = w_row(g);
+#pragma unroll
+    for (int st = 0; st < PF; ++st) load_w(Wc, st, wr[st]);
+
+    __syncthreads();
+
+    const bool mrow = n < M;                          // A operand row (x row n of this lane)
+    for (; g < ngroups; g += G) {
+        // ---- MFMAs over this wave's K range; the last PF steps prefetch
+        // the next group's first PF
+        const bool has_next = g + G < ngroups;
+        const T *Wn = w_row(has_next ? g + G : g);
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < nsp; s0 += PF) {
+#pragma unroll
+            for (int j = 0; j < PF; ++j) {
+                const int st = s0 + j;
+                const int64_t k = kbeg + (int64_t)st * 64 + 8 * cq;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const bool in_k = k + 32 * h < kend;
+                    const u32x4 xa = (mrow && in_k)
+                                         ? *reinterpret_cast<const u32x4 *>(sx + (int64_t)n * a.K + k + 32 * h)
+                                         : u32x4{0, 0, 0, 0};
+                    acc = Mfma<T>::m16(as_frag<frag>(xa), as_frag<frag>(wr[j][h]), acc);
+                }
+                if (st + PF < nsp) load_w(Wc, st + PF, wr[j]);
+                else if (has_next) load_w(Wn, st + PF - nsp, wr[j]);
+            }
+        }
+        // acc[i]: x row 4 * cq + i, output n.  Waves summed in wave order.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
+        __syncthreads();
+        if (tid < 256) {
+            const int m = tid >> 4, o = tid & 15;
+            const int l = (m >> 2) * 16 + o, i = m & 3;
+            float v = red[0][i][l];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) v += red[w][i][l];
+            vals[m][o] = v;
+        }
+        __syncthreads();
+        if (tid < 256 && (tid >> 4) < M) decode_mrows_epilogue<T, OK>(a, g, tid >> 4, tid & 15, vals);
+        Wc = Wn;
+    }
+}
+
+// dynamic LDS for the staged rows of x; with the 17 KiB of static reduction
+// arrays of 16 waves it stays within the CU's 160 KiB
+constexpr int64_t kDecMaxLds = 140 * 1024;
+
+template <typename T, int XK, int OK, int NW>
+static hipError_t decode_mrows_launch1(const DecMArgs &a, unsigned grid, size_t lds, hipStream_t st) {
+    // more than 64 KB of dynamic LDS has to be allowed per kernel first
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_mrows_kernel<T, XK, OK, NW>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecMaxLds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((decode_mrows_kernel<T, XK, OK, NW>), dim3(grid), dim3(NW * 64), lds, st, a);
+    return hipSuccess;
+}
+
+template <typename T, int XK, int OK>
+static hipError_t decode_mrows_launch2(const DecMArgs &a, int nw, unsigned grid, size_t lds, hipStream_t st) {
+    if (nw == 16) return decode_mrows_launch1<T, XK, OK, 16>(a, grid, lds, st);
+    if (nw == 8) return decode_mrows_launch1<T, XK, OK, 8>(a, grid, lds, st);
+    return decode_mrows_launch1<T, XK, OK, 4>(a, grid, lds, st);
+}
+
+template <typename T, int XK>
+static hipError_t decode_mrows_launch(const DecMArgs &a, int out_kind, int nw, unsigned grid, size_t lds,
+                                      hipStream_t st) {
+    switch (out_kind) {
+        case kOutPlain: return decode_mrows_launch2<T, XK, kOutPlain>(a, nw, grid, lds, st);
+        case kOutSwiGlu: return decode_mrows_launch2<T, XK, kOutSwiGlu>(a, nw, grid, lds, st);
+        default: return decode_mrows_launch2<T, XK, kOutRope>(a, nw, grid, lds, st);
+    }
+}
+
 }  // namespace kuiops
 
 using namespace kuiops;
+
+extern "C" int kuiops_decode_rows_batched(
+    int64_t M, int64_t N, int64_t K, int dtype, int x_kind, int out_kind, const void *in, int64_t ld_in,
+    const int64_t *in_row, int64_t in_rows, const void *in_add, int64_t ld_add, const void *norm_w, float eps,
+    void *h_out, int64_t ld_h, const void *W, int64_t ldw, void *out, int64_t ld_out, int64_t pair_off,
+    int64_t hq, int64_t hkv, int64_t hd, const float *inv_freq, const int32_t *pos, void *k_cache,
+    const int64_t sk[3], void *v_cache, const int64_t sv[3], int64_t cache_cap, void *stream) {
+    if (M < 0 || N < 0 || K < 0) return KUIOPS_E_INVALID;
+    if (x_kind != kXPlain && x_kind != kXRmsNorm && x_kind != kXSwiGlu) return KUIOPS_E_INVALID;
+    if (out_kind != kOutPlain && out_kind != kOutSwiGlu && out_kind != kOutRope) return KUIOPS_E_INVALID;
+    if (M == 0 || N == 0) return KUIOPS_OK;
+    if (!in || !W || !out || (x_kind == kXRmsNorm && !norm_w)) return KUIOPS_E_INVALID;
+    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
+    if (M > 16 || K == 0 || K % 8 || ldw % 8 || ldw < K || ld_in % 8 || (in_add && ld_add % 8) ||
+        (h_out && ld_h % 8))
+        return KUIOPS_E_UNSUPPORTED;
+    if (x_kind == kXSwiGlu ? ld_in < 2 * K : (ld_in < K && !in_row && M > 1)) return KUIOPS_E_INVALID;
+    if ((int64_t)M * K * 2 > kDecMaxLds) return KUIOPS_E_UNSUPPORTED;
+    if (!aligned16(in) || !aligned16(W) || (in_add && !aligned16(in_add)) || (norm_w && !aligned16(norm_w)) ||
+        (h_out && !aligned16(h_out)))
+        return KUIOPS_E_UNSUPPORTED;
+    if (in_row && (in_rows <= 0)) return KUIOPS_E_INVALID;
+    if (out_kind != kOutPlain && (N % 2 || pair_off <= 0)) return KUIOPS_E_INVALID;
+    if (out_kind == kOutRope) {
+        if (hq < 0 || hkv < 0 || hd <= 0 || hd % 2 || 2 * pair_off != hd || N != (hq + 2 * hkv) * hd) return KUIOPS_E_INVALID;
+        if (!inv_freq || !k_cache || !v_cache || !sk || !sv || !pos) return KUIOPS_E_INVALID;
+    }
+    DecMArgs a{};
+    a.M = M; a.N = N; a.K = K; a.in = in; a.ld_in = ld_in; a.in_row = in_row; a.in_rows = in_rows;
+    a.in_add = in_add; a.ld_add = ld_add; a.norm_w = norm_w; a.eps = eps; a.h_out = h_out; a.ld_h = ld_h;
+    a.W = W; a.ldw = ldw; a.out = out; a.ld_out = ld_out;
+    a.pair_off = pair_off; a.pair_shift = log2_exact(pair_off);
+    a.hq = hq; a.hkv = hkv; a.hd = hd; a.inv_freq = inv_freq; a.pos = pos;
+    if (out_kind == kOutRope) {
+        a.kc = k_cache; a.sk0 = sk[0]; a.sk1 = sk[1]; a.sk2 = sk[2];
+        a.vc = v_cache; a.sv0 = sv[0]; a.sv1 = sv[1]; a.sv2 = sv[2];
+    }
+    a.cap = cache_cap;
+    // Output groups per work-group: enough work-groups for every CU, each
+    // staging x once for up to 8 groups.
+    const int64_t ngroups = out_kind == kOutPlain ? cdiv(N, 16) : cdiv(N / 2, 8);
+    const int64_t gpw = std::max<int64_t>(1, std::min<int64_t>(8, ngroups / 256));
+    const int64_t grid = cdiv(ngroups, gpw);
+    if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    // Waves per work-group: K is split over more waves when the output
+    // groups alone would leave CUs idle (N = 2048 is 128 work-groups), as
+    // long as each wave keeps at least two 64-k steps.
+    int nw = 4;
+    while (nw < 16 && grid * nw < 2048 && K >= (int64_t)nw * 2 * 128) nw *= 2;
+    a.kq = cdiv(cdiv(K, nw), 64) * 64;
+    const size_t lds = (size_t)M * K * 2;
+    hipStream_t st = as_stream(stream);
+#define KUIOPS_DECM(T)                                                                                   \
+    switch (x_kind) {                                                                                    \
+        case kXPlain: err = decode_mrows_launch<T, kXPlain>(a, out_kind, nw, (unsigned)grid, lds, st); break;     \
+        case kXRmsNorm: err = decode_mrows_launch<T, kXRmsNorm>(a, out_kind, nw, (unsigned)grid, lds, st); break; \
+        default: err = decode_mrows_launch<T, kXSwiGlu>(a, out_kind, nw, (unsigned)grid, lds, st); break;         \
+    }
+    hipError_t err;
+    if (dtype == KUIOPS_BF16) { KUIOPS_DECM(bf16_t) } else { KUIOPS_DECM(f16_t) }
+    if (err != hipSuccess) return KUIOPS_E_HIP;
+#undef KUIOPS_DECM
+    return launch_status();
+}
 
 extern "C" int kuiops_rmsnorm(int64_t m, int64_t n, int dtype, const void *x, int64_t ldx, const void *residual,
                               int64_t ldr, void *res_out, int64_t ldro, const void *weight, float eps, void *y,

@@ -112,26 +112,39 @@ class LlamaDecoder:
         self.pos, self.kv_len = self.step_state[0], self.step_state[1]
         self.graph = None
         self.fused = self.n == 1 and s.d <= 4096 and s.ffn <= 8192 and s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0
-        if self.fused:
+        # batches of 2..16: the batched form of the same fused projections
+        # (every row of x staged in LDS: n * max(d, ffn) * 2 <= 140 KiB)
+        self.fused_batched = (2 <= self.n <= 16 and self.n * max(s.d, s.ffn) * 2 <= 140 * 1024
+                              and s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0)
+        if self.fused or self.fused_batched:
             self._setup_fused()
 
     def _setup_fused(self):
         """Static buffers of the batch-1 decode step, whose projections carry
         their input stage (RMSNorm) and epilogue (rotary + KV append, SwiGLU):
         5 launches per layer."""
-        s, dev = self.s, self.dev
+        s, dev, n = self.s, self.dev, self.n
         bf = dict(dtype=self.dtype, device=dev)
-        self.h_buf = [torch.empty(s.d, **bf), torch.empty(s.d, **bf)]
-        self.q1 = torch.empty(1, s.hq, 1, s.hd, **bf)
-        self.att1 = torch.empty(1, 1, s.hq * s.hd, **bf)
-        self.o1 = torch.empty(s.d, **bf)
-        self.a1 = torch.empty(s.ffn, **bf)
-        self.down1 = torch.empty(s.d, **bf)
-        self.logits1 = torch.empty(s.vocab, **bf)
-        self.top_v = torch.empty(1, 1, dtype=torch.float32, device=dev)
+        if n == 1:
+            self.h_buf = [torch.empty(s.d, **bf), torch.empty(s.d, **bf)]
+            self.q1 = torch.empty(1, s.hq, 1, s.hd, **bf)
+            self.att1 = torch.empty(1, 1, s.hq * s.hd, **bf)
+            self.o1 = torch.empty(s.d, **bf)
+            self.a1 = torch.empty(s.ffn, **bf)
+            self.down1 = torch.empty(s.d, **bf)
+            self.logits1 = torch.empty(s.vocab, **bf)
+        else:
+            self.h_buf = [torch.empty(n, s.d, **bf), torch.empty(n, s.d, **bf)]
+            self.qb = torch.empty(n, s.hq * s.hd, **bf)
+            self.attb = torch.empty(n, s.hq * s.hd, **bf)
+            self.ob = torch.empty(n, s.d, **bf)
+            self.ab = torch.empty(n, s.ffn, **bf)
+            self.downb = torch.empty(n, s.d, **bf)
+            self.logitsb = torch.empty(n, s.vocab, **bf)
+        self.top_v = torch.empty(n, 1, dtype=torch.float32, device=dev)
         # token chosen at each position (written by the step itself, so a
         # replayed step needs no copy out)
-        self.history = torch.zeros(1, self.cap + 1, dtype=torch.int64, device=dev)
+        self.history = torch.zeros(n, self.cap + 1, dtype=torch.int64, device=dev)
 
     @classmethod
     def from_hf(cls, model, capacity: int, batch: int = 1, device="cuda"):
@@ -197,6 +210,8 @@ class LlamaDecoder:
     def _decode_step(self):
         if self.fused:
             return self._decode_step_fused()
+        if self.fused_batched:
+            return self._decode_step_fused_batched()
         h = ops.index(self.embed, 0, self.tok)
         pending, res = self._layers(h, 1, self.pos, self.kv_len)
         logits, nxt = self._head(pending, res, 1)
@@ -238,6 +253,37 @@ class LlamaDecoder:
                          pos=self.pos, kv_len=self.kv_len, history=self.history)
         return self.logits1.view(1, -1)
 
+    def _decode_step_fused_batched(self):
+        """One decode step for a batch of 2..16 sequences with the batched
+        fused projections (kuiops_decode_rows_batched): the same 5 launches per
+        layer as the batch-1 step, each sequence at its own position."""
+        s, n = self.s, self.n
+        hb = self.h_buf
+        cur = 0
+        q4 = self.qb.view(n, s.hq, 1, s.hd)
+        att4 = self.attb.view(n, s.hq, 1, s.hd)
+        down = None
+        for i, L in enumerate(self.layers):
+            kc, vc = self.kcache[i], self.vcache[i]
+            src = self.embed if i == 0 else hb[cur]
+            ops.decode_rows_batched(src, L["wqkv"], "rmsnorm", "rope", in_add=down, norm_w=L["ln1"], eps=s.eps,
+                                    h_out=hb[1 - cur], out=self.qb, row=self.tok if i == 0 else None,
+                                    hq=s.hq, hkv=s.hkv, hd=s.hd, inv_freq=self.inv_freq, pos=self.pos,
+                                    k_cache=kc, v_cache=vc)
+            cur = 1 - cur
+            ops.sdpa_decode(q4, kc, vc, causal=True, kv_len=self.kv_len, out=att4)
+            ops.decode_rows_batched(self.attb, L["wo"], "plain", "plain", out=self.ob)
+            ops.decode_rows_batched(hb[cur], L["wgu"], "rmsnorm", "swiglu", in_add=self.ob, norm_w=L["ln2"],
+                                    eps=s.eps, h_out=hb[1 - cur], out=self.ab)
+            cur = 1 - cur
+            ops.decode_rows_batched(self.ab, L["wd"], "plain", "plain", out=self.downb)
+            down = self.downb
+        ops.decode_rows_batched(hb[cur], self.head, "rmsnorm", "plain", in_add=down, norm_w=self.norm, eps=s.eps,
+                                out=self.logitsb)
+        ops.softmax_top1(self.logitsb, index_out=self.tok, prob_out=self.top_v.view(n),
+                         pos=self.pos, kv_len=self.kv_len, history=self.history)
+        return self.logitsb
+
     def capture(self):
         """Record one decode step (all its kernels) in a HIP graph.  The step
         reads the token, position and key count from device memory and
@@ -276,9 +322,9 @@ class LlamaDecoder:
                 self.graph.replay()
             else:
                 self._decode_step()
-            if not self.fused:
+            if not (self.fused or self.fused_batched):
                 out[i].copy_(self.tok)
-        if self.fused and n_new > 1:
+        if (self.fused or self.fused_batched) and n_new > 1:
             # the fused step recorded the token of position p at history[p]
             out[1:].copy_(self.history[:, p0:p0 + n_new - 1].t())
         return out.t()

@@ -979,3 +979,59 @@ def cat(tensors, dim: int = 0) -> torch.Tensor:
         n, (ctypes.c_void_p * max(n, 1))(*ptrs), _lib.i64_array(widths), _lib.i64_array(strides), outer,
         ref.element_size(), out.data_ptr(), _stream(ref.device)))
     return out
+
+
+_OUT_KIND = {"plain": 0, "swiglu": 1, "rope": 2}
+
+
+def decode_rows_batched(x, W, x_kind="plain", out_kind="plain", in_add=None, norm_w=None, eps=1e-5,
+                        h_out=None, out=None, row=None, pair_off=0, hq=0, hkv=0, hd=0, inv_freq=None,
+                        pos=None, k_cache=None, v_cache=None):
+    """Batched (M <= 16 rows) decode projection with the fused input stage and
+    epilogue of ``decode_linear`` / ``decode_gate_up`` / ``decode_qkv_rope``
+    (one launch; see kuiops_decode_rows_batched).  W is an nn.Linear weight
+    [N, K] (K contiguous); x is [M, K] ([M, 2K] for ``swiglu``), or a
+    [rows, K] table read at the device rows ``row`` (int64 [M]).
+    ``out_kind``: ``plain`` -> out [M, N]; ``swiglu`` (rows p, p + pair_off)
+    -> out [M, pair_off]; ``rope`` (fused [q; k; v] heads) -> q into out
+    [M, hq * hd], k / v into the caches [M, hkv, capacity, hd] at pos[m]."""
+    N, K = W.shape
+    if x.dtype != W.dtype or W.stride(1) != 1 or x.stride(-1) != 1 or x.dim() != 2:
+        raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
+    if row is None:
+        M = x.shape[0]
+        rows = M
+        if x.shape[1] != (2 * K if x_kind == "swiglu" else K):
+            raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
+    else:
+        if row.dtype != torch.int64 or row.dim() != 1 or not row.is_contiguous() or x.shape[1] != K:
+            raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
+        M, rows = row.numel(), x.shape[0]
+    width = {"plain": N, "swiglu": N // 2, "rope": hq * hd}[out_kind]
+    if out is None:
+        out = torch.empty((M, width), dtype=x.dtype, device=x.device)
+    elif out.dim() != 2 or tuple(out.shape) != (M, width) or out.stride(1) != 1 or out.dtype != x.dtype:
+        raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
+    for t in (in_add, h_out):
+        if t is not None and (t.dim() != 2 or t.shape != (M, K) or t.stride(1) != 1 or t.dtype != x.dtype):
+            raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
+    sk = sv = None
+    if out_kind == "rope":
+        for c in (k_cache, v_cache):
+            if c is None or c.dim() != 4 or c.shape[0] != M or c.shape[1] != hkv or c.shape[3] != hd \
+                    or c.stride(-1) != 1 or c.dtype != x.dtype:
+                raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
+        if pos is None or pos.dtype != torch.int32 or pos.numel() != M or not pos.is_contiguous():
+            raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
+        sk, sv = _lib.strides3(*k_cache.stride()[:3]), _lib.strides3(*v_cache.stride()[:3])
+        pair_off = hd // 2
+    elif out_kind == "swiglu":
+        pair_off = N // 2
+    lib = _lib_handle()
+    _lib.check("kuiops_decode_rows_batched", lib.kuiops_decode_rows_batched(
+        M, N, K, _dt(x.dtype), _X_KIND[x_kind], _OUT_KIND[out_kind], x.data_ptr(), x.stride(0), _ptr(row), rows,
+        _ptr(in_add), in_add.stride(0) if in_add is not None else 0, _ptr(norm_w), float(eps), _ptr(h_out),
+        h_out.stride(0) if h_out is not None else 0, W.data_ptr(), W.stride(0), out.data_ptr(), out.stride(0),
+        int(pair_off), int(hq), int(hkv), int(hd), _ptr(inv_freq), _ptr(pos),
+        _ptr(k_cache), sk, _ptr(v_cache), sv, k_cache.shape[2] if k_cache is not None else 0, _stream(x.device)))
+    return out

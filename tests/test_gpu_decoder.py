@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from kuillm_amd import ops
+from kuillm_amd import _lib, ops
 from kuillm_amd.decoder import LlamaDecoder, LlamaShape
 from oracle import kuiops_oracle as O
 
@@ -332,3 +332,129 @@ def test_sdpa_decode_split_merge_keeps_counters_zero(cuda):
     torch.cuda.synchronize()
     ws = ops._WS[(cuda.index or 0, "attn")]
     assert not ws[:256].any()            # counters: 4 bytes per query row, 256-byte aligned
+
+
+def _ref_rows(x, W, x_kind, in_add=None, norm_w=None, eps=1e-5):
+    """Per-row reference for the batched decode kernel: the single-row decode
+    kernels, one row at a time."""
+    outs, hs = [], []
+    for m in range(x.shape[0]):
+        h = torch.empty(x.shape[1] if x_kind != "swiglu" else x.shape[1] // 2, dtype=x.dtype, device=x.device)
+        add = in_add[m].contiguous() if in_add is not None else None
+        outs.append(ops.decode_linear(x[m].contiguous(), W, x_kind, in_add=add, norm_w=norm_w, eps=eps,
+                                      h_out=h if x_kind == "rmsnorm" else None))
+        hs.append(h)
+    return torch.stack(outs), torch.stack(hs)
+
+
+@pytest.mark.parametrize("M", [2, 5, 16])
+@pytest.mark.parametrize("N,K", [(2048, 2048), (300, 96), (1000, 5632)])
+def test_decode_rows_batched_plain_and_rmsnorm(cuda, M, N, K):
+    """kuiops_decode_rows_batched against the one-row decode projection, row
+    by row: the residual sum h is bit-identical (same rounding points), the
+    outputs differ only by fp32 summation order (rel 1e-2)."""
+    x = bf((M, K), 60 + M).to(cuda)
+    W = bf((N, K), 61, 0.02).to(cuda)
+    nw = (1.0 + bf((K,), 62, 0.1)).to(torch.bfloat16).to(cuda)
+    add = bf((M, K), 63).to(cuda)
+    if M * K * 2 > 140 * 1024:                       # x rows must fit the work-group's LDS
+        with pytest.raises(_lib.Unsupported):
+            ops.decode_rows_batched(x, W, "plain", "plain")
+        return
+    out = ops.decode_rows_batched(x, W, "plain", "plain")
+    ref, _ = _ref_rows(x, W, "plain")
+    close(f(out), f(ref))
+    h = torch.empty(M, K, dtype=torch.bfloat16, device=cuda)
+    out = ops.decode_rows_batched(x, W, "rmsnorm", "plain", in_add=add, norm_w=nw, eps=1e-5, h_out=h)
+    ref, href = _ref_rows(x, W, "rmsnorm", in_add=add, norm_w=nw, eps=1e-5)
+    assert torch.equal(h, href)
+    close(f(out), f(ref))
+
+
+@pytest.mark.parametrize("M", [2, 7, 16])
+@pytest.mark.parametrize("ffn,K", [(5632, 2048), (64, 96)])
+def test_decode_rows_batched_swiglu(cuda, M, ffn, K):
+    """SwiGLU epilogue over the fused [gate; up] weight, and the SwiGLU input
+    stage (x = [gate | up] rows) of the down projection, against silu_mul +
+    the one-row projection."""
+    x = bf((M, K), 70 + M).to(cuda)
+    W = bf((2 * ffn, K), 71, 0.02).to(cuda)
+    nw = (1.0 + bf((K,), 72, 0.1)).to(torch.bfloat16).to(cuda)
+    h = torch.empty(M, K, dtype=torch.bfloat16, device=cuda)
+    out = ops.decode_rows_batched(x, W, "rmsnorm", "swiglu", norm_w=nw, eps=1e-5, h_out=h)
+    gu, href = _ref_rows(x, W, "rmsnorm", norm_w=nw, eps=1e-5)
+    assert torch.equal(h, href)
+    close(f(out), f(ops.silu_mul(gu)), 2e-2)
+    Wd = bf((K, ffn), 73, 0.02).to(cuda)
+    gux = bf((M, 2 * ffn), 74).to(cuda)
+    if M * ffn * 2 > 140 * 1024:                     # swiglu(x) rows must fit the work-group's LDS
+        with pytest.raises(_lib.Unsupported):
+            ops.decode_rows_batched(gux, Wd, "swiglu", "plain")
+        return
+    down = ops.decode_rows_batched(gux, Wd, "swiglu", "plain")
+    ref, _ = _ref_rows(gux, Wd, "swiglu")
+    close(f(down), f(ref), 2e-2)
+
+
+@pytest.mark.parametrize("M,hq,hkv,hd,K", [(4, 32, 8, 64, 2048), (3, 4, 2, 128, 256), (16, 8, 8, 64, 512)])
+def test_decode_rows_batched_rope(cuda, M, hq, hkv, hd, K):
+    """Rotary + cache-append epilogue with an embedding-row input stage, each
+    sequence at its own position (one past the capacity stores nothing),
+    against the one-row projection + rope_kv_append per sequence."""
+    N = (hq + 2 * hkv) * hd
+    cap = 40
+    table = bf((50, K), 80).to(cuda)
+    W = bf((N, K), 81, 0.02).to(cuda)
+    nw = (1.0 + bf((K,), 82, 0.1)).to(torch.bfloat16).to(cuda)
+    inv = torch.from_numpy(O.rope_inv_freq(hd, 10000.0)).to(cuda)
+    rows = torch.tensor([(7 * m + 3) % 50 for m in range(M)], dtype=torch.int64, device=cuda)
+    posl = [(5 * m) % cap for m in range(M)]
+    posl[-1] = cap                                   # past the cache
+    pos = torch.tensor(posl, dtype=torch.int32, device=cuda)
+    kc1 = torch.zeros(M, hkv, cap, hd, dtype=torch.bfloat16, device=cuda)
+    vc1, kc2, vc2 = kc1.clone(), kc1.clone(), kc1.clone()
+    h = torch.empty(M, K, dtype=torch.bfloat16, device=cuda)
+    q1 = ops.decode_rows_batched(table, W, "rmsnorm", "rope", norm_w=nw, eps=1e-5, h_out=h, row=rows,
+                                 hq=hq, hkv=hkv, hd=hd, inv_freq=inv, pos=pos, k_cache=kc1, v_cache=vc1)
+    x = table[rows].contiguous()
+    assert torch.equal(h, x)
+    qkv, _ = _ref_rows(x, W, "rmsnorm", norm_w=nw, eps=1e-5)
+    q2 = torch.empty(M, hq, 1, hd, dtype=torch.bfloat16, device=cuda)
+    for m in range(M):
+        ops.rope_kv_append(qkv[m].view(1, 1, -1), hq, hkv, hd, inv, pos[m:m + 1], q2[m:m + 1],
+                           kc2[m:m + 1], vc2[m:m + 1])
+    close(f(q1), f(q2.view(M, -1)), 2e-2)
+    close(f(kc1), f(kc2), 2e-2)
+    close(f(vc1), f(vc2), 2e-2)
+    assert not kc1[-1].any() and not vc1[-1].any()
+    for m in range(M - 1):
+        assert kc1[m, :, posl[m]].abs().sum() > 0 and vc1[m, :, posl[m]].abs().sum() > 0
+
+
+def test_batched_fused_decode_step_matches_unfused(cuda):
+    """The batched fused decode step (4 sequences) against the unfused one
+    from the same state, step by step: logits within fp32-reordering noise,
+    the same next tokens unless the top two logits tie within that noise."""
+    m = hf_model(TINY, cuda)
+    prompt = torch.randint(0, TINY["vocab"], (4, 20), generator=torch.Generator().manual_seed(9))
+    dec = LlamaDecoder.from_hf(m, capacity=64, batch=4)
+    assert dec.fused_batched and not dec.fused
+    dec.prefill(prompt)
+    names = ("tok", "pos", "kv_len", "kcache", "vcache")
+    for step in range(8):
+        state = [getattr(dec, a).clone() for a in names]
+        lf = dec._decode_step().float().clone()
+        tok_f = dec.tok.clone()
+        after = [getattr(dec, a).clone() for a in names]
+        for a, src in zip(names, state):
+            getattr(dec, a).copy_(src)
+        dec.fused_batched = False
+        lu = dec._decode_step().float()
+        dec.fused_batched = True
+        close(f(lf), f(lu), 2e-2)
+        for b in range(4):
+            if not torch.equal(tok_f[b], dec.tok[b]):
+                top2 = torch.topk(lu[b], 2).values
+                assert float(top2[0] - top2[1]) < 2e-2
+        for a, src in zip(names, after):
+            getattr(dec, a).copy_(src)
