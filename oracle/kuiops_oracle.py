@@ -290,7 +290,7 @@ def sdpa(q, k, v, causal=False, scale=None, bias=None, align="top_left"):
     v = np.repeat(v, g, axis=1)
     if scale is None:
         scale = 1.0 / math.sqrt(e)
-    sc = scale * np.einsum("nhle,nhse->nhls", q, k)
+    sc = scale * np.matmul(q, np.swapaxes(k, -1, -2))
     if bias is not None:
         sc = sc + np.asarray(bias, dtype=np.float64)
     if causal:
@@ -303,7 +303,7 @@ def sdpa(q, k, v, causal=False, scale=None, bias=None, align="top_left"):
     p = np.exp(sc - m_safe)
     denom = np.sum(p, axis=-1, keepdims=True)
     with np.errstate(invalid="ignore", divide="ignore"):
-        out = np.where(denom > 0, np.einsum("nhls,nhsv->nhlv", p, v) / np.where(denom > 0, denom, 1), 0.0)
+        out = np.where(denom > 0, np.matmul(p, v) / np.where(denom > 0, denom, 1), 0.0)
         lse = np.where(denom[..., 0] > 0, np.log(np.where(denom[..., 0] > 0, denom[..., 0], 1)) + m_safe[..., 0], -np.inf)
     return out, lse
 

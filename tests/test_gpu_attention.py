@@ -2,6 +2,7 @@
 golden fixtures.  Tolerance (north star): rel 1e-2 / abs 1e-2 elementwise on
 the output; the LSE (fp32) within 1e-3 absolute."""
 import math
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -161,19 +162,21 @@ def test_sdpa_closed_forms(cuda):
 
 
 @pytest.mark.parametrize("S", [2048, 4096])
-def test_sdpa_full_size_one_head(cuda, S):
-    """B=1, H=32, S, D=128 causal; heads 0 and 31 checked
-    against the oracle in full, every head for finiteness and row sums."""
+def test_sdpa_full_size_all_heads(cuda, S):
+    """B=1, H=32, S, D=128 causal; every head against the
+    oracle in full (output and log-sum-exp)."""
     torch.manual_seed(S)
     q = torch.randn(1, 32, S, 128, device=cuda).to(torch.bfloat16)
     k = torch.randn_like(q)
     v = torch.randn_like(q)
     out, lse = ops.sdpa(q, k, v, is_causal=True, scale=1 / math.sqrt(128))
-    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
-    for h in (0, 31):
-        ref, lref = O.sdpa(npy(q[:, h:h + 1]), npy(k[:, h:h + 1]), npy(v[:, h:h + 1]), causal=True)
-        close(out[:, h:h + 1], ref)
-        np.testing.assert_allclose(npy(lse[:, h:h + 1]), lref, atol=1e-3, rtol=1e-4)
+    qn, kn, vn = npy(q), npy(k), npy(v)
+    # one head per task: numpy's BLAS and ufuncs release the GIL
+    with ThreadPoolExecutor(8) as pool:
+        refs = list(pool.map(lambda h: O.sdpa(qn[:, h:h + 1], kn[:, h:h + 1], vn[:, h:h + 1], causal=True),
+                             range(32)))
+    close(out, np.concatenate([r[0] for r in refs], axis=1))
+    np.testing.assert_allclose(npy(lse), np.concatenate([r[1] for r in refs], axis=1), atol=1e-3, rtol=1e-4)
 
 
 DECODE = [  # n, hq, hkv, l, s, d

@@ -21,6 +21,7 @@ class Block(torch.nn.Module):
         self.up = torch.nn.Linear(d, 4 * d)
         self.down = torch.nn.Linear(4 * d, d)
         self.head = torch.nn.Linear(d, vocab, bias=False)
+        self.k = 8                              # how many top probabilities to return
 
     def forward(self, x):
         b, s, d = x.shape
@@ -29,7 +30,7 @@ class Block(torch.nn.Module):
         x = x + a.transpose(1, 2).reshape(b, s, d)
         x = x + self.down(F.silu(self.up(x)))
         logits = self.head(x[:, -1]).float()
-        return torch.topk(torch.softmax(logits, -1), 8)
+        return torch.topk(torch.softmax(logits, -1), self.k)
 
 
 def test_compiled_block_uses_kuiops(cuda):
@@ -49,5 +50,14 @@ def test_compiled_block_uses_kuiops(cuda):
     assert any("scaled_dot_product" in str(t) for t in got), got
     err = (v - ref_v).abs() - (1e-2 + 1e-2 * ref_v.abs())
     assert err.max() <= 0
-    # the top-8 sets agree where the probabilities are not within tolerance of a tie
-    assert (i[:, :4] == ref_i[:, :4]).float().mean() >= 0.75
+    # the top-8 indices agree except where the index we chose has a stock
+    # probability within 10% of the stock value at that rank (a near-tie
+    # that bf16 rounding of the logits, ~0.03 at their magnitude, can order
+    # either way)
+    m.k = 1000
+    with torch.no_grad():
+        full_v, full_i = m(x)
+    stock_p = torch.empty_like(full_v).scatter_(1, full_i, full_v)
+    for b, j in (i != ref_i).nonzero().tolist():
+        gap = (stock_p[b, i[b, j]] - ref_v[b, j]).abs().item()
+        assert gap <= 0.1 * ref_v[b, j].item(), (b, j, i[b].tolist(), ref_i[b].tolist())
