@@ -498,7 +498,7 @@ KUIOPS_API int kuiops_mean_lastdim(int64_t m, int64_t n, int dtype, const void *
 KUIOPS_API int kuiops_cat(int n_inputs, const void *const *inputs, const int64_t *widths,
                const int64_t *outer_strides, int64_t outer, int elem_bytes, void *out, void *stream);
 
-/* Batched decode projection for 1 <= M <= 16 sequences: the fused input
+/* Batched decode projection for 1 <= M <= 64 sequences: the fused input
  * stage and epilogue of kuiops_decode_linear / kuiops_decode_gate_up /
  * kuiops_decode_qkv_rope, per row, over one nn.Linear weight W [N, K]
  * (K contiguous, row stride ldw).  Row m of x comes from `in` at row
@@ -516,7 +516,9 @@ KUIOPS_API int kuiops_cat(int n_inputs, const void *const *inputs, const int64_t
  *   position} when pos[m] < cache_cap.
  * Rounding points as the batch-1 entry points (h bit-identical; the dot
  * products differ from them only in fp32 summation order).
- * M * K * 2 <= 140 KiB, else KUIOPS_E_UNSUPPORTED.  No reference
+ * Input stages (RMSNorm, SwiGLU) and embedding rows need M <= 16 and
+ * M * K * 2 <= 140 KiB (x staged in LDS); plain x takes any M <= 64.
+ * Otherwise KUIOPS_E_UNSUPPORTED.  No reference
  * counterpart: it fuses the mm launcher with the RMSNorm / SwiGLU / rotary /
  * KV-cache cat launches of a batched decode step (infer.py:57-89 generates
  * in batches).                                                              */

@@ -880,9 +880,23 @@ static bool decode_single_split(int64_t s, int64_t ev, int R) {
 // Measured on the Llama-1B decode step (32 q / 8 kv heads, 640-key cache):
 // 8 waves x 12 keys 6.2 us, 16 x 6 6.6 us, 4 x 20 6.7 us; 2 rows per
 // work-group 8.6 us, 4 rows 16.2 us; split-KV with in-kernel merge 10.6 us.
-constexpr int kDecodeWideWaves = 8, kDecodeWideNB = 12;
-static bool decode_row_wide(int64_t s, int64_t hd) {
-    return s <= kDecodeWideWaves * (64 / (hd / 8)) * kDecodeWideNB;
+// With many query rows (a batch of sequences) the row groups alone fill the
+// GPU, and one work-group per row would re-read each KV head once per query
+// head of its group, so the row-wide kernel is kept for at most
+// kDecodeWideMaxRows rows.
+constexpr int kDecodeWideWaves = 8, kDecodeWideNB = 12, kDecodeWideMaxRows = 256;
+static bool decode_row_wide(int64_t s, int64_t hd, int64_t rows) {
+    return s <= kDecodeWideWaves * (64 / (hd / 8)) * kDecodeWideNB && rows <= kDecodeWideMaxRows;
+}
+
+// Keys per split for a launch of `groups` row-group work-groups per split:
+// enough splits for about two work-groups per CU, at most 32, and never
+// fewer keys than decode_chunk (the workspace is sized by it).
+static int64_t decode_chunk_for(int64_t s, int64_t groups) {
+    const int64_t want = cdiv(2 * (int64_t)num_cus(), groups > 0 ? groups : 1);
+    const int64_t splits = want < 1 ? 1 : (want > 32 ? 32 : want);
+    const int64_t c = cdiv(cdiv(s, splits), 64) * 64;
+    return c < decode_chunk(s) ? decode_chunk(s) : c;
 }
 
 // Workspace: split arrival counters (one per work-group row group, at most
@@ -931,7 +945,7 @@ template <typename T, int HD>
 static int launch_decode(AttnArgs a, hipStream_t st) {
     const int G = (int)(a.hq / a.hkv);
     const int rows_kv = G * (int)a.l;
-    if (decode_row_wide(a.s, HD) && a.hkv * rows_kv <= 65535) {
+    if (decode_row_wide(a.s, HD, a.n * a.hkv * rows_kv) && a.hkv * rows_kv <= 65535) {
         // short caches: one 8-wave work-group per query row loads every key
         // in one step (one memory round trip, no split merge); the rows of a
         // KV head share its K / V through L2
@@ -1043,9 +1057,9 @@ extern "C" int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l,
     fill_args(a, n, hq, hkv, l, s, Q, sq, K, sk, V, sv, O, so, lse, scale, causal);
     a.kv_len = kv_len;
     const int64_t ss = s > 0 ? s : 1;
-    a.chunk = decode_chunk(ss);
-    if (decode_row_wide(ss, ev) || decode_single_split(ss, ev, decode_rows_per_group((int)((hq / hkv) * l))))
-        a.chunk = ss;
+    const int R = decode_rows_per_group((int)((hq / hkv) * l));
+    a.chunk = decode_chunk_for(ss, n * hkv * cdiv((hq / hkv) * l, R));
+    if (decode_row_wide(ss, ev, n * hq * l) || decode_single_split(ss, ev, R)) a.chunk = ss;
     a.splits = (int)cdiv(ss, a.chunk);
     const int64_t rows = n * hq * l;
     const size_t need = decode_workspace_bytes(rows, s, ev);

@@ -731,6 +731,141 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     }
 }
 
+// Wide batched decode projection (17..64 rows of plain x, or rows too long
+// to stage): each lane reads its A operand (8 k of one row of x, 16 bytes)
+// straight from global memory, where x (at most 64 rows) stays in L2; MB
+// blocks of 16 rows share each W fragment and GW output groups share each x
+// fragment.  A work-group owns GW consecutive 16-output groups, its NW waves
+// split K, the wave sums meet in LDS in wave order and the plain / SwiGLU /
+// rotary epilogues follow.  PF = 2 steps of W and x in flight per wave.
+template <typename T, int OK, int NW, int MB, int GW>
+__global__ __launch_bounds__(NW * 64) void decode_mrows_wide_kernel(DecMArgs a) {
+    typedef typename Mfma<T>::frag frag;
+    constexpr int PF = 2;
+    __shared__ float red[NW][MB][4][64];
+    __shared__ float vals[64][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, cq = lane >> 4;
+    const int M = (int)a.M;
+    const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
+    const int64_t g0 = (int64_t)blockIdx.x * GW;
+    const T *Wr[GW];
+#pragma unroll
+    for (int gi = 0; gi < GW; ++gi) {
+        const int64_t g = g0 + gi;
+        int64_t wrow;
+        bool wvalid;
+        if constexpr (OK == kOutPlain) {
+            wrow = g * 16 + n;
+            wvalid = wrow < a.N;
+        } else {
+            const int64_t p = g * 8 + (n & 7), e = n >> 3;
+            wvalid = p < a.N / 2;
+            if constexpr (OK == kOutSwiGlu) {
+                wrow = p + e * a.pair_off;
+            } else {
+                const int64_t half = a.pair_off, head = pair_div_m(a, p);
+                wrow = head * a.hd + (p - head * half) + e * half;
+            }
+        }
+        Wr[gi] = reinterpret_cast<const T *>(a.W) + (wvalid ? wrow : 0) * a.ldw;
+    }
+    const T *X = reinterpret_cast<const T *>(a.in);
+    const int64_t kbeg = (int64_t)wave * a.kq;
+    const int64_t kend = min(a.K, kbeg + a.kq);
+    const int nsp = (int)(((a.kq / 64) + PF - 1) / PF) * PF;
+    u32x4 wr[PF][GW][2], xr[PF][MB][2];
+    auto load = [&](int st, int j) __attribute__((always_inline)) {
+        const int64_t k = kbeg + (int64_t)st * 64 + 8 * cq;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool in_k = k + 32 * h < kend;
+#pragma unroll
+            for (int gi = 0; gi < GW; ++gi)
+                wr[j][gi][h] = in_k ? *reinterpret_cast<const u32x4 *>(Wr[gi] + k + 32 * h) : u32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int m = mb * 16 + n;
+                xr[j][mb][h] = (in_k && m < M) ? *reinterpret_cast<const u32x4 *>(X + m * a.ld_in + k + 32 * h)
+                                               : u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < PF; ++j) load(j, j);
+    f32x4 acc[GW][MB];
+#pragma unroll
+    for (int gi = 0; gi < GW; ++gi)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[gi][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nsp; s0 += PF) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int gi = 0; gi < GW; ++gi)
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+                        acc[gi][mb] = Mfma<T>::m16(as_frag<frag>(xr[j][mb][h]), as_frag<frag>(wr[j][gi][h]),
+                                                   acc[gi][mb]);
+            if (s0 + j + PF < nsp) load(s0 + j + PF, j);
+        }
+    }
+    // acc[gi][mb][i]: x row 16 * mb + 4 * cq + i, output n of group g0 + gi.
+    // Waves summed in wave order, one group at a time.
+#pragma unroll
+    for (int gi = 0; gi < GW; ++gi) {
+        if (gi > 0) __syncthreads();                  // the previous group's epilogue has read vals
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][mb][i][lane] = acc[gi][mb][i];
+        __syncthreads();
+        for (int idx = tid; idx < M * 16; idx += NW * 64) {
+            const int m = idx >> 4, o = idx & 15, mb = m >> 4, mm = m & 15;
+            const int l = (mm >> 2) * 16 + o, i = mm & 3;
+            float v = red[0][mb][i][l];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) v += red[w][mb][i][l];
+            vals[m][o] = v;
+        }
+        __syncthreads();
+        if (g0 + gi < ngroups)
+            for (int idx = tid; idx < M * 16; idx += NW * 64)
+                decode_mrows_epilogue<T, OK>(a, g0 + gi, idx >> 4, idx & 15, vals);
+    }
+}
+
+template <typename T, int OK, int NW, int GW>
+static void decode_wide_launch2(const DecMArgs &a, unsigned grid, hipStream_t st) {
+    switch ((a.M + 15) / 16) {
+        case 1: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 1, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 2, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 3, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
+        default: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 4, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
+    }
+}
+
+// Wide-kernel shapes: output groups per work-group (x reuse) traded against
+// waves per work-group (K split), within the registers of a lane:
+// (GW, NW) = (4, 4), (2, 8) or (1, 16).
+template <typename T, int OK>
+static void decode_wide_launch1(const DecMArgs &a, int gw, unsigned grid, hipStream_t st) {
+    if (gw == 4) decode_wide_launch2<T, OK, 4, 4>(a, grid, st);
+    else if (gw == 2) decode_wide_launch2<T, OK, 8, 2>(a, grid, st);
+    else decode_wide_launch2<T, OK, 16, 1>(a, grid, st);
+}
+
+template <typename T>
+static void decode_wide_launch(const DecMArgs &a, int out_kind, int gw, unsigned grid, hipStream_t st) {
+    switch (out_kind) {
+        case kOutPlain: decode_wide_launch1<T, kOutPlain>(a, gw, grid, st); break;
+        case kOutSwiGlu: decode_wide_launch1<T, kOutSwiGlu>(a, gw, grid, st); break;
+        default: decode_wide_launch1<T, kOutRope>(a, gw, grid, st); break;
+    }
+}
+
 // dynamic LDS for the staged rows of x; with the 17 KiB of static reduction
 // arrays of 16 waves it stays within the CU's 160 KiB
 constexpr int64_t kDecMaxLds = 140 * 1024;
@@ -780,11 +915,14 @@ extern "C" int kuiops_decode_rows_batched(
     if (M == 0 || N == 0) return KUIOPS_OK;
     if (!in || !W || !out || (x_kind == kXRmsNorm && !norm_w)) return KUIOPS_E_INVALID;
     if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
-    if (M > 16 || K == 0 || K % 8 || ldw % 8 || ldw < K || ld_in % 8 || (in_add && ld_add % 8) ||
+    if (M > 64 || K == 0 || K % 8 || ldw % 8 || ldw < K || ld_in % 8 || (in_add && ld_add % 8) ||
         (h_out && ld_h % 8))
         return KUIOPS_E_UNSUPPORTED;
     if (x_kind == kXSwiGlu ? ld_in < 2 * K : (ld_in < K && !in_row && M > 1)) return KUIOPS_E_INVALID;
-    if ((int64_t)M * K * 2 > kDecMaxLds) return KUIOPS_E_UNSUPPORTED;
+    // x rows staged in LDS (any input stage) up to 16 rows and 140 KiB; the
+    // wide kernel takes 17..64 rows of plain x read from L2
+    const bool wide = M > 16 || (int64_t)M * K * 2 > kDecMaxLds;
+    if (wide ? (x_kind != kXPlain || in_row) : (int64_t)M * K * 2 > kDecMaxLds) return KUIOPS_E_UNSUPPORTED;
     if (!aligned16(in) || !aligned16(W) || (in_add && !aligned16(in_add)) || (norm_w && !aligned16(norm_w)) ||
         (h_out && !aligned16(h_out)))
         return KUIOPS_E_UNSUPPORTED;
@@ -806,9 +944,10 @@ extern "C" int kuiops_decode_rows_batched(
     }
     a.cap = cache_cap;
     // Output groups per work-group: enough work-groups for every CU, each
-    // staging x once for up to 8 groups.
+    // staging x once for up to 8 groups (one per work-group in the wide
+    // kernel, which stages nothing).
     const int64_t ngroups = out_kind == kOutPlain ? cdiv(N, 16) : cdiv(N / 2, 8);
-    const int64_t gpw = std::max<int64_t>(1, std::min<int64_t>(8, ngroups / 256));
+    const int64_t gpw = wide ? 1 : std::max<int64_t>(1, std::min<int64_t>(8, ngroups / 256));
     const int64_t grid = cdiv(ngroups, gpw);
     if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     // Waves per work-group: K is split over more waves when the output
@@ -824,6 +963,16 @@ extern "C" int kuiops_decode_rows_batched(
         case kXPlain: err = decode_mrows_launch<T, kXPlain>(a, out_kind, nw, (unsigned)grid, lds, st); break;     \
         case kXRmsNorm: err = decode_mrows_launch<T, kXRmsNorm>(a, out_kind, nw, (unsigned)grid, lds, st); break; \
         default: err = decode_mrows_launch<T, kXSwiGlu>(a, out_kind, nw, (unsigned)grid, lds, st); break;         \
+    }
+    if (wide) {
+        // groups per work-group: as many as still leave a work-group per CU
+        const int gw = ngroups >= 4 * 256 ? 4 : (ngroups >= 2 * 256 ? 2 : 1);
+        const int wnw = gw == 4 ? 4 : (gw == 2 ? 8 : 16);
+        a.kq = cdiv(cdiv(K, wnw), 64) * 64;
+        const unsigned wgrid = (unsigned)cdiv(ngroups, gw);
+        if (dtype == KUIOPS_BF16) decode_wide_launch<bf16_t>(a, out_kind, gw, wgrid, st);
+        else decode_wide_launch<f16_t>(a, out_kind, gw, wgrid, st);
+        return launch_status();
     }
     hipError_t err;
     if (dtype == KUIOPS_BF16) { KUIOPS_DECM(bf16_t) } else { KUIOPS_DECM(f16_t) }

@@ -114,9 +114,12 @@ class LlamaDecoder:
         self.fused = self.n == 1 and s.d <= 4096 and s.ffn <= 8192 and s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0
         # batches of 2..16: the batched form of the same fused projections
         # (every row of x staged in LDS: n * max(d, ffn) * 2 <= 140 KiB)
-        self.fused_batched = (2 <= self.n <= 16 and self.n * max(s.d, s.ffn) * 2 <= 140 * 1024
-                              and s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0)
-        if self.fused or self.fused_batched:
+        shapes_ok = s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0
+        self.fused_batched = 2 <= self.n <= 16 and self.n * max(s.d, s.ffn) * 2 <= 140 * 1024 and shapes_ok
+        # larger batches (up to 64): RMSNorm in its own launch, projections of
+        # plain x (read from L2) with the rotary / SwiGLU epilogues fused
+        self.fused_wide = not self.fused_batched and 2 <= self.n <= 64 and shapes_ok
+        if self.fused or self.fused_batched or self.fused_wide:
             self._setup_fused()
 
     def _setup_fused(self):
@@ -141,6 +144,7 @@ class LlamaDecoder:
             self.ab = torch.empty(n, s.ffn, **bf)
             self.downb = torch.empty(n, s.d, **bf)
             self.logitsb = torch.empty(n, s.vocab, **bf)
+            self.xnb = torch.empty(n, s.d, **bf)          # wide step: normalised rows
         self.top_v = torch.empty(n, 1, dtype=torch.float32, device=dev)
         # token chosen at each position (written by the step itself, so a
         # replayed step needs no copy out)
@@ -212,6 +216,8 @@ class LlamaDecoder:
             return self._decode_step_fused()
         if self.fused_batched:
             return self._decode_step_fused_batched()
+        if self.fused_wide:
+            return self._decode_step_wide()
         h = ops.index(self.embed, 0, self.tok)
         pending, res = self._layers(h, 1, self.pos, self.kv_len)
         logits, nxt = self._head(pending, res, 1)
@@ -284,6 +290,35 @@ class LlamaDecoder:
                          pos=self.pos, kv_len=self.kv_len, history=self.history)
         return self.logitsb
 
+    def _decode_step_wide(self):
+        """One decode step for a batch of up to 64 sequences: the unfused
+        step's arithmetic with the projections on kuiops_decode_rows_batched
+        (plain x; rotary + KV append and SwiGLU in their epilogues), 7
+        launches per layer."""
+        s, n = self.s, self.n
+        res, xn = self.h_buf[0], self.xnb
+        q4 = self.qb.view(n, s.hq, 1, s.hd)
+        att4 = self.attb.view(n, s.hq, 1, s.hd)
+        ops.index(self.embed, 0, self.tok, out=res)
+        for i, L in enumerate(self.layers):
+            kc, vc = self.kcache[i], self.vcache[i]
+            if i == 0:
+                ops.rmsnorm(res, L["ln1"], s.eps, out=xn)
+            else:
+                ops.rmsnorm(self.downb, L["ln1"], s.eps, residual=res, res_out=res, out=xn)
+            ops.decode_rows_batched(xn, L["wqkv"], "plain", "rope", out=self.qb, hq=s.hq, hkv=s.hkv, hd=s.hd,
+                                    inv_freq=self.inv_freq, pos=self.pos, k_cache=kc, v_cache=vc)
+            ops.sdpa_decode(q4, kc, vc, causal=True, kv_len=self.kv_len, out=att4)
+            ops.decode_rows_batched(self.attb, L["wo"], "plain", "plain", out=self.ob)
+            ops.rmsnorm(self.ob, L["ln2"], s.eps, residual=res, res_out=res, out=xn)
+            ops.decode_rows_batched(xn, L["wgu"], "plain", "swiglu", out=self.ab)
+            ops.decode_rows_batched(self.ab, L["wd"], "plain", "plain", out=self.downb)
+        ops.rmsnorm(self.downb, self.norm, s.eps, residual=res, out=xn)
+        ops.decode_rows_batched(xn, self.head, "plain", "plain", out=self.logitsb)
+        ops.softmax_top1(self.logitsb, index_out=self.tok, prob_out=self.top_v.view(n),
+                         pos=self.pos, kv_len=self.kv_len, history=self.history)
+        return self.logitsb
+
     def capture(self):
         """Record one decode step (all its kernels) in a HIP graph.  The step
         reads the token, position and key count from device memory and
@@ -322,9 +357,9 @@ class LlamaDecoder:
                 self.graph.replay()
             else:
                 self._decode_step()
-            if not (self.fused or self.fused_batched):
+            if not (self.fused or self.fused_batched or self.fused_wide):
                 out[i].copy_(self.tok)
-        if (self.fused or self.fused_batched) and n_new > 1:
+        if (self.fused or self.fused_batched or self.fused_wide) and n_new > 1:
             # the fused step recorded the token of position p at history[p]
             out[1:].copy_(self.history[:, p0:p0 + n_new - 1].t())
         return out.t()

@@ -367,23 +367,25 @@ def _ref_rows(x, W, x_kind, in_add=None, norm_w=None, eps=1e-5):
     return torch.stack(outs), torch.stack(hs)
 
 
-@pytest.mark.parametrize("M", [2, 5, 16])
+@pytest.mark.parametrize("M", [2, 5, 16, 17, 40, 64])
 @pytest.mark.parametrize("N,K", [(2048, 2048), (300, 96), (1000, 5632)])
 def test_decode_rows_batched_plain_and_rmsnorm(cuda, M, N, K):
     """kuiops_decode_rows_batched against the one-row decode projection, row
     by row: the residual sum h is bit-identical (same rounding points), the
-    outputs differ only by fp32 summation order (rel 1e-2)."""
+    outputs differ only by fp32 summation order (rel 1e-2).  Beyond 16 rows
+    or 140 KiB of x (the wide kernel: x read from L2) only plain x is
+    accepted."""
     x = bf((M, K), 60 + M).to(cuda)
     W = bf((N, K), 61, 0.02).to(cuda)
     nw = (1.0 + bf((K,), 62, 0.1)).to(torch.bfloat16).to(cuda)
     add = bf((M, K), 63).to(cuda)
-    if M * K * 2 > 140 * 1024:                       # x rows must fit the work-group's LDS
-        with pytest.raises(_lib.Unsupported):
-            ops.decode_rows_batched(x, W, "plain", "plain")
-        return
     out = ops.decode_rows_batched(x, W, "plain", "plain")
     ref, _ = _ref_rows(x, W, "plain")
     close(f(out), f(ref))
+    if M > 16 or M * K * 2 > 140 * 1024:             # input stages need the rows of x staged in LDS
+        with pytest.raises(_lib.Unsupported):
+            ops.decode_rows_batched(x, W, "rmsnorm", "plain", in_add=add, norm_w=nw, eps=1e-5)
+        return
     h = torch.empty(M, K, dtype=torch.bfloat16, device=cuda)
     out = ops.decode_rows_batched(x, W, "rmsnorm", "plain", in_add=add, norm_w=nw, eps=1e-5, h_out=h)
     ref, href = _ref_rows(x, W, "rmsnorm", in_add=add, norm_w=nw, eps=1e-5)
@@ -449,6 +451,69 @@ def test_decode_rows_batched_rope(cuda, M, hq, hkv, hd, K):
     assert not kc1[-1].any() and not vc1[-1].any()
     for m in range(M - 1):
         assert kc1[m, :, posl[m]].abs().sum() > 0 and vc1[m, :, posl[m]].abs().sum() > 0
+
+
+@pytest.mark.parametrize("M", [16, 33, 64])
+def test_decode_rows_batched_wide_epilogues(cuda, M):
+    """The wide kernel's SwiGLU and rotary + KV-append epilogues (plain x, 17..64
+    rows, or 16 rows of K = 5632 that do not fit LDS) against the one-row
+    projection followed by silu_mul / rope_kv_append."""
+    hq, hkv, hd, cap = 8, 2, 64, 40
+    K = 5632 if M == 16 else 512
+    x = bf((M, K), 90 + M).to(cuda)
+    ffn = 96
+    W = bf((2 * ffn, K), 91, 0.02).to(cuda)
+    out = ops.decode_rows_batched(x, W, "plain", "swiglu")
+    gu, _ = _ref_rows(x, W, "plain")
+    close(f(out), f(ops.silu_mul(gu)), 2e-2)
+    N = (hq + 2 * hkv) * hd
+    Wq = bf((N, K), 92, 0.02).to(cuda)
+    inv = torch.from_numpy(O.rope_inv_freq(hd, 10000.0)).to(cuda)
+    posl = [(3 * m) % cap for m in range(M)]
+    posl[0] = cap                                    # past the cache: q only
+    pos = torch.tensor(posl, dtype=torch.int32, device=cuda)
+    kc1 = torch.zeros(M, hkv, cap, hd, dtype=torch.bfloat16, device=cuda)
+    vc1, kc2, vc2 = kc1.clone(), kc1.clone(), kc1.clone()
+    q1 = ops.decode_rows_batched(x, Wq, "plain", "rope", hq=hq, hkv=hkv, hd=hd, inv_freq=inv, pos=pos,
+                                 k_cache=kc1, v_cache=vc1)
+    qkv, _ = _ref_rows(x, Wq, "plain")
+    q2 = torch.empty(M, hq, 1, hd, dtype=torch.bfloat16, device=cuda)
+    for m in range(M):
+        ops.rope_kv_append(qkv[m].view(1, 1, -1), hq, hkv, hd, inv, pos[m:m + 1], q2[m:m + 1],
+                           kc2[m:m + 1], vc2[m:m + 1])
+    close(f(q1), f(q2.view(M, -1)), 2e-2)
+    close(f(kc1), f(kc2), 2e-2)
+    close(f(vc1), f(vc2), 2e-2)
+    assert not kc1[0].any() and not vc1[0].any()
+
+
+@pytest.mark.parametrize("batch", [24, 64])
+def test_wide_decode_step_matches_unfused(cuda, batch):
+    """The wide batched decode step (separate RMSNorm, projections on the
+    wide kernel) against the unfused step from the same state."""
+    m = hf_model(TINY, cuda)
+    prompt = torch.randint(0, TINY["vocab"], (batch, 12), generator=torch.Generator().manual_seed(10))
+    dec = LlamaDecoder.from_hf(m, capacity=40, batch=batch)
+    assert dec.fused_wide and not dec.fused_batched
+    dec.prefill(prompt)
+    names = ("tok", "pos", "kv_len", "kcache", "vcache")
+    for step in range(4):
+        state = [getattr(dec, a).clone() for a in names]
+        lf = dec._decode_step().float().clone()
+        tok_f = dec.tok.clone()
+        after = [getattr(dec, a).clone() for a in names]
+        for a, src in zip(names, state):
+            getattr(dec, a).copy_(src)
+        dec.fused_wide = False
+        lu = dec._decode_step().float()
+        dec.fused_wide = True
+        close(f(lf), f(lu), 2e-2)
+        for b in range(batch):
+            if not torch.equal(tok_f[b], dec.tok[b]):
+                top2 = torch.topk(lu[b], 2).values
+                assert float(top2[0] - top2[1]) < 2e-2
+        for a, src in zip(names, after):
+            getattr(dec, a).copy_(src)
 
 
 def test_batched_fused_decode_step_matches_unfused(cuda):
