@@ -849,11 +849,10 @@ static void decode_wide_launch2(const DecMArgs &a, unsigned grid, hipStream_t st
 
 // Wide-kernel shapes: output groups per work-group (x reuse) traded against
 // waves per work-group (K split), within the registers of a lane:
-// (GW, NW) = (4, 4), (2, 8) or (1, 16).
+// (GW, NW) = (4, 4) or (1, 16).
 template <typename T, int OK>
 static void decode_wide_launch1(const DecMArgs &a, int gw, unsigned grid, hipStream_t st) {
     if (gw == 4) decode_wide_launch2<T, OK, 4, 4>(a, grid, st);
-    else if (gw == 2) decode_wide_launch2<T, OK, 8, 2>(a, grid, st);
     else decode_wide_launch2<T, OK, 16, 1>(a, grid, st);
 }
 
@@ -965,9 +964,14 @@ extern "C" int kuiops_decode_rows_batched(
         default: err = decode_mrows_launch<T, kXSwiGlu>(a, out_kind, nw, (unsigned)grid, lds, st); break;         \
     }
     if (wide) {
-        // groups per work-group: as many as still leave a work-group per CU
-        const int gw = ngroups >= 4 * 256 ? 4 : (ngroups >= 2 * 256 ? 2 : 1);
-        const int wnw = gw == 4 ? 4 : (gw == 2 ? 8 : 16);
+        // groups per work-group: 4 (x read once per 64 outputs) once that
+        // still leaves ~128 work-groups, else 1 with K split over 16 waves.
+        // Measured at M = 64 / 32, cold W: 11264 x 2048 25.9 / 19.4 us with
+        // 4 groups against 32.5 / 22.5 (2) and 37.7 / 25.2 (1); 32000 x 2048
+        // 50.8 / 37.1 against 93.4 / 62.6; 2048-output shapes are fastest
+        // with 1 group (2048 x 5632: 31.5 against 55.1 with 4).
+        const int gw = ngroups >= 512 ? 4 : 1;
+        const int wnw = gw == 4 ? 4 : 16;
         a.kq = cdiv(cdiv(K, wnw), 64) * 64;
         const unsigned wgrid = (unsigned)cdiv(ngroups, gw);
         if (dtype == KUIOPS_BF16) decode_wide_launch<bf16_t>(a, out_kind, gw, wgrid, st);
