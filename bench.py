@@ -465,6 +465,8 @@ def extra_workloads(torch, ops, steps, warmup, dev):
     ms = graph_time_ms(torch, lambda: ops.sample_top_p(logits, 0.9, uniforms=u), steps, warmup, reps=10)
     out["sampling_top_p_V32000"] = {"value": round(ms * 1e3, 2), "unit": "us"}
     out["llama1b_greedy"] = llama_workload(torch, dev)
+    out["llama1b_greedy_batch8"] = llama_workload(torch, dev, batch=8)
+    out["llama1b_greedy_batch64"] = llama_workload(torch, dev, batch=64, reps=2)
     return out
 
 
@@ -508,16 +510,18 @@ def llama_decode_bytes(c, kv_tokens):
 ALGO_BYTES["llama1b_decode_token"] = llama_decode_bytes(LLAMA1B, 513)
 
 
-def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3):
+def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3, batch=1):
     """random-init Llama-style 1B decoder (16 layers, d 2048,
     32 q / 8 kv heads, head_dim 64, FFN 5632 SwiGLU, vocab 32000), bf16; a
-    512-token uniform-random prompt, then 128 greedy tokens (softmax + top-1).
-    Prefill runs eagerly; each decode step is one HIP-graph replay."""
+    512-token uniform-random prompt per sequence, then 128 greedy tokens
+    (softmax + top-1).  Prefill runs eagerly; each decode step is one
+    HIP-graph replay.  ``batch`` > 1 decodes that many sequences together
+    (the reference app's batched generate)."""
     from kuillm_amd.decoder import LlamaDecoder, LlamaShape
     c = LLAMA1B
     shape = LlamaShape(**c)
-    dec = LlamaDecoder(shape, llama_state(torch, c, dev), capacity=prompt_len + n_new, device=dev)
-    prompt = torch.randint(0, c["vocab"], (1, prompt_len), generator=torch.Generator().manual_seed(0))
+    dec = LlamaDecoder(shape, llama_state(torch, c, dev), capacity=prompt_len + n_new, batch=batch, device=dev)
+    prompt = torch.randint(0, c["vocab"], (batch, prompt_len), generator=torch.Generator().manual_seed(0))
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     dec.generate(prompt, n_new)                              # warm-up + graph capture
     pre_ms, dec_ms = [], []
@@ -534,21 +538,28 @@ def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3):
         dec_ms.append(b.elapsed_time(e))
     pre, dms = min(pre_ms), min(dec_ms)
     step_ms = dms / (n_new - 1)
-    tok_s = 1e3 / step_ms
-    # bytes of the average step: KV grows from prompt_len + 1 to prompt_len + n_new - 1 keys
-    step_bytes = llama_decode_bytes(c, prompt_len + n_new / 2)
-    gbs = step_bytes * tok_s / 1e9
-    flops_prefill = 2 * prompt_len * (llama_decode_bytes(c, 0) / 2) + \
-        c["layers"] * 2 * 2 * c["hq"] * (c["d"] // c["hq"]) * prompt_len * prompt_len / 2
+    tok_s = batch * 1e3 / step_ms
+    # bytes of the average step: the weights once, plus every sequence's KV
+    # (growing from prompt_len + 1 to prompt_len + n_new - 1 keys)
+    kv = llama_decode_bytes(c, prompt_len + n_new / 2) - llama_decode_bytes(c, 0)
+    step_bytes = llama_decode_bytes(c, 0) + batch * kv
+    gbs = step_bytes / (step_ms * 1e-3) / 1e9
+    flops_prefill = batch * (2 * prompt_len * (llama_decode_bytes(c, 0) / 2) +
+                             c["layers"] * 2 * 2 * c["hq"] * (c["d"] // c["hq"]) * prompt_len * prompt_len / 2)
+    mode = "batch-1 fused" if dec.fused else ("batched fused (LDS-staged rows)" if dec.fused_batched else
+                                             ("batched wide" if dec.fused_wide else "unfused"))
     del dec
-    return {"value": round(tok_s, 1), "unit": "tokens/s", "decode_ms_per_token": round(step_ms, 4),
-            "prefill_ms": round(pre, 3), "prefill_tokens_per_s": round(prompt_len / pre * 1e3, 1),
-            "prefill_tflops": round(flops_prefill / (pre * 1e-3) / 1e12, 1),
-            "end_to_end_tokens_per_s": round(n_new / ((pre + dms) * 1e-3), 1),
-            "decode_bytes_per_token": int(step_bytes),
-            "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes("llama1b_decode_token")),
-            "config": "random-init Llama-style 1B (16 x d2048, GQA 32/8, hd 64, FFN 5632, vocab 32000), "
-                      "bf16, batch 1, 512-token prompt, 128 greedy tokens"}
+    out = {"value": round(tok_s, 1), "unit": "tokens/s", "decode_ms_per_step": round(step_ms, 4),
+           "prefill_ms": round(pre, 3), "prefill_tokens_per_s": round(batch * prompt_len / pre * 1e3, 1),
+           "prefill_tflops": round(flops_prefill / (pre * 1e-3) / 1e12, 1),
+           "end_to_end_tokens_per_s": round(batch * n_new / ((pre + dms) * 1e-3), 1),
+           "decode_bytes_per_step": int(step_bytes), "decode_path": mode,
+           "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes("llama1b_decode_token") if batch == 1 else None),
+           "config": "random-init Llama-style 1B (16 x d2048, GQA 32/8, hd 64, FFN 5632, vocab 32000), "
+                     f"bf16, batch {batch}, 512-token prompt, 128 greedy tokens"}
+    if batch == 1:
+        out["decode_ms_per_token"] = out["decode_ms_per_step"]
+    return out
 
 
 def main():
