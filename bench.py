@@ -139,7 +139,8 @@ def roofline(bound, achieved, unit, traffic=None, segment=None):
 PROFILE_REPS = 3
 PROFILE_SEGMENTS = ("addmm_4096", "decode_gemm_M1", "decode_gemm_M4", "decode_gemm_M16",
                     "sdpa_causal_S2048", "sdpa_causal_S4096", "sdpa_decode_kv4096",
-                    "bmm_32x2048x128x2048", "llama1b_decode_token", "copy_256MiB")
+                    "bmm_32x2048x128x2048", "llama1b_decode_token", "llama1b_b8_decode_step",
+                    "llama1b_b64_decode_step", "copy_256MiB")
 # algorithmic HBM bytes per step of each segment (the "achieved" numerators)
 ALGO_BYTES = {
     "addmm_4096": 3 * 4096 * 4096 * 2 + 4096 * 2,
@@ -154,6 +155,7 @@ ALGO_BYTES = {
 }
 # the profiled decode step runs after a 512-token prefill: 513 cached keys
 ALGO_BYTES["llama1b_decode_token"] = None     # filled in below, after llama_decode_bytes
+ALGO_BYTES["llama1b_b8_decode_step"] = ALGO_BYTES["llama1b_b64_decode_step"] = None
 
 
 def profile_kernels(torch, ops, dev):
@@ -201,6 +203,11 @@ def profile_kernels(torch, ops, dev):
     dec.prefill(torch.randint(0, c["vocab"], (1, 512), generator=torch.Generator().manual_seed(0)))
     segment("llama1b_decode_token", dec._decode_step)
     del dec
+    for n in (8, 64):
+        dec = LlamaDecoder(LlamaShape(**c), llama_state(torch, c, dev), capacity=1024, batch=n, device=dev)
+        dec.prefill(torch.randint(0, c["vocab"], (n, 512), generator=torch.Generator().manual_seed(0)))
+        segment(f"llama1b_b{n}_decode_step", dec._decode_step)
+        del dec
     src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     segment("copy_256MiB", lambda: dst.copy_(src))
@@ -508,6 +515,9 @@ def llama_decode_bytes(c, kv_tokens):
 
 
 ALGO_BYTES["llama1b_decode_token"] = llama_decode_bytes(LLAMA1B, 513)
+for _n in (8, 64):      # batched steps: the weights once, every sequence's 513 keys
+    ALGO_BYTES[f"llama1b_b{_n}_decode_step"] = llama_decode_bytes(LLAMA1B, 0) + _n * (
+        llama_decode_bytes(LLAMA1B, 513) - llama_decode_bytes(LLAMA1B, 0))
 
 
 def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3, batch=1):
@@ -554,7 +564,8 @@ def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3, batch=1):
            "prefill_tflops": round(flops_prefill / (pre * 1e-3) / 1e12, 1),
            "end_to_end_tokens_per_s": round(batch * n_new / ((pre + dms) * 1e-3), 1),
            "decode_bytes_per_step": int(step_bytes), "decode_path": mode,
-           "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes("llama1b_decode_token") if batch == 1 else None),
+           "roofline": roofline("hbm", gbs, "GB/s", traffic_bytes("llama1b_decode_token" if batch == 1 else
+                                                                  f"llama1b_b{batch}_decode_step")),
            "config": "random-init Llama-style 1B (16 x d2048, GQA 32/8, hd 64, FFN 5632, vocab 32000), "
                      f"bf16, batch {batch}, 512-token prompt, 128 greedy tokens"}
     if batch == 1:
