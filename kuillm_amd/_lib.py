@@ -91,6 +91,11 @@ SIGNATURES = {
     "kuiops_decode_qkv_rope": (_int, [_i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _i64, _i64, _vp, _vp, _flt,
                                       _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                       _vp]),
+    "kuiops_decode_step_sync_bytes": (_sz, [_i64]),
+    "kuiops_decode_step": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _flt, _vp, _i64, _i64,
+                                  _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                                  _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "kuiops_decode_step_error": (_int, [_vp, _i64, _vp]),
 }
 
 

@@ -1,0 +1,388 @@
+// Split-KV decode attention (few query rows per head over a long KV cache),
+// shared by the attention library and the persistent decode-step kernel.
+#pragma once
+
+#include "common.hpp"
+
+namespace kuiops {
+
+struct AttnArgs {
+    int64_t n, hq, hkv, l, s;
+    const void *Q, *K, *V;
+    void *O;
+    int64_t sq0, sq1, sq2, sk0, sk1, sk2, sv0, sv1, sv2, so0, so1, so2;
+    float *lse;
+    float scale_log2;   // softmax scale * log2(e)
+    int causal;
+    int nqb;            // query blocks per (batch, head)
+    int pair;           // causal prefill: a work-group runs query blocks p and nqb-1-p
+    // decode
+    int splits;
+    int64_t chunk;      // keys per split
+    int rows_per_group; // query rows handled by one work-group
+    int row_groups;
+    float *ws_ml;       // [rows_total][splits][2]
+    float *ws_o;        // [rows_total][splits][ev]
+    unsigned *counters; // [n][hkv][row_groups] split arrival counters (zero between calls)
+    const int32_t *kv_len;  // decode: per-batch key count in device memory (<= s), or null
+    // additive attention bias (fa_fwd_kernel BIAS): element (b, h, q, key) at
+    // bias + b*sb0 + h*sb1 + q*sb2 + key, in the dtype of Q; added to the raw
+    // scores pre-divided by the scale (softmax(scale * (QK^T + bias / scale)))
+    const void *bias;
+    int64_t sb0, sb1, sb2;
+    float inv_scale;
+};
+
+constexpr float kLn2 = 0.69314718055994530942f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+
+// Merges online-softmax state (m2, l2, o2) into (m1, l1, o1).
+template <int ND>
+__device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, float m2, float l2, const float *o2) {
+    const float M = fmaxf(m1, m2);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    const float a1 = fast_exp2(m1 - Mu), a2 = fast_exp2(m2 - Mu);
+    l1 = l1 * a1 + l2 * a2;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) o1[d] = o1[d] * a1 + o2[d] * a2;
+    m1 = M;
+}
+
+// One work-group of fa_decode_kernel: split `split` of the row group `unit`
+// (KV head * row_groups + row group) of batch entry b.
+// IO carries the query reads and the output stores (CoherentIO when the
+// query comes from, and the output goes to, work-groups of the same launch).
+//
+// `wait` runs after the first step's K / V loads are issued and before the
+// query is read (the persistent decode step waits there for the qkv
+// projection; older cache rows do not depend on it).  Key `fresh` (>= 0),
+// written by that projection, is then read again through IO.
+struct NoWaitAttn {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+template <typename T, int HD, int R, int NWV = 4, int NB = 4, typename IO = PlainIO, typename Wait = NoWaitAttn>
+__device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, int unit, int64_t b,
+                                                const Wait &wait = Wait{}, int64_t fresh = -1) {
+    // NB: keys per lane group per step; all K / V loads of a step are issued
+    // before any is used, so a step is one memory round trip.
+    constexpr int NT = NWV * 64;
+    constexpr int LPK = HD / 8;       // lanes per key (8 d values each)
+    constexpr int KPW = 64 / LPK;     // keys per wave step
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kg = lane / LPK, dl = lane % LPK;
+    const int hk = unit / a.row_groups, rg = unit % a.row_groups;
+    // head / query index arithmetic in 32 bits (a 64-bit division is a long
+    // instruction sequence ahead of the Q loads); decode row counts are small
+    const int G = (int)a.hq / (int)a.hkv;
+    const int LQ = (int)a.l;
+    const int rows_kv = G * (int)a.l;            // query rows sharing this KV head
+    const int r0 = rg * a.rows_per_group;
+
+    const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
+    const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
+    // keys of this batch entry: s, or the cache length read from device
+    // memory (a graph-captured decode step keeps s at the cache capacity)
+    const int64_t s_b = a.kv_len ? max((int64_t)0, min((int64_t)a.kv_len[b], a.s)) : a.s;
+    const int64_t kbeg = (int64_t)split * a.chunk;
+    const int64_t kend = min(s_b, kbeg + a.chunk);
+
+    float m[R], lsum[R], o[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m[r] = -INFINITY;
+        lsum[r] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[r][e] = 0.f;
+    }
+
+    // The loop runs over the split's keys within the capacity s (known at
+    // launch), not over the device key count: the K / V loads then need not
+    // wait for kv_len.  Keys at or past kend are masked after loading.
+    const int64_t kend_cap = min(a.s, kbeg + a.chunk);
+    u32x4 kr[NB], vr[NB];
+    auto load_kv = [&](int64_t kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int64_t key = min(kb + j * KPW + kg, kend_cap - 1);    // in-bounds address
+            kr[j] = *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + dl * 8);
+            vr[j] = *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dl * 8);
+        }
+    };
+    const int64_t kb0 = kbeg + (int64_t)wave * KPW * NB;
+    if (kb0 < kend_cap) load_kv(kb0);
+    wait();
+
+    // Query rows: row r -> head hk*G + (r / l), query index r % l.
+    float q[R][8];
+    int64_t last_key[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int rr = r0 + r;
+        const bool ok = rr < rows_kv && r < a.rows_per_group;
+        const int64_t head = hk * G + (ok ? rr / LQ : 0);
+        const int64_t qi = ok ? rr % LQ : 0;
+        const T *Qp = reinterpret_cast<const T *>(a.Q) + b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8;
+        u32x4 raw = ok ? IO::ld(reinterpret_cast<const u32x4 *>(Qp)) : u32x4{0, 0, 0, 0};
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        t8 qv = __builtin_bit_cast(t8, raw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[r][e] = to_f32(qv[e]) * a.scale_log2;
+        // keys visible to this row (exclusive bound)
+        last_key[r] = ok ? (a.causal ? s_b - a.l + qi + 1 : s_b) : 0;
+    }
+
+    for (int64_t kb = kb0; kb < kend_cap; kb += NWV * KPW * NB) {
+        float s[R][NB];
+        if (kb != kb0) load_kv(kb);
+        if (fresh >= 0) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                if (kb + j * KPW + kg == fresh) {
+                    kr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Kp + fresh * a.sk2 + dl * 8));
+                    vr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Vp + fresh * a.sv2 + dl * 8));
+                }
+            }
+        }
+        // keys past the device count are zeroed (their scores are masked
+        // below; a zero V keeps a NaN in unused cache rows out of the sum)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            if (kb + j * KPW + kg >= kend) {
+                kr[j] = u32x4{0, 0, 0, 0};
+                vr[j] = u32x4{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            typedef T t8 __attribute__((ext_vector_type(8)));
+            t8 kv = __builtin_bit_cast(t8, kr[j]);
+            float kf[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kf[e] = to_f32(kv[e]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d += q[r][e] * kf[e];
+                d = group_sum<LPK>(d);
+                s[r][j] = d;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float mb = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int64_t key = kb + j * KPW + kg;
+                if (key >= kend || key >= last_key[r]) s[r][j] = -INFINITY;
+                mb = fmaxf(mb, s[r][j]);
+            }
+            const float m_new = fmaxf(m[r], mb);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = fast_exp2(m[r] - m_use);
+            float p[NB], ps = 0.f;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                p[j] = fast_exp2(s[r][j] - m_use);
+                ps += p[j];
+            }
+            lsum[r] = lsum[r] * alpha + ps;
+            m[r] = m_new;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[r][e] *= alpha;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                typedef T t8 __attribute__((ext_vector_type(8)));
+                t8 vv = __builtin_bit_cast(t8, vr[j]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[r][e] += p[j] * to_f32(vv[e]);
+            }
+        }
+    }
+
+    // Merge the KPW key slots of a wave (lanes with equal dl) by a butterfly
+    // over the lane bits above dl: partners compute the same commutative
+    // merge, so every lane ends with the wave's bitwise-same state.  Then the
+    // waves' states merge through LDS in wave order; a single split writes
+    // the normalised output, otherwise the split's state goes to the
+    // workspace.
+#pragma unroll
+    for (int sh = LPK; sh < 64; sh <<= 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float m2 = __shfl_xor(m[r], sh, 64), l2 = __shfl_xor(lsum[r], sh, 64);
+            float o2[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o2[e] = __shfl_xor(o[r][e], sh, 64);
+            merge_state<8>(m[r], lsum[r], o[r], m2, l2, o2);
+        }
+    }
+    constexpr int NSL = NWV;
+    __shared__ float sm[NSL][R], sl[NSL][R], so[NSL][R][HD];
+    if (kg == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (dl == 0) { sm[wave][r] = m[r]; sl[wave][r] = lsum[r]; }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) so[wave][r][dl * 8 + e] = o[r][e];
+        }
+    }
+    __syncthreads();
+    const int nrows = min(a.rows_per_group, rows_kv - r0);
+    for (int idx = tid; idx < R * HD; idx += NT) {
+        const int r = idx / HD, d = idx % HD;
+        if (r >= nrows) continue;
+        // max over the slots, then one weight per slot for its sum and output
+        // (independent terms, summed in slot order)
+        float mm = -INFINITY;
+        for (int sv = 0; sv < NSL; ++sv) mm = fmaxf(mm, sm[sv][r]);
+        const float mu = (mm == -INFINITY) ? 0.f : mm;
+        float ll = 0.f, oo = 0.f;
+        for (int sv = 0; sv < NSL; ++sv) {
+            const float wgt = fast_exp2(sm[sv][r] - mu);
+            ll = __builtin_fmaf(sl[sv][r], wgt, ll);
+            oo = __builtin_fmaf(so[sv][r][d], wgt, oo);
+        }
+        const int rr = r0 + r;
+        const int64_t head = hk * G + rr / LQ, qi = rr % LQ;
+        const int64_t grow = (b * a.hq + head) * a.l + qi;
+        if (a.splits == 1) {
+            T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
+            IO::st(Op + d, from_f32<T>(oo * (ll > 0.f ? 1.f / ll : 0.f)));
+            if (a.lse && d == 0) a.lse[grow] = ll > 0.f ? (mm + __log2f(ll)) * kLn2 : -INFINITY;
+            continue;
+        }
+        if (!a.counters) {
+            // merged by the separate merge kernel
+            a.ws_o[(grow * a.splits + split) * HD + d] = oo;
+            if (d == 0) {
+                a.ws_ml[(grow * a.splits + split) * 2 + 0] = mm;
+                a.ws_ml[(grow * a.splits + split) * 2 + 1] = ll;
+            }
+            continue;
+        }
+        // agent-coherent stores (written through the XCD's L2): the
+        // work-group that merges the splits may run on another XCD
+        __hip_atomic_store(&a.ws_o[(grow * a.splits + split) * HD + d], oo, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+            __hip_atomic_store(&a.ws_ml[(grow * a.splits + split) * 2 + 0], mm, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.ws_ml[(grow * a.splits + split) * 2 + 1], ll, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (a.splits == 1 || !a.counters) return;
+
+    // The last of the group's split work-groups to arrive merges the splits
+    // in split order (bitwise repeatable whatever the arrival order).
+    // Ordering (as in the decode GEMM's merge): the split states are
+    // agent-scope relaxed atomic stores (`global_store sc1`, written through
+    // the per-XCD L2); each thread waits for their acknowledgements
+    // (s_waitcnt(0)) before the barrier that precedes tid 0's agent-scope
+    // counter RMW, and the merging work-group reads them with sc1 buffer
+    // loads, which miss the non-coherent caches.  This relies on the hardware
+    // rule that an acknowledged sc1 store is visible at the agent's coherence
+    // point before a later RMW of the same agent, not on a release / acquire
+    // pair (which would add an L2 write-back per XCD to every work-group).
+    __shared__ int s_last;
+    __shared__ float s_w[R][64];
+    __shared__ float s_M[R], s_L[R];
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned *ctr = a.counters + (b * a.hkv + hk) * a.row_groups + rg;
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(a.splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // The split states are read with agent-coherent (sc1) buffer loads, which
+    // unlike atomics can be batched.  Wave w turns row w's split maxima into
+    // weights (splits <= 64, one per lane); thread (r, d) then sums
+    // weight * o[split][d] in split order.
+    const __amdgpu_buffer_rsrc_t rs_ml = __builtin_amdgcn_make_buffer_rsrc((void *)a.ws_ml, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc((void *)a.ws_o, (short)0, 0x7fffffff, 0x00020000);
+    constexpr int kSc1 = 16;                    // cache policy: system-coherent level 1 (agent scope)
+    auto grow_of = [&](int r) {
+        const int rr = r0 + r;
+        return (b * a.hq + hk * G + rr / LQ) * a.l + rr % LQ;
+    };
+    // Thread (r, d) = tid issues its o loads (at most 32 splits) before the
+    // weights are known, so both arrive in one memory round trip.
+    constexpr int kMaxSplits = 32;
+    float ov[kMaxSplits];
+    const bool pre = a.splits <= kMaxSplits && nrows * HD <= NT && tid < nrows * HD;
+    if (pre) {
+        const uint32_t base = (uint32_t)((grow_of(tid / HD) * a.splits * HD + tid % HD) * 4);
+#pragma unroll
+        for (int z = 0; z < kMaxSplits; ++z)
+            ov[z] = z < a.splits ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                       rs_o, base + (uint32_t)(z * HD * 4), 0, kSc1))
+                                 : 0.f;
+    }
+    for (int r = wave; r < nrows; r += NWV) {
+        const uint32_t base = (uint32_t)(grow_of(r) * a.splits * 2) * 4;
+        // (the b32 loads return raw bits)
+        const float mz = lane < a.splits
+                             ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs_ml, base + lane * 8, 0, kSc1))
+                             : -INFINITY;
+        const float lz = lane < a.splits
+                             ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs_ml, base + lane * 8 + 4, 0, kSc1))
+                             : 0.f;
+        const float M = wave_max(mz);
+        const float Mu = (M == -INFINITY) ? 0.f : M;
+        const float w = lane < a.splits ? fast_exp2(mz - Mu) : 0.f;
+        s_w[r][lane] = w;
+        const float L = wave_sum(w * lz);
+        if (lane == 0) { s_M[r] = M; s_L[r] = L; }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < nrows * HD; idx += NT) {
+        const int r = idx / HD, d = idx % HD;
+        const int64_t grow = grow_of(r);
+        float acc = 0.f;
+        if (pre) {
+#pragma unroll
+            for (int z = 0; z < kMaxSplits; ++z)
+                if (z < a.splits) acc += s_w[r][z] * ov[z];
+        } else {
+            const uint32_t base = (uint32_t)((grow * a.splits * HD + d) * 4);
+            for (int z0 = 0; z0 < a.splits; z0 += 8) {
+                float o8[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    o8[j] = z0 + j < a.splits ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                                    rs_o, base + (uint32_t)((z0 + j) * HD * 4), 0, kSc1))
+                                              : 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (z0 + j < a.splits) acc += s_w[r][z0 + j] * o8[j];
+            }
+        }
+        const float L = s_L[r];
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        const int rr = r0 + r;
+        const int64_t head = hk * G + rr / LQ, qi = rr % LQ;
+        T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
+        IO::st(Op + d, from_f32<T>(acc * inv));
+        if (a.lse && d == 0) a.lse[grow] = L > 0.f ? (s_M[r] + __log2f(L)) * kLn2 : -INFINITY;
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T, int HD, int R, int NWV = 4, int NB = 4>
+__global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
+    // One split, many row groups: work-groups are dispatched round-robin
+    // over the 8 XCDs, so consecutive (KV head, row group) units are spread
+    // to give all row groups of a KV head one XCD (its K / V then come from
+    // that XCD's L2 after the first read).
+    int unit = blockIdx.y;
+    if (gridDim.x == 1 && (gridDim.y & 7) == 0) unit = (unit & 7) * (gridDim.y >> 3) + (unit >> 3);
+    fa_decode_block<T, HD, R, NWV, NB>(a, blockIdx.x, unit, blockIdx.z);
+}
+
+}  // namespace kuiops

@@ -108,6 +108,58 @@ __device__ __forceinline__ void transpose4x8_b16(const u32x4 in[4], u32x2 out[8]
     }
 }
 
+// ------------------------------------------------------ I/O policies
+// Loads / stores of the activations that the shared kernel bodies exchange.
+// PlainIO: ordinary accesses (the data crosses a kernel boundary).
+// CoherentIO: agent-scope relaxed atomic accesses, which gfx942 / gfx950
+// perform with sc1 (stores written through the per-XCD L2, loads served
+// past the non-coherent L1 / L2), for data exchanged between work-groups of
+// one launch on different XCDs.  16-byte transfers go as two 8-byte atomics.
+struct PlainIO {
+    template <typename V> static __device__ __forceinline__ V ld(const V *p) { return *p; }
+    template <typename V> static __device__ __forceinline__ void st(V *p, V v) { *p = v; }
+};
+struct CoherentIO {
+    template <typename V> static __device__ __forceinline__ V ld(const V *p) {
+        static_assert(sizeof(V) == 16 || sizeof(V) == 8 || sizeof(V) == 4 || sizeof(V) == 2, "size");
+        if constexpr (sizeof(V) == 16) {
+            const uint64_t *q = reinterpret_cast<const uint64_t *>(p);
+            typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+            const u64x2 r = {__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                             __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+            return __builtin_bit_cast(V, r);
+        } else if constexpr (sizeof(V) == 8) {
+            return __builtin_bit_cast(V, __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT));
+        } else if constexpr (sizeof(V) == 4) {
+            return __builtin_bit_cast(V, __hip_atomic_load(reinterpret_cast<const uint32_t *>(p), __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT));
+        } else {
+            return __builtin_bit_cast(V, __hip_atomic_load(reinterpret_cast<const uint16_t *>(p), __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT));
+        }
+    }
+    template <typename V> static __device__ __forceinline__ void st(V *p, V v) {
+        static_assert(sizeof(V) == 16 || sizeof(V) == 8 || sizeof(V) == 4 || sizeof(V) == 2, "size");
+        if constexpr (sizeof(V) == 16) {
+            typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+            const u64x2 r = __builtin_bit_cast(u64x2, v);
+            uint64_t *q = reinterpret_cast<uint64_t *>(p);
+            __hip_atomic_store(q, r[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(q + 1, r[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if constexpr (sizeof(V) == 8) {
+            __hip_atomic_store(reinterpret_cast<uint64_t *>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        } else if constexpr (sizeof(V) == 4) {
+            __hip_atomic_store(reinterpret_cast<uint32_t *>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            __hip_atomic_store(reinterpret_cast<uint16_t *>(p), __builtin_bit_cast(uint16_t, v), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+};
+
 // ------------------------------------------------------- wave64 reductions
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -127,6 +179,20 @@ __device__ __forceinline__ double wave_max(double v) {
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Sum over aligned groups of N (2, 4, 8 or 16) lanes with DPP lane moves
+// (no LDS round trip): quad swaps, then the half-row and row mirrors.  Each
+// step adds two partial sums that are equal in both lanes of a pair, so every
+// lane of a group ends with the bitwise same total.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+    if (N >= 4) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // lane ^ 2
+    if (N >= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)); // 7 - lane (in 8)
+    if (N >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)); // 15 - lane (in 16)
     return v;
 }
 

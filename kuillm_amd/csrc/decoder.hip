@@ -7,31 +7,11 @@
 // result to the tensor dtype), so a decoder built on them tracks the stock
 // PyTorch model op for op.  Floating-point contraction is off in this file:
 // an FMA would skip the rounding of a product that the stock ops round.
-#include "common.hpp"
+#include "decode_rows.hpp"
 
 #pragma clang fp contract(off)
 
 namespace kuiops {
-
-template <typename T>
-__device__ __forceinline__ float rnd(float x) { return to_f32(from_f32<T>(x)); }
-
-template <typename T>
-__device__ __forceinline__ void unpack8(u32x4 raw, float *f) {
-    typedef T t8 __attribute__((ext_vector_type(8)));
-    const t8 v = __builtin_bit_cast(t8, raw);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = to_f32(v[e]);
-}
-
-template <typename T>
-__device__ __forceinline__ u32x4 pack8f(const float *f) {
-    typedef T t8 __attribute__((ext_vector_type(8)));
-    t8 v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = from_f32<T>(f[e]);
-    return __builtin_bit_cast(u32x4, v);
-}
 
 // ------------------------------------------------------------ RMSNorm
 
@@ -165,275 +145,6 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
     const int64_t hv = h - a.hq - a.hkv;
     T *v = reinterpret_cast<T *>(a.vc) + b * a.sv0 + hv * a.sv1 + pos * a.sv2;
     for (int64_t i = lane; i < a.hd; i += 64) v[i] = row[h * a.hd + i];
-}
-
-// ------------------------------------- batch-1 decode projection
-
-constexpr int kXPlain = 1, kXRmsNorm = 2, kXSwiGlu = 3;   // kuiops_x_kind
-constexpr int kDecodeMaxK = 8192;
-
-constexpr int kOutPlain = 0, kOutSwiGlu = 1, kOutRope = 2;   // decode_rows_kernel epilogues
-
-struct DecLinArgs {
-    int64_t N, K;
-    const void *in, *in_add;           // x source; RMSNorm: h = round(in + in_add)
-    const void *norm_w;
-    float eps;
-    void *h_out;
-    const void *W; int64_t ldw;        // [N, K] rows, K contiguous
-    const void *bias;
-    void *out;
-    int rpw;                           // rows per wave
-    // optional device row index of `in` (in += in_row[0] * ld_in, clamped to in_rows)
-    const int64_t *in_row; int64_t ld_in, in_rows;
-    // paired epilogues: logical row 2p + e is W row base(p) + e * pair_off
-    int64_t pair_off;
-    int pair_shift;                    // log2(pair_off) when a power of two, else -1
-    // rotary epilogue (kOutRope): rows are [q heads | k heads | v heads] of hd
-    int64_t hq, hkv, hd;
-    const float *inv_freq;
-    const int32_t *pos;                // device position of the token
-    void *kc; int64_t sk1, sk2;        // k cache: head, position strides
-    void *vc; int64_t sv1, sv2;
-    int64_t cap;
-};
-
-// W row of logical row j: identity, or the pair mapping of the paired
-// epilogues (SwiGLU: rows p and p + ffn; rotary: rows i and i + hd/2 of a
-// head, so that one wave holds both halves of each rotated pair).
-// p / pair_off (a shift for the power-of-two head halves of real models: a
-// 64-bit division would sit on the W loads' address path)
-__device__ __forceinline__ int64_t pair_div(const DecLinArgs &a, int64_t p) {
-    return a.pair_shift >= 0 ? p >> a.pair_shift : p / a.pair_off;
-}
-
-template <int OK>
-__device__ __forceinline__ int64_t dec_row(const DecLinArgs &a, int64_t j) {
-    if constexpr (OK == kOutPlain) return j;
-    const int64_t p = j >> 1, e = j & 1;
-    if constexpr (OK == kOutSwiGlu) return p + e * a.pair_off;
-    const int64_t half = a.pair_off, head = pair_div(a, p);
-    return head * a.hd + (p - head * half) + e * half;
-}
-
-// out[n] = dot(W[n, :], x) (+ bias[n]) with x computed by every work-group
-// into LDS (the fused input stage), then held in registers: lane l owns
-// 16-byte chunks l, l + 64, ... of x and of each W row, so a wave reads a row
-// as whole 1 KB segments and the row's dot product is a wave sum.  A wave
-// owns rpw <= RG rows; their W loads are issued before the input stage, so
-// the stage's own global reads and reduction hide under the W latency.
-//   kXPlain    x = in
-//   kXRmsNorm  h = round(in + in_add), x = round(w * round(h * rsqrt(mean(h^2) + eps)));
-//              work-group 0 stores h to h_out
-//   kXSwiGlu   x = round(round(silu(in[k])) * in[K + k])      (in = [gate | up])
-// Epilogues (OK):
-//   kOutPlain   out[n] = round(dot) (+ bias)
-//   kOutSwiGlu  rows (p, p + ffn) of a [gate; up] weight: out[p] = round(round(silu(g)) * u),
-//               g, u the rounded projections (as silu_mul_kernel)
-//   kOutRope    rows (i, i + hd/2) of each head of a fused qkv weight: q and k
-//               pairs rotated at position pos (as rope_kv_kernel), q to out
-//               [hq * hd], k and v stored into the caches at pos (if < cap)
-template <typename T, int XK, int KC, int OK = kOutPlain>
-__global__ __launch_bounds__(256) void decode_rows_kernel(DecLinArgs a) {
-    constexpr int RG = KC <= 4 ? 4 : (KC <= 8 ? 2 : 1);    // rows per wave (host: rpw == RG)
-    static_assert(OK == kOutPlain || RG % 2 == 0, "paired epilogues need two rows per wave");
-    constexpr int XCH = kDecodeMaxK / 8 / 256;      // x chunks per thread in the input stage
-    typedef T t8 __attribute__((ext_vector_type(8)));
-    __shared__ u32x4 sx[kDecodeMaxK / 8];
-    __shared__ float red[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nch = (int)(a.K / 8);
-    const T *in = reinterpret_cast<const T *>(a.in);
-    if (a.in_row) in += max((int64_t)0, min(a.in_row[0], a.in_rows - 1)) * a.ld_in;
-
-    // ---- this wave's W rows, in flight during the input stage
-    const T *W = reinterpret_cast<const T *>(a.W);
-    const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * a.rpw;
-    const int64_t r1 = min(a.N, r0 + a.rpw);
-    // Rotary epilogue operands (the token position and the pair's inverse
-    // frequency), loaded first so that their latency hides under the W loads
-    // instead of following the dot products.
-    int64_t rope_pos = 0;
-    float rope_freq = 0.f;
-    if constexpr (OK == kOutRope) {
-        rope_pos = a.pos ? (int64_t)a.pos[0] : 0;
-        if (lane < RG / 2) {
-            const int64_t p = (r0 + 2 * lane) >> 1, half = a.pair_off, head = pair_div(a, p);
-            if (head < a.hq + a.hkv && r0 + 2 * lane + 1 < r1) rope_freq = a.inv_freq[p - head * half];
-        }
-    }
-    u32x4 wv[RG][KC];
-#pragma unroll
-    for (int g = 0; g < RG; ++g) {
-        const int64_t r = dec_row<OK>(a, min(r0 + g, a.N - 1));   // clamped: never stored
-#pragma unroll
-        for (int j = 0; j < KC; ++j) {
-            const int ch = j * 64 + lane;
-            wv[g][j] = ch < nch ? *reinterpret_cast<const u32x4 *>(W + r * a.ldw + ch * 8) : u32x4{0, 0, 0, 0};
-        }
-    }
-    // Rotary cos / sin of this lane's pair, computed while the W rows are in
-    // flight (their loads were issued after the two operands above, so only
-    // those are waited for); computed in the epilogue they would lengthen
-    // the kernel's final dependency chain by ~0.7 us.
-    float rope_c = 0.f, rope_s = 0.f;
-    if constexpr (OK == kOutRope) {
-        if (lane < RG / 2) {
-            const float ang = (float)rope_pos * rope_freq;
-            rope_c = rnd<T>(cosf(ang));
-            rope_s = rnd<T>(sinf(ang));
-        }
-    }
-    // ---- input stage
-    float h[XCH][8];
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < XCH; ++c) {
-        const int ch = c * 256 + tid;
-        if (ch >= nch) continue;
-        unpack8<T>(*reinterpret_cast<const u32x4 *>(in + ch * 8), h[c]);
-        if constexpr (XK == kXRmsNorm) {
-            if (a.in_add) {
-                float o[8];
-                unpack8<T>(*reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.in_add) + ch * 8), o);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) h[c][e] = rnd<T>(h[c][e] + o[e]);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss += h[c][e] * h[c][e];
-        }
-    }
-    float inv = 0.f;
-    if constexpr (XK == kXRmsNorm) {
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        inv = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.K + a.eps);
-    }
-    const bool store_h = XK == kXRmsNorm && a.h_out && blockIdx.x == 0;
-#pragma unroll
-    for (int c = 0; c < XCH; ++c) {
-        const int ch = c * 256 + tid;
-        if (ch >= nch) continue;
-        float xo[8];
-        if constexpr (XK == kXRmsNorm) {
-            float wv[8];
-            unpack8<T>(*reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.norm_w) + ch * 8), wv);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xo[e] = wv[e] * rnd<T>(h[c][e] * inv);
-            if (store_h) *reinterpret_cast<u32x4 *>(reinterpret_cast<T *>(a.h_out) + ch * 8) = pack8f<T>(h[c]);
-        } else if constexpr (XK == kXSwiGlu) {
-            float uv[8];
-            unpack8<T>(*reinterpret_cast<const u32x4 *>(in + a.K + ch * 8), uv);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xo[e] = rnd<T>(h[c][e] / (1.f + expf(-h[c][e]))) * uv[e];
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xo[e] = h[c][e];
-        }
-        sx[ch] = pack8f<T>(xo);
-    }
-    __syncthreads();
-
-    // ---- rows
-    float xf[KC][8];
-#pragma unroll
-    for (int j = 0; j < KC; ++j) {
-        const int ch = j * 64 + lane;
-        if (ch < nch) unpack8<T>(sx[ch], xf[j]);
-        else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xf[j][e] = 0.f;
-        }
-    }
-    float accs[RG];
-#pragma unroll
-    for (int g = 0; g < RG; ++g) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < KC; ++j) {
-            float w8[8];
-            unpack8<T>(wv[g][j], w8);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w8[e], xf[j][e], acc);
-        }
-        accs[g] = wave_sum(acc);
-    }
-    if constexpr (OK == kOutPlain) {
-        if (lane != 0) return;
-#pragma unroll
-        for (int g = 0; g < RG; ++g) {
-            const int64_t r = r0 + g;
-            if (r < r1) {
-                float acc = accs[g];
-                if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
-                reinterpret_cast<T *>(a.out)[r] = from_f32<T>(acc);
-            }
-        }
-    } else {
-        // every lane holds every row's sum (wave_sum is a butterfly): lane
-        // g / 2 finishes pair g / 2, so the pairs' epilogues run side by side.
-        // The results go through LDS: the work-group's pairs are consecutive
-        // (pg0 ..), so each output half is one contiguous run, stored with a
-        // single 16-byte write (2-byte stores from every wave of every
-        // work-group cost the qkv kernel ~1.5 us).
-        constexpr int PW = RG / 2, PG = 4 * PW;       // pairs per wave / work-group
-        __shared__ __attribute__((aligned(16))) T s_o[2][PG];
-        const int64_t pg0 = (int64_t)blockIdx.x * PG;
-        const int np = (int)min((int64_t)PG, a.N / 2 - pg0);
-        const int64_t pos = rope_pos;
-        const bool store_kv = pos >= 0 && pos < a.cap;
-#pragma unroll
-        for (int g = 0; g < RG; g += 2) {
-            const int64_t r = r0 + g;                    // even: rows r, r + 1 form pair r / 2
-            if (lane != g / 2 || r + 1 >= r1) continue;
-            const int64_t p = r >> 1;
-            const int slot = wave * PW + g / 2;
-            const float x1 = rnd<T>(accs[g]), x2 = rnd<T>(accs[g + 1]);
-            if constexpr (OK == kOutSwiGlu) {
-                s_o[0][slot] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
-            } else {
-                const int64_t head = pair_div(a, p);
-                if (head < a.hq + a.hkv) {
-                    const float c = rope_c, sn = rope_s;
-                    s_o[0][slot] = from_f32<T>(rnd<T>(x1 * c) + rnd<T>(-x2 * sn));
-                    s_o[1][slot] = from_f32<T>(rnd<T>(x2 * c) + rnd<T>(x1 * sn));
-                } else {
-                    s_o[0][slot] = from_f32<T>(x1);
-                    s_o[1][slot] = from_f32<T>(x2);
-                }
-            }
-        }
-        __syncthreads();
-        // destination of pair p's half e: SwiGLU out[p]; rotary q -> out,
-        // k -> k cache, v -> v cache at position pos (element i, or i + hd/2)
-        auto dst_of = [&](int64_t p, int e) -> T * {
-            if constexpr (OK == kOutSwiGlu) {
-                return reinterpret_cast<T *>(a.out) + p;
-            } else {
-                const int64_t half = a.pair_off, head = pair_div(a, p), i = p - head * half + e * half;
-                if (head < a.hq) return reinterpret_cast<T *>(a.out) + head * a.hd + i;
-                if (!store_kv) return nullptr;
-                if (head < a.hq + a.hkv) return reinterpret_cast<T *>(a.kc) + (head - a.hq) * a.sk1 + pos * a.sk2 + i;
-                return reinterpret_cast<T *>(a.vc) + (head - a.hq - a.hkv) * a.sv1 + pos * a.sv2 + i;
-            }
-        };
-        constexpr int NE = OK == kOutSwiGlu ? 1 : 2;
-        if (tid < NE && np > 0) {
-            const int e = tid;
-            T *d0 = dst_of(pg0, e);
-            // one run when all pairs are present and share the first pair's head
-            const bool one_run = np == PG && (OK == kOutSwiGlu || (pg0 - pair_div(a, pg0) * a.pair_off) + PG <= a.pair_off);
-            if (PG * sizeof(T) == 16 && one_run && d0 && aligned16(d0)) {
-                *reinterpret_cast<u32x4 *>(d0) = *reinterpret_cast<const u32x4 *>(s_o[e]);
-            } else {
-                for (int k = 0; k < np; ++k) {
-                    T *d = dst_of(pg0 + k, e);
-                    if (d) *d = s_o[e][k];
-                }
-            }
-        }
-    }
 }
 
 template <typename T, int XK, int OK>

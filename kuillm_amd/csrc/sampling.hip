@@ -15,7 +15,7 @@
 // (key descending, index ascending).  Values are copied bit-exactly.
 // There is no reference kernel (kuiops/topk/.gitkeep); aten.topk is the
 // reference's result.
-#include "common.hpp"
+#include "top1.hpp"
 
 namespace kuiops {
 
@@ -24,8 +24,6 @@ namespace kuiops {
 template <typename T> struct AccT { typedef float type; };
 template <> struct AccT<double> { typedef double type; };
 
-__device__ __forceinline__ float acc_exp(float x) { return __expf(x); }
-__device__ __forceinline__ double acc_exp(double x) { return exp(x); }
 
 template <typename A>
 __device__ __forceinline__ void sm_merge(A &m, A &s, A m2, A s2) {
@@ -75,8 +73,6 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(int64_t m, int64_t n,
 // Longer rows: one 1024-thread work-group per row.  Rows of at most
 // 32 * 1024 elements stay in registers (one read); longer rows use an online
 // (max, sum) pass and a second read.
-constexpr int kSmThreads = 1024;
-constexpr int kSmCache = 32;
 
 template <typename T>
 __global__ __launch_bounds__(kSmThreads) void softmax_row_kernel(int64_t n, const T *X, T *Y) {
@@ -150,13 +146,6 @@ __global__ __launch_bounds__(kSmThreads) void softmax_row_kernel(int64_t n, cons
 
 // ------------------------------------------------------------------ topk
 
-__device__ __forceinline__ uint32_t order_key(float v, bool largest) {
-    uint32_t b = __float_as_uint(v);
-    uint32_t k;
-    if (v != v) k = 0xffffffffu;                       // NaN: above everything
-    else k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return largest ? k : ~k;                           // smallest: NaN lands last
-}
 
 template <typename T> __device__ __forceinline__ float load_f(const T *p) { return to_f32(*p); }
 
@@ -436,92 +425,18 @@ size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
 
 // ------------------------------------------------- greedy decode tail
 
-// softmax + top-1 of one row per work-group, for rows of at most 32 K
-// elements (the register-cached path of softmax_row_kernel, with the same
-// arithmetic, so the probabilities are bitwise those of the softmax kernel),
-// followed by the arg-max with topk's ordering (NaN largest, lowest index on
-// ties).  Thread 0 writes the index (and the probability), records it at
-// history[row][pos[row]] when given, then advances the row's decode state:
-// pos[row] += 1, kv_len[row] += 1 when given.
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int off) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, off, 64), hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
+// softmax + top-1 of one row per work-group (rows of at most 32 K
+// elements; the arithmetic of softmax_row_kernel's register-cached path, so
+// the probabilities are bitwise those of the softmax kernel), then the
+// decode-state advance of that row (softmax_top1_row).
 template <typename T>
 __global__ __launch_bounds__(kSmThreads) void softmax_top1_kernel(int64_t n, const T *X, float *prob, int64_t *index,
                                                                    int32_t *pos, int32_t *kv_len, int64_t *history,
                                                                    int64_t hist_len) {
-    typedef float A;
     const int64_t row = blockIdx.x;
-    const T *x = X + row * n;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ A s_a[kSmThreads / 64], s_b[kSmThreads / 64];
-    __shared__ unsigned long long s_k[kSmThreads / 64];
-    // the decode state is read up front, so the final writes wait on nothing
-    int32_t pos0 = 0, kv0 = 0;
-    if (tid == 0) {
-        if (pos) pos0 = pos[row];
-        if (kv_len) kv0 = kv_len[row];
-    }
-    A v[kSmCache];
-    A m = -(A)INFINITY, s = 0;
-#pragma unroll
-    for (int j = 0; j < kSmCache; ++j) {
-        const int64_t i = tid + (int64_t)kSmThreads * j;
-        v[j] = i < n ? (A)to_f32_or_self(x[i]) : -(A)INFINITY;
-        m = (v[j] > m || v[j] != v[j]) ? v[j] : m;
-    }
-    m = wave_max(m);
-    if (lane == 0) s_a[wave] = m;
-    __syncthreads();
-    m = s_a[0];
-#pragma unroll
-    for (int w = 1; w < kSmThreads / 64; ++w) m = (s_a[w] > m || s_a[w] != s_a[w]) ? s_a[w] : m;
-#pragma unroll
-    for (int j = 0; j < kSmCache; ++j) {
-        v[j] = acc_exp(v[j] - m);
-        if (tid + (int64_t)kSmThreads * j < n) s += v[j];
-    }
-    s = wave_sum(s);
-    if (lane == 0) s_b[wave] = s;
-    __syncthreads();
-    s = 0;
-#pragma unroll
-    for (int w = 0; w < kSmThreads / 64; ++w) s += s_b[w];
-    const A inv = (A)1 / s;
-    // (order key of the probability, complement of the index): the maximum
-    // is the largest probability at the lowest index
-    unsigned long long best = 0ull;
-#pragma unroll
-    for (int j = 0; j < kSmCache; ++j) {
-        const int64_t i = tid + (int64_t)kSmThreads * j;
-        if (i >= n) continue;
-        const unsigned long long k = ((unsigned long long)order_key(v[j] * inv, true) << 32) |
-                                     (0xffffffffu - (uint32_t)i);
-        best = k > best ? k : best;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = shfl_xor_u64(best, off);
-        best = o > best ? o : best;
-    }
-    if (lane == 0) s_k[wave] = best;
-    __syncthreads();
-    if (tid == 0) {
-        best = s_k[0];
-#pragma unroll
-        for (int w = 1; w < kSmThreads / 64; ++w) best = s_k[w] > best ? s_k[w] : best;
-        const int64_t i = (int64_t)(0xffffffffu - (uint32_t)best);
-        index[row] = i;
-        // the winner's probability is in the key: order_key of a value >= 0
-        // is its bit pattern with the top bit set (NaN: all ones)
-        const uint32_t pk = (uint32_t)(best >> 32);
-        if (prob) prob[row] = pk == 0xffffffffu ? __builtin_nanf("") : __uint_as_float(pk & 0x7fffffffu);
-        if (history && pos && pos0 >= 0 && pos0 < hist_len) history[row * hist_len + pos0] = i;
-        if (pos) pos[row] = pos0 + 1;
-        if (kv_len) kv_len[row] = kv0 + 1;
-    }
+    softmax_top1_row<T, kSmThreads>(n, X + row * n, prob ? prob + row : nullptr, index + row,
+                                    pos ? pos + row : nullptr, kv_len ? kv_len + row : nullptr,
+                                    history ? history + row * hist_len : nullptr, hist_len);
 }
 
 }  // namespace kuiops

@@ -119,6 +119,13 @@ class LlamaDecoder:
         # larger batches (up to 64): RMSNorm in its own launch, projections of
         # plain x (read from L2) with the rotary / SwiGLU epilogues fused
         self.fused_wide = not self.fused_batched and 2 <= self.n <= 64 and shapes_ok
+        # batch 1: the whole step as one persistent launch
+        # (kuiops_decode_step) when its attention has the one-pass row-wide
+        # form of the per-op path (the cache fits 8 waves x 12 keys per lane
+        # group), so both paths give the same bits
+        row_wide_keys = 8 * (64 // (s.hd // 8)) * 12
+        self.persistent = (self.fused and s.d == s.hq * s.hd and s.d <= 4096 and s.vocab <= 32768
+                           and self.cap <= row_wide_keys)
         if self.fused or self.fused_batched or self.fused_wide:
             self._setup_fused()
 
@@ -146,6 +153,12 @@ class LlamaDecoder:
             self.logitsb = torch.empty(n, s.vocab, **bf)
             self.xnb = torch.empty(n, s.d, **bf)          # wide step: normalised rows
         self.top_v = torch.empty(n, 1, dtype=torch.float32, device=dev)
+        if self.persistent:
+            ptrs = [[L[k].data_ptr() for k in ("wqkv", "wo", "wgu", "wd", "ln1", "ln2")]
+                    + [self.kcache[i, 0].data_ptr(), self.vcache[i, 0].data_ptr()]
+                    for i, L in enumerate(self.layers)]
+            self.layer_table = torch.tensor(ptrs, dtype=torch.int64, device=dev)
+            self.step_sync = torch.zeros(ops.decode_step_sync_bytes(s.layers), dtype=torch.uint8, device=dev)
         # token chosen at each position (written by the step itself, so a
         # replayed step needs no copy out)
         self.history = torch.zeros(n, self.cap + 1, dtype=torch.int64, device=dev)
@@ -230,8 +243,16 @@ class LlamaDecoder:
         (every rounding point kept), in 5 launches per layer plus LM head and
         a fused softmax / top-1 / state-advance launch: qkv (embedding
         lookup / RMSNorm stage, rotary + cache append epilogue) -> attention
-        -> o -> gate|up (RMSNorm stage, SwiGLU epilogue) -> down."""
+        -> o -> gate|up (RMSNorm stage, SwiGLU epilogue) -> down.  With
+        ``persistent`` the same work, bit for bit, runs as one launch."""
         s = self.s
+        if self.persistent:
+            ops.decode_step(self.layer_table, s.layers, s.d, s.ffn, s.hq, s.hkv, s.hd, s.vocab, s.eps,
+                            self.kcache[0, 0], self.vcache[0, 0], self.embed, self.norm, self.head, self.inv_freq,
+                            self.tok, self.pos, self.kv_len, self.history[0], self.top_v.view(1),
+                            (self.h_buf[0], self.h_buf[1], self.q1, self.att1, self.o1, self.a1, self.down1,
+                             self.logits1), self.step_sync)
+            return self.logits1.view(1, -1)
         hb = self.h_buf
         cur = 0
         att4 = self.att1.view(1, 1, s.hq, s.hd).transpose(1, 2)

@@ -543,3 +543,94 @@ def test_batched_fused_decode_step_matches_unfused(cuda):
                 assert float(top2[0] - top2[1]) < 2e-2
         for a, src in zip(names, after):
             getattr(dec, a).copy_(src)
+
+
+def random_llama(c, device, seed):
+    """Random-init Llama weights under transformers parameter names (linear
+    and embedding N(0, 0.02), norm weights around 1)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    hd = c["d"] // c["hq"]
+
+    def w(o, i):
+        return (torch.randn(o, i, device=device, generator=g) * 0.02).to(torch.bfloat16)
+
+    def norm(n):
+        return (1 + 0.1 * torch.randn(n, device=device, generator=g)).to(torch.bfloat16)
+
+    st = {"model.embed_tokens.weight": w(c["vocab"], c["d"]), "lm_head.weight": w(c["vocab"], c["d"]),
+          "model.norm.weight": norm(c["d"])}
+    for i in range(c["layers"]):
+        p = f"model.layers.{i}."
+        st[p + "self_attn.q_proj.weight"] = w(c["hq"] * hd, c["d"])
+        st[p + "self_attn.k_proj.weight"] = w(c["hkv"] * hd, c["d"])
+        st[p + "self_attn.v_proj.weight"] = w(c["hkv"] * hd, c["d"])
+        st[p + "self_attn.o_proj.weight"] = w(c["d"], c["hq"] * hd)
+        st[p + "mlp.gate_proj.weight"] = w(c["ffn"], c["d"])
+        st[p + "mlp.up_proj.weight"] = w(c["ffn"], c["d"])
+        st[p + "mlp.down_proj.weight"] = w(c["d"], c["ffn"])
+        st[p + "input_layernorm.weight"] = norm(c["d"])
+        st[p + "post_attention_layernorm.weight"] = norm(c["d"])
+    return st
+
+
+def _step_state(dec):
+    return [t.clone() for t in (dec.tok, dec.step_state, dec.kcache, dec.vcache, dec.history, dec.top_v)]
+
+
+def _set_state(dec, st):
+    for dst, src in zip((dec.tok, dec.step_state, dec.kcache, dec.vcache, dec.history, dec.top_v), st):
+        dst.copy_(src)
+
+
+@pytest.mark.parametrize("shape,cap,prompt_len,steps", [
+    (TINY, 64, 24, 8),
+    (dict(TINY, d=512, hq=4, hkv=1, ffn=1536, layers=3), 300, 200, 6),   # head dim 128, ffn K-chunks 3 -> 4
+    (CONFIG5, 512 + 128, 512, 4),
+])
+def test_persistent_step_bitwise_per_op(cuda, shape, cap, prompt_len, steps):
+    """The one-launch decode step (kuiops_decode_step) against the per-op
+    fused step from the same state, step by step: logits, token, history,
+    position / key count, KV caches and the winner's probability all
+    bit-identical; the completion counters are left zero and no wait
+    expired."""
+    print(f"persistent step: {shape} cap {cap}", flush=True)
+    dec = LlamaDecoder(LlamaShape(**shape), random_llama(shape, cuda, 11), capacity=cap)
+    assert dec.persistent
+    prompt = torch.randint(0, shape["vocab"], (1, prompt_len), generator=torch.Generator().manual_seed(12))
+    dec.prefill(prompt)
+    for step in range(steps):
+        before = _step_state(dec)
+        lp = dec._decode_step_fused().clone()
+        torch.cuda.synchronize()
+        after = _step_state(dec)
+        assert not ops.decode_step_error(dec.step_sync, shape["layers"])
+        assert int(dec.step_sync.count_nonzero()) == 0
+        _set_state(dec, before)
+        dec.persistent = False
+        try:
+            lu = dec._decode_step_fused().clone()
+        finally:
+            dec.persistent = True
+        ref = _step_state(dec)
+        assert torch.equal(lp, lu), f"step {step}: logits differ"
+        for name, a, b in zip(("tok", "pos/kv_len", "k cache", "v cache", "history", "prob"), after, ref):
+            assert torch.equal(a, b), f"step {step}: {name} differs"
+        _set_state(dec, after)
+
+
+def test_persistent_graph_decode_matches_per_op(cuda):
+    """Greedy tokens of a graph-replayed persistent step equal the per-op
+    graph's (the step needs no host work between replays)."""
+    dec = LlamaDecoder(LlamaShape(**TINY), random_llama(TINY, cuda, 13), capacity=72)
+    assert dec.persistent
+    prompt = torch.randint(0, TINY["vocab"], (1, 20), generator=torch.Generator().manual_seed(14))
+    fast = dec.generate(prompt, 40, use_graph=True)
+    again = dec.generate(prompt, 40, use_graph=True)
+    dec.persistent = False
+    dec.graph = None
+    dec.kcache.zero_()
+    dec.vcache.zero_()
+    slow = dec.generate(prompt, 40, use_graph=True)
+    assert torch.equal(fast, again)
+    assert torch.equal(fast, slow)
+    assert not ops.decode_step_error(dec.step_sync, TINY["layers"])
