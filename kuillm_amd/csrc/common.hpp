@@ -196,6 +196,18 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// a.x * b.x + a.y * b.y + c for packed pairs (fp32 accumulate)
+template <typename T>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (__is_same(T, bf16_t)) {
+        typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c, false);
+    } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+    }
+}
+
 // --------------------------------------------------------------- host side
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 

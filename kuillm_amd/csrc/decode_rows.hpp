@@ -258,27 +258,22 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
     __syncthreads();
 
     // ---- rows
-    float xf[KC][8];
+    // x stays packed (bf16 / f16 pairs): v_dot2 takes a W pair and an x pair
+    // per instruction (products exact in fp32, fp32 accumulate)
+    u32x4 xv[KC];
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
         const int ch = j * 64 + lane;
-        if (ch < nch) unpack8<T>(sx[ch], xf[j]);
-        else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xf[j][e] = 0.f;
-        }
+        xv[j] = ch < nch ? sx[ch] : u32x4{0, 0, 0, 0};
     }
     float accs[RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < KC; ++j) {
-            float w8[8];
-            unpack8<T>(wv[g][j], w8);
+        for (int j = 0; j < KC; ++j)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w8[e], xf[j][e], acc);
-        }
+            for (int e = 0; e < 4; ++e) acc = dot2<T>(wv[g][j][e], xv[j][e], acc);
         accs[g] = acc;
     }
     // row lane / (64 / RG)'s total in every lane of its group; the next row's

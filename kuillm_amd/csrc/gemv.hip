@@ -445,17 +445,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_strip_kernel(GemvArgs a) {
 // arrive (agent-coherent partials and counter, as in the strip kernel), so
 // the result is bitwise repeatable.
 //
-// a.x * b.x + a.y * b.y + c for packed pairs (fp32 accumulate)
-template <typename T>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    if constexpr (__is_same(T, bf16_t)) {
-        typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c, false);
-    } else {
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
-    }
-}
 
 template <typename T, typename Tout, int MR, int P>
 __global__ __launch_bounds__(512) void gemv_rows_kernel(GemvArgs a) {
