@@ -55,15 +55,18 @@ __device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, flo
 // IO carries the query reads and the output stores (CoherentIO when the
 // query comes from, and the output goes to, work-groups of the same launch).
 //
-// `wait` runs after the first step's K / V loads are issued and before the
-// query is read (the persistent decode step waits there for the qkv
-// projection; older cache rows do not depend on it).  Key `fresh` (>= 0),
-// written by that projection, is then read again through IO.
+// With PF, `wait` runs after the first step's K / V loads are issued and
+// before the query is read (the persistent decode step waits there for the
+// qkv projection; older cache rows do not depend on it), and key `fresh`
+// (>= 0), written by that projection, is then read again through IO.
+// Without PF the query is read first and every step loads its keys in the
+// loop (fewer registers live).  The arithmetic is the same either way.
 struct NoWaitAttn {
     __device__ __forceinline__ void operator()() const {}
 };
 
-template <typename T, int HD, int R, int NWV = 4, int NB = 4, typename IO = PlainIO, typename Wait = NoWaitAttn>
+template <typename T, int HD, int R, int NWV = 4, int NB = 4, typename IO = PlainIO, typename Wait = NoWaitAttn,
+          bool PF = false>
 __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, int unit, int64_t b,
                                                 const Wait &wait = Wait{}, int64_t fresh = -1) {
     // NB: keys per lane group per step; all K / V loads of a step are issued
@@ -112,8 +115,10 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         }
     };
     const int64_t kb0 = kbeg + (int64_t)wave * KPW * NB;
-    if (kb0 < kend_cap) load_kv(kb0);
-    wait();
+    if constexpr (PF) {
+        if (kb0 < kend_cap) load_kv(kb0);
+        wait();
+    }
 
     // Query rows: row r -> head hk*G + (r / l), query index r % l.
     float q[R][8];
@@ -136,8 +141,8 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
 
     for (int64_t kb = kb0; kb < kend_cap; kb += NWV * KPW * NB) {
         float s[R][NB];
-        if (kb != kb0) load_kv(kb);
-        if (fresh >= 0) {
+        if (!PF || kb != kb0) load_kv(kb);
+        if (PF && fresh >= 0) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 if (kb + j * KPW + kg == fresh) {

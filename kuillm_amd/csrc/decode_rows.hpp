@@ -138,17 +138,37 @@ struct NoWait {
 // nothing).  IO carries the activation reads and every output store
 // (PlainIO, or CoherentIO when consumers in the same launch read them).  The input stage runs on the first 256 threads, so its sums
 // are those of the 4-wave kernel whatever NWV is.
-template <typename T, int XK, int KC, int OK, int NWV, typename Wait, typename IO = PlainIO, int RGO = 0>
-__device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t blk, const Wait &wait) {
+typedef __attribute__((address_space(3))) char lds_bytes;
+
+// RGL > 0: each wave owns RGL more rows whose W chunks go global -> LDS
+// (LDS-DMA, issued with the register loads) into `wl` (NWV * RGL * KC KB,
+// wave w's rows at w * RGL * KC KB), so a work-group keeps more weight
+// bytes in flight than its registers hold.
+// xs (non-null): LDS for the staged input x (K * 2 bytes) in place of the
+// body's own array (the persistent decode step shares one buffer between its
+// job kinds).
+template <typename T, int XK, int KC, int OK, int NWV, typename Wait, typename IO = PlainIO, int RGO = 0, int RGL = 0,
+          bool EXTX = false>
+__device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t blk, const Wait &wait,
+                                                  lds_bytes *wl = nullptr, lds_bytes *xs = nullptr) {
 #pragma clang fp contract(off)
     static_assert(NWV == 4 || NWV == 8, "waves");
-    // rows per wave (host: rpw == RG); RGO overrides the default (a row's dot
-    // product is the same whichever wave computes it)
+    static_assert(RGL == 0 || OK != kOutRope, "LDS rows: plain or SwiGLU epilogues");
+    static_assert(OK == kOutPlain || RGL % 2 == 0, "paired epilogues: whole pairs of LDS rows");
+    // register rows per wave; RGO overrides the default (a row's dot product
+    // is the same whichever wave computes it).  Host: rpw == RG + RGL.
     constexpr int RG = RGO ? RGO : (KC <= 4 ? 4 : (KC <= 8 ? 2 : 1));
     static_assert(OK == kOutPlain || RG % 2 == 0, "paired epilogues need two rows per wave");
     constexpr int XCH = KC * 64 / 256 > 0 ? KC * 64 / 256 : 1;   // x chunks per thread in the input stage (K <= 512 KC)
     typedef T t8 __attribute__((ext_vector_type(8)));
-    __shared__ u32x4 sx[KC * 64];
+    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+    lds_u32x4 *sx;
+    if constexpr (EXTX) {
+        sx = (lds_u32x4 *)xs;
+    } else {
+        __shared__ u32x4 sx_own[KC * 64];
+        sx = (lds_u32x4 *)sx_own;
+    }
     __shared__ float red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nch = (int)(a.K / 8);
@@ -180,6 +200,19 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
         for (int j = 0; j < KC; ++j) {
             const int ch = j * 64 + lane;
             wv[g][j] = ch < nch ? *reinterpret_cast<const u32x4 *>(W + r * a.ldw + ch * 8) : u32x4{0, 0, 0, 0};
+        }
+    }
+    if constexpr (RGL > 0) {
+        // chunks past K read a valid neighbour; x is zero there
+#pragma unroll
+        for (int g = 0; g < RGL; ++g) {
+            const int64_t r = dec_row<OK>(a, min(r0 + RG + g, a.N - 1));
+#pragma unroll
+            for (int j = 0; j < KC; ++j) {
+                const int ch = min(j * 64 + lane, nch - 1);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(W + r * a.ldw + ch * 8),
+                                                 wl + ((wave * RGL + g) * KC + j) * 1024, 16, 0, 0);
+            }
         }
     }
     // Rotary cos / sin of this lane's pair, computed while the W rows are in
@@ -279,33 +312,53 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
     // row lane / (64 / RG)'s total in every lane of its group; the next row's
     // total comes from the group above (paired epilogues: rows 2q, 2q + 1)
     const float tot = multi_row_sum<RG>(accs, lane);
-    if constexpr (OK == kOutPlain) {
-        if (lane % (64 / RG) != 0) return;
-        const int64_t r = r0 + lane / (64 / RG);
-        if (r < r1) {
-            float acc = tot;
-            if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
-            IO::st(reinterpret_cast<T *>(a.out) + r, from_f32<T>(acc));
+    // the LDS rows RG .. RG + RGL - 1 (their own reduction: the same sums)
+    float totl = 0.f;
+    if constexpr (RGL > 0) {
+        __builtin_amdgcn_s_waitcnt(0);              // this wave's LDS-DMA has landed
+        float accl[RGL];
+#pragma unroll
+        for (int g = 0; g < RGL; ++g) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < KC; ++j) {
+                const u32x4 w = *(const __attribute__((address_space(3))) u32x4 *)(wl + ((wave * RGL + g) * KC + j) * 1024 + lane * 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = dot2<T>(w[e], xv[j][e], acc);
+            }
+            accl[g] = acc;
         }
+        totl = multi_row_sum<RGL>(accl, lane);
+    }
+    if constexpr (OK == kOutPlain) {
+        auto put = [&](int64_t r, float acc) {
+            if (r < r1) {
+                if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
+                IO::st(reinterpret_cast<T *>(a.out) + r, from_f32<T>(acc));
+            }
+        };
+        if (lane % (64 / RG) == 0) put(r0 + lane / (64 / RG), tot);
+        if constexpr (RGL > 0)
+            if (lane % (64 / RGL) == 0) put(r0 + RG + lane / (64 / RGL), totl);
     } else {
         const float nxt = __shfl_down(tot, 64 / RG, 64);
+        const float nxtl = RGL >= 2 ? __shfl_down(totl, 64 / (RGL >= 2 ? RGL : 1), 64) : 0.f;
         // lane 2q * (64 / RG) finishes pair q, so the pairs' epilogues run
         // side by side.  The results go through LDS: the work-group's pairs
         // are consecutive (pg0 ..), so each output half is one contiguous
         // run, stored as 16-byte writes (2-byte stores from every wave of
         // every work-group cost the qkv kernel ~1.5 us).
-        constexpr int PW = RG / 2, PG = NWV * PW;     // pairs per wave / work-group
+        constexpr int PW = (RG + RGL) / 2, PG = NWV * PW;   // pairs per wave / work-group
         __shared__ __attribute__((aligned(16))) T s_o[2][PG];
         const int64_t pg0 = blk * PG;
         const int np = (int)min((int64_t)PG, a.N / 2 - pg0);
         const int64_t pos = rope_pos;
         const bool store_kv = pos >= 0 && pos < a.cap;
-        if (lane % (128 / RG) == 0) {
-            const int g = 2 * (lane / (128 / RG));
+        auto finish_pair = [&](int g, float t1, float t2) {
             const int64_t r = r0 + g;                    // even: rows r, r + 1 form pair r / 2
             const int64_t p = r >> 1;
             const int slot = wave * PW + g / 2;
-            const float x1 = rnd<T>(tot), x2 = rnd<T>(nxt);
+            const float x1 = rnd<T>(t1), x2 = rnd<T>(t2);
             if (r + 1 < r1) {
                 if constexpr (OK == kOutSwiGlu) {
                     s_o[0][slot] = from_f32<T>(rnd<T>(x1 / (1.f + expf(-x1))) * x2);
@@ -321,7 +374,10 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
                     }
                 }
             }
-        }
+        };
+        if (lane % (128 / RG) == 0) finish_pair(2 * (lane / (128 / RG)), tot, nxt);
+        if constexpr (RGL >= 2)
+            if (lane % (128 / RGL) == 0) finish_pair(RG + 2 * (lane / (128 / RGL)), totl, nxtl);
         __syncthreads();
         // destination of pair p's half e: SwiGLU out[p]; rotary q -> out,
         // k -> k cache, v -> v cache at position pos (element i, or i + hd/2)

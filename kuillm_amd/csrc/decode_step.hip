@@ -137,8 +137,16 @@ struct StepWait {
 };
 
 // Rows per wave of a projection job: 32 registers of W chunks (128 VGPRs),
-// so a work-group holds 128-256 KB of weights in flight while it waits.
+// so a work-group holds 128-256 KB of weights in flight while it waits; the
+// large projections (gate|up, down, LM head) hold 16 more chunks per wave in
+// LDS (kLdsRowBytes per work-group).  With them the layer's qkv, attention,
+// o and gate|up jobs fit one round of the grid, and the down jobs land on
+// work-groups that finished early, whose weight loads then run during the
+// gate|up phase.
 constexpr int rows_per_wave(int kc) { return kc <= 4 ? 8 : (kc <= 8 ? 4 : 2); }
+constexpr int lds_rows_per_wave(int kc) { return kc <= 4 ? 4 : (kc <= 8 ? 2 : 1); }
+constexpr int kLdsRowBytes = kStepWaves * 16 * 1024;
+constexpr int kLdsXBytes = kDecodeMaxK * 2;         // the staged input x
 
 // The projection of layer `l` of one kind, as the per-op entry points set it up.
 __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int l, int rpw) {
@@ -189,10 +197,11 @@ __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int
 
 // The job kinds, each its own function: inlined into one loop, the bodies'
 // register demands add up (spills); as calls each gets its own allocation.
-template <typename T, int XK, int KC, int OK>
-__device__ __attribute__((noinline)) void step_proj(const StepArgs &a, int kind, int l, int idx, int phase) {
-    decode_rows_block<T, XK, KC, OK, kStepWaves, StepWait, CoherentIO, rows_per_wave(KC)>(
-        proj_args(a, kind, l, rows_per_wave(KC)), idx, StepWait{&a, phase - 1});
+template <typename T, int XK, int KC, int OK, int RGL = 0>
+__device__ __attribute__((noinline)) void step_proj(const StepArgs &a, int kind, int l, int idx, int phase,
+                                                    lds_bytes *wl) {
+    decode_rows_block<T, XK, KC, OK, kStepWaves, StepWait, CoherentIO, rows_per_wave(KC), RGL, true>(
+        proj_args(a, kind, l, rows_per_wave(KC) + RGL), idx, StepWait{&a, phase - 1}, wl, wl + kLdsRowBytes);
 }
 
 // attention row `idx` (query head) of layer l, as the per-op row-wide launch
@@ -216,7 +225,7 @@ __device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int 
     at.splits = 1; at.chunk = a.cap;
     at.rows_per_group = 1; at.row_groups = (int)(a.hq / a.hkv);
     at.kv_len = a.kv_len;
-    fa_decode_block<T, HD, 1, kStepWaves, 12, CoherentIO>(at, 0, idx, 0, StepWait{&a, phase - 1}, fresh);
+    fa_decode_block<T, HD, 1, kStepWaves, 12, CoherentIO, StepWait, true>(at, 0, idx, 0, StepWait{&a, phase - 1}, fresh);
 }
 
 // softmax + top-1 of the logits and the decode-state advance; every other
@@ -234,6 +243,9 @@ __device__ __attribute__((noinline)) void step_sample(const StepArgs &a, int pha
 
 template <typename T, int HD, int KCD, int KCF>
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
+    constexpr int RLD = lds_rows_per_wave(KCD), RLF = lds_rows_per_wave(KCF);
+    __shared__ __attribute__((aligned(1024))) char s_wl[kLdsRowBytes + kLdsXBytes];
+    lds_bytes *wl = (lds_bytes *)s_wl;
     const int G = gridDim.x;
     const int lp = kLayerKinds * a.layers;
     for (int j = blockIdx.x; j < a.total; j += G) {
@@ -252,12 +264,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
             phase = lp + (kind - kLayerKinds);
         }
         switch (kind) {
-            case 0: step_proj<T, kXRmsNorm, KCD, kOutRope>(a, 0, l, idx, phase); break;
+            case 0: step_proj<T, kXRmsNorm, KCD, kOutRope>(a, 0, l, idx, phase, wl); break;
             case 1: step_attention<T, HD>(a, l, idx, phase); break;
-            case 2: step_proj<T, kXPlain, KCD, kOutPlain>(a, 2, l, idx, phase); break;
-            case 3: step_proj<T, kXRmsNorm, KCD, kOutSwiGlu>(a, 3, l, idx, phase); break;
-            case 4: step_proj<T, kXPlain, KCF, kOutPlain>(a, 4, l, idx, phase); break;
-            case 5: step_proj<T, kXRmsNorm, KCD, kOutPlain>(a, 5, l, idx, phase); break;
+            case 2: step_proj<T, kXPlain, KCD, kOutPlain>(a, 2, l, idx, phase, wl); break;
+            case 3: step_proj<T, kXRmsNorm, KCD, kOutSwiGlu, RLD>(a, 3, l, idx, phase, wl); break;
+            case 4: step_proj<T, kXPlain, KCF, kOutPlain, RLF>(a, 4, l, idx, phase, wl); break;
+            case 5: step_proj<T, kXRmsNorm, KCD, kOutPlain, RLD>(a, 5, l, idx, phase, wl); break;
             default: step_sample<T>(a, phase); continue;
         }
         step_signal(a, phase, idx);
@@ -350,9 +362,10 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
     a.h0 = h0; a.h1 = h1; a.q = q; a.att = att; a.o = o; a.act = act; a.down = down; a.logits = logits;
     a.sync = reinterpret_cast<unsigned *>(sync);
     const int64_t rows_d = (int64_t)kStepWaves * rows_per_wave(kcd);
-    const int64_t rows_f = (int64_t)kStepWaves * rows_per_wave(kcf);
-    const int64_t nj[kKinds] = {cdiv((hq + 2 * hkv) * hd, rows_d), hq, cdiv(d, rows_d), cdiv(2 * ffn, rows_d),
-                                cdiv(d, rows_f), cdiv(vocab, rows_d), 1};
+    const int64_t rows_dl = (int64_t)kStepWaves * (rows_per_wave(kcd) + lds_rows_per_wave(kcd));
+    const int64_t rows_fl = (int64_t)kStepWaves * (rows_per_wave(kcf) + lds_rows_per_wave(kcf));
+    const int64_t nj[kKinds] = {cdiv((hq + 2 * hkv) * hd, rows_d), hq, cdiv(d, rows_d), cdiv(2 * ffn, rows_dl),
+                                cdiv(d, rows_fl), cdiv(vocab, rows_dl), 1};
     int64_t per_layer = 0;
     for (int k = 0; k < kLayerKinds; ++k) per_layer += nj[k];
     const int64_t total = n_layers * per_layer + nj[5] + nj[6];
