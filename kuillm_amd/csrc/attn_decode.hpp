@@ -31,6 +31,12 @@ struct AttnArgs {
     const void *bias;
     int64_t sb0, sb1, sb2;
     float inv_scale;
+    // epoch-tagged exchange (the persistent decode step, IO = LLIO): the
+    // epochs of the query and output writes, epoch-tagged copies [hkv * e]
+    // of the new k / v rows (key `fresh`), and the expired-wait flag
+    uint32_t ep_q, ep_o;
+    const void *kfresh, *vfresh;
+    unsigned *err;
 };
 
 constexpr float kLn2 = 0.69314718055994530942f;
@@ -123,16 +129,47 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
     // Query rows: row r -> head hk*G + (r / l), query index r % l.
     float q[R][8];
     int64_t last_key[R];
+    u32x4 qraw[R];
+    // epoch-tagged form: this lane's chunk of the new k / v rows as well
+    u32x4 kfr = {0, 0, 0, 0}, vfr = {0, 0, 0, 0};
+    auto load_q = [&]() -> bool {
+        bool all = true;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int rr = r0 + r;
+            const bool ok = rr < rows_kv && r < a.rows_per_group;
+            const int64_t head = hk * G + (ok ? rr / LQ : 0);
+            const int64_t qi = ok ? rr % LQ : 0;
+            if (ok) all = IO::ld8(a.Q, b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8, a.ep_q, qraw[r]) && all;
+            else qraw[r] = u32x4{0, 0, 0, 0};
+        }
+        if constexpr (IO::kLL) {
+            if (fresh >= 0) {
+                all = IO::ld8(a.kfresh, hk * HD + dl * 8, a.ep_q, kfr) && all;
+                all = IO::ld8(a.vfresh, hk * HD + dl * 8, a.ep_q, vfr) && all;
+            }
+        }
+        return all;
+    };
+    if constexpr (IO::kLL) {
+        // every lane reads its query chunk (and the new k / v chunk) until it
+        // is the expected write; the work-group leaves together
+        bool ok = load_q();
+        for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
+            if (__syncthreads_or(ll_give_up(it, a.err))) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (!ok) ok = load_q();
+        }
+    } else {
+        load_q();
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int rr = r0 + r;
         const bool ok = rr < rows_kv && r < a.rows_per_group;
-        const int64_t head = hk * G + (ok ? rr / LQ : 0);
         const int64_t qi = ok ? rr % LQ : 0;
-        const T *Qp = reinterpret_cast<const T *>(a.Q) + b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8;
-        u32x4 raw = ok ? IO::ld(reinterpret_cast<const u32x4 *>(Qp)) : u32x4{0, 0, 0, 0};
         typedef T t8 __attribute__((ext_vector_type(8)));
-        t8 qv = __builtin_bit_cast(t8, raw);
+        t8 qv = __builtin_bit_cast(t8, qraw[r]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) q[r][e] = to_f32(qv[e]) * a.scale_log2;
         // keys visible to this row (exclusive bound)
@@ -146,8 +183,13 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 if (kb + j * KPW + kg == fresh) {
-                    kr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Kp + fresh * a.sk2 + dl * 8));
-                    vr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Vp + fresh * a.sv2 + dl * 8));
+                    if constexpr (IO::kLL) {
+                        kr[j] = kfr;
+                        vr[j] = vfr;
+                    } else {
+                        kr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Kp + fresh * a.sk2 + dl * 8));
+                        vr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Vp + fresh * a.sv2 + dl * 8));
+                    }
                 }
             }
         }
@@ -255,8 +297,17 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         const int64_t head = hk * G + rr / LQ, qi = rr % LQ;
         const int64_t grow = (b * a.hq + head) * a.l + qi;
         if (a.splits == 1) {
-            T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
-            IO::st(Op + d, from_f32<T>(oo * (ll > 0.f ? 1.f / ll : 0.f)));
+            const T ov = from_f32<T>(oo * (ll > 0.f ? 1.f / ll : 0.f));
+            const int64_t oidx = b * a.so0 + head * a.so1 + qi * a.so2 + d;
+            if constexpr (IO::kLL) {
+                // element pairs (d, d + 1) in one epoch-tagged word: lanes d, d + 1
+                // are neighbours of one wave (R == 1, HD even)
+                static_assert(R == 1, "epoch-tagged output: one row per work-group");
+                const uint16_t nb = (uint16_t)__shfl_down((int)__builtin_bit_cast(uint16_t, ov), 1, 64);
+                if ((d & 1) == 0) IO::st2(reinterpret_cast<T *>(a.O), oidx, ov, __builtin_bit_cast(T, nb), a.ep_o);
+            } else {
+                IO::st(reinterpret_cast<T *>(a.O) + oidx, ov);
+            }
             if (a.lse && d == 0) a.lse[grow] = ll > 0.f ? (mm + __log2f(ll)) * kLn2 : -INFINITY;
             continue;
         }
@@ -373,7 +424,7 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         const int rr = r0 + r;
         const int64_t head = hk * G + rr / LQ, qi = rr % LQ;
         T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
-        IO::st(Op + d, from_f32<T>(acc * inv));
+        if constexpr (!IO::kLL) IO::st(Op + d, from_f32<T>(acc * inv));   // (epoch-tagged use: one split)
         if (a.lse && d == 0) a.lse[grow] = L > 0.f ? (s_M[r] + __log2f(L)) * kLn2 : -INFINITY;
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -115,11 +115,30 @@ __device__ __forceinline__ void transpose4x8_b16(const u32x4 in[4], u32x2 out[8]
 // perform with sc1 (stores written through the per-XCD L2, loads served
 // past the non-coherent L1 / L2), for data exchanged between work-groups of
 // one launch on different XCDs.  16-byte transfers go as two 8-byte atomics.
+//
+// Vector accesses used by the shared bodies (16-bit elements; idx an element
+// index, a multiple of 8 for ld8 / st8 and of 2 for st2; ep the epoch of an
+// epoch-tagged vector, ignored by the plain forms): ld8 reads 8 elements and
+// reports whether they are the expected write (always, here), st8 / st2
+// write 8 / 2 elements.
 struct PlainIO {
+    static constexpr bool kLL = false;
     template <typename V> static __device__ __forceinline__ V ld(const V *p) { return *p; }
     template <typename V> static __device__ __forceinline__ void st(V *p, V v) { *p = v; }
+    static __device__ __forceinline__ bool ld8(const void *base, int64_t idx, uint32_t, u32x4 &v) {
+        v = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(base) + idx * 2);
+        return true;
+    }
+    static __device__ __forceinline__ void st8(void *base, int64_t idx, uint32_t, u32x4 v) {
+        *reinterpret_cast<u32x4 *>(reinterpret_cast<char *>(base) + idx * 2) = v;
+    }
+    template <typename T> static __device__ __forceinline__ void st2(T *base, int64_t idx, T v0, T v1, uint32_t) {
+        base[idx] = v0;
+        base[idx + 1] = v1;
+    }
 };
 struct CoherentIO {
+    static constexpr bool kLL = false;
     template <typename V> static __device__ __forceinline__ V ld(const V *p) {
         static_assert(sizeof(V) == 16 || sizeof(V) == 8 || sizeof(V) == 4 || sizeof(V) == 2, "size");
         if constexpr (sizeof(V) == 16) {
@@ -157,6 +176,53 @@ struct CoherentIO {
             __hip_atomic_store(reinterpret_cast<uint16_t *>(p), __builtin_bit_cast(uint16_t, v), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         }
+    }
+    static __device__ __forceinline__ bool ld8(const void *base, int64_t idx, uint32_t, u32x4 &v) {
+        v = ld(reinterpret_cast<const u32x4 *>(reinterpret_cast<const char *>(base) + idx * 2));
+        return true;
+    }
+    static __device__ __forceinline__ void st8(void *base, int64_t idx, uint32_t, u32x4 v) {
+        st(reinterpret_cast<u32x4 *>(reinterpret_cast<char *>(base) + idx * 2), v);
+    }
+    template <typename T> static __device__ __forceinline__ void st2(T *base, int64_t idx, T v0, T v1, uint32_t) {
+        st(base + idx, v0);
+        st(base + idx + 1, v1);
+    }
+};
+
+
+// Epoch-tagged vectors for data handed between work-groups of one launch:
+// element pair (2w, 2w + 1) and the epoch of its write share the 8-byte word
+// w (element 2w in the low 16 bits, the epoch in the high 32), written with
+// one agent-scope atomic store.  A reader knows which write it needs (its
+// epoch) and polls the words themselves: no completion counter, and no
+// wait for store acknowledgements before signalling.
+struct LLIO {
+    static constexpr bool kLL = true;
+    static __device__ __forceinline__ uint64_t word(const void *base, int64_t w) {
+        return __hip_atomic_load(reinterpret_cast<const uint64_t *>(base) + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    static __device__ __forceinline__ void put(void *base, int64_t w, uint32_t pair, uint32_t ep) {
+        __hip_atomic_store(reinterpret_cast<uint64_t *>(base) + w, (uint64_t)pair | ((uint64_t)ep << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    static __device__ __forceinline__ bool ld8(const void *base, int64_t idx, uint32_t ep, u32x4 &v) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint64_t w = word(base, idx / 2 + i);
+            v[i] = (uint32_t)w;
+            ok = ok && (uint32_t)(w >> 32) == ep;
+        }
+        return ok;
+    }
+    static __device__ __forceinline__ void st8(void *base, int64_t idx, uint32_t ep, u32x4 v) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) put(base, idx / 2 + i, v[i], ep);
+    }
+    template <typename T> static __device__ __forceinline__ void st2(T *base, int64_t idx, T v0, T v1, uint32_t ep) {
+        const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
+        put(base, idx / 2, pair, ep);
     }
 };
 
@@ -206,6 +272,43 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
     }
+}
+
+constexpr unsigned kLLSpinLimit = 1u << 20;      // polls of one epoch-tagged wait (~1 s)
+
+// True when the wait that owns iteration `it` must stop: its bound is
+// reached (then *err is raised) or another wait already raised *err.
+__device__ __forceinline__ bool ll_give_up(unsigned it, unsigned *err) {
+    if (!err) return it >= kLLSpinLimit;
+    if (it >= kLLSpinLimit) {
+        if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    }
+    return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
+// Wave 0 polls 64 words spread over the first `nwords` words of an
+// epoch-tagged vector until all carry epoch `ep` (bounded: then *err is
+// raised; a raised *err ends the wait at once); the other waves wait at the
+// barrier.  Reading a sample keeps the
+// polling traffic small while the producers are still running.
+__device__ __forceinline__ void ll_poll_sample(const void *base, uint32_t ep, int64_t nwords, unsigned *err) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int64_t w = nwords > 0 ? (int64_t)lane * nwords / 64 : 0;
+        for (unsigned it = 0;; ++it) {
+            const bool ok = nwords <= 0 || (uint32_t)(LLIO::word(base, w) >> 32) == ep;
+            if (__all(ok)) break;
+            // an expired wait elsewhere: stop waiting (the step's results are void)
+            if (err && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+            if (it >= kLLSpinLimit) {
+                if (lane == 0 && err) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
 }
 
 // --------------------------------------------------------------- host side

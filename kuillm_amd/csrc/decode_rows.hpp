@@ -58,6 +58,12 @@ struct DecLinArgs {
     void *kc; int64_t sk1, sk2;        // k cache: head, position strides
     void *vc; int64_t sv1, sv2;
     int64_t cap;
+    // epoch-tagged exchange (the persistent decode step): the epochs of the
+    // input, addend and output writes, and epoch-tagged copies [hkv * hd]
+    // of the new k / v rows (kOutRope, optional)
+    uint32_t ep_in, ep_add, ep_out;
+    void *kfresh, *vfresh;
+    unsigned *err;                     // raised when an epoch-tagged wait expires
 };
 
 // W row of logical row j: identity, or the pair mapping of the paired
@@ -147,8 +153,11 @@ typedef __attribute__((address_space(3))) char lds_bytes;
 // xs (non-null): LDS for the staged input x (K * 2 bytes) in place of the
 // body's own array (the persistent decode step shares one buffer between its
 // job kinds).
+// IO reads the input vectors, OIO writes the outputs (epoch-tagged LLIO
+// inputs are polled until the expected write is there, bounded: on expiry
+// *a_err (if set) is raised and the stale values are used).
 template <typename T, int XK, int KC, int OK, int NWV, typename Wait, typename IO = PlainIO, int RGO = 0, int RGL = 0,
-          bool EXTX = false>
+          bool EXTX = false, typename OIO = IO>
 __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t blk, const Wait &wait,
                                                   lds_bytes *wl = nullptr, lds_bytes *xs = nullptr) {
 #pragma clang fp contract(off)
@@ -159,6 +168,8 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
     // is the same whichever wave computes it).  Host: rpw == RG + RGL.
     constexpr int RG = RGO ? RGO : (KC <= 4 ? 4 : (KC <= 8 ? 2 : 1));
     static_assert(OK == kOutPlain || RG % 2 == 0, "paired epilogues need two rows per wave");
+    static_assert(!OIO::kLL || OK == kOutPlain || (RG % 2 == 0 && RGL % 2 == 0),
+                  "epoch-tagged paired outputs: whole pairs per wave");
     constexpr int XCH = KC * 64 / 256 > 0 ? KC * 64 / 256 : 1;   // x chunks per thread in the input stage (K <= 512 KC)
     typedef T t8 __attribute__((ext_vector_type(8)));
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
@@ -240,17 +251,58 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
         }
     }
     wait();
+    // raw input chunks (and the addend's / SwiGLU up half's), read through IO
+    const bool has_add = XK == kXRmsNorm && a.in_add;
+    u32x4 rin[XCH], radd[XCH];
+    auto load_input = [&]() -> bool {
+        bool ok = true;
+#pragma unroll
+        for (int c = 0; c < XCH; ++c) {
+            const int ch = c * 256 + tid;
+            if (!stage || ch >= nch) continue;
+            ok = IO::ld8(in, (int64_t)ch * 8, a.ep_in, rin[c]) && ok;
+            if (has_add) ok = IO::ld8(a.in_add, (int64_t)ch * 8, a.ep_add, radd[c]) && ok;
+            if constexpr (XK == kXSwiGlu) ok = IO::ld8(in, a.K + (int64_t)ch * 8, a.ep_in, radd[c]) && ok;
+        }
+        return ok;
+    };
+    if constexpr (IO::kLL) {
+        // every thread reads its chunks; while a chunk is not the expected
+        // write it probes only the chunk's first word (8 bytes per poll), then
+        // reads the chunk again; the work-group leaves together
+        auto probe = [&]() -> bool {
+            bool ok = true;
+#pragma unroll
+            for (int c = 0; c < XCH; ++c) {
+                const int ch = c * 256 + tid;
+                if (!stage || ch >= nch) continue;
+                ok = ok && (uint32_t)(LLIO::word(in, (int64_t)ch * 4) >> 32) == a.ep_in;
+                if (has_add) ok = ok && (uint32_t)(LLIO::word(a.in_add, (int64_t)ch * 4) >> 32) == a.ep_add;
+            }
+            return ok;
+        };
+        bool ok = load_input();
+        for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
+            // (the give-up decision is the same in every thread: a uniform
+            // iteration count and one word read by all)
+            if (__syncthreads_or(ll_give_up(it, a.err))) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (!ok && probe()) ok = load_input();
+        }
+    } else {
+        load_input();
+    }
     float h[XCH][8];
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < XCH; ++c) {
         const int ch = c * 256 + tid;
         if (!stage || ch >= nch) continue;
-        unpack8<T>(IO::ld(reinterpret_cast<const u32x4 *>(in + ch * 8)), h[c]);
+        unpack8<T>(rin[c], h[c]);
         if constexpr (XK == kXRmsNorm) {
-            if (a.in_add) {
+            if (has_add) {
                 float o[8];
-                unpack8<T>(IO::ld(reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.in_add) + ch * 8)), o);
+                unpack8<T>(radd[c], o);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) h[c][e] = rnd<T>(h[c][e] + o[e]);
             }
@@ -276,10 +328,10 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
             unpack8<T>(nwv[c], wv);
 #pragma unroll
             for (int e = 0; e < 8; ++e) xo[e] = wv[e] * rnd<T>(h[c][e] * inv);
-            if (store_h) IO::st(reinterpret_cast<u32x4 *>(reinterpret_cast<T *>(a.h_out) + ch * 8), pack8f<T>(h[c]));
+            if (store_h) OIO::st8(a.h_out, (int64_t)ch * 8, a.ep_out, pack8f<T>(h[c]));
         } else if constexpr (XK == kXSwiGlu) {
             float uv[8];
-            unpack8<T>(IO::ld(reinterpret_cast<const u32x4 *>(in + a.K + ch * 8)), uv);
+            unpack8<T>(radd[c], uv);
 #pragma unroll
             for (int e = 0; e < 8; ++e) xo[e] = rnd<T>(h[c][e] / (1.f + expf(-h[c][e]))) * uv[e];
         } else {
@@ -331,15 +383,40 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
         totl = multi_row_sum<RGL>(accl, lane);
     }
     if constexpr (OK == kOutPlain) {
-        auto put = [&](int64_t r, float acc) {
-            if (r < r1) {
-                if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
-                IO::st(reinterpret_cast<T *>(a.out) + r, from_f32<T>(acc));
-            }
+        auto val = [&](int64_t r, float acc) {
+            if (a.bias) acc += to_f32(reinterpret_cast<const T *>(a.bias)[r]);
+            return from_f32<T>(acc);
         };
-        if (lane % (64 / RG) == 0) put(r0 + lane / (64 / RG), tot);
-        if constexpr (RGL > 0)
-            if (lane % (64 / RGL) == 0) put(r0 + RG + lane / (64 / RGL), totl);
+        if constexpr (OIO::kLL) {
+            // the work-group's rows (consecutive from blk * NWV * rpw) meet in
+            // LDS, then go out as row pairs, one epoch-tagged word each
+            constexpr int RW = RG + RGL, RJ = NWV * RW;
+            static_assert(RJ % 2 == 0, "whole row pairs per work-group");
+            __shared__ __attribute__((aligned(16))) T s_rows[RJ];
+            const int64_t rj0 = blk * RJ;
+            if (lane % (64 / RG) == 0) {
+                const int64_t r = r0 + lane / (64 / RG);
+                if (r < r1) s_rows[r - rj0] = val(r, tot);
+            }
+            if constexpr (RGL > 0) {
+                if (lane % (64 / RGL) == 0) {
+                    const int64_t r = r0 + RG + lane / (64 / RGL);
+                    if (r < r1) s_rows[r - rj0] = val(r, totl);
+                }
+            }
+            __syncthreads();
+            const int64_t nr = min((int64_t)RJ, a.N - rj0);
+            if (2 * tid < nr)
+                OIO::st2(reinterpret_cast<T *>(a.out), rj0 + 2 * tid, s_rows[2 * tid],
+                         2 * tid + 1 < nr ? s_rows[2 * tid + 1] : from_f32<T>(0.f), a.ep_out);
+        } else {
+            auto put = [&](int64_t r, float acc) {
+                if (r < r1) OIO::st(reinterpret_cast<T *>(a.out) + r, val(r, acc));
+            };
+            if (lane % (64 / RG) == 0) put(r0 + lane / (64 / RG), tot);
+            if constexpr (RGL > 0)
+                if (lane % (64 / RGL) == 0) put(r0 + RG + lane / (64 / RGL), totl);
+        }
     } else {
         const float nxt = __shfl_down(tot, 64 / RG, 64);
         const float nxtl = RGL >= 2 ? __shfl_down(totl, 64 / (RGL >= 2 ? RGL : 1), 64) : 0.f;
@@ -380,17 +457,24 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
             if (lane % (128 / RGL) == 0) finish_pair(RG + 2 * (lane / (128 / RGL)), totl, nxtl);
         __syncthreads();
         // destination of pair p's half e: SwiGLU out[p]; rotary q -> out,
-        // k -> k cache, v -> v cache at position pos (element i, or i + hd/2)
-        auto dst_of = [&](int64_t p, int e) -> T * {
+        // k -> k cache, v -> v cache at position pos (element i, or i + hd/2),
+        // plus the epoch-tagged fresh k / v rows when given.  kind: 0 out,
+        // 1 k, 2 v, -1 nothing; idx: element index in out, or within the head.
+        auto dst_of = [&](int64_t p, int e, int &kind, int64_t &head_kv) -> int64_t {
             if constexpr (OK == kOutSwiGlu) {
-                return reinterpret_cast<T *>(a.out) + p;
+                kind = 0;
+                return p;
             } else {
                 const int64_t half = a.pair_off, head = pair_div(a, p), i = p - head * half + e * half;
-                if (head < a.hq) return reinterpret_cast<T *>(a.out) + head * a.hd + i;
-                if (!store_kv) return nullptr;
-                if (head < a.hq + a.hkv) return reinterpret_cast<T *>(a.kc) + (head - a.hq) * a.sk1 + pos * a.sk2 + i;
-                return reinterpret_cast<T *>(a.vc) + (head - a.hq - a.hkv) * a.sv1 + pos * a.sv2 + i;
+                if (head < a.hq) { kind = 0; return head * a.hd + i; }
+                kind = head < a.hq + a.hkv ? 1 : 2;
+                head_kv = kind == 1 ? head - a.hq : head - a.hq - a.hkv;
+                return i;
             }
+        };
+        T *const kc = reinterpret_cast<T *>(a.kc), *const vc = reinterpret_cast<T *>(a.vc);
+        auto cache_idx = [&](int kind, int64_t hkv, int64_t i) {
+            return kind == 1 ? hkv * a.sk1 + pos * a.sk2 + i : hkv * a.sv1 + pos * a.sv2 + i;
         };
         constexpr int NE = OK == kOutSwiGlu ? 1 : 2;
         // a run of whole 16-byte pieces goes out as NV vector stores
@@ -398,15 +482,40 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
         constexpr int NV = VEC ? PG * (int)sizeof(T) / 16 : 1;
         if (tid < NE * NV && np > 0) {
             const int e = tid / NV, v = tid % NV;
-            T *d0 = dst_of(pg0, e);
+            int kind0 = -1;
+            int64_t hkv0 = 0;
+            const int64_t i0 = dst_of(pg0, e, kind0, hkv0);
             // one run when all pairs are present and share the first pair's head
             const bool one_run = np == PG && (OK == kOutSwiGlu || (pg0 - pair_div(a, pg0) * a.pair_off) + PG <= a.pair_off);
-            if (VEC && one_run && d0 && aligned16(d0)) {
-                IO::st(reinterpret_cast<u32x4 *>(d0) + v, reinterpret_cast<const u32x4 *>(s_o[e])[v]);
+            const u32x4 piece = reinterpret_cast<const u32x4 *>(s_o[e])[v];
+            if (VEC && one_run && (i0 & 7) == 0 && (kind0 == 0 || (store_kv && (cache_idx(kind0, hkv0, i0) & 7) == 0))) {
+                if (kind0 == 0) {
+                    OIO::st8(a.out, i0 + v * 8, a.ep_out, piece);
+                } else {
+                    PlainIO::st8(kind0 == 1 ? a.kc : a.vc, cache_idx(kind0, hkv0, i0) + v * 8, 0, piece);
+                    void *fr = kind0 == 1 ? a.kfresh : a.vfresh;
+                    if (fr) OIO::st8(fr, hkv0 * a.hd + i0 + v * 8, a.ep_out, piece);
+                }
             } else if (v == 0) {
-                for (int k = 0; k < np; ++k) {
-                    T *d = dst_of(pg0 + k, e);
-                    if (d) IO::st(d, s_o[e][k]);
+                // element by element (pairs for epoch-tagged vectors: the run
+                // starts at an even element and holds whole pairs)
+                for (int k = 0; k < np; k += (OIO::kLL ? 2 : 1)) {
+                    int kind = -1;
+                    int64_t hkv = 0;
+                    const int64_t i = dst_of(pg0 + k, e, kind, hkv);
+                    const T x0 = s_o[e][k], x1 = OIO::kLL && k + 1 < np ? s_o[e][k + 1] : from_f32<T>(0.f);
+                    if (kind == 0) {
+                        if constexpr (OIO::kLL) OIO::st2(reinterpret_cast<T *>(a.out), i, x0, x1, a.ep_out);
+                        else OIO::st(reinterpret_cast<T *>(a.out) + i, x0);
+                    } else if (kind > 0 && store_kv) {
+                        T *c = kind == 1 ? kc : vc;
+                        c[cache_idx(kind, hkv, i)] = x0;
+                        if constexpr (OIO::kLL) {
+                            if (k + 1 < np) c[cache_idx(kind, hkv, i) + 1] = x1;
+                            void *fr = kind == 1 ? a.kfresh : a.vfresh;
+                            if (fr) OIO::st2(reinterpret_cast<T *>(fr), hkv * a.hd + i, x0, x1, a.ep_out);
+                        }
+                    }
                 }
             }
         }

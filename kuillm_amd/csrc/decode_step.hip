@@ -13,32 +13,31 @@
 //   then        LM-head row blocks | the softmax + top-1 row
 //
 // Work-group w takes jobs w, w + G, w + 2G, ... (G = grid size).  A job of
-// phase p needs every job of phase p - 1 (the next projection's input is the
-// whole previous vector: RMSNorm needs the full row); it issues its weight
-// loads first, then waits on the phase's completion counters, so the weight
-// stream of later phases runs while earlier phases finish.  Jobs only wait on
-// jobs with lower indices, so with all G work-groups resident (one per CU,
-// nothing else running) the lowest unfinished job can always run: the step
-// cannot deadlock.  Every wait is bounded; on expiry the step stops waiting,
-// sets the error word and runs to the end (results undefined, no hang).
+// phase p needs the whole output of phase p - 1 (the next projection's input
+// is the whole previous vector: RMSNorm needs the full row); it issues its
+// weight loads first (and attention its older cache rows), then waits for its
+// input, so the weight stream of later phases runs while earlier phases
+// finish.  Jobs only wait on jobs with lower indices, so with all G
+// work-groups resident (one per CU, nothing else running) the lowest
+// unfinished job can always run: the step cannot deadlock.  Every wait is
+// bounded; on expiry the step stops waiting, sets the error word and runs to
+// the end (results undefined, no hang).
 //
-// Ordering: every activation a job hands to another job (projection
-// outputs, the new K / V rows, attention rows, logits) is written with
-// agent-scope relaxed atomic stores (sc1: written through the per-XCD L2)
-// and read with agent-scope relaxed atomic loads (sc1: served past the
-// non-coherent caches).  A finished job's threads wait for their stores'
-// acknowledgements (s_waitcnt 0) before the work-group barrier that
-// precedes one relaxed agent-scope add on a completion counter; a waiting
-// work-group polls the counters with relaxed agent-scope loads and its
-// barrier precedes its input reads.  This relies on the gfx942 / gfx950
-// rule that an acknowledged sc1 store is visible at the agent's coherence
-// point before a later atomic of the same agent (the rule the split-K
-// merges of the decode GEMM and decode attention use); release / acquire
-// fences would write back / invalidate the whole L2 per job, which costs
-// more than the step itself (measured 2.5 ms against 0.9 ms per token).
-// Weights and the older cache rows are read with ordinary loads: nothing
-// in the launch writes them.
-
+// Hand-off: the vectors that pass between jobs (residual, q, attention rows,
+// o, SwiGLU activations, down, the new k / v rows) are epoch-tagged: each
+// 8-byte word holds two elements and the epoch of its write (step counter x
+// layer), written with one agent-scope atomic store (sc1: through the per-XCD
+// L2).  A consumer polls a 64-word sample of its input, then reads every word
+// with agent-scope atomic loads and retries until all carry the epoch it
+// expects.  So a hand-off costs no store acknowledgement wait, no counter
+// and no separate poll: the reader detects the data itself.  Only the LM
+// head's logits (read by the sampling job) go through completion counters
+// (stores acknowledged with s_waitcnt 0, barrier, one relaxed agent-scope
+// add; the rule the split-K merges use).  The KV cache rows are written with
+// ordinary stores (read by later launches; this launch's attention takes the
+// new row from its epoch-tagged copy), and weights and older cache rows are
+// read with ordinary loads: nothing in the launch writes them.
+//
 // The job bodies are the library's own (decode_rows_block, fa_decode_block,
 // softmax_top1_row), with the launch shapes and summation orders of the
 // per-op kernels, so the step is bitwise the per-op sequence.
@@ -52,7 +51,7 @@ constexpr int kStepWaves = 8;
 constexpr int kStepThreads = kStepWaves * 64;
 constexpr int kKinds = 7;                 // qkv, attention, o, gate|up, down, LM head, sampling
 constexpr int kLayerKinds = 5;
-constexpr int kSubCounters = 8;           // completion counters per phase (spread contention)
+constexpr int kSubCounters = 8;           // completion counters of the LM-head phase (spread contention)
 constexpr int kCounterStride = 32;        // uint32 apart: one 128-byte line each
 constexpr unsigned kSpinLimit = 1u << 20; // polls per wait (~1 s)
 
@@ -70,38 +69,35 @@ struct StepArgs {
     int64_t *history;
     int64_t hist_len;
     float *prob;
-    void *h0, *h1, *q, *att, *o, *act, *down, *logits;
+    void *h0, *h1, *q, *att, *o, *act, *down, *kf, *vf;   // epoch-tagged (scratch)
+    void *logits;
     unsigned *sync;
     int njobs[kKinds];
     int per_layer, total;
 };
 
-__device__ __forceinline__ int n_phases(const StepArgs &a) { return kLayerKinds * a.layers + 2; }
+// sync: kSubCounters counters of the LM-head phase, the error word, the step
+// epoch (one 128-byte line each)
+__device__ __forceinline__ unsigned *counter_of(const StepArgs &a, int k) { return a.sync + k * kCounterStride; }
+__device__ __forceinline__ unsigned *error_word(const StepArgs &a) { return a.sync + kSubCounters * kCounterStride; }
+__device__ __forceinline__ unsigned *epoch_word(const StepArgs &a) { return a.sync + (kSubCounters + 1) * kCounterStride; }
 
-__device__ __forceinline__ unsigned *counter_of(const StepArgs &a, int phase, int k) {
-    return a.sync + ((int64_t)phase * kSubCounters + k) * kCounterStride;
-}
-__device__ __forceinline__ unsigned *error_word(const StepArgs &a) {
-    return a.sync + (int64_t)n_phases(a) * kSubCounters * kCounterStride;
-}
-
-__device__ __forceinline__ int kind_of_phase(const StepArgs &a, int phase) {
-    const int lp = kLayerKinds * a.layers;
-    return phase < lp ? phase % kLayerKinds : kLayerKinds + (phase - lp);
+// Epoch of the vectors written by layer l (l = layers: none) in this step.
+__device__ __forceinline__ uint32_t epoch_of(const StepArgs &a, uint32_t step, int l) {
+    return step * (uint32_t)(a.layers + 1) + (uint32_t)l + 1u;
 }
 
-// Waits until every job of `phase` has signalled (phase < 0: nothing to wait
-// for).  Wave 0 polls the phase's counters (lanes 0..7) and the error word
-// (lane 8); all threads leave through the barrier.
-__device__ __forceinline__ void step_wait(const StepArgs &a, int phase) {
-    if (phase < 0) return;
+// Waits until every LM-head job has signalled.  Wave 0 polls the counters
+// (lanes 0..7) and the error word (lane 8); all threads leave through the
+// barrier.
+__device__ __forceinline__ void wait_head(const StepArgs &a) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        const unsigned need = (unsigned)a.njobs[kind_of_phase(a, phase)];
+        const unsigned need = (unsigned)a.njobs[5];
         for (unsigned it = 0;; ++it) {
             unsigned v = 0, err = 0;
             if (lane < kSubCounters)
-                v = __hip_atomic_load(counter_of(a, phase, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v = __hip_atomic_load(counter_of(a, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             else if (lane == kSubCounters)
                 err = __hip_atomic_load(error_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             v += __shfl_xor(v, 1, 64);
@@ -120,21 +116,15 @@ __device__ __forceinline__ void step_wait(const StepArgs &a, int phase) {
     __syncthreads();
 }
 
-// Publishes the calling work-group's job `idx` of `phase`.
-__device__ __forceinline__ void step_signal(const StepArgs &a, int phase, int idx) {
+// Publishes the calling work-group's LM-head job `idx`.
+__device__ __forceinline__ void signal_head(const StepArgs &a, int idx) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(counter_of(a, phase, idx % kSubCounters), 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(counter_of(a, idx % kSubCounters), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-struct StepWait {
-    const StepArgs *a;
-    int phase;
-    __device__ __forceinline__ void operator()() const { step_wait(*a, phase); }
-};
 
 // Rows per wave of a projection job: 32 registers of W chunks (128 VGPRs),
 // so a work-group holds 128-256 KB of weights in flight while it waits; the
@@ -149,17 +139,22 @@ constexpr int kLdsRowBytes = kStepWaves * 16 * 1024;
 constexpr int kLdsXBytes = kDecodeMaxK * 2;         // the staged input x
 
 // The projection of layer `l` of one kind, as the per-op entry points set it up.
-__device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int l, int rpw) {
+__device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int l, int rpw, uint32_t step) {
     DecLinArgs p{};
     p.eps = a.eps;
     p.rpw = rpw;
     p.pair_shift = -1;
+    p.err = error_word(a);
     if (kind == 5) {                      // LM head: RMSNorm(h0 + down) input
         p.N = a.vocab; p.K = a.d;
         p.in = a.h0; p.in_add = a.down; p.norm_w = a.norm;
+        p.ep_in = p.ep_add = epoch_of(a, step, a.layers - 1);
         p.W = a.head; p.ldw = a.d; p.out = a.logits;
         return p;
     }
+    // inputs from this layer's earlier phases, or (qkv) the previous layer's
+    p.ep_in = p.ep_add = epoch_of(a, step, kind == 0 ? l - 1 : l);
+    p.ep_out = epoch_of(a, step, l);
     const kuiops_step_layer &L = a.layer[l];
     switch (kind) {
         case 0:                           // qkv: RMSNorm(h0 + down) (layer 0: the embedding row), rotary + KV
@@ -176,6 +171,7 @@ __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int
             p.kc = L.k_cache; p.sk1 = a.sk1; p.sk2 = a.sk2;
             p.vc = L.v_cache; p.sv1 = a.sv1; p.sv2 = a.sv2;
             p.cap = a.cap;
+            p.kfresh = a.kf; p.vfresh = a.vf;
             break;
         case 2:                           // o: plain input (the attention rows)
             p.N = a.d; p.K = a.hq * a.hd;
@@ -197,21 +193,23 @@ __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int
 
 // The job kinds, each its own function: inlined into one loop, the bodies'
 // register demands add up (spills); as calls each gets its own allocation.
-template <typename T, int XK, int KC, int OK, int RGL = 0>
-__device__ __attribute__((noinline)) void step_proj(const StepArgs &a, int kind, int l, int idx, int phase,
+template <typename T, int XK, int KC, int OK, int RGL, typename IO, typename OIO>
+__device__ __attribute__((noinline)) void step_proj(const StepArgs &a, int kind, int l, int idx, uint32_t step,
                                                     lds_bytes *wl) {
-    decode_rows_block<T, XK, KC, OK, kStepWaves, StepWait, CoherentIO, rows_per_wave(KC), RGL, true>(
-        proj_args(a, kind, l, rows_per_wave(KC) + RGL), idx, StepWait{&a, phase - 1}, wl, wl + kLdsRowBytes);
+    decode_rows_block<T, XK, KC, OK, kStepWaves, NoWait, IO, rows_per_wave(KC), RGL, true, OIO>(
+        proj_args(a, kind, l, rows_per_wave(KC) + RGL, step), idx, NoWait{}, wl, wl + kLdsRowBytes);
 }
 
 // attention row `idx` (query head) of layer l, as the per-op row-wide launch
 // runs it: one work-group per query row, every key in one pass.  The cache
 // rows before this token's position do not depend on the qkv phase: their
-// loads are issued before the wait, and the row at the position (written by
-// the qkv phase) is read again after it.
+// loads are issued before the query is awaited, and the row at the position
+// comes from the qkv phase's epoch-tagged copy.
 template <typename T, int HD>
-__device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int l, int idx, int phase) {
-    const int64_t fresh = *a.pos;
+__device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int l, int idx, uint32_t step) {
+    // (the qkv phase writes the new row only when it is inside the cache)
+    const int64_t p = *a.pos;
+    const int64_t fresh = p >= 0 && p < a.cap ? p : -1;
     const kuiops_step_layer &L = a.layer[l];
     AttnArgs at{};
     at.n = 1; at.hq = a.hq; at.hkv = a.hkv; at.l = 1; at.s = a.cap;
@@ -225,20 +223,24 @@ __device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int 
     at.splits = 1; at.chunk = a.cap;
     at.rows_per_group = 1; at.row_groups = (int)(a.hq / a.hkv);
     at.kv_len = a.kv_len;
-    fa_decode_block<T, HD, 1, kStepWaves, 12, CoherentIO, StepWait, true>(at, 0, idx, 0, StepWait{&a, phase - 1}, fresh);
+    at.ep_q = at.ep_o = epoch_of(a, step, l);
+    at.kfresh = a.kf; at.vfresh = a.vf;
+    at.err = error_word(a);
+    fa_decode_block<T, HD, 1, kStepWaves, 12, LLIO, NoWaitAttn, true>(at, 0, idx, 0, NoWaitAttn{}, fresh);
 }
 
 // softmax + top-1 of the logits and the decode-state advance; every other
 // job has finished by then (each phase waited on the one before it), so the
-// counters are left zero for the next step
+// counters are left zero and the step epoch advances for the next step
 template <typename T>
-__device__ __attribute__((noinline)) void step_sample(const StepArgs &a, int phase) {
-    step_wait(a, phase - 1);
-    softmax_top1_row<T, kStepThreads, CoherentIO>(a.vocab, reinterpret_cast<const T *>(a.logits), a.prob, a.tok, a.pos,
-                                      a.kv_len, a.history, a.hist_len);
+__device__ __attribute__((noinline)) void step_sample(const StepArgs &a) {
+    wait_head(a);
+    softmax_top1_row<T, kStepThreads, CoherentIO>(a.vocab, reinterpret_cast<const T *>(a.logits), a.prob, a.tok,
+                                                  a.pos, a.kv_len, a.history, a.hist_len);
     __syncthreads();
-    for (int i = threadIdx.x; i < n_phases(a) * kSubCounters; i += kStepThreads)
-        __hip_atomic_store(a.sync + (int64_t)i * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < kSubCounters)
+        __hip_atomic_store(counter_of(a, threadIdx.x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) *epoch_word(a) += 1u;
 }
 
 template <typename T, int HD, int KCD, int KCF>
@@ -247,32 +249,39 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
     __shared__ __attribute__((aligned(1024))) char s_wl[kLdsRowBytes + kLdsXBytes];
     lds_bytes *wl = (lds_bytes *)s_wl;
     const int G = gridDim.x;
-    const int lp = kLayerKinds * a.layers;
+    // the step counter: advanced only by the sampling job, which runs after
+    // every other job has finished (and so has read it)
+    const uint32_t step = *epoch_word(a);
     for (int j = blockIdx.x; j < a.total; j += G) {
-        int l, kind, idx, phase;
+        int l, kind, idx;
         if (j < a.layers * a.per_layer) {
             l = j / a.per_layer;
             idx = j - l * a.per_layer;
             kind = 0;
             while (idx >= a.njobs[kind]) idx -= a.njobs[kind++];
-            phase = l * kLayerKinds + kind;
         } else {
             l = a.layers;
             idx = j - a.layers * a.per_layer;
             kind = idx < a.njobs[5] ? 5 : 6;
             if (kind == 6) idx -= a.njobs[5];
-            phase = lp + (kind - kLayerKinds);
         }
         switch (kind) {
-            case 0: step_proj<T, kXRmsNorm, KCD, kOutRope>(a, 0, l, idx, phase, wl); break;
-            case 1: step_attention<T, HD>(a, l, idx, phase); break;
-            case 2: step_proj<T, kXPlain, KCD, kOutPlain>(a, 2, l, idx, phase, wl); break;
-            case 3: step_proj<T, kXRmsNorm, KCD, kOutSwiGlu, RLD>(a, 3, l, idx, phase, wl); break;
-            case 4: step_proj<T, kXPlain, KCF, kOutPlain, RLF>(a, 4, l, idx, phase, wl); break;
-            case 5: step_proj<T, kXRmsNorm, KCD, kOutPlain, RLD>(a, 5, l, idx, phase, wl); break;
-            default: step_sample<T>(a, phase); continue;
+            case 0:
+                if (l == 0) step_proj<T, kXRmsNorm, KCD, kOutRope, 0, PlainIO, LLIO>(a, 0, l, idx, step, wl);
+                else step_proj<T, kXRmsNorm, KCD, kOutRope, 0, LLIO, LLIO>(a, 0, l, idx, step, wl);
+                break;
+            case 1: step_attention<T, HD>(a, l, idx, step); break;
+            case 2: step_proj<T, kXPlain, KCD, kOutPlain, 0, LLIO, LLIO>(a, 2, l, idx, step, wl); break;
+            case 3: step_proj<T, kXRmsNorm, KCD, kOutSwiGlu, RLD, LLIO, LLIO>(a, 3, l, idx, step, wl); break;
+            case 4: step_proj<T, kXPlain, KCF, kOutPlain, RLF, LLIO, LLIO>(a, 4, l, idx, step, wl); break;
+            case 5:
+                step_proj<T, kXRmsNorm, KCD, kOutPlain, RLD, LLIO, CoherentIO>(a, 5, l, idx, step, wl);
+                signal_head(a, idx);
+                break;
+            default: step_sample<T>(a); break;
         }
-        step_signal(a, phase, idx);
+        // the LDS buffers are free for the next job
+        __syncthreads();
     }
 }
 
@@ -313,9 +322,28 @@ static void launch_step(const StepArgs &a, int kcd, int kcf, dim3 grid, hipStrea
 
 using namespace kuiops;
 
+// Epoch-tagged scratch vectors, in elements: h0, h1 [d], q, att [hq*hd],
+// o [d], act [ffn], down [d], k / v copies [hkv*hd]; two elements per 8-byte
+// word, each vector 256-byte aligned.
+static size_t step_scratch_layout(int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd, size_t off[9]) {
+    const int64_t n[9] = {d, d, hq * hd, hq * hd, d, ffn, d, hkv * hd, hkv * hd};
+    size_t o = 0;
+    for (int i = 0; i < 9; ++i) {
+        off[i] = o;
+        o += (size_t)cdiv(n[i] / 2 * 8, 256) * 256;
+    }
+    return o;
+}
+
 extern "C" size_t kuiops_decode_step_sync_bytes(int64_t n_layers) {
-    if (n_layers < 0) return 0;
-    return (size_t)((kLayerKinds * n_layers + 2) * kSubCounters + 1) * kCounterStride * sizeof(unsigned);
+    (void)n_layers;
+    return (size_t)(kSubCounters + 2) * kCounterStride * sizeof(unsigned);
+}
+
+extern "C" size_t kuiops_decode_step_scratch_bytes(int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd) {
+    if (d <= 0 || ffn <= 0 || hq <= 0 || hkv <= 0 || hd <= 0) return 0;
+    size_t off[9];
+    return step_scratch_layout(d, ffn, hq, hkv, hd, off);
 }
 
 extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd,
@@ -323,14 +351,14 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
                                   const kuiops_step_layer *layers, int64_t sk_head, int64_t sk_pos,
                                   int64_t sv_head, int64_t sv_pos, const void *embed, const void *final_norm,
                                   const void *lm_head, const float *inv_freq, int64_t *tok, int32_t *pos,
-                                  int32_t *kv_len, int64_t *history, int64_t hist_len, float *prob, void *h0,
-                                  void *h1, void *q, void *att, void *o, void *act, void *down, void *logits,
-                                  void *sync, size_t sync_bytes, void *stream) {
+                                  int32_t *kv_len, int64_t *history, int64_t hist_len, float *prob, void *logits,
+                                  void *scratch, size_t scratch_bytes, void *sync, size_t sync_bytes,
+                                  void *stream) {
     if (n_layers <= 0 || d <= 0 || ffn <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || vocab <= 0 || cache_cap <= 0)
         return KUIOPS_E_INVALID;
     if (hq % hkv || hd % 2) return KUIOPS_E_INVALID;
-    if (!layers || !embed || !final_norm || !lm_head || !inv_freq || !tok || !pos || !kv_len || !h0 || !h1 ||
-        !q || !att || !o || !act || !down || !logits || !sync)
+    if (!layers || !embed || !final_norm || !lm_head || !inv_freq || !tok || !pos || !kv_len || !logits ||
+        !scratch || !sync)
         return KUIOPS_E_INVALID;
     if (history && hist_len <= 0) return KUIOPS_E_INVALID;
     if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
@@ -339,10 +367,10 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
     if (kcd == 0 || kcd > 8 || kcf == 0) return KUIOPS_E_UNSUPPORTED;   // paired epilogues: d <= 4096
     if (vocab > (int64_t)kSmThreads * kSmCache || vocab > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     if (n_layers > 1024 || cache_cap > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    size_t off[9];
+    if (scratch_bytes < step_scratch_layout(d, ffn, hq, hkv, hd, off) || !aligned16(scratch)) return KUIOPS_E_WORKSPACE;
     if (sync_bytes < kuiops_decode_step_sync_bytes(n_layers) || !aligned16(sync)) return KUIOPS_E_WORKSPACE;
-    for (const void *p : {embed, final_norm, lm_head, (const void *)h0, (const void *)h1, (const void *)q,
-                          (const void *)att, (const void *)o, (const void *)act, (const void *)down,
-                          (const void *)logits})
+    for (const void *p : {embed, final_norm, lm_head, (const void *)logits})
         if (!aligned16(p)) return KUIOPS_E_UNSUPPORTED;
     if (sk_pos % 8 || sv_pos % 8 || sk_head % 8 || sv_head % 8) return KUIOPS_E_UNSUPPORTED;
 
@@ -359,7 +387,10 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
     a.layer = layers;
     a.embed = embed; a.norm = final_norm; a.head = lm_head; a.inv_freq = inv_freq;
     a.tok = tok; a.pos = pos; a.kv_len = kv_len; a.history = history; a.hist_len = hist_len; a.prob = prob;
-    a.h0 = h0; a.h1 = h1; a.q = q; a.att = att; a.o = o; a.act = act; a.down = down; a.logits = logits;
+    char *sc = reinterpret_cast<char *>(scratch);
+    void **vec[9] = {&a.h0, &a.h1, &a.q, &a.att, &a.o, &a.act, &a.down, &a.kf, &a.vf};
+    for (int i = 0; i < 9; ++i) *vec[i] = sc + off[i];
+    a.logits = logits;
     a.sync = reinterpret_cast<unsigned *>(sync);
     const int64_t rows_d = (int64_t)kStepWaves * rows_per_wave(kcd);
     const int64_t rows_dl = (int64_t)kStepWaves * (rows_per_wave(kcd) + lds_rows_per_wave(kcd));
@@ -383,8 +414,9 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
 }
 
 extern "C" int kuiops_decode_step_error(void *sync, int64_t n_layers, void *stream) {
-    if (!sync || n_layers <= 0) return KUIOPS_E_INVALID;
-    unsigned *w = reinterpret_cast<unsigned *>(sync) + (kLayerKinds * n_layers + 2) * kSubCounters * kCounterStride;
+    (void)n_layers;
+    if (!sync) return KUIOPS_E_INVALID;
+    unsigned *w = reinterpret_cast<unsigned *>(sync) + kSubCounters * kCounterStride;
     unsigned v = 0;
     hipStream_t st = as_stream(stream);
     if (hipMemcpyAsync(&v, w, sizeof(v), hipMemcpyDeviceToHost, st) != hipSuccess) return KUIOPS_E_HIP;

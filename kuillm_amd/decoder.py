@@ -159,6 +159,8 @@ class LlamaDecoder:
                     for i, L in enumerate(self.layers)]
             self.layer_table = torch.tensor(ptrs, dtype=torch.int64, device=dev)
             self.step_sync = torch.zeros(ops.decode_step_sync_bytes(s.layers), dtype=torch.uint8, device=dev)
+            self.step_scratch = torch.zeros(ops.decode_step_scratch_bytes(s.d, s.ffn, s.hq, s.hkv, s.hd),
+                                            dtype=torch.uint8, device=dev)
         # token chosen at each position (written by the step itself, so a
         # replayed step needs no copy out)
         self.history = torch.zeros(n, self.cap + 1, dtype=torch.int64, device=dev)
@@ -250,8 +252,7 @@ class LlamaDecoder:
             ops.decode_step(self.layer_table, s.layers, s.d, s.ffn, s.hq, s.hkv, s.hd, s.vocab, s.eps,
                             self.kcache[0, 0], self.vcache[0, 0], self.embed, self.norm, self.head, self.inv_freq,
                             self.tok, self.pos, self.kv_len, self.history[0], self.top_v.view(1),
-                            (self.h_buf[0], self.h_buf[1], self.q1, self.att1, self.o1, self.a1, self.down1,
-                             self.logits1), self.step_sync)
+                            self.logits1, self.step_scratch, self.step_sync)
             return self.logits1.view(1, -1)
         hb = self.h_buf
         cur = 0

@@ -829,18 +829,24 @@ def decode_qkv_rope(x, W, hq, hkv, hd, inv_freq, pos, q_out, k_cache, v_cache, x
 
 
 def decode_step_sync_bytes(n_layers: int) -> int:
-    """Bytes of the completion-counter buffer kuiops_decode_step needs."""
+    """Bytes of the counter / step-counter buffer kuiops_decode_step needs."""
     return int(_lib_handle().kuiops_decode_step_sync_bytes(n_layers))
 
 
+def decode_step_scratch_bytes(d: int, ffn: int, hq: int, hkv: int, hd: int) -> int:
+    """Bytes of the epoch-tagged vector buffer kuiops_decode_step needs."""
+    return int(_lib_handle().kuiops_decode_step_scratch_bytes(d, ffn, hq, hkv, hd))
+
+
 def decode_step(layer_table, n_layers, d, ffn, hq, hkv, hd, vocab, eps, k_cache, v_cache, embed, final_norm,
-                lm_head, inv_freq, tok, pos, kv_len, history, prob, bufs, sync):
+                lm_head, inv_freq, tok, pos, kv_len, history, prob, logits, scratch, sync):
     """One whole batch-1 greedy decode step in one persistent launch (see
     kuiops_decode_step).  ``layer_table`` is a device int64 [n_layers, 8]
     tensor of per-layer pointers (wqkv, wo, wgu, wd, ln1, ln2, k cache,
     v cache); k_cache / v_cache give the cache strides ([hkv, cap, hd] views
-    of layer 0); ``bufs`` = (h0, h1, q, att, o, act, down, logits); ``sync``
-    a zeroed uint8 buffer of decode_step_sync_bytes(n_layers)."""
+    of layer 0); ``logits`` [vocab] receives the LM head's output;
+    ``scratch`` / ``sync`` are zeroed uint8 buffers of
+    decode_step_scratch_bytes / decode_step_sync_bytes, kept across steps."""
     if layer_table.dtype != torch.int64 or tuple(layer_table.shape) != (n_layers, 8) or not layer_table.is_contiguous():
         raise _lib.KuiopsError("decode_step", _lib.E_INVALID)
     if tok.dtype != torch.int64 or pos.dtype != torch.int32 or kv_len.dtype != torch.int32:
@@ -849,21 +855,20 @@ def decode_step(layer_table, n_layers, d, ffn, hq, hkv, hd, vocab, eps, k_cache,
         raise _lib.KuiopsError("decode_step", _lib.E_INVALID)
     if prob is not None and prob.dtype != torch.float32:
         raise _lib.KuiopsError("decode_step", _lib.E_INVALID)
-    for t in bufs + (embed, final_norm, lm_head):
+    for t in (logits, embed, final_norm, lm_head):
         if not t.is_contiguous() or t.dtype != embed.dtype:
             raise _lib.KuiopsError("decode_step", _lib.E_INVALID)
     for c in (k_cache, v_cache):
         if c.dim() != 3 or c.shape[0] != hkv or c.shape[2] != hd or c.stride(-1) != 1 or c.dtype != embed.dtype:
             raise _lib.KuiopsError("decode_step", _lib.E_INVALID)
     lib = _lib_handle()
-    h0, h1, q, att, o, act, down, logits = bufs
     _lib.check("kuiops_decode_step", lib.kuiops_decode_step(
         n_layers, d, ffn, hq, hkv, hd, vocab, k_cache.shape[1], _dt(embed.dtype), float(eps), layer_table.data_ptr(),
         k_cache.stride(0), k_cache.stride(1), v_cache.stride(0), v_cache.stride(1), embed.data_ptr(),
         final_norm.data_ptr(), lm_head.data_ptr(), inv_freq.data_ptr(), tok.data_ptr(), pos.data_ptr(),
         kv_len.data_ptr(), _ptr(history), history.numel() if history is not None else 0, _ptr(prob),
-        h0.data_ptr(), h1.data_ptr(), q.data_ptr(), att.data_ptr(), o.data_ptr(), act.data_ptr(), down.data_ptr(),
-        logits.data_ptr(), sync.data_ptr(), sync.numel(), _stream(embed.device)))
+        logits.data_ptr(), scratch.data_ptr(), scratch.numel(), sync.data_ptr(), sync.numel(),
+        _stream(embed.device)))
     return logits
 
 

@@ -591,20 +591,22 @@ def test_persistent_step_bitwise_per_op(cuda, shape, cap, prompt_len, steps):
     """The one-launch decode step (kuiops_decode_step) against the per-op
     fused step from the same state, step by step: logits, token, history,
     position / key count, KV caches and the winner's probability all
-    bit-identical; the completion counters are left zero and no wait
-    expired."""
+    bit-identical; the completion counters are left zero, no wait expired
+    and the step counter advanced."""
     print(f"persistent step: {shape} cap {cap}", flush=True)
     dec = LlamaDecoder(LlamaShape(**shape), random_llama(shape, cuda, 11), capacity=cap)
     assert dec.persistent
     prompt = torch.randint(0, shape["vocab"], (1, prompt_len), generator=torch.Generator().manual_seed(12))
     dec.prefill(prompt)
     for step in range(steps):
+        epoch = int(dec.step_sync[9 * 128:9 * 128 + 4].view(torch.int32)[0])
         before = _step_state(dec)
         lp = dec._decode_step_fused().clone()
         torch.cuda.synchronize()
         after = _step_state(dec)
         assert not ops.decode_step_error(dec.step_sync, shape["layers"])
-        assert int(dec.step_sync.count_nonzero()) == 0
+        assert int(dec.step_sync[:9 * 128].count_nonzero()) == 0      # counters and error word
+        assert int(dec.step_sync[9 * 128:9 * 128 + 4].view(torch.int32)[0]) == epoch + 1
         _set_state(dec, before)
         dec.persistent = False
         try:
