@@ -199,12 +199,12 @@ def profile_kernels(torch, ops, dev):
     del A3, B3
     from kuillm_amd.decoder import LlamaDecoder, LlamaShape
     c = LLAMA1B
-    dec = LlamaDecoder(LlamaShape(**c), llama_state(torch, c, dev), capacity=1024, device=dev)
+    dec = LlamaDecoder(LlamaShape(**c), llama_state(torch, c, dev), capacity=512 + 128, device=dev)
     dec.prefill(torch.randint(0, c["vocab"], (1, 512), generator=torch.Generator().manual_seed(0)))
     segment("llama1b_decode_token", dec._decode_step)
     del dec
     for n in (8, 64):
-        dec = LlamaDecoder(LlamaShape(**c), llama_state(torch, c, dev), capacity=1024, batch=n, device=dev)
+        dec = LlamaDecoder(LlamaShape(**c), llama_state(torch, c, dev), capacity=512 + 128, batch=n, device=dev)
         dec.prefill(torch.randint(0, c["vocab"], (n, 512), generator=torch.Generator().manual_seed(0)))
         segment(f"llama1b_b{n}_decode_step", dec._decode_step)
         del dec

@@ -157,7 +157,7 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         bool ok = load_q();
         for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
             if (__syncthreads_or(ll_give_up(it, a.err))) break;
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok) ok = load_q();
         }
     } else {

@@ -275,6 +275,13 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 constexpr unsigned kLLSpinLimit = 1u << 20;      // polls of one epoch-tagged wait (~1 s)
+// s_sleep argument (units of 64 clocks) between two polls of an epoch-tagged
+// wait: every poll of a waiting work-group re-reads its whole input past the
+// per-XCD L2, so a longer pause trades wake-up latency for fabric traffic
+#ifndef KUIOPS_LL_SLEEP
+#define KUIOPS_LL_SLEEP 1
+#endif
+constexpr int kLLSleep = KUIOPS_LL_SLEEP;
 
 // True when the wait that owns iteration `it` must stop: its bound is
 // reached (then *err is raised) or another wait already raised *err.
@@ -285,30 +292,6 @@ __device__ __forceinline__ bool ll_give_up(unsigned it, unsigned *err) {
         return true;
     }
     return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-}
-
-// Wave 0 polls 64 words spread over the first `nwords` words of an
-// epoch-tagged vector until all carry epoch `ep` (bounded: then *err is
-// raised; a raised *err ends the wait at once); the other waves wait at the
-// barrier.  Reading a sample keeps the
-// polling traffic small while the producers are still running.
-__device__ __forceinline__ void ll_poll_sample(const void *base, uint32_t ep, int64_t nwords, unsigned *err) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const int64_t w = nwords > 0 ? (int64_t)lane * nwords / 64 : 0;
-        for (unsigned it = 0;; ++it) {
-            const bool ok = nwords <= 0 || (uint32_t)(LLIO::word(base, w) >> 32) == ep;
-            if (__all(ok)) break;
-            // an expired wait elsewhere: stop waiting (the step's results are void)
-            if (err && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-            if (it >= kLLSpinLimit) {
-                if (lane == 0 && err) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
-    __syncthreads();
 }
 
 // --------------------------------------------------------------- host side

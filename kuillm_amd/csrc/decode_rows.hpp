@@ -286,7 +286,7 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
             // (the give-up decision is the same in every thread: a uniform
             // iteration count and one word read by all)
             if (__syncthreads_or(ll_give_up(it, a.err))) break;
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok && probe()) ok = load_input();
         }
     } else {

@@ -671,22 +671,10 @@ static int64_t strip_part(int64_t K, int splits, int nw, int ns) {
     return cdiv(cdiv(K, (int64_t)splits * nw), g) * g;
 }
 
-// Measurement switches, read once per process: KUIOPS_GEMV_NO_STRIP /
-// KUIOPS_GEMV_NO_ROWS take the strip / row-streaming kernel out of the
-// selection below (the call then takes the next kernel), for A/B timing.
-static bool strip_switched_off() {
-    static const bool off = getenv("KUIOPS_GEMV_NO_STRIP") != nullptr;
-    return off;
-}
-static bool rows_switched_off() {
-    static const bool off = getenv("KUIOPS_GEMV_NO_ROWS") != nullptr;
-    return off;
-}
-
 static bool strip_eligible(const GemvArgs &a, bool wcol) {
     if (wcol || a.N % 8 || a.ldw % 8 || a.K % 8 || cdiv(a.N, kStripW) * 4 > (int64_t)kGemvCounterBytes) return false;
     if (cdiv(a.N, kStripW) * strip_splits(a.N, a.K) < 128) return false;
-    return ((a.K - 1) * a.ldw + a.N) * 2 < ((int64_t)1 << 31) && !strip_switched_off();
+    return ((a.K - 1) * a.ldw + a.N) * 2 < ((int64_t)1 << 31);
 }
 
 template <typename T, typename Tout, int MB, int NW, int NS>
@@ -711,7 +699,6 @@ static int strip_dispatch(const GemvArgs &a, hipStream_t st) {
 static bool rows_eligible(const GemvArgs &a, bool wcol) {
     if (wcol || a.M > kRowsMaxM || a.N % 8 || a.ldw % 8 || a.K % 8 || a.N < kRowsCB) return false;
     if (cdiv(a.N, kRowsCB) * 4 > (int64_t)kGemvCounterBytes) return false;
-    if (rows_switched_off()) return false;
     return true;
 }
 
