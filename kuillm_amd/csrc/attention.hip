@@ -593,7 +593,7 @@ static int launch_decode(AttnArgs a, hipStream_t st) {
         a.rows_per_group = 1;
         a.row_groups = rows_kv;
         dim3 grid(1u, (unsigned)(a.hkv * rows_kv), (unsigned)a.n);
-        hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1, kDecodeWideWaves, kDecodeWideNB>), grid,
+        hipLaunchKernelGGL((fa_decode_onepass_kernel<T, HD, kDecodeWideWaves, kDecodeWideNB>), grid,
                            dim3(kDecodeWideWaves * 64), 0, st, a);
         return launch_status();
     }

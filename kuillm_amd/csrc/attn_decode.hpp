@@ -430,6 +430,170 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// One query row (unit = KV head * row_groups + row, rows_per_group 1) over a
+// cache whose capacity a.s fits one step of the work-group (a.s <= NWV *
+// KPW * NB keys): lane group kg of wave w holds keys w * KPW * NB + j * KPW
+// + kg (j < NB), all loaded at once.  Scores are dot products of the bf16 /
+// f16 query and key pairs (exact products, fp32 sums) times scale * log2(e).
+// The work-group's maximum score is found first, so the key slots' sums of
+// p = exp2(score - max) and p * v merge by plain addition (lanes of a wave by
+// a butterfly, then the waves in wave order), with no rescaling.
+//
+// With PF the K / V loads are issued before the query is read (the
+// persistent decode step reads the query, and key `fresh` >= 0, through IO
+// from work-groups of the same launch, polling epoch-tagged words).
+template <typename T, int HD, int NWV, int NB, typename IO = PlainIO, bool PF = false>
+__device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int unit, int64_t b, int64_t fresh = -1) {
+    constexpr int LPK = HD / 8;       // lanes per key (8 d values each)
+    constexpr int KPW = 64 / LPK;     // keys per wave per j
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kg = lane / LPK, dl = lane % LPK;
+    const int G = (int)a.hq / (int)a.hkv;
+    const int LQ = (int)a.l;
+    const int hk = unit / a.row_groups, rr = unit % a.row_groups;
+    const int head = hk * G + rr / LQ, qi = rr % LQ;
+    const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
+    const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
+    const int64_t s_b = a.kv_len ? max((int64_t)0, min((int64_t)a.kv_len[b], a.s)) : a.s;
+    const int64_t kw = (int64_t)wave * KPW * NB + kg;             // this lane group's key j = 0
+
+    u32x4 kr[NB], vr[NB];
+    auto load_kv = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int64_t key = min(kw + j * KPW, a.s - 1);          // in-bounds address
+            kr[j] = *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + dl * 8);
+            vr[j] = *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dl * 8);
+        }
+    };
+    if constexpr (PF) load_kv();
+
+    u32x4 qraw, kfr = {0, 0, 0, 0}, vfr = {0, 0, 0, 0};
+    auto load_q = [&]() -> bool {
+        bool ok = IO::ld8(a.Q, b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8, a.ep_q, qraw);
+        if constexpr (IO::kLL) {
+            if (fresh >= 0) {
+                ok = IO::ld8(a.kfresh, hk * HD + dl * 8, a.ep_q, kfr) && ok;
+                ok = IO::ld8(a.vfresh, hk * HD + dl * 8, a.ep_q, vfr) && ok;
+            }
+        }
+        return ok;
+    };
+    if constexpr (IO::kLL) {
+        // every lane reads its query chunk (and the new k / v chunk) until it
+        // is the expected write; the work-group leaves together
+        bool ok = load_q();
+        for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
+            if (__syncthreads_or(ll_give_up(it, a.err))) break;
+            __builtin_amdgcn_s_sleep(kLLSleep);
+            if (!ok) ok = load_q();
+        }
+    } else {
+        load_q();
+    }
+    if constexpr (!PF) load_kv();
+    if (PF && fresh >= 0) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            if (kw + j * KPW == fresh) {
+                if constexpr (IO::kLL) {
+                    kr[j] = kfr;
+                    vr[j] = vfr;
+                } else {
+                    kr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Kp + fresh * a.sk2 + dl * 8));
+                    vr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Vp + fresh * a.sv2 + dl * 8));
+                }
+            }
+        }
+    }
+
+    // keys visible to this row (exclusive bound); V of the others is zeroed
+    // (their p is 0, and a NaN in an unused cache row stays out of the sums)
+    const int64_t lim = min(s_b, a.causal ? s_b - a.l + qi + 1 : s_b);
+    float sc[NB];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d = dot2<T>(kr[j][e], qraw[e], d);
+        d = group_sum<LPK>(d);
+        const bool vis = kw + j * KPW < lim;
+        sc[j] = vis ? d * a.scale_log2 : -INFINITY;
+        if (!vis) vr[j] = u32x4{0, 0, 0, 0};
+        mx = fmaxf(mx, sc[j]);
+    }
+    if constexpr (LPK <= 8) mx = xor_max<8>(mx);
+    if constexpr (LPK <= 16) mx = xor_max<16>(mx);
+    mx = xor_max<32>(mx);
+    __shared__ float s_mx[NWV], s_l[NWV], s_o[NWV][HD];
+    if (lane == 0) s_mx[wave] = mx;
+    __syncthreads();
+    float M = s_mx[0];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) M = fmaxf(M, s_mx[w]);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+
+    float l = 0.f, o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const float pj = fast_exp2(sc[j] - Mu);
+        l += pj;
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        const t8 vv = __builtin_bit_cast(t8, vr[j]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(pj, to_f32(vv[e]), o[e]);
+    }
+    // lanes with equal dl: sums commute, so partners hold bitwise-equal totals
+    if constexpr (LPK <= 8) {
+        l = xor_add<8>(l);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = xor_add<8>(o[e]);
+    }
+    if constexpr (LPK <= 16) {
+        l = xor_add<16>(l);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = xor_add<16>(o[e]);
+    }
+    l = xor_add<32>(l);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = xor_add<32>(o[e]);
+    if (kg == 0) {
+        if (dl == 0) s_l[wave] = l;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_o[wave][dl * 8 + e] = o[e];
+    }
+    __syncthreads();
+    if (tid >= HD) return;
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) {
+        L += s_l[w];
+        O += s_o[w][tid];
+    }
+    const T ov = from_f32<T>(O * (L > 0.f ? 1.f / L : 0.f));
+    const int64_t oidx = b * a.so0 + (int64_t)head * a.so1 + (int64_t)qi * a.so2 + tid;
+    if constexpr (IO::kLL) {
+        // element pairs (d, d + 1) in one epoch-tagged word (neighbour lanes)
+        const uint16_t nb = (uint16_t)__shfl_down((int)__builtin_bit_cast(uint16_t, ov), 1, 64);
+        if ((tid & 1) == 0) IO::st2(reinterpret_cast<T *>(a.O), oidx, ov, __builtin_bit_cast(T, nb), a.ep_o);
+    } else {
+        IO::st(reinterpret_cast<T *>(a.O) + oidx, ov);
+    }
+    if (a.lse && tid == 0) a.lse[((int64_t)b * a.hq + head) * a.l + qi] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+}
+
+template <typename T, int HD, int NWV, int NB>
+__global__ __launch_bounds__(NWV * 64) void fa_decode_onepass_kernel(AttnArgs a) {
+    // consecutive (KV head, row) units spread so that all rows of a KV head
+    // run on one XCD (its K / V then come from that XCD's L2 after the first read)
+    int unit = blockIdx.y;
+    if ((gridDim.y & 7) == 0) unit = (unit & 7) * (gridDim.y >> 3) + (unit >> 3);
+    fa_decode_onepass_block<T, HD, NWV, NB>(a, unit, blockIdx.z);
+}
+
 template <typename T, int HD, int R, int NWV = 4, int NB = 4>
 __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     // One split, many row groups: work-groups are dispatched round-robin

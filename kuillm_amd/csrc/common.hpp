@@ -262,6 +262,43 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Lane exchanges across lane bit 5, 4 or 3 without an LDS round trip
+// (v_permlane32_swap / v_permlane16_swap on gfx950, DPP row rotate by 8).
+// swap_rows<B>(x, y): in every lane, the pair {p, q} with p + q the sum of
+// x over the lane and its partner (lane ^ B) when the lane's bit B is clear,
+// and the sum of y over the pair when it is set.  Float addition commutes,
+// so both partners' sums have the same bits.
+template <int B>
+__device__ __forceinline__ void swap_rows(float x, float y, float &p, float &q) {
+    static_assert(B == 8 || B == 16 || B == 32, "lane bit");
+    if constexpr (B == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+        p = __uint_as_float(r[0]);
+        q = __uint_as_float(r[1]);
+    } else if constexpr (B == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+        p = __uint_as_float(r[0]);
+        q = __uint_as_float(r[1]);
+    } else {
+        const bool hi = (__lane_id() & 8) != 0;
+        p = hi ? y : x;
+        q = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(hi ? x : y), 0x128, 0xF, 0xF, false));
+    }
+}
+// v + v of lane ^ B, the same bits in both lanes
+template <int B>
+__device__ __forceinline__ float xor_add(float v) {
+    float p, q;
+    swap_rows<B>(v, v, p, q);
+    return p + q;
+}
+template <int B>
+__device__ __forceinline__ float xor_max(float v) {
+    float p, q;
+    swap_rows<B>(v, v, p, q);
+    return fmaxf(p, q);
+}
+
 // a.x * b.x + a.y * b.y + c for packed pairs (fp32 accumulate)
 template <typename T>
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {

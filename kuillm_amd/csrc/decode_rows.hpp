@@ -109,12 +109,13 @@ __device__ __forceinline__ int64_t dec_row(const DecLinArgs &a, int64_t j) {
 // would take RG x 6 dependent cross-lane exchanges.)
 template <int N, int MASK>
 __device__ __forceinline__ void halve_rows(float *v, int lane) {
-    const bool hi = (lane & MASK) != 0;
+    // the lane keeps row i (bit MASK clear) or i + N / 2 (set) and adds its
+    // partner's value of that row
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
-        const float send = hi ? v[i] : v[i + N / 2];
-        const float keep = hi ? v[i + N / 2] : v[i];
-        v[i] = keep + __shfl_xor(send, MASK, 64);
+        float p, q;
+        swap_rows<MASK>(v[i], v[i + N / 2], p, q);
+        v[i] = p + q;
     }
 }
 
@@ -125,11 +126,11 @@ __device__ __forceinline__ float multi_row_sum(float *v, int lane) {
     // by DPP, so a row's total has the same bits whatever RG is.
     static_assert(RG == 1 || RG == 2 || RG == 4 || RG == 8, "rows");
     if constexpr (RG >= 2) halve_rows<RG, 32>(v, lane);
-    else v[0] += __shfl_xor(v[0], 32, 64);
+    else v[0] = xor_add<32>(v[0]);
     if constexpr (RG >= 4) halve_rows<RG / 2, 16>(v, lane);
-    else v[0] += __shfl_xor(v[0], 16, 64);
+    else v[0] = xor_add<16>(v[0]);
     if constexpr (RG >= 8) halve_rows<2, 8>(v, lane);
-    else v[0] += __shfl_xor(v[0], 8, 64);
+    else v[0] = xor_add<8>(v[0]);
     return group_sum<8>(v[0]);
 }
 

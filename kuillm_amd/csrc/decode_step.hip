@@ -226,7 +226,7 @@ __device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int 
     at.ep_q = at.ep_o = epoch_of(a, step, l);
     at.kfresh = a.kf; at.vfresh = a.vf;
     at.err = error_word(a);
-    fa_decode_block<T, HD, 1, kStepWaves, 12, LLIO, NoWaitAttn, true>(at, 0, idx, 0, NoWaitAttn{}, fresh);
+    fa_decode_onepass_block<T, HD, kStepWaves, 12, LLIO, true>(at, idx, 0, fresh);
 }
 
 // softmax + top-1 of the logits and the decode-state advance; every other
@@ -243,6 +243,21 @@ __device__ __attribute__((noinline)) void step_sample(const StepArgs &a) {
     if (threadIdx.x == 0) *epoch_word(a) += 1u;
 }
 
+// Job j of the step's list: layer, kind and index within the kind.
+__device__ __forceinline__ void job_of(const StepArgs &a, int j, int &l, int &kind, int &idx) {
+    if (j < a.layers * a.per_layer) {
+        l = j / a.per_layer;
+        idx = j - l * a.per_layer;
+        kind = 0;
+        while (idx >= a.njobs[kind]) idx -= a.njobs[kind++];
+    } else {
+        l = a.layers;
+        idx = j - a.layers * a.per_layer;
+        kind = idx < a.njobs[5] ? 5 : 6;
+        if (kind == 6) idx -= a.njobs[5];
+    }
+}
+
 template <typename T, int HD, int KCD, int KCF>
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
     constexpr int RLD = lds_rows_per_wave(KCD), RLF = lds_rows_per_wave(KCF);
@@ -254,17 +269,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
     const uint32_t step = *epoch_word(a);
     for (int j = blockIdx.x; j < a.total; j += G) {
         int l, kind, idx;
-        if (j < a.layers * a.per_layer) {
-            l = j / a.per_layer;
-            idx = j - l * a.per_layer;
-            kind = 0;
-            while (idx >= a.njobs[kind]) idx -= a.njobs[kind++];
-        } else {
-            l = a.layers;
-            idx = j - a.layers * a.per_layer;
-            kind = idx < a.njobs[5] ? 5 : 6;
-            if (kind == 6) idx -= a.njobs[5];
-        }
+        job_of(a, j, l, kind, idx);
         switch (kind) {
             case 0:
                 if (l == 0) step_proj<T, kXRmsNorm, KCD, kOutRope, 0, PlainIO, LLIO>(a, 0, l, idx, step, wl);
