@@ -155,10 +155,12 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         // every lane reads its query chunk (and the new k / v chunk) until it
         // is the expected write; the work-group leaves together
         bool ok = load_q();
+        unsigned e = ll_err_read(a.err);
         for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
-            if (__syncthreads_or(ll_give_up(it, a.err))) break;
+            if (__syncthreads_or(ll_expired(it, e, a.err))) break;
             __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok) ok = load_q();
+            e = ll_err_read(a.err);
         }
     } else {
         load_q();
@@ -432,12 +434,15 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
 
 // One query row (unit = KV head * row_groups + row, rows_per_group 1) over a
 // cache whose capacity a.s fits one step of the work-group (a.s <= NWV *
-// KPW * NB keys): lane group kg of wave w holds keys w * KPW * NB + j * KPW
-// + kg (j < NB), all loaded at once.  Scores are dot products of the bf16 /
-// f16 query and key pairs (exact products, fp32 sums) times scale * log2(e).
-// The work-group's maximum score is found first, so the key slots' sums of
-// p = exp2(score - max) and p * v merge by plain addition (lanes of a wave by
-// a butterfly, then the waves in wave order), with no rescaling.
+// KPW * NB keys): lane group kg of wave w holds keys j * NWV * KPW + w * KPW
+// + kg (j < NB), all loaded at once; interleaved so that every wave holds
+// about the same number of visible keys, and a j whose keys are all past the
+// visible count is skipped by the whole wave.  Scores are dot products of
+// the bf16 / f16 query and key pairs (exact products, fp32 sums) times
+// scale * log2(e).  The work-group's maximum score is found first, so the
+// key slots' sums of p = exp2(score - max) and p * v merge by plain addition
+// (lanes of a wave by a butterfly, then the waves in wave order), with no
+// rescaling.
 //
 // With PF the K / V loads are issued before the query is read (the
 // persistent decode step reads the query, and key `fresh` >= 0, through IO
@@ -455,13 +460,14 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
     const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
     const int64_t s_b = a.kv_len ? max((int64_t)0, min((int64_t)a.kv_len[b], a.s)) : a.s;
-    const int64_t kw = (int64_t)wave * KPW * NB + kg;             // this lane group's key j = 0
+    constexpr int KPJ = NWV * KPW;                                 // keys per j
+    const int64_t kw = (int64_t)wave * KPW + kg;                  // this lane group's key j = 0
 
     u32x4 kr[NB], vr[NB];
     auto load_kv = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int64_t key = min(kw + j * KPW, a.s - 1);          // in-bounds address
+            const int64_t key = min(kw + j * KPJ, a.s - 1);          // in-bounds address
             kr[j] = *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + dl * 8);
             vr[j] = *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dl * 8);
         }
@@ -483,10 +489,12 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
         // every lane reads its query chunk (and the new k / v chunk) until it
         // is the expected write; the work-group leaves together
         bool ok = load_q();
+        unsigned e = ll_err_read(a.err);
         for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
-            if (__syncthreads_or(ll_give_up(it, a.err))) break;
+            if (__syncthreads_or(ll_expired(it, e, a.err))) break;
             __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok) ok = load_q();
+            e = ll_err_read(a.err);
         }
     } else {
         load_q();
@@ -495,7 +503,7 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     if (PF && fresh >= 0) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            if (kw + j * KPW == fresh) {
+            if (kw + j * KPJ == fresh) {
                 if constexpr (IO::kLL) {
                     kr[j] = kfr;
                     vr[j] = vfr;
@@ -510,18 +518,24 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     // keys visible to this row (exclusive bound); V of the others is zeroed
     // (their p is 0, and a NaN in an unused cache row stays out of the sums)
     const int64_t lim = min(s_b, a.causal ? s_b - a.l + qi + 1 : s_b);
+    // j < nj: the j whose keys of this wave are not all past lim (uniform)
+    const int64_t w0 = (int64_t)wave * KPW;
+    const int nj = lim > w0 ? (int)min((int64_t)NB, (lim - w0 + KPJ - 1) / KPJ) : 0;
     float sc[NB];
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-        float d = 0.f;
+        sc[j] = -INFINITY;
+        if (j < nj) {
+            float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) d = dot2<T>(kr[j][e], qraw[e], d);
-        d = group_sum<LPK>(d);
-        const bool vis = kw + j * KPW < lim;
-        sc[j] = vis ? d * a.scale_log2 : -INFINITY;
-        if (!vis) vr[j] = u32x4{0, 0, 0, 0};
-        mx = fmaxf(mx, sc[j]);
+            for (int e = 0; e < 4; ++e) d = dot2<T>(kr[j][e], qraw[e], d);
+            d = group_sum<LPK>(d);
+            const bool vis = kw + j * KPJ < lim;
+            sc[j] = vis ? d * a.scale_log2 : -INFINITY;
+            if (!vis) vr[j] = u32x4{0, 0, 0, 0};
+            mx = fmaxf(mx, sc[j]);
+        }
     }
     if constexpr (LPK <= 8) mx = xor_max<8>(mx);
     if constexpr (LPK <= 16) mx = xor_max<16>(mx);
@@ -539,12 +553,14 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     for (int e = 0; e < 8; ++e) o[e] = 0.f;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-        const float pj = fast_exp2(sc[j] - Mu);
-        l += pj;
-        typedef T t8 __attribute__((ext_vector_type(8)));
-        const t8 vv = __builtin_bit_cast(t8, vr[j]);
+        if (j < nj) {
+            const float pj = fast_exp2(sc[j] - Mu);
+            l += pj;
+            typedef T t8 __attribute__((ext_vector_type(8)));
+            const t8 vv = __builtin_bit_cast(t8, vr[j]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(pj, to_f32(vv[e]), o[e]);
+            for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(pj, to_f32(vv[e]), o[e]);
+        }
     }
     // lanes with equal dl: sums commute, so partners hold bitwise-equal totals
     if constexpr (LPK <= 8) {
@@ -577,7 +593,7 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     const int64_t oidx = b * a.so0 + (int64_t)head * a.so1 + (int64_t)qi * a.so2 + tid;
     if constexpr (IO::kLL) {
         // element pairs (d, d + 1) in one epoch-tagged word (neighbour lanes)
-        const uint16_t nb = (uint16_t)__shfl_down((int)__builtin_bit_cast(uint16_t, ov), 1, 64);
+        const uint16_t nb = (uint16_t)lane_xor1((int)__builtin_bit_cast(uint16_t, ov));
         if ((tid & 1) == 0) IO::st2(reinterpret_cast<T *>(a.O), oidx, ov, __builtin_bit_cast(T, nb), a.ep_o);
     } else {
         IO::st(reinterpret_cast<T *>(a.O) + oidx, ov);

@@ -299,6 +299,25 @@ __device__ __forceinline__ float xor_max(float v) {
     return fmaxf(p, q);
 }
 
+// Value of lane ^ B, for lanes with bit B clear (lane + B).
+template <int B>
+__device__ __forceinline__ float from_lane_above(float v) {
+    float p, q;
+    swap_rows<B>(v, v, p, q);
+    return q;
+}
+// Value of lane ^ 1 (DPP quad permute).
+__device__ __forceinline__ int lane_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+
+// Wave total by lane moves only (DPP within rows of 16, then lane swaps
+// across rows): every lane ends with the same bits.  (A different order
+// from wave_sum.)
+__device__ __forceinline__ float wave_sum_swaps(float v) {
+    v = group_sum<16>(v);
+    v = xor_add<16>(v);
+    return xor_add<32>(v);
+}
+
 // a.x * b.x + a.y * b.y + c for packed pairs (fp32 accumulate)
 template <typename T>
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -320,15 +339,22 @@ constexpr unsigned kLLSpinLimit = 1u << 20;      // polls of one epoch-tagged wa
 #endif
 constexpr int kLLSleep = KUIOPS_LL_SLEEP;
 
-// True when the wait that owns iteration `it` must stop: its bound is
-// reached (then *err is raised) or another wait already raised *err.
-__device__ __forceinline__ bool ll_give_up(unsigned it, unsigned *err) {
-    if (!err) return it >= kLLSpinLimit;
+// The expired-wait flag, read by thread 0 together with a poll's loads (so
+// that checking it adds no memory round trip to a poll); 0 elsewhere.
+__device__ __forceinline__ unsigned ll_err_read(const unsigned *err) {
+    return (err && threadIdx.x == 0) ? __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+}
+
+// True (in the thread that decides) when the wait that owns iteration `it`
+// must stop: its bound is reached (then *err is raised), or `e`, the flag
+// read with the last poll, shows that another wait raised it.  Combined over
+// the work-group with __syncthreads_or.
+__device__ __forceinline__ bool ll_expired(unsigned it, unsigned e, unsigned *err) {
     if (it >= kLLSpinLimit) {
-        if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (err && threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return true;
     }
-    return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    return e != 0;
 }
 
 // --------------------------------------------------------------- host side

@@ -283,12 +283,12 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
             return ok;
         };
         bool ok = load_input();
+        unsigned e = ll_err_read(a.err);
         for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
-            // (the give-up decision is the same in every thread: a uniform
-            // iteration count and one word read by all)
-            if (__syncthreads_or(ll_give_up(it, a.err))) break;
+            if (__syncthreads_or(ll_expired(it, e, a.err))) break;
             __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok && probe()) ok = load_input();
+            e = ll_err_read(a.err);
         }
     } else {
         load_input();
@@ -313,7 +313,7 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
     }
     float inv = 0.f;
     if constexpr (XK == kXRmsNorm) {
-        ss = wave_sum(ss);
+        ss = wave_sum_swaps(ss);
         if (lane == 0 && stage) red[wave] = ss;
         __syncthreads();
         inv = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)a.K + a.eps);
@@ -419,8 +419,9 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
                 if (lane % (64 / RGL) == 0) put(r0 + RG + lane / (64 / RGL), totl);
         }
     } else {
-        const float nxt = __shfl_down(tot, 64 / RG, 64);
-        const float nxtl = RGL >= 2 ? __shfl_down(totl, 64 / (RGL >= 2 ? RGL : 1), 64) : 0.f;
+        const float nxt = from_lane_above<64 / RG>(tot);
+        float nxtl = 0.f;
+        if constexpr (RGL >= 2) nxtl = from_lane_above<64 / RGL>(totl);
         // lane 2q * (64 / RG) finishes pair q, so the pairs' epilogues run
         // side by side.  The results go through LDS: the work-group's pairs
         // are consecutive (pg0 ..), so each output half is one contiguous
