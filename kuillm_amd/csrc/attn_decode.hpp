@@ -153,15 +153,16 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
     };
     if constexpr (IO::kLL) {
         // every lane reads its query chunk (and the new k / v chunk) until it
-        // is the expected write; the work-group leaves together
+        // is the expected write (each wave on its own), then the work-group meets
         bool ok = load_q();
         unsigned e = ll_err_read(a.err);
-        for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
-            if (__syncthreads_or(ll_expired(it, e, a.err))) break;
+        for (unsigned it = 0; !__all(ok); ++it) {
+            if (ll_expired(it, e, a.err)) break;
             __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok) ok = load_q();
             e = ll_err_read(a.err);
         }
+        __syncthreads();
     } else {
         load_q();
     }
@@ -487,15 +488,16 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     };
     if constexpr (IO::kLL) {
         // every lane reads its query chunk (and the new k / v chunk) until it
-        // is the expected write; the work-group leaves together
+        // is the expected write (each wave on its own), then the work-group meets
         bool ok = load_q();
         unsigned e = ll_err_read(a.err);
-        for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
-            if (__syncthreads_or(ll_expired(it, e, a.err))) break;
+        for (unsigned it = 0; !__all(ok); ++it) {
+            if (ll_expired(it, e, a.err)) break;
             __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok) ok = load_q();
             e = ll_err_read(a.err);
         }
+        __syncthreads();
     } else {
         load_q();
     }

@@ -339,22 +339,26 @@ constexpr unsigned kLLSpinLimit = 1u << 20;      // polls of one epoch-tagged wa
 #endif
 constexpr int kLLSleep = KUIOPS_LL_SLEEP;
 
-// The expired-wait flag, read by thread 0 together with a poll's loads (so
-// that checking it adds no memory round trip to a poll); 0 elsewhere.
+// Epoch-tagged waits spin per wave: a wave polls its own input words until
+// all carry the expected epoch (a wave vote, no work-group reduction per
+// poll), then the work-group meets at one barrier.  The expired-wait flag is
+// read by each wave's lane 0 together with the wave's poll loads (checking
+// it adds no memory round trip to a poll).
 __device__ __forceinline__ unsigned ll_err_read(const unsigned *err) {
-    return (err && threadIdx.x == 0) ? __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+    return (err && (threadIdx.x & 63) == 0) ? __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                             : 0u;
 }
 
-// True (in the thread that decides) when the wait that owns iteration `it`
-// must stop: its bound is reached (then *err is raised), or `e`, the flag
-// read with the last poll, shows that another wait raised it.  Combined over
-// the work-group with __syncthreads_or.
+// True (wave-uniform) when the wave's wait must stop at iteration `it`: its
+// bound is reached (then *err is raised), or `e`, the flag read with the
+// wave's last poll, shows that another wait raised it.  A stopped wait lets
+// the work-group run on; the step's results are then void (*err is set).
 __device__ __forceinline__ bool ll_expired(unsigned it, unsigned e, unsigned *err) {
     if (it >= kLLSpinLimit) {
-        if (err && threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (err && (threadIdx.x & 63) == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return true;
     }
-    return e != 0;
+    return __builtin_amdgcn_readfirstlane(e) != 0;
 }
 
 // --------------------------------------------------------------- host side

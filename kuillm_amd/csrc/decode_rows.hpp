@@ -270,7 +270,8 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
     if constexpr (IO::kLL) {
         // every thread reads its chunks; while a chunk is not the expected
         // write it probes only the chunk's first word (8 bytes per poll), then
-        // reads the chunk again; the work-group leaves together
+        // reads the chunk again; each wave spins on its own chunks, then the
+        // work-group meets
         auto probe = [&]() -> bool {
             bool ok = true;
 #pragma unroll
@@ -284,12 +285,13 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
         };
         bool ok = load_input();
         unsigned e = ll_err_read(a.err);
-        for (unsigned it = 0; !__syncthreads_and(ok); ++it) {
-            if (__syncthreads_or(ll_expired(it, e, a.err))) break;
+        for (unsigned it = 0; !__all(ok); ++it) {
+            if (ll_expired(it, e, a.err)) break;
             __builtin_amdgcn_s_sleep(kLLSleep);
             if (!ok && probe()) ok = load_input();
             e = ll_err_read(a.err);
         }
+        __syncthreads();
     } else {
         load_input();
     }
