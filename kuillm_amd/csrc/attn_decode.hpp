@@ -365,7 +365,7 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
     // weight * o[split][d] in split order.
     const __amdgpu_buffer_rsrc_t rs_ml = __builtin_amdgcn_make_buffer_rsrc((void *)a.ws_ml, (short)0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc((void *)a.ws_o, (short)0, 0x7fffffff, 0x00020000);
-    constexpr int kSc1 = 16;                    // cache policy: system-coherent level 1 (agent scope)
+    constexpr int kSc1 = kSc1Aux;
     auto grow_of = [&](int r) {
         const int rr = r0 + r;
         return (b * a.hq + hk * G + rr / LQ) * a.l + rr % LQ;

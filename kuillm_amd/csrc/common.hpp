@@ -121,6 +121,9 @@ __device__ __forceinline__ void transpose4x8_b16(const u32x4 in[4], u32x2 out[8]
 // epoch-tagged vector, ignored by the plain forms): ld8 reads 8 elements and
 // reports whether they are the expected write (always, here), st8 / st2
 // write 8 / 2 elements.
+// Buffer-load cache policy bits for an agent-coherent (sc1) read.
+constexpr int kSc1Aux = 16;
+
 struct PlainIO {
     static constexpr bool kLL = false;
     template <typename V> static __device__ __forceinline__ V ld(const V *p) { return *p; }
@@ -194,11 +197,15 @@ struct CoherentIO {
 // Epoch-tagged vectors for data handed between work-groups of one launch:
 // element pair (2w, 2w + 1) and the epoch of its write share the 8-byte word
 // w (element 2w in the low 16 bits, the epoch in the high 32), written with
-// one agent-scope atomic store.  A reader knows which write it needs (its
+// one agent-coherent (sc1) store.  A reader knows which write it needs (its
 // epoch) and polls the words themselves: no completion counter, and no
 // wait for store acknowledgements before signalling.
 struct LLIO {
     static constexpr bool kLL = true;
+    static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+    }
+    static constexpr int kLdAux = kSc1Aux | (int)(1u << 31);     // sc1, volatile
     static __device__ __forceinline__ uint64_t word(const void *base, int64_t w) {
         return __hip_atomic_load(reinterpret_cast<const uint64_t *>(base) + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -206,19 +213,24 @@ struct LLIO {
         __hip_atomic_store(reinterpret_cast<uint64_t *>(base) + w, (uint64_t)pair | ((uint64_t)ep << 32),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // 8 elements (4 words) as two 16-byte agent-coherent (sc1) buffer
+    // accesses; each 8-byte word of a 16-byte access is read or written
+    // whole, so a word still carries its own element pair and epoch (a
+    // reader may see one half of a chunk before the other, and then reads
+    // again).  The loads are volatile: a polling loop re-issues them.
     static __device__ __forceinline__ bool ld8(const void *base, int64_t idx, uint32_t ep, u32x4 &v) {
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint64_t w = word(base, idx / 2 + i);
-            v[i] = (uint32_t)w;
-            ok = ok && (uint32_t)(w >> 32) == ep;
-        }
-        return ok;
+        const __amdgpu_buffer_rsrc_t rs = rsrc(base);
+        const uint32_t off = (uint32_t)(idx / 2) * 8u;
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kLdAux);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16u, 0, kLdAux);
+        v = u32x4{a[0], a[2], b[0], b[2]};
+        return a[1] == ep && a[3] == ep && b[1] == ep && b[3] == ep;
     }
     static __device__ __forceinline__ void st8(void *base, int64_t idx, uint32_t ep, u32x4 v) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) put(base, idx / 2 + i, v[i], ep);
+        const __amdgpu_buffer_rsrc_t rs = rsrc(base);
+        const uint32_t off = (uint32_t)(idx / 2) * 8u;
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[0], ep, v[1], ep}, rs, off, 0, kSc1Aux);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{v[2], ep, v[3], ep}, rs, off + 16u, 0, kSc1Aux);
     }
     template <typename T> static __device__ __forceinline__ void st2(T *base, int64_t idx, T v0, T v1, uint32_t ep) {
         const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);

@@ -56,12 +56,40 @@ __device__ __forceinline__ void softmax_top1_row(int64_t n, const T *x, float *p
     }
     A v[F][kSmCache];
     A m = -(A)INFINITY;
+    // every load is issued before any is used: an index past the row reads
+    // the last element (masked below), so no load sits behind a branch (a
+    // coherent load there would wait for its own round trip)
+    // (32-bit indices: n <= kSmThreads * kSmCache)
+    const int nn = (int)n;
+    if constexpr (__is_same(IO, PlainIO)) {
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+#pragma unroll
+            for (int j = 0; j < kSmCache; ++j) {
+                const int i = tid + NTH * f + kSmThreads * j;
+                v[f][j] = (A)to_f32_or_self(x[i < nn ? i : nn - 1]);
+            }
+    } else {
+        // written by other work-groups of the launch: agent-coherent (sc1)
+        // buffer loads, which unlike atomic loads issue back to back
+        static_assert(sizeof(T) == 2, "coherent rows: 16-bit elements");
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(x), (short)0, nn * 2, 0x00020000);
+#pragma unroll
+        for (int f = 0; f < F; ++f)
+#pragma unroll
+            for (int j = 0; j < kSmCache; ++j) {
+                const int i = tid + NTH * f + kSmThreads * j;
+                const unsigned short b = __builtin_amdgcn_raw_buffer_load_b16(rs, (i < nn ? i : nn - 1) * 2, 0, kSc1Aux);
+                v[f][j] = (A)to_f32(__builtin_bit_cast(T, b));
+            }
+    }
 #pragma unroll
     for (int f = 0; f < F; ++f)
 #pragma unroll
         for (int j = 0; j < kSmCache; ++j) {
-            const int64_t i = tid + NTH * f + (int64_t)kSmThreads * j;
-            v[f][j] = i < n ? (A)to_f32_or_self(IO::ld(x + i)) : -(A)INFINITY;
+            const int i = tid + NTH * f + kSmThreads * j;
+            if (i >= nn) v[f][j] = -(A)INFINITY;
             m = (v[f][j] > m || v[f][j] != v[f][j]) ? v[f][j] : m;
         }
     m = wave_max(m);
@@ -76,7 +104,7 @@ __device__ __forceinline__ void softmax_top1_row(int64_t n, const T *x, float *p
 #pragma unroll
         for (int j = 0; j < kSmCache; ++j) {
             v[f][j] = acc_exp(v[f][j] - m);
-            if (tid + NTH * f + (int64_t)kSmThreads * j < n) s += v[f][j];
+            if (tid + NTH * f + kSmThreads * j < nn) s += v[f][j];
         }
         s = wave_sum(s);
         if (lane == 0) s_b[wave + (NTH / 64) * f] = s;
@@ -93,8 +121,8 @@ __device__ __forceinline__ void softmax_top1_row(int64_t n, const T *x, float *p
     for (int f = 0; f < F; ++f)
 #pragma unroll
         for (int j = 0; j < kSmCache; ++j) {
-            const int64_t i = tid + NTH * f + (int64_t)kSmThreads * j;
-            if (i >= n) continue;
+            const int i = tid + NTH * f + kSmThreads * j;
+            if (i >= nn) continue;
             const unsigned long long k = ((unsigned long long)order_key(v[f][j] * inv, true) << 32) |
                                          (0xffffffffu - (uint32_t)i);
             best = k > best ? k : best;
