@@ -10,7 +10,8 @@
 //
 //   per layer   qkv row blocks | attention rows (one per query head) |
 //               o row blocks | gate|up row blocks | down row blocks
-//   then        LM-head row blocks | the softmax + top-1 row
+//   then        LM-head row blocks (one full-size block per work-group,
+//               the rest in small blocks) | the softmax + top-1 row
 //
 // Work-group w takes jobs w, w + G, w + 2G, ... (G = grid size).  A job of
 // phase p needs the whole output of phase p - 1 (the next projection's input
@@ -41,6 +42,8 @@
 // The job bodies are the library's own (decode_rows_block, fa_decode_block,
 // softmax_top1_row), with the launch shapes and summation orders of the
 // per-op kernels, so the step is bitwise the per-op sequence.
+#include <algorithm>
+
 #include "attn_decode.hpp"
 #include "top1.hpp"
 #include "decode_rows.hpp"
@@ -49,7 +52,8 @@ namespace kuiops {
 
 constexpr int kStepWaves = 8;
 constexpr int kStepThreads = kStepWaves * 64;
-constexpr int kKinds = 7;                 // qkv, attention, o, gate|up, down, LM head, sampling
+constexpr int kKinds = 8;                 // qkv, attention, o, gate|up, down, LM head (two sizes), sampling
+constexpr int kHeadTailRows = 4;          // rows per wave of the LM head's second-round jobs
 constexpr int kLayerKinds = 5;
 constexpr int kSubCounters = 8;           // completion counters of the LM-head phase (spread contention)
 constexpr int kCounterStride = 32;        // uint32 apart: one 128-byte line each
@@ -74,6 +78,7 @@ struct StepArgs {
     unsigned *sync;
     int njobs[kKinds];
     int per_layer, total;
+    int64_t head_split;                   // LM-head rows of the full-size jobs (kind 5); kind 6 takes the rest
 };
 
 // sync: kSubCounters counters of the LM-head phase, the error word, the step
@@ -93,7 +98,7 @@ __device__ __forceinline__ uint32_t epoch_of(const StepArgs &a, uint32_t step, i
 __device__ __forceinline__ void wait_head(const StepArgs &a) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        const unsigned need = (unsigned)a.njobs[5];
+        const unsigned need = (unsigned)(a.njobs[5] + a.njobs[6]);
         for (unsigned it = 0;; ++it) {
             unsigned v = 0, err = 0;
             if (lane < kSubCounters)
@@ -145,11 +150,13 @@ __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int
     p.rpw = rpw;
     p.pair_shift = -1;
     p.err = error_word(a);
-    if (kind == 5) {                      // LM head: RMSNorm(h0 + down) input
-        p.N = a.vocab; p.K = a.d;
+    if (kind >= 5) {                      // LM head: RMSNorm(h0 + down) input; kind 6 from row head_split
+        const int64_t r0 = kind == 6 ? a.head_split : 0;
+        p.N = a.vocab - r0; p.K = a.d;
         p.in = a.h0; p.in_add = a.down; p.norm_w = a.norm;
         p.ep_in = p.ep_add = epoch_of(a, step, a.layers - 1);
-        p.W = a.head; p.ldw = a.d; p.out = a.logits;
+        p.W = reinterpret_cast<const char *>(a.head) + r0 * a.d * 2; p.ldw = a.d;
+        p.out = reinterpret_cast<char *>(a.logits) + r0 * 2;
         return p;
     }
     // inputs from this layer's earlier phases, or (qkv) the previous layer's
@@ -193,11 +200,11 @@ __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int
 
 // The job kinds, each its own function: inlined into one loop, the bodies'
 // register demands add up (spills); as calls each gets its own allocation.
-template <typename T, int XK, int KC, int OK, int RGL, typename IO, typename OIO>
+template <typename T, int XK, int KC, int OK, int RGL, typename IO, typename OIO, int RG = rows_per_wave(KC)>
 __device__ __attribute__((noinline)) void step_proj(const StepArgs &a, int kind, int l, int idx, uint32_t step,
                                                     lds_bytes *wl) {
-    decode_rows_block<T, XK, KC, OK, kStepWaves, NoWait, IO, rows_per_wave(KC), RGL, true, OIO>(
-        proj_args(a, kind, l, rows_per_wave(KC) + RGL, step), idx, NoWait{}, wl, wl + kLdsRowBytes);
+    decode_rows_block<T, XK, KC, OK, kStepWaves, NoWait, IO, RG, RGL, true, OIO>(
+        proj_args(a, kind, l, RG + RGL, step), idx, NoWait{}, wl, wl + kLdsRowBytes);
 }
 
 // attention row `idx` (query head) of layer l, as the per-op row-wide launch
@@ -233,10 +240,10 @@ __device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int 
 // job has finished by then (each phase waited on the one before it), so the
 // counters are left zero and the step epoch advances for the next step
 template <typename T>
-__device__ __attribute__((noinline)) void step_sample(const StepArgs &a) {
+__device__ __attribute__((noinline)) void step_sample(const StepArgs &a, lds_bytes *wl) {
     wait_head(a);
     softmax_top1_row<T, kStepThreads, CoherentIO>(a.vocab, reinterpret_cast<const T *>(a.logits), a.prob, a.tok,
-                                                  a.pos, a.kv_len, a.history, a.hist_len);
+                                                  a.pos, a.kv_len, a.history, a.hist_len, wl);
     __syncthreads();
     if (threadIdx.x < kSubCounters)
         __hip_atomic_store(counter_of(a, threadIdx.x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -253,8 +260,8 @@ __device__ __forceinline__ void job_of(const StepArgs &a, int j, int &l, int &ki
     } else {
         l = a.layers;
         idx = j - a.layers * a.per_layer;
-        kind = idx < a.njobs[5] ? 5 : 6;
-        if (kind == 6) idx -= a.njobs[5];
+        kind = 5;
+        while (kind < kKinds - 1 && idx >= a.njobs[kind]) idx -= a.njobs[kind++];
     }
 }
 
@@ -283,7 +290,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
                 step_proj<T, kXRmsNorm, KCD, kOutPlain, RLD, LLIO, CoherentIO>(a, 5, l, idx, step, wl);
                 signal_head(a, idx);
                 break;
-            default: step_sample<T>(a); break;
+            case 6:
+                step_proj<T, kXRmsNorm, KCD, kOutPlain, 0, LLIO, CoherentIO, kHeadTailRows>(a, 6, l, idx, step, wl);
+                signal_head(a, idx);
+                break;
+            default: step_sample<T>(a, wl); break;
         }
         // the LDS buffers are free for the next job
         __syncthreads();
@@ -400,18 +411,26 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
     const int64_t rows_d = (int64_t)kStepWaves * rows_per_wave(kcd);
     const int64_t rows_dl = (int64_t)kStepWaves * (rows_per_wave(kcd) + lds_rows_per_wave(kcd));
     const int64_t rows_fl = (int64_t)kStepWaves * (rows_per_wave(kcf) + lds_rows_per_wave(kcf));
+    // LM head: at most one full-size job per work-group (their weights load
+    // while the last layer runs), the remaining rows in small jobs spread
+    // over the grid (a second full-size round would load its weights only
+    // after the first)
+    const int64_t G = num_cus();
+    const int64_t head_a = std::min(cdiv(vocab, rows_dl), G);
+    const int64_t split = std::min(vocab, head_a * rows_dl);
     const int64_t nj[kKinds] = {cdiv((hq + 2 * hkv) * hd, rows_d), hq, cdiv(d, rows_d), cdiv(2 * ffn, rows_dl),
-                                cdiv(d, rows_fl), cdiv(vocab, rows_dl), 1};
+                                cdiv(d, rows_fl), head_a, cdiv(vocab - split, (int64_t)kStepWaves * kHeadTailRows), 1};
+    a.head_split = split;
     int64_t per_layer = 0;
     for (int k = 0; k < kLayerKinds; ++k) per_layer += nj[k];
-    const int64_t total = n_layers * per_layer + nj[5] + nj[6];
+    const int64_t total = n_layers * per_layer + nj[5] + nj[6] + nj[7];
     if (total > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     for (int k = 0; k < kKinds; ++k) a.njobs[k] = (int)nj[k];
     a.per_layer = (int)per_layer;
     a.total = (int)total;
     // one work-group per CU: all resident at once (a job waits only on jobs
     // with lower indices, which resident work-groups run)
-    const dim3 grid((unsigned)num_cus());
+    const dim3 grid((unsigned)G);
     hipStream_t st = as_stream(stream);
     if (dtype == KUIOPS_BF16) launch_step<bf16_t>(a, kcd, kcf, grid, st);
     else launch_step<f16_t>(a, kcd, kcf, grid, st);
