@@ -452,48 +452,53 @@ typedef struct kuiops_step_layer {
     void *k_cache, *v_cache;
 } kuiops_step_layer;
 
-/* One greedy decode step of a Llama-style decoder for one sequence.
- * `layers` points to a DEVICE array of n_layers kuiops_step_layer.  The
- * token id is read from tok[0] (device int64, an index into embed
- * [vocab, d]), the position from pos[0] and the key count from kv_len[0]
- * (device int32).  Results: logits [vocab] (device, dtype, 16-byte aligned);
- * tok[0] = arg-max of softmax(logits) (lowest index on ties); prob[0] = its
- * probability (optional); history[pos] = tok when history is non-null and
- * pos < hist_len; then pos[0] += 1 and kv_len[0] += 1.  The arithmetic,
- * rounding points and summation orders are those of the per-op sequence
- * kuiops_decode_qkv_rope -> kuiops_sdpa_decode -> kuiops_decode_linear (o) ->
- * kuiops_decode_gate_up -> kuiops_decode_linear (down) per layer, then
- * kuiops_decode_linear (LM head, RMSNorm input) and kuiops_softmax_top1, so
- * its results are bitwise those of that sequence.  One persistent launch:
- * work-groups take the projection row blocks, attention rows and the
- * sampling row in order; the vectors they hand each other live in `scratch`
- * (kuiops_decode_step_scratch_bytes(d, ffn, hq, hkv, hd) bytes, 16-byte
- * aligned, zero before the first call) as epoch-tagged words, and `sync`
- * (kuiops_decode_step_sync_bytes(n_layers) bytes, zero before the first
- * call) holds the LM head's completion counters, an error word and the step
- * counter.  Keep both buffers for the life of the decoder (the step counter
- * keeps old scratch contents from matching).  A work-group issues its weight
- * loads before it waits for its input, so weight streaming overlaps the
- * phase boundaries.  If a wait exceeds its bound (work-groups not
- * co-resident) the step stops waiting, its results are undefined and the
- * error word is set: kuiops_decode_step_error reads and clears it.  Calls must
- * not overlap on one `sync` / `scratch` pair.  Attention runs one
- * work-group per query row over every key (the row-wide form of
- * kuiops_sdpa_decode), so long caches are slow here.  Shapes: bf16 / f16, hd
- * 64 or 128, d = hq*hd <= 4096, ffn <= 8192, ffn % 8 == 0, vocab <= 32768;
- * otherwise KUIOPS_E_UNSUPPORTED.  No reference counterpart: it replaces the
- * whole per-token launch sequence of a batch-1 greedy decode (the reference
- * runs each aten op of generate() as its own launch, infer.py:14-31,
- * KERNELS.md).                                                             */
+/* n_steps (1 .. 16) greedy decode steps of a Llama-style decoder for one
+ * sequence, in one launch.  `layers` points to a DEVICE array of n_layers
+ * kuiops_step_layer.  The token id is read from tok[0] (device int64, an
+ * index into embed [vocab, d]), the position from pos[0] and the key count
+ * from kv_len[0] (device int32).  Each step: logits [vocab] (device, dtype,
+ * 16-byte aligned); its token = arg-max of softmax(logits) (lowest index on
+ * ties), recorded at history[pos] when history is non-null and pos <
+ * hist_len; pos and kv_len advance by one and the token feeds the next step.
+ * After the call tok[0], pos[0] and kv_len[0] hold the state after the last
+ * step, prob[0] (optional) the last token's probability and logits the last
+ * step's.  The arithmetic, rounding points and summation orders are those of
+ * the per-op sequence kuiops_decode_qkv_rope -> kuiops_sdpa_decode ->
+ * kuiops_decode_linear (o) -> kuiops_decode_gate_up -> kuiops_decode_linear
+ * (down) per layer, then kuiops_decode_linear (LM head, RMSNorm input) and
+ * kuiops_softmax_top1, so its results are bitwise those of that sequence run
+ * n_steps times.  One persistent launch: work-groups take the projection row
+ * blocks, attention rows and sampling rows of every step in order (the next
+ * step's weights stream while a step's LM head and sampling run); the
+ * vectors they hand each other live in `scratch`
+ * (kuiops_decode_step_scratch_bytes(n_layers, n_steps, d, ffn, hq, hkv, hd)
+ * bytes, 16-byte aligned, zero before the first call) as epoch-tagged words,
+ * and `sync` (kuiops_decode_step_sync_bytes(n_layers) bytes, zero before the
+ * first call) holds the LM head's completion counters, an error word, the
+ * step counter and the token hand-over word.  Keep both buffers for the life
+ * of the decoder (the step counter keeps old scratch contents from
+ * matching).  A work-group issues its weight loads before it waits for its
+ * input, so weight streaming overlaps the phase boundaries.  If a wait
+ * exceeds its bound (work-groups not co-resident) the step stops waiting,
+ * its results are undefined and the error word is set:
+ * kuiops_decode_step_error reads and clears it.  Calls must not overlap on
+ * one `sync` / `scratch` pair.  Attention runs one work-group per query row
+ * over every key (the row-wide form of kuiops_sdpa_decode), so long caches
+ * are slow here.  Shapes: bf16 / f16, hd 64 or 128, d = hq*hd <= 4096, ffn
+ * <= 8192, ffn % 8 == 0, vocab <= 32768; otherwise KUIOPS_E_UNSUPPORTED.  No
+ * reference counterpart: it replaces the whole per-token launch sequence of a
+ * batch-1 greedy decode (the reference runs each aten op of generate() as its
+ * own launch, infer.py:14-31, KERNELS.md).                                 */
 KUIOPS_API size_t kuiops_decode_step_sync_bytes(int64_t n_layers);
-KUIOPS_API size_t kuiops_decode_step_scratch_bytes(int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd);
+KUIOPS_API size_t kuiops_decode_step_scratch_bytes(int64_t n_layers, int64_t n_steps, int64_t d, int64_t ffn,
+                                                   int64_t hq, int64_t hkv, int64_t hd);
 KUIOPS_API int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd,
                        int64_t vocab, int64_t cache_cap, int dtype, float eps,
                        const kuiops_step_layer *layers, int64_t sk_head, int64_t sk_pos, int64_t sv_head,
                        int64_t sv_pos, const void *embed, const void *final_norm, const void *lm_head,
                        const float *inv_freq, int64_t *tok, int32_t *pos, int32_t *kv_len,
-                       int64_t *history, int64_t hist_len, float *prob, void *logits, void *scratch,
-                       size_t scratch_bytes, void *sync, size_t sync_bytes, void *stream);
+                       int64_t *history, int64_t hist_len, float *prob, void *logits, int64_t n_steps,
+                       void *scratch, size_t scratch_bytes, void *sync, size_t sync_bytes, void *stream);
 /* 1 when a previous kuiops_decode_step on `sync` hit its wait bound (then
  * clears the flag), else 0; <0 on a HIP error.  Synchronises the stream.   */
 KUIOPS_API int kuiops_decode_step_error(void *sync, int64_t n_layers, void *stream);

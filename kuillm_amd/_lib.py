@@ -92,10 +92,10 @@ SIGNATURES = {
                                       _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                       _vp]),
     "kuiops_decode_step_sync_bytes": (_sz, [_i64]),
-    "kuiops_decode_step_scratch_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "kuiops_decode_step_scratch_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "kuiops_decode_step": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _flt, _vp, _i64, _i64,
-                                  _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _sz,
-                                  _vp, _sz, _vp]),
+                                  _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp,
+                                  _sz, _vp, _sz, _vp]),
     "kuiops_decode_step_error": (_int, [_vp, _i64, _vp]),
 }
 

@@ -37,6 +37,13 @@ struct AttnArgs {
     uint32_t ep_q, ep_o;
     const void *kfresh, *vfresh;
     unsigned *err;
+    // one-pass form: the key count itself (use_s_len), and the keys
+    // fresh_lo .. fresh read from epoch-tagged slots: key fresh_lo + i at
+    // kfresh / vfresh + i * fresh_stride elements, written with epoch
+    // ep_fresh0 + i * ep_fresh_step
+    int64_t s_len; int use_s_len;
+    int64_t fresh_lo, fresh_stride;
+    uint32_t ep_fresh0, ep_fresh_step;
 };
 
 constexpr float kLn2 = 0.69314718055994530942f;
@@ -460,7 +467,8 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     const int head = hk * G + rr / LQ, qi = rr % LQ;
     const T *Kp = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
     const T *Vp = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
-    const int64_t s_b = a.kv_len ? max((int64_t)0, min((int64_t)a.kv_len[b], a.s)) : a.s;
+    const int64_t s_b = a.use_s_len ? max((int64_t)0, min(a.s_len, a.s))
+                                    : a.kv_len ? max((int64_t)0, min((int64_t)a.kv_len[b], a.s)) : a.s;
     constexpr int KPJ = NWV * KPW;                                 // keys per j
     const int64_t kw = (int64_t)wave * KPW + kg;                  // this lane group's key j = 0
 
@@ -475,13 +483,27 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     };
     if constexpr (PF) load_kv();
 
+    // this lane's key among fresh_lo .. fresh (keys of a lane are KPJ apart,
+    // so at most one when the range is shorter than KPJ): its j, or -1
+    int jw = -1;
+    int64_t sw = 0;
+    if (IO::kLL && fresh >= 0) {
+        const int64_t lo = min(a.fresh_lo, fresh);
+        const int64_t jj = lo > kw ? (lo - kw + KPJ - 1) / KPJ : 0;
+        if (jj < NB && kw + jj * KPJ <= fresh) {
+            jw = (int)jj;
+            sw = kw + jj * KPJ - lo;
+        }
+    }
     u32x4 qraw, kfr = {0, 0, 0, 0}, vfr = {0, 0, 0, 0};
     auto load_q = [&]() -> bool {
         bool ok = IO::ld8(a.Q, b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8, a.ep_q, qraw);
         if constexpr (IO::kLL) {
-            if (fresh >= 0) {
-                ok = IO::ld8(a.kfresh, hk * HD + dl * 8, a.ep_q, kfr) && ok;
-                ok = IO::ld8(a.vfresh, hk * HD + dl * 8, a.ep_q, vfr) && ok;
+            if (jw >= 0) {
+                const int64_t e = sw * a.fresh_stride + hk * HD + dl * 8;
+                const uint32_t ep = a.ep_fresh0 + (uint32_t)sw * a.ep_fresh_step;
+                ok = IO::ld8(a.kfresh, e, ep, kfr) && ok;
+                ok = IO::ld8(a.vfresh, e, ep, vfr) && ok;
             }
         }
         return ok;
@@ -505,7 +527,7 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     if (PF && fresh >= 0) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            if (kw + j * KPJ == fresh) {
+            if (IO::kLL ? j == jw : kw + j * KPJ == fresh) {
                 if constexpr (IO::kLL) {
                     kr[j] = kfr;
                     vr[j] = vfr;

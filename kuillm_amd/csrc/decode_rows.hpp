@@ -46,8 +46,11 @@ struct DecLinArgs {
     const void *bias;
     void *out;
     int rpw;                           // rows per wave
-    // optional device row index of `in` (in += in_row[0] * ld_in, clamped to in_rows)
+    // optional device row index of `in` (in += in_row[0] * ld_in, clamped to
+    // in_rows), or (row_ll) an epoch-tagged word holding the row index in its
+    // low 32 bits, awaited with epoch ep_row before the input is read
     const int64_t *in_row; int64_t ld_in, in_rows;
+    const void *row_ll; uint32_t ep_row;
     // paired epilogues: logical row 2p + e is W row base(p) + e * pair_off
     int64_t pair_off;
     int pair_shift;                    // log2(pair_off) when a power of two, else -1
@@ -55,6 +58,7 @@ struct DecLinArgs {
     int64_t hq, hkv, hd;
     const float *inv_freq;
     const int32_t *pos;                // device position of the token
+    int64_t pos_val; int use_pos_val;  // or the position itself
     void *kc; int64_t sk1, sk2;        // k cache: head, position strides
     void *vc; int64_t sv1, sv2;
     int64_t cap;
@@ -197,7 +201,7 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
     int64_t rope_pos = 0;
     float rope_freq = 0.f;
     if constexpr (OK == kOutRope) {
-        rope_pos = a.pos ? (int64_t)a.pos[0] : 0;
+        rope_pos = a.use_pos_val ? a.pos_val : (a.pos ? (int64_t)a.pos[0] : 0);
         if (lane % (128 / RG) == 0) {               // the lane that finishes pair lane / (128 / RG)
             const int g = 2 * (lane / (128 / RG));
             const int64_t p = (r0 + g) >> 1, half = a.pair_off, head = pair_div(a, p);
@@ -293,6 +297,19 @@ __device__ __forceinline__ void decode_rows_block(const DecLinArgs &a, int64_t b
         }
         __syncthreads();
     } else {
+        if (a.row_ll) {
+            // the row index comes from another work-group of the launch
+            uint64_t w = LLIO::word(a.row_ll, 0);
+            unsigned e = ll_err_read(a.err);
+            for (unsigned it = 0; !__all((uint32_t)(w >> 32) == a.ep_row); ++it) {
+                if (ll_expired(it, e, a.err)) break;
+                __builtin_amdgcn_s_sleep(kLLSleep);
+                w = LLIO::word(a.row_ll, 0);
+                e = ll_err_read(a.err);
+            }
+            in = reinterpret_cast<const T *>(a.in) +
+                 max((int64_t)0, min((int64_t)(uint32_t)w, a.in_rows - 1)) * a.ld_in;
+        }
         load_input();
     }
     float h[XCH][8];

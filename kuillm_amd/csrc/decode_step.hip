@@ -58,6 +58,7 @@ constexpr int kLayerKinds = 5;
 constexpr int kSubCounters = 8;           // completion counters of the LM-head phase (spread contention)
 constexpr int kCounterStride = 32;        // uint32 apart: one 128-byte line each
 constexpr unsigned kSpinLimit = 1u << 20; // polls per wait (~1 s)
+constexpr int kMaxSteps = 16;             // tokens per launch (the attention window of fresh keys < 32)
 
 struct StepArgs {
     int layers;
@@ -73,32 +74,54 @@ struct StepArgs {
     int64_t *history;
     int64_t hist_len;
     float *prob;
-    void *h0, *h1, *q, *att, *o, *act, *down, *kf, *vf;   // epoch-tagged (scratch)
+    void *h0, *h1, *q, *att, *o, *act, *down;   // epoch-tagged (scratch)
+    void *kf, *vf;                        // epoch-tagged new k / v rows, [layers][steps][hkv * hd]
     void *logits;
     unsigned *sync;
     int njobs[kKinds];
-    int per_layer, total;
+    int per_layer, per_token, steps, total;
     int64_t head_split;                   // LM-head rows of the full-size jobs (kind 5); kind 6 takes the rest
 };
 
+// The job functions take the launch's arguments by reference.  (The
+// compiler gives the kernel's by-value parameter a per-lane copy in scratch
+// for it; measured against a constant- or LDS-address-space reference,
+// whose bodies spill, this is the faster form.)
+typedef const StepArgs &StepArgsRef;
+
 // sync: kSubCounters counters of the LM-head phase, the error word, the step
-// epoch (one 128-byte line each)
-__device__ __forceinline__ unsigned *counter_of(const StepArgs &a, int k) { return a.sync + k * kCounterStride; }
-__device__ __forceinline__ unsigned *error_word(const StepArgs &a) { return a.sync + kSubCounters * kCounterStride; }
-__device__ __forceinline__ unsigned *epoch_word(const StepArgs &a) { return a.sync + (kSubCounters + 1) * kCounterStride; }
+// epoch, the epoch-tagged sampled token (one 128-byte line each)
+__device__ __forceinline__ unsigned *counter_of(StepArgsRef a, int k) { return a.sync + k * kCounterStride; }
+__device__ __forceinline__ unsigned *error_word(StepArgsRef a) { return a.sync + kSubCounters * kCounterStride; }
+__device__ __forceinline__ unsigned *epoch_word(StepArgsRef a) { return a.sync + (kSubCounters + 1) * kCounterStride; }
+__device__ __forceinline__ void *token_word(StepArgsRef a) { return a.sync + (kSubCounters + 2) * kCounterStride; }
+
+// Token t of a launch: its step (epoch counter), position and key count.
+// Each sampling job advances the position and the key count by one, so
+// token t's are the launch's starting values plus t.
+struct StepTok {
+    int t;
+    uint32_t step;
+    int64_t pos, kv;
+};
+
+// The epoch-tagged new k / v rows of layer l, token t (element offset).
+__device__ __forceinline__ int64_t fresh_slot(StepArgsRef a, int l, int t) {
+    return ((int64_t)l * a.steps + t) * a.hkv * a.hd;
+}
 
 // Epoch of the vectors written by layer l (l = layers: none) in this step.
-__device__ __forceinline__ uint32_t epoch_of(const StepArgs &a, uint32_t step, int l) {
+__device__ __forceinline__ uint32_t epoch_of(StepArgsRef a, uint32_t step, int l) {
     return step * (uint32_t)(a.layers + 1) + (uint32_t)l + 1u;
 }
 
-// Waits until every LM-head job has signalled.  Wave 0 polls the counters
-// (lanes 0..7) and the error word (lane 8); all threads leave through the
-// barrier.
-__device__ __forceinline__ void wait_head(const StepArgs &a) {
+// Waits until every LM-head job of tokens 0 .. t has signalled (the
+// counters accumulate over the launch).  Wave 0 polls the counters (lanes
+// 0..7) and the error word (lane 8); all threads leave through the barrier.
+__device__ __forceinline__ void wait_head(StepArgsRef a, int t) {
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        const unsigned need = (unsigned)(a.njobs[5] + a.njobs[6]);
+        const unsigned need = (unsigned)((t + 1) * (a.njobs[5] + a.njobs[6]));
         for (unsigned it = 0;; ++it) {
             unsigned v = 0, err = 0;
             if (lane < kSubCounters)
@@ -122,7 +145,7 @@ __device__ __forceinline__ void wait_head(const StepArgs &a) {
 }
 
 // Publishes the calling work-group's LM-head job `idx`.
-__device__ __forceinline__ void signal_head(const StepArgs &a, int idx) {
+__device__ __forceinline__ void signal_head(StepArgsRef a, int idx) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -144,7 +167,8 @@ constexpr int kLdsRowBytes = kStepWaves * 16 * 1024;
 constexpr int kLdsXBytes = kDecodeMaxK * 2;         // the staged input x
 
 // The projection of layer `l` of one kind, as the per-op entry points set it up.
-__device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int l, int rpw, uint32_t step) {
+__device__ __forceinline__ DecLinArgs proj_args(StepArgsRef a, int kind, int l, int rpw, const StepTok tk) {
+    const uint32_t step = tk.step;
     DecLinArgs p{};
     p.eps = a.eps;
     p.rpw = rpw;
@@ -167,18 +191,28 @@ __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int
         case 0:                           // qkv: RMSNorm(h0 + down) (layer 0: the embedding row), rotary + KV
             p.N = (a.hq + 2 * a.hkv) * a.hd; p.K = a.d;
             if (l == 0) {
-                p.in = a.embed; p.in_row = a.tok; p.ld_in = a.d; p.in_rows = a.vocab;
+                // the embedding row of the token: from the previous launch, or
+                // (later tokens) from this launch's sampling job
+                p.in = a.embed; p.ld_in = a.d; p.in_rows = a.vocab;
+                if (tk.t == 0) {
+                    p.in_row = a.tok;
+                } else {
+                    p.row_ll = token_word(a);
+                    p.ep_row = step;
+                }
             } else {
                 p.in = a.h0; p.in_add = a.down;
             }
             p.norm_w = L.ln1; p.h_out = a.h1;
             p.W = L.wqkv; p.ldw = a.d; p.out = a.q;
             p.pair_off = a.hd / 2; p.pair_shift = a.shift_hd;
-            p.hq = a.hq; p.hkv = a.hkv; p.hd = a.hd; p.inv_freq = a.inv_freq; p.pos = a.pos;
+            p.hq = a.hq; p.hkv = a.hkv; p.hd = a.hd; p.inv_freq = a.inv_freq;
+            p.use_pos_val = 1; p.pos_val = tk.pos;
             p.kc = L.k_cache; p.sk1 = a.sk1; p.sk2 = a.sk2;
             p.vc = L.v_cache; p.sv1 = a.sv1; p.sv2 = a.sv2;
             p.cap = a.cap;
-            p.kfresh = a.kf; p.vfresh = a.vf;
+            p.kfresh = reinterpret_cast<char *>(a.kf) + fresh_slot(a, l, tk.t) * 4;   // (2 elements per 8 bytes)
+            p.vfresh = reinterpret_cast<char *>(a.vf) + fresh_slot(a, l, tk.t) * 4;
             break;
         case 2:                           // o: plain input (the attention rows)
             p.N = a.d; p.K = a.hq * a.hd;
@@ -201,22 +235,22 @@ __device__ __forceinline__ DecLinArgs proj_args(const StepArgs &a, int kind, int
 // The job kinds, each its own function: inlined into one loop, the bodies'
 // register demands add up (spills); as calls each gets its own allocation.
 template <typename T, int XK, int KC, int OK, int RGL, typename IO, typename OIO, int RG = rows_per_wave(KC)>
-__device__ __attribute__((noinline)) void step_proj(const StepArgs &a, int kind, int l, int idx, uint32_t step,
+__device__ __attribute__((noinline)) void step_proj(StepArgsRef a, int kind, int l, int idx, const StepTok tk,
                                                     lds_bytes *wl) {
     decode_rows_block<T, XK, KC, OK, kStepWaves, NoWait, IO, RG, RGL, true, OIO>(
-        proj_args(a, kind, l, RG + RGL, step), idx, NoWait{}, wl, wl + kLdsRowBytes);
+        proj_args(a, kind, l, RG + RGL, tk), idx, NoWait{}, wl, wl + kLdsRowBytes);
 }
 
 // attention row `idx` (query head) of layer l, as the per-op row-wide launch
 // runs it: one work-group per query row, every key in one pass.  The cache
-// rows before this token's position do not depend on the qkv phase: their
-// loads are issued before the query is awaited, and the row at the position
-// comes from the qkv phase's epoch-tagged copy.
+// rows written by earlier launches do not depend on the qkv phase: their
+// loads are issued before the query is awaited; the rows of this launch's
+// tokens (positions pos - t .. pos) come from the qkv phases' epoch-tagged
+// copies.
 template <typename T, int HD>
-__device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int l, int idx, uint32_t step) {
+__device__ __attribute__((noinline)) void step_attention(StepArgsRef a, int l, int idx, const StepTok tk) {
     // (the qkv phase writes the new row only when it is inside the cache)
-    const int64_t p = *a.pos;
-    const int64_t fresh = p >= 0 && p < a.cap ? p : -1;
+    const int64_t fresh = tk.pos >= 0 && tk.pos < a.cap ? tk.pos : -1;
     const kuiops_step_layer &L = a.layer[l];
     AttnArgs at{};
     at.n = 1; at.hq = a.hq; at.hkv = a.hkv; at.l = 1; at.s = a.cap;
@@ -229,29 +263,48 @@ __device__ __attribute__((noinline)) void step_attention(const StepArgs &a, int 
     at.causal = 1;
     at.splits = 1; at.chunk = a.cap;
     at.rows_per_group = 1; at.row_groups = (int)(a.hq / a.hkv);
-    at.kv_len = a.kv_len;
-    at.ep_q = at.ep_o = epoch_of(a, step, l);
-    at.kfresh = a.kf; at.vfresh = a.vf;
+    at.use_s_len = 1; at.s_len = tk.kv;
+    at.ep_q = at.ep_o = epoch_of(a, tk.step, l);
+    at.kfresh = reinterpret_cast<const char *>(a.kf) + fresh_slot(a, l, 0) * 4;
+    at.vfresh = reinterpret_cast<const char *>(a.vf) + fresh_slot(a, l, 0) * 4;
+    at.fresh_lo = tk.pos - tk.t; at.fresh_stride = a.hkv * a.hd;
+    at.ep_fresh0 = epoch_of(a, tk.step - (uint32_t)tk.t, l); at.ep_fresh_step = (uint32_t)(a.layers + 1);
     at.err = error_word(a);
     fa_decode_onepass_block<T, HD, kStepWaves, 12, LLIO, true>(at, idx, 0, fresh);
 }
 
-// softmax + top-1 of the logits and the decode-state advance; every other
-// job has finished by then (each phase waited on the one before it), so the
-// counters are left zero and the step epoch advances for the next step
+// softmax + top-1 of token t's logits.  The token goes to history[pos] and,
+// for the next token of the launch, to the epoch-tagged token word.  The
+// last token's sampling job runs after every other job of the launch has
+// finished (each phase waited on the one before it): it writes the decode
+// state for the next launch (token, position, key count, probability), zeroes
+// the counters and advances the step epoch.
 template <typename T>
-__device__ __attribute__((noinline)) void step_sample(const StepArgs &a, lds_bytes *wl) {
-    wait_head(a);
-    softmax_top1_row<T, kStepThreads, CoherentIO>(a.vocab, reinterpret_cast<const T *>(a.logits), a.prob, a.tok,
-                                                  a.pos, a.kv_len, a.history, a.hist_len, wl);
+__device__ __attribute__((noinline)) void step_sample(StepArgsRef a, const StepTok tk, lds_bytes *wl) {
+    const bool last = tk.t == a.steps - 1;
+    wait_head(a, tk.t);
+    __shared__ int64_t s_tok;
+    softmax_top1_row<T, kStepThreads, CoherentIO>(a.vocab, reinterpret_cast<const T *>(a.logits),
+                                                  last ? a.prob : nullptr, &s_tok, nullptr, nullptr, nullptr, 0, wl);
     __syncthreads();
-    if (threadIdx.x < kSubCounters)
+    if (threadIdx.x == 0) {
+        const int64_t i = s_tok;
+        if (a.history && tk.pos >= 0 && tk.pos < a.hist_len) a.history[tk.pos] = i;
+        if (!last) {
+            LLIO::put(token_word(a), 0, (uint32_t)i, tk.step + 1u);
+        } else {
+            *a.tok = i;
+            *a.pos = (int32_t)(tk.pos + 1);
+            *a.kv_len = (int32_t)(tk.kv + 1);
+            *epoch_word(a) = tk.step + 1u;
+        }
+    }
+    if (last && threadIdx.x < kSubCounters)
         __hip_atomic_store(counter_of(a, threadIdx.x), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) *epoch_word(a) += 1u;
 }
 
 // Job j of the step's list: layer, kind and index within the kind.
-__device__ __forceinline__ void job_of(const StepArgs &a, int j, int &l, int &kind, int &idx) {
+__device__ __forceinline__ void job_of(StepArgsRef a, int j, int &l, int &kind, int &idx) {
     if (j < a.layers * a.per_layer) {
         l = j / a.per_layer;
         idx = j - l * a.per_layer;
@@ -270,31 +323,36 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
     constexpr int RLD = lds_rows_per_wave(KCD), RLF = lds_rows_per_wave(KCF);
     __shared__ __attribute__((aligned(1024))) char s_wl[kLdsRowBytes + kLdsXBytes];
     lds_bytes *wl = (lds_bytes *)s_wl;
+    StepArgsRef args = a;
     const int G = gridDim.x;
-    // the step counter: advanced only by the sampling job, which runs after
-    // every other job has finished (and so has read it)
-    const uint32_t step = *epoch_word(a);
-    for (int j = blockIdx.x; j < a.total; j += G) {
+    // The step counter and the decode state as the previous launch left
+    // them: written only by this launch's last sampling job, which runs after
+    // every other job has finished (and so every work-group has read them).
+    const uint32_t step0 = *epoch_word(args);
+    const int64_t pos0 = *args.pos, kv0 = *args.kv_len;
+    for (int j = blockIdx.x; j < args.total; j += G) {
+        const int t = j / args.per_token;
+        const StepTok tk{t, step0 + (uint32_t)t, pos0 + t, kv0 + t};
         int l, kind, idx;
-        job_of(a, j, l, kind, idx);
+        job_of(args, j - t * args.per_token, l, kind, idx);
         switch (kind) {
             case 0:
-                if (l == 0) step_proj<T, kXRmsNorm, KCD, kOutRope, 0, PlainIO, LLIO>(a, 0, l, idx, step, wl);
-                else step_proj<T, kXRmsNorm, KCD, kOutRope, 0, LLIO, LLIO>(a, 0, l, idx, step, wl);
+                if (l == 0) step_proj<T, kXRmsNorm, KCD, kOutRope, 0, PlainIO, LLIO>(args, 0, l, idx, tk, wl);
+                else step_proj<T, kXRmsNorm, KCD, kOutRope, 0, LLIO, LLIO>(args, 0, l, idx, tk, wl);
                 break;
-            case 1: step_attention<T, HD>(a, l, idx, step); break;
-            case 2: step_proj<T, kXPlain, KCD, kOutPlain, 0, LLIO, LLIO>(a, 2, l, idx, step, wl); break;
-            case 3: step_proj<T, kXRmsNorm, KCD, kOutSwiGlu, RLD, LLIO, LLIO>(a, 3, l, idx, step, wl); break;
-            case 4: step_proj<T, kXPlain, KCF, kOutPlain, RLF, LLIO, LLIO>(a, 4, l, idx, step, wl); break;
+            case 1: step_attention<T, HD>(args, l, idx, tk); break;
+            case 2: step_proj<T, kXPlain, KCD, kOutPlain, 0, LLIO, LLIO>(args, 2, l, idx, tk, wl); break;
+            case 3: step_proj<T, kXRmsNorm, KCD, kOutSwiGlu, RLD, LLIO, LLIO>(args, 3, l, idx, tk, wl); break;
+            case 4: step_proj<T, kXPlain, KCF, kOutPlain, RLF, LLIO, LLIO>(args, 4, l, idx, tk, wl); break;
             case 5:
-                step_proj<T, kXRmsNorm, KCD, kOutPlain, RLD, LLIO, CoherentIO>(a, 5, l, idx, step, wl);
-                signal_head(a, idx);
+                step_proj<T, kXRmsNorm, KCD, kOutPlain, RLD, LLIO, CoherentIO>(args, 5, l, idx, tk, wl);
+                signal_head(args, idx);
                 break;
             case 6:
-                step_proj<T, kXRmsNorm, KCD, kOutPlain, 0, LLIO, CoherentIO, kHeadTailRows>(a, 6, l, idx, step, wl);
-                signal_head(a, idx);
+                step_proj<T, kXRmsNorm, KCD, kOutPlain, 0, LLIO, CoherentIO, kHeadTailRows>(args, 6, l, idx, tk, wl);
+                signal_head(args, idx);
                 break;
-            default: step_sample<T>(a, wl); break;
+            default: step_sample<T>(args, tk, wl); break;
         }
         // the LDS buffers are free for the next job
         __syncthreads();
@@ -339,10 +397,12 @@ static void launch_step(const StepArgs &a, int kcd, int kcf, dim3 grid, hipStrea
 using namespace kuiops;
 
 // Epoch-tagged scratch vectors, in elements: h0, h1 [d], q, att [hq*hd],
-// o [d], act [ffn], down [d], k / v copies [hkv*hd]; two elements per 8-byte
-// word, each vector 256-byte aligned.
-static size_t step_scratch_layout(int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd, size_t off[9]) {
-    const int64_t n[9] = {d, d, hq * hd, hq * hd, d, ffn, d, hkv * hd, hkv * hd};
+// o [d], act [ffn], down [d], k / v copies [layers][steps][hkv*hd]; two
+// elements per 8-byte word, each vector 256-byte aligned.
+static size_t step_scratch_layout(int64_t n_layers, int64_t n_steps, int64_t d, int64_t ffn, int64_t hq,
+                                  int64_t hkv, int64_t hd, size_t off[9]) {
+    const int64_t kv = n_layers * n_steps * hkv * hd;
+    const int64_t n[9] = {d, d, hq * hd, hq * hd, d, ffn, d, kv, kv};
     size_t o = 0;
     for (int i = 0; i < 9; ++i) {
         off[i] = o;
@@ -353,13 +413,14 @@ static size_t step_scratch_layout(int64_t d, int64_t ffn, int64_t hq, int64_t hk
 
 extern "C" size_t kuiops_decode_step_sync_bytes(int64_t n_layers) {
     (void)n_layers;
-    return (size_t)(kSubCounters + 2) * kCounterStride * sizeof(unsigned);
+    return (size_t)(kSubCounters + 3) * kCounterStride * sizeof(unsigned);
 }
 
-extern "C" size_t kuiops_decode_step_scratch_bytes(int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd) {
-    if (d <= 0 || ffn <= 0 || hq <= 0 || hkv <= 0 || hd <= 0) return 0;
+extern "C" size_t kuiops_decode_step_scratch_bytes(int64_t n_layers, int64_t n_steps, int64_t d, int64_t ffn,
+                                                   int64_t hq, int64_t hkv, int64_t hd) {
+    if (n_layers <= 0 || n_steps <= 0 || d <= 0 || ffn <= 0 || hq <= 0 || hkv <= 0 || hd <= 0) return 0;
     size_t off[9];
-    return step_scratch_layout(d, ffn, hq, hkv, hd, off);
+    return step_scratch_layout(n_layers, n_steps, d, ffn, hq, hkv, hd, off);
 }
 
 extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd,
@@ -368,8 +429,8 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
                                   int64_t sv_head, int64_t sv_pos, const void *embed, const void *final_norm,
                                   const void *lm_head, const float *inv_freq, int64_t *tok, int32_t *pos,
                                   int32_t *kv_len, int64_t *history, int64_t hist_len, float *prob, void *logits,
-                                  void *scratch, size_t scratch_bytes, void *sync, size_t sync_bytes,
-                                  void *stream) {
+                                  int64_t n_steps, void *scratch, size_t scratch_bytes, void *sync,
+                                  size_t sync_bytes, void *stream) {
     if (n_layers <= 0 || d <= 0 || ffn <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || vocab <= 0 || cache_cap <= 0)
         return KUIOPS_E_INVALID;
     if (hq % hkv || hd % 2) return KUIOPS_E_INVALID;
@@ -383,8 +444,10 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
     if (kcd == 0 || kcd > 8 || kcf == 0) return KUIOPS_E_UNSUPPORTED;   // paired epilogues: d <= 4096
     if (vocab > (int64_t)kSmThreads * kSmCache || vocab > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     if (n_layers > 1024 || cache_cap > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    if (n_steps < 1 || n_steps > kMaxSteps) return KUIOPS_E_UNSUPPORTED;
     size_t off[9];
-    if (scratch_bytes < step_scratch_layout(d, ffn, hq, hkv, hd, off) || !aligned16(scratch)) return KUIOPS_E_WORKSPACE;
+    if (scratch_bytes < step_scratch_layout(n_layers, n_steps, d, ffn, hq, hkv, hd, off) || !aligned16(scratch))
+        return KUIOPS_E_WORKSPACE;
     if (sync_bytes < kuiops_decode_step_sync_bytes(n_layers) || !aligned16(sync)) return KUIOPS_E_WORKSPACE;
     for (const void *p : {embed, final_norm, lm_head, (const void *)logits})
         if (!aligned16(p)) return KUIOPS_E_UNSUPPORTED;
@@ -423,10 +486,13 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
     a.head_split = split;
     int64_t per_layer = 0;
     for (int k = 0; k < kLayerKinds; ++k) per_layer += nj[k];
-    const int64_t total = n_layers * per_layer + nj[5] + nj[6] + nj[7];
+    const int64_t per_token = n_layers * per_layer + nj[5] + nj[6] + nj[7];
+    const int64_t total = n_steps * per_token;
     if (total > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     for (int k = 0; k < kKinds; ++k) a.njobs[k] = (int)nj[k];
     a.per_layer = (int)per_layer;
+    a.per_token = (int)per_token;
+    a.steps = (int)n_steps;
     a.total = (int)total;
     // one work-group per CU: all resident at once (a job waits only on jobs
     // with lower indices, which resident work-groups run)

@@ -111,6 +111,7 @@ class LlamaDecoder:
         self.step_state = torch.zeros((2, self.n), dtype=torch.int32, device=self.dev)
         self.pos, self.kv_len = self.step_state[0], self.step_state[1]
         self.graph = None
+        self.graph_k = None
         self.fused = self.n == 1 and s.d <= 4096 and s.ffn <= 8192 and s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0
         # batches of 2..16: the batched form of the same fused projections
         # (every row of x staged in LDS: n * max(d, ffn) * 2 <= 140 KiB)
@@ -126,6 +127,9 @@ class LlamaDecoder:
         row_wide_keys = 8 * (64 // (s.hd // 8)) * 12
         self.persistent = (self.fused and s.d == s.hq * s.hd and s.d <= 4096 and s.vocab <= 32768
                            and self.cap <= row_wide_keys)
+        # persistent launches run this many steps each (the next step's
+        # weights stream while a step's LM head and sampling run)
+        self.steps_per_launch = 8 if self.persistent else 1
         if self.fused or self.fused_batched or self.fused_wide:
             self._setup_fused()
 
@@ -159,8 +163,9 @@ class LlamaDecoder:
                     for i, L in enumerate(self.layers)]
             self.layer_table = torch.tensor(ptrs, dtype=torch.int64, device=dev)
             self.step_sync = torch.zeros(ops.decode_step_sync_bytes(s.layers), dtype=torch.uint8, device=dev)
-            self.step_scratch = torch.zeros(ops.decode_step_scratch_bytes(s.d, s.ffn, s.hq, s.hkv, s.hd),
-                                            dtype=torch.uint8, device=dev)
+            self.step_scratch = torch.zeros(
+                ops.decode_step_scratch_bytes(s.layers, self.steps_per_launch, s.d, s.ffn, s.hq, s.hkv, s.hd),
+                dtype=torch.uint8, device=dev)
         # token chosen at each position (written by the step itself, so a
         # replayed step needs no copy out)
         self.history = torch.zeros(n, self.cap + 1, dtype=torch.int64, device=dev)
@@ -226,9 +231,11 @@ class LlamaDecoder:
         self.kv_len.fill_(t + 1)
         return logits, nxt
 
-    def _decode_step(self):
+    def _decode_step(self, n_steps: int = 1):
+        if n_steps != 1 and not self.persistent:
+            raise ValueError("several steps per launch need the persistent step")
         if self.fused:
-            return self._decode_step_fused()
+            return self._decode_step_fused(n_steps)
         if self.fused_batched:
             return self._decode_step_fused_batched()
         if self.fused_wide:
@@ -240,19 +247,20 @@ class LlamaDecoder:
         self.step_state.add_(1)
         return logits
 
-    def _decode_step_fused(self):
+    def _decode_step_fused(self, n_steps: int = 1):
         """One batch-1 decode step, same arithmetic as ``_layers`` + ``_head``
         (every rounding point kept), in 5 launches per layer plus LM head and
         a fused softmax / top-1 / state-advance launch: qkv (embedding
         lookup / RMSNorm stage, rotary + cache append epilogue) -> attention
         -> o -> gate|up (RMSNorm stage, SwiGLU epilogue) -> down.  With
-        ``persistent`` the same work, bit for bit, runs as one launch."""
+        ``persistent`` the same work, bit for bit, runs as one launch, which
+        can also run ``n_steps`` consecutive steps."""
         s = self.s
         if self.persistent:
             ops.decode_step(self.layer_table, s.layers, s.d, s.ffn, s.hq, s.hkv, s.hd, s.vocab, s.eps,
                             self.kcache[0, 0], self.vcache[0, 0], self.embed, self.norm, self.head, self.inv_freq,
                             self.tok, self.pos, self.kv_len, self.history[0], self.top_v.view(1),
-                            self.logits1, self.step_scratch, self.step_sync)
+                            self.logits1, self.step_scratch, self.step_sync, n_steps=n_steps)
             return self.logits1.view(1, -1)
         hb = self.h_buf
         cur = 0
@@ -342,25 +350,35 @@ class LlamaDecoder:
         return self.logitsb
 
     def capture(self):
-        """Record one decode step (all its kernels) in a HIP graph.  The step
-        reads the token, position and key count from device memory and
+        """Record one decode step (all its kernels) in a HIP graph, and with
+        the persistent step also one launch of steps_per_launch steps.  The
+        step reads the token, position and key count from device memory and
         advances them, so replays need no host work."""
         saved = (self.tok.clone(), self.pos.clone(), self.kv_len.clone(),
                  self.kcache.clone(), self.vcache.clone())
-        self._decode_step()                              # eager: allocates workspaces
-        torch.cuda.synchronize(self.dev)
-        g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(self.dev)
-        side.wait_stream(torch.cuda.current_stream(self.dev))
-        with torch.cuda.stream(side):
-            self._decode_step()
-        torch.cuda.current_stream(self.dev).wait_stream(side)
-        with torch.cuda.graph(g):
-            self.graph_logits = self._decode_step()
-        torch.cuda.synchronize(self.dev)
-        for dst, src in zip((self.tok, self.pos, self.kv_len, self.kcache, self.vcache), saved):
-            dst.copy_(src)
-        self.graph = g
+
+        def record(n_steps):
+            self._decode_step(n_steps)                   # eager: allocates workspaces
+            torch.cuda.synchronize(self.dev)
+            g = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream(self.dev)
+            side.wait_stream(torch.cuda.current_stream(self.dev))
+            with torch.cuda.stream(side):
+                self._decode_step(n_steps)
+            torch.cuda.current_stream(self.dev).wait_stream(side)
+            with torch.cuda.graph(g):
+                logits = self._decode_step(n_steps)
+            torch.cuda.synchronize(self.dev)
+            for dst, src in zip((self.tok, self.pos, self.kv_len, self.kcache, self.vcache), saved):
+                dst.copy_(src)
+            return g, logits
+
+        # (the capacity must hold the steps the recording runs)
+        k = self.steps_per_launch if self.persistent else 1
+        self.graph_k = None
+        if k > 1 and int(self.pos[0]) + 3 * k <= self.cap:
+            self.graph_k, _ = record(k)
+        self.graph, self.graph_logits = record(1)
 
     def decode(self, n_new: int, use_graph: bool = True) -> torch.Tensor:
         """Greedy-decode n_new tokens after ``prefill``; returns [n, n_new]
@@ -374,13 +392,23 @@ class LlamaDecoder:
             self.capture()
         out[0].copy_(self.tok)
         p0 = int(self.pos[0])
-        for i in range(1, n_new):
+        k = self.steps_per_launch if self.persistent else 1
+        i = 1
+        while i < n_new:
+            if n_new - i >= k > 1 and (not use_graph or self.graph_k is not None):
+                if use_graph:
+                    self.graph_k.replay()
+                else:
+                    self._decode_step(k)
+                i += k
+                continue
             if use_graph:
                 self.graph.replay()
             else:
                 self._decode_step()
             if not (self.fused or self.fused_batched or self.fused_wide):
                 out[i].copy_(self.tok)
+            i += 1
         if (self.fused or self.fused_batched or self.fused_wide) and n_new > 1:
             # the fused step recorded the token of position p at history[p]
             out[1:].copy_(self.history[:, p0:p0 + n_new - 1].t())

@@ -833,20 +833,22 @@ def decode_step_sync_bytes(n_layers: int) -> int:
     return int(_lib_handle().kuiops_decode_step_sync_bytes(n_layers))
 
 
-def decode_step_scratch_bytes(d: int, ffn: int, hq: int, hkv: int, hd: int) -> int:
-    """Bytes of the epoch-tagged vector buffer kuiops_decode_step needs."""
-    return int(_lib_handle().kuiops_decode_step_scratch_bytes(d, ffn, hq, hkv, hd))
+def decode_step_scratch_bytes(n_layers: int, n_steps: int, d: int, ffn: int, hq: int, hkv: int, hd: int) -> int:
+    """Bytes of the epoch-tagged vector buffer kuiops_decode_step needs for
+    up to n_steps steps per call."""
+    return int(_lib_handle().kuiops_decode_step_scratch_bytes(n_layers, n_steps, d, ffn, hq, hkv, hd))
 
 
 def decode_step(layer_table, n_layers, d, ffn, hq, hkv, hd, vocab, eps, k_cache, v_cache, embed, final_norm,
-                lm_head, inv_freq, tok, pos, kv_len, history, prob, logits, scratch, sync):
-    """One whole batch-1 greedy decode step in one persistent launch (see
-    kuiops_decode_step).  ``layer_table`` is a device int64 [n_layers, 8]
-    tensor of per-layer pointers (wqkv, wo, wgu, wd, ln1, ln2, k cache,
-    v cache); k_cache / v_cache give the cache strides ([hkv, cap, hd] views
-    of layer 0); ``logits`` [vocab] receives the LM head's output;
-    ``scratch`` / ``sync`` are zeroed uint8 buffers of
-    decode_step_scratch_bytes / decode_step_sync_bytes, kept across steps."""
+                lm_head, inv_freq, tok, pos, kv_len, history, prob, logits, scratch, sync, n_steps=1):
+    """``n_steps`` whole batch-1 greedy decode steps in one persistent launch
+    (see kuiops_decode_step).  ``layer_table`` is a device int64
+    [n_layers, 8] tensor of per-layer pointers (wqkv, wo, wgu, wd, ln1, ln2,
+    k cache, v cache); k_cache / v_cache give the cache strides ([hkv, cap,
+    hd] views of layer 0); ``logits`` [vocab] receives the last step's LM
+    head output; ``scratch`` / ``sync`` are zeroed uint8 buffers of
+    decode_step_scratch_bytes (for at least n_steps) /
+    decode_step_sync_bytes, kept across calls."""
     if layer_table.dtype != torch.int64 or tuple(layer_table.shape) != (n_layers, 8) or not layer_table.is_contiguous():
         raise _lib.KuiopsError("decode_step", _lib.E_INVALID)
     if tok.dtype != torch.int64 or pos.dtype != torch.int32 or kv_len.dtype != torch.int32:
@@ -867,7 +869,7 @@ def decode_step(layer_table, n_layers, d, ffn, hq, hkv, hd, vocab, eps, k_cache,
         k_cache.stride(0), k_cache.stride(1), v_cache.stride(0), v_cache.stride(1), embed.data_ptr(),
         final_norm.data_ptr(), lm_head.data_ptr(), inv_freq.data_ptr(), tok.data_ptr(), pos.data_ptr(),
         kv_len.data_ptr(), _ptr(history), history.numel() if history is not None else 0, _ptr(prob),
-        logits.data_ptr(), scratch.data_ptr(), scratch.numel(), sync.data_ptr(), sync.numel(),
+        logits.data_ptr(), int(n_steps), scratch.data_ptr(), scratch.numel(), sync.data_ptr(), sync.numel(),
         _stream(embed.device)))
     return logits
 

@@ -620,6 +620,43 @@ def test_persistent_step_bitwise_per_op(cuda, shape, cap, prompt_len, steps):
         _set_state(dec, after)
 
 
+@pytest.mark.parametrize("shape,cap,prompt_len,n_steps", [
+    (TINY, 64, 24, 3),
+    (TINY, 64, 30, 8),
+    (dict(TINY, d=512, hq=4, hkv=1, ffn=1536, layers=3), 300, 200, 5),   # head dim 128
+    (CONFIG5, 512 + 128, 512, 8),
+])
+def test_persistent_steps_per_launch_bitwise(cuda, shape, cap, prompt_len, n_steps):
+    """n_steps steps in one persistent launch against n_steps one-step
+    launches from the same state: the last logits, every token (history),
+    position / key count, KV caches and the last probability bit-identical;
+    counters zero, no wait expired, the step counter advanced by n_steps."""
+    print(f"persistent steps per launch: {shape} cap {cap} n {n_steps}", flush=True)
+    dec = LlamaDecoder(LlamaShape(**shape), random_llama(shape, cuda, 21), capacity=cap)
+    assert dec.persistent and dec.steps_per_launch >= n_steps
+    prompt = torch.randint(0, shape["vocab"], (1, prompt_len), generator=torch.Generator().manual_seed(22))
+    dec.prefill(prompt)
+    dec._decode_step_fused()                 # the cache row of an earlier launch in play
+    torch.cuda.synchronize()
+    before = _step_state(dec)
+    epoch = int(dec.step_sync[9 * 128:9 * 128 + 4].view(torch.int32)[0])
+    lm = dec._decode_step_fused(n_steps).clone()
+    torch.cuda.synchronize()
+    multi = _step_state(dec)
+    assert not ops.decode_step_error(dec.step_sync, shape["layers"])
+    assert int(dec.step_sync[:9 * 128].count_nonzero()) == 0
+    assert int(dec.step_sync[9 * 128:9 * 128 + 4].view(torch.int32)[0]) == epoch + n_steps
+    _set_state(dec, before)
+    for _ in range(n_steps):
+        l1 = dec._decode_step_fused().clone()
+    torch.cuda.synchronize()
+    single = _step_state(dec)
+    assert torch.equal(lm, l1), "last logits differ"
+    for name, a, b in zip(("tok", "pos/kv_len", "k cache", "v cache", "history", "prob"), multi, single):
+        assert torch.equal(a, b), f"{name} differs"
+    assert int(single[1][0, 0]) == int(before[1][0, 0]) + n_steps
+
+
 def test_persistent_graph_decode_matches_per_op(cuda):
     """Greedy tokens of a graph-replayed persistent step equal the per-op
     graph's (the step needs no host work between replays)."""
