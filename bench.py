@@ -556,7 +556,7 @@ def llama_workload(torch, dev, prompt_len=512, n_new=128, reps=3, batch=1):
     gbs = step_bytes / (step_ms * 1e-3) / 1e9
     flops_prefill = batch * (2 * prompt_len * (llama_decode_bytes(c, 0) / 2) +
                              c["layers"] * 2 * 2 * c["hq"] * (c["d"] // c["hq"]) * prompt_len * prompt_len / 2)
-    mode = ("batch-1 persistent (one launch per token)" if dec.persistent else "batch-1 fused") if dec.fused else \
+    mode = (f"batch-1 persistent ({dec.steps_per_launch} steps per launch)" if dec.persistent else "batch-1 fused") if dec.fused else \
         ("batched fused (LDS-staged rows)" if dec.fused_batched else ("batched wide" if dec.fused_wide else "unfused"))
     del dec
     out = {"value": round(tok_s, 1), "unit": "tokens/s", "decode_ms_per_step": round(step_ms, 4),
