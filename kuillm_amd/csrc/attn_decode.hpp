@@ -64,24 +64,10 @@ __device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, flo
 }
 
 // One work-group of fa_decode_kernel: split `split` of the row group `unit`
-// (KV head * row_groups + row group) of batch entry b.
-// IO carries the query reads and the output stores (CoherentIO when the
-// query comes from, and the output goes to, work-groups of the same launch).
-//
-// With PF, `wait` runs after the first step's K / V loads are issued and
-// before the query is read (the persistent decode step waits there for the
-// qkv projection; older cache rows do not depend on it), and key `fresh`
-// (>= 0), written by that projection, is then read again through IO.
-// Without PF the query is read first and every step loads its keys in the
-// loop (fewer registers live).  The arithmetic is the same either way.
-struct NoWaitAttn {
-    __device__ __forceinline__ void operator()() const {}
-};
-
-template <typename T, int HD, int R, int NWV = 4, int NB = 4, typename IO = PlainIO, typename Wait = NoWaitAttn,
-          bool PF = false>
-__device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, int unit, int64_t b,
-                                                const Wait &wait = Wait{}, int64_t fresh = -1) {
+// (KV head * row_groups + row group) of batch entry b.  The query is read
+// first, then every step loads its keys.
+template <typename T, int HD, int R, int NWV = 4, int NB = 4>
+__device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, int unit, int64_t b) {
     // NB: keys per lane group per step; all K / V loads of a step are issued
     // before any is used, so a step is one memory round trip.
     constexpr int NT = NWV * 64;
@@ -128,50 +114,20 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         }
     };
     const int64_t kb0 = kbeg + (int64_t)wave * KPW * NB;
-    if constexpr (PF) {
-        if (kb0 < kend_cap) load_kv(kb0);
-        wait();
-    }
 
     // Query rows: row r -> head hk*G + (r / l), query index r % l.
     float q[R][8];
     int64_t last_key[R];
     u32x4 qraw[R];
-    // epoch-tagged form: this lane's chunk of the new k / v rows as well
-    u32x4 kfr = {0, 0, 0, 0}, vfr = {0, 0, 0, 0};
-    auto load_q = [&]() -> bool {
-        bool all = true;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int rr = r0 + r;
-            const bool ok = rr < rows_kv && r < a.rows_per_group;
-            const int64_t head = hk * G + (ok ? rr / LQ : 0);
-            const int64_t qi = ok ? rr % LQ : 0;
-            if (ok) all = IO::ld8(a.Q, b * a.sq0 + head * a.sq1 + qi * a.sq2 + dl * 8, a.ep_q, qraw[r]) && all;
-            else qraw[r] = u32x4{0, 0, 0, 0};
-        }
-        if constexpr (IO::kLL) {
-            if (fresh >= 0) {
-                all = IO::ld8(a.kfresh, hk * HD + dl * 8, a.ep_q, kfr) && all;
-                all = IO::ld8(a.vfresh, hk * HD + dl * 8, a.ep_q, vfr) && all;
-            }
-        }
-        return all;
-    };
-    if constexpr (IO::kLL) {
-        // every lane reads its query chunk (and the new k / v chunk) until it
-        // is the expected write (each wave on its own), then the work-group meets
-        bool ok = load_q();
-        unsigned e = ll_err_read(a.err);
-        for (unsigned it = 0; !__all(ok); ++it) {
-            if (ll_expired(it, e, a.err)) break;
-            __builtin_amdgcn_s_sleep(kLLSleep);
-            if (!ok) ok = load_q();
-            e = ll_err_read(a.err);
-        }
-        __syncthreads();
-    } else {
-        load_q();
+    for (int r = 0; r < R; ++r) {
+        const int rr = r0 + r;
+        const bool ok = rr < rows_kv && r < a.rows_per_group;
+        const int64_t head = hk * G + (ok ? rr / LQ : 0);
+        const int64_t qi = ok ? rr % LQ : 0;
+        qraw[r] = ok ? *reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.Q) + b * a.sq0 + head * a.sq1 +
+                                                        qi * a.sq2 + dl * 8)
+                     : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -188,21 +144,7 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
 
     for (int64_t kb = kb0; kb < kend_cap; kb += NWV * KPW * NB) {
         float s[R][NB];
-        if (!PF || kb != kb0) load_kv(kb);
-        if (PF && fresh >= 0) {
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                if (kb + j * KPW + kg == fresh) {
-                    if constexpr (IO::kLL) {
-                        kr[j] = kfr;
-                        vr[j] = vfr;
-                    } else {
-                        kr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Kp + fresh * a.sk2 + dl * 8));
-                        vr[j] = IO::ld(reinterpret_cast<const u32x4 *>(Vp + fresh * a.sv2 + dl * 8));
-                    }
-                }
-            }
-        }
+        load_kv(kb);
         // keys past the device count are zeroed (their scores are masked
         // below; a zero V keeps a NaN in unused cache rows out of the sum)
 #pragma unroll
@@ -309,15 +251,7 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         if (a.splits == 1) {
             const T ov = from_f32<T>(oo * (ll > 0.f ? 1.f / ll : 0.f));
             const int64_t oidx = b * a.so0 + head * a.so1 + qi * a.so2 + d;
-            if constexpr (IO::kLL) {
-                // element pairs (d, d + 1) in one epoch-tagged word: lanes d, d + 1
-                // are neighbours of one wave (R == 1, HD even)
-                static_assert(R == 1, "epoch-tagged output: one row per work-group");
-                const uint16_t nb = (uint16_t)__shfl_down((int)__builtin_bit_cast(uint16_t, ov), 1, 64);
-                if ((d & 1) == 0) IO::st2(reinterpret_cast<T *>(a.O), oidx, ov, __builtin_bit_cast(T, nb), a.ep_o);
-            } else {
-                IO::st(reinterpret_cast<T *>(a.O) + oidx, ov);
-            }
+            reinterpret_cast<T *>(a.O)[oidx] = ov;
             if (a.lse && d == 0) a.lse[grow] = ll > 0.f ? (mm + __log2f(ll)) * kLn2 : -INFINITY;
             continue;
         }
@@ -434,7 +368,7 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         const int rr = r0 + r;
         const int64_t head = hk * G + rr / LQ, qi = rr % LQ;
         T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + head * a.so1 + qi * a.so2;
-        if constexpr (!IO::kLL) IO::st(Op + d, from_f32<T>(acc * inv));   // (epoch-tagged use: one split)
+        Op[d] = from_f32<T>(acc * inv);
         if (a.lse && d == 0) a.lse[grow] = L > 0.f ? (s_M[r] + __log2f(L)) * kLn2 : -INFINITY;
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -25,21 +25,29 @@
 // the end (results undefined, no hang).
 //
 // Hand-off: the vectors that pass between jobs (residual, q, attention rows,
-// o, SwiGLU activations, down, the new k / v rows) are epoch-tagged: each
-// 8-byte word holds two elements and the epoch of its write (step counter x
-// layer), written with one agent-scope atomic store (sc1: through the per-XCD
-// L2).  A consumer polls a 64-word sample of its input, then reads every word
-// with agent-scope atomic loads and retries until all carry the epoch it
-// expects.  So a hand-off costs no store acknowledgement wait, no counter
+// o, SwiGLU activations, down, the new k / v rows, the sampled token) are
+// epoch-tagged: each 8-byte word holds two elements and the epoch of its
+// write (step counter x layer), written with agent-coherent stores (sc1:
+// through the per-XCD L2; 8 elements as two 16-byte stores, each 8-byte word
+// whole).  A consumer's waves read their chunks, probe the first word of a
+// chunk that is not yet the expected write and read it again, until every
+// word carries the epoch they expect; then the work-group meets at a
+// barrier.  So a hand-off costs no store acknowledgement wait, no counter
 // and no separate poll: the reader detects the data itself.  Only the LM
 // head's logits (read by the sampling job) go through completion counters
 // (stores acknowledged with s_waitcnt 0, barrier, one relaxed agent-scope
 // add; the rule the split-K merges use).  The KV cache rows are written with
 // ordinary stores (read by later launches; this launch's attention takes the
-// new row from its epoch-tagged copy), and weights and older cache rows are
-// read with ordinary loads: nothing in the launch writes them.
+// rows of this launch's steps from their epoch-tagged copies), and weights
+// and older cache rows are read with ordinary loads: nothing in the launch
+// writes them.
 //
-// The job bodies are the library's own (decode_rows_block, fa_decode_block,
+// A launch can run several steps: the job list repeats per step, the
+// position and key count of step t are the launch's starting values plus t,
+// and the sampled token reaches the next step's layer-0 jobs as an
+// epoch-tagged word.
+//
+// The job bodies are the library's own (decode_rows_block, fa_decode_onepass_block,
 // softmax_top1_row), with the launch shapes and summation orders of the
 // per-op kernels, so the step is bitwise the per-op sequence.
 #include <algorithm>
