@@ -257,7 +257,7 @@ void fa_fwd_kernel(AttnArgs a) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int e = 0; e < 16; ++e) mx = fmaxf(mx, cur[t][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.scale_log2;
+        mx = xor_max<32>(mx) * a.scale_log2;
         // Lazy rescale: move the reference max only when it grew by more
         // than the slack (or is still -inf), for the whole wave at once.
         if (__any(mx > m_used + kRescaleSlack)) {
@@ -378,7 +378,7 @@ void fa_fwd_kernel(AttnArgs a) {
         }
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float l_tot = xor_add<32>(l_run);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if (myq < a.l) {
         T *Op = reinterpret_cast<T *>(a.O) + b * a.so0 + h * a.so1 + myq * a.so2;
