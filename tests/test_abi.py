@@ -135,3 +135,27 @@ def test_no_kernel_launch_stub_left_undefined(lib):
     import subprocess
     out = subprocess.run(["nm", "-D", "--undefined-only", str(C.LIB_PATH)], capture_output=True, text=True).stdout
     assert "__device_stub__" not in out
+
+
+def test_decode_step_host_checks(lib):
+    """The persistent decode step's buffer sizes and argument checks (host
+    only): the scratch grows with the steps per launch (one slot of new k / v
+    rows per layer and step), and step counts outside 1..16 or a short
+    scratch are refused before any launch."""
+    L, d, ffn, hq, hkv, hd = 16, 2048, 5632, 32, 8, 64
+    one = lib.kuiops_decode_step_scratch_bytes(L, 1, d, ffn, hq, hkv, hd)
+    eight = lib.kuiops_decode_step_scratch_bytes(L, 8, d, ffn, hq, hkv, hd)
+    slot = L * hkv * hd * 4                       # two 16-bit elements per 8-byte word
+    assert eight - one == 2 * 7 * slot
+    assert lib.kuiops_decode_step_scratch_bytes(L, 0, d, ffn, hq, hkv, hd) == 0
+    assert lib.kuiops_decode_step_sync_bytes(L) == 11 * 128
+    p = ctypes.c_void_p(1 << 20)                  # never dereferenced: the checks come first
+
+    def call(n_steps, scratch_bytes):
+        return lib.kuiops_decode_step(L, d, ffn, hq, hkv, hd, 32000, 640, _lib.BF16, 1e-5, p, 640 * hd, hd,
+                                      640 * hd, hd, p, p, p, p, p, p, p, p, 1024, p, p, n_steps, p, scratch_bytes,
+                                      p, 11 * 128, None)
+
+    assert call(0, eight) == _lib.E_UNSUPPORTED
+    assert call(17, 1 << 30) == _lib.E_UNSUPPORTED
+    assert call(8, one) == _lib.E_WORKSPACE
