@@ -111,7 +111,7 @@ class LlamaDecoder:
         self.step_state = torch.zeros((2, self.n), dtype=torch.int32, device=self.dev)
         self.pos, self.kv_len = self.step_state[0], self.step_state[1]
         self.graph = None
-        self.graph_k = None
+        self.graphs_k = {}
         self.fused = self.n == 1 and s.d <= 4096 and s.ffn <= 8192 and s.d % 8 == 0 and s.ffn % 8 == 0 and s.hd % 2 == 0
         # batches of 2..16: the batched form of the same fused projections
         # (every row of x staged in LDS: n * max(d, ffn) * 2 <= 140 KiB)
@@ -127,9 +127,10 @@ class LlamaDecoder:
         row_wide_keys = 8 * (64 // (s.hd // 8)) * 12
         self.persistent = (self.fused and s.d == s.hq * s.hd and s.d <= 4096 and s.vocab <= 32768
                            and self.cap <= row_wide_keys)
-        # persistent launches run this many steps each (the next step's
-        # weights stream while a step's LM head and sampling run)
-        self.steps_per_launch = 8 if self.persistent else 1
+        # persistent launches run up to this many steps each (the next step's
+        # weights stream while a step's LM head and sampling run); decode()
+        # covers a token count with launches of 16, 8, 4, 2 and 1 steps
+        self.steps_per_launch = 16 if self.persistent else 1
         if self.fused or self.fused_batched or self.fused_wide:
             self._setup_fused()
 
@@ -373,11 +374,14 @@ class LlamaDecoder:
                 dst.copy_(src)
             return g, logits
 
-        # (the capacity must hold the steps the recording runs)
-        k = self.steps_per_launch if self.persistent else 1
-        self.graph_k = None
-        if k > 1 and int(self.pos[0]) + 3 * k <= self.cap:
-            self.graph_k, _ = record(k)
+        # graphs of 2, 4, ... steps_per_launch steps (the capacity must hold
+        # the steps the recording runs)
+        self.graphs_k = {}
+        if self.persistent:
+            k = 2
+            while k <= self.steps_per_launch and int(self.pos[0]) + 3 * k <= self.cap:
+                self.graphs_k[k], _ = record(k)
+                k *= 2
         self.graph, self.graph_logits = record(1)
 
     def decode(self, n_new: int, use_graph: bool = True) -> torch.Tensor:
@@ -392,12 +396,15 @@ class LlamaDecoder:
             self.capture()
         out[0].copy_(self.tok)
         p0 = int(self.pos[0])
-        k = self.steps_per_launch if self.persistent else 1
         i = 1
         while i < n_new:
-            if n_new - i >= k > 1 and (not use_graph or self.graph_k is not None):
+            # the largest multi-step launch that fits the tokens left
+            k = self.steps_per_launch if self.persistent else 1
+            while k > 1 and (k > n_new - i or (use_graph and k not in self.graphs_k)):
+                k //= 2
+            if k > 1:
                 if use_graph:
-                    self.graph_k.replay()
+                    self.graphs_k[k].replay()
                 else:
                     self._decode_step(k)
                 i += k

@@ -623,8 +623,10 @@ def test_persistent_step_bitwise_per_op(cuda, shape, cap, prompt_len, steps):
 @pytest.mark.parametrize("shape,cap,prompt_len,n_steps", [
     (TINY, 64, 24, 3),
     (TINY, 64, 30, 8),
+    (TINY, 64, 30, 16),
     (dict(TINY, d=512, hq=4, hkv=1, ffn=1536, layers=3), 300, 200, 5),   # head dim 128
     (CONFIG5, 512 + 128, 512, 8),
+    (CONFIG5, 512 + 128, 512, 16),
 ])
 def test_persistent_steps_per_launch_bitwise(cuda, shape, cap, prompt_len, n_steps):
     """n_steps steps in one persistent launch against n_steps one-step
