@@ -349,12 +349,10 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 
 constexpr unsigned kLLSpinLimit = 1u << 20;      // polls of one epoch-tagged wait (~1 s)
 // s_sleep argument (units of 64 clocks) between two polls of an epoch-tagged
-// wait: every poll of a waiting work-group re-reads its whole input past the
-// per-XCD L2, so a longer pause trades wake-up latency for fabric traffic
-#ifndef KUIOPS_LL_SLEEP
-#define KUIOPS_LL_SLEEP 1
-#endif
-constexpr int kLLSleep = KUIOPS_LL_SLEEP;
+// wait: a poll reads past the per-XCD L2, so a longer pause trades wake-up
+// latency for fabric traffic (persistent Llama-1B step: sleep 4 / 16 cost
+// 3 / 17 us per token more than 1)
+constexpr int kLLSleep = 1;
 
 // Epoch-tagged waits spin per wave: a wave polls its own input words until
 // all carry the expected epoch (a wave vote, no work-group reduction per
