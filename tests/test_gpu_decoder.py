@@ -659,6 +659,24 @@ def test_persistent_steps_per_launch_bitwise(cuda, shape, cap, prompt_len, n_ste
     assert int(single[1][0, 0]) == int(before[1][0, 0]) + n_steps
 
 
+@pytest.mark.parametrize("n_new", [1, 2, 3, 17, 32, 47])
+def test_persistent_launch_sizes_cover_token_counts(cuda, n_new):
+    """decode() covers a token count with graphs of 16, 8, 4, 2 and 1 steps;
+    the tokens, position and key count equal eager one-step launches."""
+    print(f"persistent launch sizes: n_new {n_new}", flush=True)
+    dec = LlamaDecoder(LlamaShape(**TINY), random_llama(TINY, cuda, 31), capacity=80)
+    assert dec.persistent and dec.steps_per_launch == 16
+    prompt = torch.randint(0, TINY["vocab"], (1, 24), generator=torch.Generator().manual_seed(32))
+    fast = dec.generate(prompt, n_new, use_graph=True)
+    assert sorted(dec.graphs_k) == [2, 4, 8, 16]
+    pos_fast = int(dec.pos[0])
+    dec.steps_per_launch = 1                   # one step per eager launch
+    slow = dec.generate(prompt, n_new, use_graph=False)
+    assert torch.equal(fast, slow)
+    assert pos_fast == int(dec.pos[0]) == 24 + n_new - 1
+    assert not ops.decode_step_error(dec.step_sync, TINY["layers"])
+
+
 def test_persistent_graph_decode_matches_per_op(cuda):
     """Greedy tokens of a graph-replayed persistent step equal the per-op
     graph's (the step needs no host work between replays)."""
