@@ -452,7 +452,7 @@ typedef struct kuiops_step_layer {
     void *k_cache, *v_cache;
 } kuiops_step_layer;
 
-/* n_steps (1 .. 16) greedy decode steps of a Llama-style decoder for one
+/* n_steps (1 .. 32) greedy decode steps of a Llama-style decoder for one
  * sequence, in one launch.  `layers` points to a DEVICE array of n_layers
  * kuiops_step_layer.  The token id is read from tok[0] (device int64, an
  * index into embed [vocab, d]), the position from pos[0] and the key count

@@ -66,7 +66,8 @@ constexpr int kLayerKinds = 5;
 constexpr int kSubCounters = 8;           // completion counters of the LM-head phase (spread contention)
 constexpr int kCounterStride = 32;        // uint32 apart: one 128-byte line each
 constexpr unsigned kSpinLimit = 1u << 20; // polls per wait (~1 s)
-constexpr int kMaxSteps = 16;             // tokens per launch (the attention window of fresh keys < 32)
+constexpr int kMaxSteps = 32;             // tokens per launch (the window of fresh keys, at most 31,
+                                           // is narrower than the 32-key spacing of a lane's keys)
 
 struct StepArgs {
     int layers;

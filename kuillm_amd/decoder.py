@@ -129,8 +129,8 @@ class LlamaDecoder:
                            and self.cap <= row_wide_keys)
         # persistent launches run up to this many steps each (the next step's
         # weights stream while a step's LM head and sampling run); decode()
-        # covers a token count with launches of 16, 8, 4, 2 and 1 steps
-        self.steps_per_launch = 16 if self.persistent else 1
+        # covers a token count with launches of 32, 16, 8, 4, 2 and 1 steps
+        self.steps_per_launch = 32 if self.persistent else 1
         if self.fused or self.fused_batched or self.fused_wide:
             self._setup_fused()
 

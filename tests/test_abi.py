@@ -157,5 +157,5 @@ def test_decode_step_host_checks(lib):
                                       p, 11 * 128, None)
 
     assert call(0, eight) == _lib.E_UNSUPPORTED
-    assert call(17, 1 << 30) == _lib.E_UNSUPPORTED
+    assert call(33, 1 << 30) == _lib.E_UNSUPPORTED
     assert call(8, one) == _lib.E_WORKSPACE

@@ -624,9 +624,11 @@ def test_persistent_step_bitwise_per_op(cuda, shape, cap, prompt_len, steps):
     (TINY, 64, 24, 3),
     (TINY, 64, 30, 8),
     (TINY, 64, 30, 16),
+    (TINY, 64, 30, 32),
     (dict(TINY, d=512, hq=4, hkv=1, ffn=1536, layers=3), 300, 200, 5),   # head dim 128
     (CONFIG5, 512 + 128, 512, 8),
     (CONFIG5, 512 + 128, 512, 16),
+    (CONFIG5, 512 + 128, 512, 32),
 ])
 def test_persistent_steps_per_launch_bitwise(cuda, shape, cap, prompt_len, n_steps):
     """n_steps steps in one persistent launch against n_steps one-step
@@ -661,11 +663,12 @@ def test_persistent_steps_per_launch_bitwise(cuda, shape, cap, prompt_len, n_ste
 
 @pytest.mark.parametrize("n_new", [1, 2, 3, 17, 32, 47])
 def test_persistent_launch_sizes_cover_token_counts(cuda, n_new):
-    """decode() covers a token count with graphs of 16, 8, 4, 2 and 1 steps;
+    """decode() covers a token count with graphs of 16, 8, 4, 2 and 1 steps
+    (the 32-step graph needs more cache than this decoder has);
     the tokens, position and key count equal eager one-step launches."""
     print(f"persistent launch sizes: n_new {n_new}", flush=True)
     dec = LlamaDecoder(LlamaShape(**TINY), random_llama(TINY, cuda, 31), capacity=80)
-    assert dec.persistent and dec.steps_per_launch == 16
+    assert dec.persistent and dec.steps_per_launch == 32
     prompt = torch.randint(0, TINY["vocab"], (1, 24), generator=torch.Generator().manual_seed(32))
     fast = dec.generate(prompt, n_new, use_graph=True)
     assert sorted(dec.graphs_k) == [2, 4, 8, 16]
