@@ -483,9 +483,11 @@ typedef struct kuiops_step_layer {
  * its results are undefined and the error word is set:
  * kuiops_decode_step_error reads and clears it.  Calls must not overlap on
  * one `sync` / `scratch` pair.  Attention runs one work-group per query row
- * over every key (the row-wide form of kuiops_sdpa_decode), so long caches
- * are slow here.  Shapes: bf16 / f16, hd 64 or 128, d = hq*hd <= 4096, ffn
- * <= 8192, ffn % 8 == 0, vocab <= 32768; otherwise KUIOPS_E_UNSUPPORTED.  No
+ * over every key (the one-pass row-wide form of kuiops_sdpa_decode), so
+ * cache_cap must be at most 8 * (512 / hd) * 12 keys (768 at hd 64, 384 at
+ * hd 128).  Shapes: bf16 / f16, hd 64 or 128, d = hq*hd <= 4096, ffn
+ * <= 8192, ffn % 8 == 0, vocab <= 32768; otherwise KUIOPS_E_UNSUPPORTED, as
+ * when the step's work-group does not fit a CU (occupancy query).  No
  * reference counterpart: it replaces the whole per-token launch sequence of a
  * batch-1 greedy decode (the reference runs each aten op of generate() as its
  * own launch, infer.py:14-31, KERNELS.md).                                 */
@@ -500,8 +502,20 @@ KUIOPS_API int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
                        int64_t *history, int64_t hist_len, float *prob, void *logits, int64_t n_steps,
                        void *scratch, size_t scratch_bytes, void *sync, size_t sync_bytes, void *stream);
 /* 1 when a previous kuiops_decode_step on `sync` hit its wait bound (then
- * clears the flag), else 0; <0 on a HIP error.  Synchronises the stream.   */
+ * clears the flag), else 0; <0 on a HIP error.  Synchronises the stream.
+ * The flag latches: while it is set, kuiops_decode_step launches do no work
+ * (the decode state they would read is void).                              */
 KUIOPS_API int kuiops_decode_step_error(void *sync, int64_t n_layers, void *stream);
+/* KUIOPS_OK when kuiops_decode_step serves this shape on the current device,
+ * else KUIOPS_E_UNSUPPORTED / KUIOPS_E_INVALID: the host shape gate of
+ * kuiops_decode_step (including cache_cap <= 8 * (512 / hd) * 12 keys, the
+ * one-pass attention's range: 768 at hd 64, 384 at hd 128) and an occupancy
+ * query that one 512-thread step work-group fits a CU, which the step's
+ * cross-work-group waits need (one work-group per CU, all resident).  No
+ * reference counterpart: the caller's choice between the persistent step
+ * and the per-op launch sequence.                                          */
+KUIOPS_API int kuiops_decode_step_supported(int64_t n_layers, int64_t d, int64_t ffn, int64_t hq, int64_t hkv,
+                                            int64_t hd, int64_t vocab, int64_t cache_cap, int dtype);
 
 /* ----------------------------------------------- elementwise / mean / cat --
  * The reference's generic glue families: ElementwiseImpl

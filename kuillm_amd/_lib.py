@@ -97,6 +97,7 @@ SIGNATURES = {
                                   _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp,
                                   _sz, _vp, _sz, _vp]),
     "kuiops_decode_step_error": (_int, [_vp, _i64, _vp]),
+    "kuiops_decode_step_supported": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int]),
 }
 
 

@@ -22,7 +22,11 @@
 // work-groups resident (one per CU, nothing else running) the lowest
 // unfinished job can always run: the step cannot deadlock.  Every wait is
 // bounded; on expiry the step stops waiting, sets the error word and runs to
-// the end (results undefined, no hang).
+// the end (results undefined, no hang).  The error word latches: a launch
+// that finds it set does no work, until the host reads and clears it
+// (kuiops_decode_step_error).  Before launching, the host refuses shapes
+// whose work-group does not fit a CU (occupancy query) and caches longer
+// than the one-pass attention covers.
 //
 // Hand-off: the vectors that pass between jobs (residual, q, attention rows,
 // o, SwiGLU activations, down, the new k / v rows, the sampled token) are
@@ -337,6 +341,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
     // The step counter and the decode state as the previous launch left
     // them: written only by this launch's last sampling job, which runs after
     // every other job has finished (and so every work-group has read them).
+    // A latched error (a bounded wait of an earlier launch expired, and the
+    // host has not cleared it) voids the decode state: do no work.
+    __shared__ unsigned s_err;
+    if (threadIdx.x == 0) s_err = __hip_atomic_load(error_word(args), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_err) return;
     const uint32_t step0 = *epoch_word(args);
     const int64_t pos0 = *args.pos, kv0 = *args.kv_len;
     for (int j = blockIdx.x; j < args.total; j += G) {
@@ -380,30 +390,80 @@ static int log2_of(int64_t v) {
     return k;
 }
 
+// The kernel instance for a shape (hd 64 / 128, the K-chunk buckets of d and ffn).
 template <typename T, int HD, int KCD>
-static void launch_step_kcf(const StepArgs &a, int kcf, dim3 grid, hipStream_t st) {
+static const void *step_kernel_kcf(int kcf) {
     switch (kcf) {
-        case 4: hipLaunchKernelGGL((decode_step_kernel<T, HD, KCD, 4>), grid, dim3(kStepThreads), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((decode_step_kernel<T, HD, KCD, 8>), grid, dim3(kStepThreads), 0, st, a); break;
-        case 12: hipLaunchKernelGGL((decode_step_kernel<T, HD, KCD, 12>), grid, dim3(kStepThreads), 0, st, a); break;
-        default: hipLaunchKernelGGL((decode_step_kernel<T, HD, KCD, 16>), grid, dim3(kStepThreads), 0, st, a); break;
+        case 4: return reinterpret_cast<const void *>(&decode_step_kernel<T, HD, KCD, 4>);
+        case 8: return reinterpret_cast<const void *>(&decode_step_kernel<T, HD, KCD, 8>);
+        case 12: return reinterpret_cast<const void *>(&decode_step_kernel<T, HD, KCD, 12>);
+        default: return reinterpret_cast<const void *>(&decode_step_kernel<T, HD, KCD, 16>);
     }
 }
 
 template <typename T>
-static void launch_step(const StepArgs &a, int kcd, int kcf, dim3 grid, hipStream_t st) {
-    if (a.hd == 64) {
-        if (kcd == 4) launch_step_kcf<T, 64, 4>(a, kcf, grid, st);
-        else launch_step_kcf<T, 64, 8>(a, kcf, grid, st);
-    } else {
-        if (kcd == 4) launch_step_kcf<T, 128, 4>(a, kcf, grid, st);
-        else launch_step_kcf<T, 128, 8>(a, kcf, grid, st);
+static const void *step_kernel(int64_t hd, int kcd, int kcf) {
+    if (hd == 64) return kcd == 4 ? step_kernel_kcf<T, 64, 4>(kcf) : step_kernel_kcf<T, 64, 8>(kcf);
+    return kcd == 4 ? step_kernel_kcf<T, 128, 4>(kcf) : step_kernel_kcf<T, 128, 8>(kcf);
+}
+
+// Keys the one-pass row-wide attention covers: 8 waves x (64 / (hd / 8))
+// lane groups x 12 keys per lane (768 at hd 64, 384 at hd 128).  A key past
+// that range would be dropped, so larger caches are refused.
+static int64_t step_max_keys(int64_t hd) { return (int64_t)kStepWaves * (64 / (hd / 8)) * 12; }
+
+// Whether one work-group of `fn` fits on a CU with nothing else running
+// (LDS, registers): the step's jobs wait on each other across work-groups,
+// which is only safe when the whole one-per-CU grid is resident at once.
+// Queried once per device and kernel instance.
+static bool step_resident(const void *fn) {
+    static const void *seen_fn[64][32];
+    static int seen_ok[64][32];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    for (int i = 0; i < 32; ++i) {
+        if (seen_fn[dev][i] == fn) return seen_ok[dev][i] == 1;
+        if (!seen_fn[dev][i]) {
+            int nb = 0;
+            const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kStepThreads, 0) == hipSuccess &&
+                            nb >= 1;
+            seen_ok[dev][i] = ok ? 1 : 2;
+            seen_fn[dev][i] = fn;
+            return ok;
+        }
     }
+    return false;
 }
 
 }  // namespace kuiops
 
 using namespace kuiops;
+
+// Shape gate of the persistent step (host only, no GPU call); on success the
+// K-chunk buckets of d and ffn.
+static int step_gate(int64_t n_layers, int64_t d, int64_t ffn, int64_t hq, int64_t hkv, int64_t hd, int64_t vocab,
+                     int64_t cache_cap, int dtype, int &kcd, int &kcf) {
+    if (n_layers <= 0 || d <= 0 || ffn <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || vocab <= 0 || cache_cap <= 0)
+        return KUIOPS_E_INVALID;
+    if (hq % hkv || hd % 2) return KUIOPS_E_INVALID;
+    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
+    if ((hd != 64 && hd != 128) || d != hq * hd || d % 8 || ffn % 8) return KUIOPS_E_UNSUPPORTED;
+    kcd = kc_bucket(d);
+    kcf = kc_bucket(ffn);
+    if (kcd == 0 || kcd > 8 || kcf == 0) return KUIOPS_E_UNSUPPORTED;   // paired epilogues: d <= 4096
+    if (vocab > (int64_t)kSmThreads * kSmCache || vocab > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    if (n_layers > 1024 || cache_cap > step_max_keys(hd)) return KUIOPS_E_UNSUPPORTED;
+    return KUIOPS_OK;
+}
+
+extern "C" int kuiops_decode_step_supported(int64_t n_layers, int64_t d, int64_t ffn, int64_t hq, int64_t hkv,
+                                            int64_t hd, int64_t vocab, int64_t cache_cap, int dtype) {
+    int kcd = 0, kcf = 0;
+    const int rc = step_gate(n_layers, d, ffn, hq, hkv, hd, vocab, cache_cap, dtype, kcd, kcf);
+    if (rc != KUIOPS_OK) return rc;
+    const void *fn = dtype == KUIOPS_BF16 ? step_kernel<bf16_t>(hd, kcd, kcf) : step_kernel<f16_t>(hd, kcd, kcf);
+    return step_resident(fn) ? KUIOPS_OK : KUIOPS_E_UNSUPPORTED;
+}
 
 // Epoch-tagged scratch vectors, in elements: h0, h1 [d], q, att [hq*hd],
 // o [d], act [ffn], down [d], k / v copies [layers][steps][hkv*hd]; two
@@ -440,19 +500,13 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
                                   int32_t *kv_len, int64_t *history, int64_t hist_len, float *prob, void *logits,
                                   int64_t n_steps, void *scratch, size_t scratch_bytes, void *sync,
                                   size_t sync_bytes, void *stream) {
-    if (n_layers <= 0 || d <= 0 || ffn <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || vocab <= 0 || cache_cap <= 0)
-        return KUIOPS_E_INVALID;
-    if (hq % hkv || hd % 2) return KUIOPS_E_INVALID;
+    int kcd = 0, kcf = 0;
+    const int gate = step_gate(n_layers, d, ffn, hq, hkv, hd, vocab, cache_cap, dtype, kcd, kcf);
+    if (gate != KUIOPS_OK) return gate;
     if (!layers || !embed || !final_norm || !lm_head || !inv_freq || !tok || !pos || !kv_len || !logits ||
         !scratch || !sync)
         return KUIOPS_E_INVALID;
     if (history && hist_len <= 0) return KUIOPS_E_INVALID;
-    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16) return KUIOPS_E_UNSUPPORTED;
-    if ((hd != 64 && hd != 128) || d != hq * hd || d % 8 || ffn % 8) return KUIOPS_E_UNSUPPORTED;
-    const int kcd = kc_bucket(d), kcf = kc_bucket(ffn);
-    if (kcd == 0 || kcd > 8 || kcf == 0) return KUIOPS_E_UNSUPPORTED;   // paired epilogues: d <= 4096
-    if (vocab > (int64_t)kSmThreads * kSmCache || vocab > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
-    if (n_layers > 1024 || cache_cap > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     if (n_steps < 1 || n_steps > kMaxSteps) return KUIOPS_E_UNSUPPORTED;
     size_t off[9];
     if (scratch_bytes < step_scratch_layout(n_layers, n_steps, d, ffn, hq, hkv, hd, off) || !aligned16(scratch))
@@ -506,9 +560,10 @@ extern "C" int kuiops_decode_step(int64_t n_layers, int64_t d, int64_t ffn, int6
     // one work-group per CU: all resident at once (a job waits only on jobs
     // with lower indices, which resident work-groups run)
     const dim3 grid((unsigned)G);
-    hipStream_t st = as_stream(stream);
-    if (dtype == KUIOPS_BF16) launch_step<bf16_t>(a, kcd, kcf, grid, st);
-    else launch_step<f16_t>(a, kcd, kcf, grid, st);
+    const void *fn = dtype == KUIOPS_BF16 ? step_kernel<bf16_t>(hd, kcd, kcf) : step_kernel<f16_t>(hd, kcd, kcf);
+    if (!step_resident(fn)) return KUIOPS_E_UNSUPPORTED;
+    void *kargs[] = {&a};
+    if (hipLaunchKernel(fn, grid, dim3(kStepThreads), kargs, 0, as_stream(stream)) != hipSuccess) return KUIOPS_E_HIP;
     return launch_status();
 }
 

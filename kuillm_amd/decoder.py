@@ -62,6 +62,28 @@ def rope_inv_freq(hd: int, theta: float) -> torch.Tensor:
     return 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).float() / hd))
 
 
+class DecodeStepError(RuntimeError):
+    """A persistent decode launch gave up a bounded wait (its work-groups
+    were not all resident at once): the tokens of that call are void."""
+
+
+def persistent_step_ok(s: LlamaShape, batch: int, capacity: int, dtype, fused: bool,
+                       supported=None) -> bool:
+    """Whether batch-1 decode runs as the persistent step (kuiops_decode_step):
+    the fused per-op step must apply, the cache must fit the one-pass
+    attention (8 waves x 512 / hd lane groups x 12 keys: the persistent
+    attention is the per-op row-wide form, so both give the same bits), and
+    the library must accept the shape on this device (its shape gate plus an
+    occupancy query that a step work-group fits a CU).  Otherwise decode
+    takes the per-op graph."""
+    row_wide_keys = 8 * (64 // (s.hd // 8)) * 12
+    if not (fused and batch == 1 and s.d == s.hq * s.hd and s.d <= 4096 and s.vocab <= 32768
+            and capacity <= row_wide_keys):
+        return False
+    check = supported if supported is not None else ops.decode_step_supported
+    return bool(check(s.layers, s.d, s.ffn, s.hq, s.hkv, s.hd, s.vocab, capacity, dtype))
+
+
 class LlamaDecoder:
     """Greedy generation for one batch of equal-length prompts.
 
@@ -124,9 +146,7 @@ class LlamaDecoder:
         # (kuiops_decode_step) when its attention has the one-pass row-wide
         # form of the per-op path (the cache fits 8 waves x 12 keys per lane
         # group), so both paths give the same bits
-        row_wide_keys = 8 * (64 // (s.hd // 8)) * 12
-        self.persistent = (self.fused and s.d == s.hq * s.hd and s.d <= 4096 and s.vocab <= 32768
-                           and self.cap <= row_wide_keys)
+        self.persistent = persistent_step_ok(s, self.n, self.cap, dtype, self.fused)
         # persistent launches run up to this many steps each (the next step's
         # weights stream while a step's LM head and sampling run); decode()
         # covers a token count with launches of 32, 16, 8, 4, 2 and 1 steps
@@ -416,10 +436,20 @@ class LlamaDecoder:
             if not (self.fused or self.fused_batched or self.fused_wide):
                 out[i].copy_(self.tok)
             i += 1
+        if self.persistent:
+            self.check_step_error()
         if (self.fused or self.fused_batched or self.fused_wide) and n_new > 1:
             # the fused step recorded the token of position p at history[p]
             out[1:].copy_(self.history[:, p0:p0 + n_new - 1].t())
         return out.t()
+
+    def check_step_error(self):
+        """Raises DecodeStepError when a persistent launch on this decoder
+        gave up a bounded wait (one 4-byte read, synchronising the stream;
+        the flag is cleared, and launches do no work while it is set)."""
+        if ops.decode_step_error(self.step_sync, self.s.layers):
+            raise DecodeStepError("persistent decode step: a cross-work-group wait expired "
+                                  "(work-groups not co-resident); the decoded tokens are void")
 
     def generate(self, prompt: torch.Tensor, n_new: int, use_graph: bool = True) -> torch.Tensor:
         self.prefill(prompt)

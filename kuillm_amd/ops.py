@@ -50,38 +50,72 @@ def _dt(dtype) -> int:
 
 
 # ----------------------------------------------------------------- workspace
-# One buffer per (device, kind).  "gemv" and "attn" hold split arrival
-# counters (decode GEMM, decode attention), which must start at zero: they
-# are zero-filled when allocated and the kernels leave the counters at zero.
-# "scratch" is plain partial-result space.
+# One buffer per (device, stream, kind), so calls in flight on two streams
+# never share split counters or partials.  "gemv" and "attn" hold split
+# arrival counters (decode GEMM, decode attention), which must start at
+# zero: they are zero-filled when allocated and the kernels leave the
+# counters at zero.  "scratch" is plain partial-result space.
 #
-# A HIP graph records the raw address of the buffer it was captured with, so
-# a buffer is never freed once handed out: when a call needs more bytes, the
-# old buffer moves to _RETIRED (kept alive for the life of the process, its
-# counters still zero) and a larger one replaces it for later calls.  Growing
-# during capture would put the new allocation and its zero fill inside the
-# graph, so it is refused: run the largest shape once eagerly first.
-# Kernels that use one kind of workspace on one device must not run
-# concurrently on two streams (the counters would be shared).
+# A HIP graph records the raw address of the buffer it was captured with.
+# Growing during capture would put the new allocation and its zero fill
+# inside the graph, so it is refused: run the largest shape once eagerly
+# first.  A capture stream with no buffer of its own (the eager warm-up ran
+# on another stream, as torch.cuda.graph's default capture stream does)
+# takes the device's largest buffer of that kind; replays of that graph must
+# then not overlap eager calls on the warm-up stream.  When a call needs more
+# bytes, the old buffer is released (stream-ordered, through torch's caching
+# allocator) unless a graph was captured with it: those are kept in
+# _RETIRED for the life of the process, counters still zero.
 _WS = {}
 _RETIRED = []
+_CAPTURED = set()        # data_ptr of every buffer handed out during a capture
+
+
+def _stream_key(device: torch.device) -> int:
+    """The stream a workspace is keyed on: torch's current stream on the device."""
+    if device.type != "cuda":
+        return 0
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _capturing(device: torch.device) -> bool:
+    return device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
+
+def _ws_key(device: torch.device, kind: str):
+    dev = device.index if device.index is not None else (
+        torch.cuda.current_device() if device.type == "cuda" else 0)
+    return dev, _stream_key(device), kind
 
 
 def workspace(device: torch.device, nbytes: int, kind: str = "scratch") -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), kind)
+    capturing = _capturing(device)
+    key = _ws_key(device, kind)
     buf = _WS.get(key)
+    if buf is None and capturing:
+        same = [b for (d, _, k), b in _WS.items() if d == key[0] and k == kind and b.numel() >= nbytes]
+        if same:
+            buf = max(same, key=lambda t: t.numel())
+            _WS[key] = buf
     if buf is None or buf.numel() < nbytes:
-        if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+        if capturing:
             raise RuntimeError(
                 f"kuiops workspace '{kind}' must grow to {nbytes} bytes during HIP graph capture; "
                 "run the same calls once outside capture first")
         size = max(int(nbytes), 1 << 20)
         size = (size + (1 << 20) - 1) // (1 << 20) * (1 << 20)
-        if buf is not None:
+        if buf is not None and buf.data_ptr() in _CAPTURED:
             _RETIRED.append(buf)
         buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _WS[key] = buf
+    if capturing:
+        _CAPTURED.add(buf.data_ptr())
     return buf
+
+
+def workspace_buffer(device: torch.device, kind: str) -> torch.Tensor | None:
+    """The current stream's workspace of ``kind`` on ``device`` (None if none yet)."""
+    return _WS.get(_ws_key(device, kind))
 
 
 # -------------------------------------------------------------------- layout
@@ -872,6 +906,15 @@ def decode_step(layer_table, n_layers, d, ffn, hq, hkv, hd, vocab, eps, k_cache,
         logits.data_ptr(), int(n_steps), scratch.data_ptr(), scratch.numel(), sync.data_ptr(), sync.numel(),
         _stream(embed.device)))
     return logits
+
+
+def decode_step_supported(n_layers, d, ffn, hq, hkv, hd, vocab, cache_cap, dtype) -> bool:
+    """Whether kuiops_decode_step serves this shape on the current device:
+    the host shape gate (including a cache no longer than the one-pass
+    attention covers) and an occupancy query that one step work-group fits
+    a CU.  False means the caller takes the per-op step."""
+    return _lib_handle().kuiops_decode_step_supported(n_layers, d, ffn, hq, hkv, hd, vocab, cache_cap,
+                                                      _dt(dtype)) == _lib.OK
 
 
 def decode_step_error(sync, n_layers) -> bool:

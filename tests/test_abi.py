@@ -140,8 +140,9 @@ def test_no_kernel_launch_stub_left_undefined(lib):
 def test_decode_step_host_checks(lib):
     """The persistent decode step's buffer sizes and argument checks (host
     only): the scratch grows with the steps per launch (one slot of new k / v
-    rows per layer and step), and step counts outside 1..16 or a short
-    scratch are refused before any launch."""
+    rows per layer and step), and step counts outside 1..32, a cache longer
+    than the one-pass attention covers (768 keys at head dim 64, 384 at 128)
+    or a short scratch are refused before any launch."""
     L, d, ffn, hq, hkv, hd = 16, 2048, 5632, 32, 8, 64
     one = lib.kuiops_decode_step_scratch_bytes(L, 1, d, ffn, hq, hkv, hd)
     eight = lib.kuiops_decode_step_scratch_bytes(L, 8, d, ffn, hq, hkv, hd)
@@ -151,11 +152,19 @@ def test_decode_step_host_checks(lib):
     assert lib.kuiops_decode_step_sync_bytes(L) == 11 * 128
     p = ctypes.c_void_p(1 << 20)                  # never dereferenced: the checks come first
 
-    def call(n_steps, scratch_bytes):
-        return lib.kuiops_decode_step(L, d, ffn, hq, hkv, hd, 32000, 640, _lib.BF16, 1e-5, p, 640 * hd, hd,
-                                      640 * hd, hd, p, p, p, p, p, p, p, p, 1024, p, p, n_steps, p, scratch_bytes,
-                                      p, 11 * 128, None)
+    def call(n_steps, scratch_bytes, cap=640, hd_=hd, hq_=hq):
+        return lib.kuiops_decode_step(L, d, ffn, hq_, hkv, hd_, 32000, cap, _lib.BF16, 1e-5, p, cap * hd_, hd_,
+                                      cap * hd_, hd_, p, p, p, p, p, p, p, p, 1024, p, p, n_steps, p,
+                                      scratch_bytes, p, 11 * 128, None)
 
     assert call(0, eight) == _lib.E_UNSUPPORTED
     assert call(33, 1 << 30) == _lib.E_UNSUPPORTED
     assert call(8, one) == _lib.E_WORKSPACE
+    # the one-pass attention covers 8 waves x (512 / hd) lane groups x 12 keys
+    assert call(8, 1 << 30, cap=769) == _lib.E_UNSUPPORTED
+    assert call(8, 1 << 30, cap=385, hd_=128, hq_=16) == _lib.E_UNSUPPORTED
+    sup = lib.kuiops_decode_step_supported
+    assert sup(L, d, ffn, hq, hkv, hd, 32000, 769, _lib.BF16) == _lib.E_UNSUPPORTED
+    assert sup(L, d, ffn, 16, hkv, 128, 32000, 385, _lib.BF16) == _lib.E_UNSUPPORTED
+    assert sup(L, d, ffn, hq, hkv, hd, 32000, 640, _lib.F32) == _lib.E_UNSUPPORTED
+    assert sup(L, d, ffn, hq, hkv, hd, 32000, 0, _lib.BF16) == _lib.E_INVALID

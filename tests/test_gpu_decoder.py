@@ -350,7 +350,7 @@ def test_sdpa_decode_split_merge_keeps_counters_zero(cuda):
             else:
                 assert torch.equal(out, firsts[s])
     torch.cuda.synchronize()
-    ws = ops._WS[(cuda.index or 0, "attn")]
+    ws = ops.workspace_buffer(cuda, "attn")
     assert not ws[:256].any()            # counters: 4 bytes per query row, 256-byte aligned
 
 
@@ -696,3 +696,28 @@ def test_persistent_graph_decode_matches_per_op(cuda):
     assert torch.equal(fast, again)
     assert torch.equal(fast, slow)
     assert not ops.decode_step_error(dec.step_sync, TINY["layers"])
+
+
+def test_persistent_error_word_raises(cuda):
+    """A latched error word (a bounded wait that expired) makes decode()
+    raise instead of returning tokens: the word is pre-set from the host (no
+    wait is made to expire), the launches then do no work (position and key
+    count unchanged), and the check clears the flag."""
+    from kuillm_amd.decoder import DecodeStepError
+    print("persistent error word", flush=True)
+    dec = LlamaDecoder(LlamaShape(**TINY), random_llama(TINY, cuda, 41), capacity=64)
+    assert dec.persistent
+    prompt = torch.randint(0, TINY["vocab"], (1, 20), generator=torch.Generator().manual_seed(42))
+    dec.prefill(prompt)
+    torch.cuda.synchronize()
+    state = dec.step_state.clone()
+    dec.step_sync.view(torch.int32)[8 * 32] = 1          # the error word (after 8 counters of 128 bytes)
+    with pytest.raises(DecodeStepError):
+        dec.decode(6, use_graph=False)
+    assert torch.equal(dec.step_state, state)
+    assert not ops.decode_step_error(dec.step_sync, TINY["layers"])
+    # cleared: the next decode runs and matches a fresh per-op decode
+    fast = dec.generate(prompt, 6, use_graph=False)
+    dec.persistent = False
+    slow = dec.generate(prompt, 6, use_graph=False)
+    assert torch.equal(fast, slow)

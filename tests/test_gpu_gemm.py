@@ -244,7 +244,7 @@ def test_decode_gemm_split_sequence_keeps_counters_zero(cuda):
             else:
                 assert torch.equal(out, firsts[(M, N, K)])
     torch.cuda.synchronize()
-    ws = ops._WS[(cuda.index or 0, "gemv")]
+    ws = ops.workspace_buffer(cuda, "gemv")
     assert not ws[:16384].any()
 
 
@@ -268,7 +268,7 @@ def test_decode_gemm_row_stream(cuda, M, N, K, dtype):
     ob = ops.addmm(b.to(cuda), x.to(cuda), Wd)
     assert_tol(ob, O.addmm(npy(b), npy(x), npy(Wbig[:, 8:8 + N])), dtype)
     torch.cuda.synchronize()
-    assert not ops._WS[(cuda.index or 0, "gemv")][:16384].any()
+    assert not ops.workspace_buffer(cuda, "gemv")[:16384].any()
 
 
 @pytest.mark.parametrize("M", [1, 2])
