@@ -26,6 +26,8 @@
 // test oracle, kuipy/kuiops.py:403-564, tests/test_jit_ops.py:51-112).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace kuiops {
@@ -576,6 +578,320 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
             store_tile32<Tout>(a, acc[i][j], m0 + wm * WTM + i * 32, n0 + wn * WTN + j * 32 + lrow, lk);
 }
 
+// ------------------------------------------------------------------------
+// gemm_wave_kernel: 256x256x64 work-group tiles, 4 waves (one per SIMD),
+// each wave a 128x128 quarter built from 32x32x16 MFMAs whose 256 fp32
+// accumulators live in AGPRs.  Against the 8-wave gemm_dma_kernel (128x64
+// per wave) each LDS fragment feeds two MFMAs instead of 1.5, which cuts the
+// LDS reads per stage from 192 KB to 128 KB: LDS bandwidth (reads plus the
+// DMA's writes) is what bounds this loop.  With one wave per SIMD nothing
+// hides latency, so the schedule is explicit:
+//   * the MFMAs of k-step kk run with the fragments of kk + 1 being read
+//     under them (one LDS read issued after each MFMA);
+//   * before the last k-step of a stage each wave waits for its own DMA of
+//     the next stage, the work-group meets at one bare s_barrier (every wave
+//     has then read the current stage), and the next stage's first
+//     fragments plus the DMA refill of the current stage's buffers with
+//     stage s + 2 are issued under the last k-step's MFMAs;
+//   * the loop is unrolled over the two LDS stages with the last two stages
+//     peeled, so no conditional DMA sits inside it (the compiler's wait
+//     insertion is not path-sensitive: a conditional refill makes it wait
+//     for every DMA before each stage's first LDS read).
+// The MFMA operands are swapped (the B fragment is the first operand), so a
+// lane's accumulator holds one output row and 4 consecutive columns per
+// 8-column group: the epilogue writes 8-byte runs into an LDS image of the
+// tile (16-byte chunks XOR-swizzled by row) and the work-group stores whole
+// 512-byte row segments.  Loads and the LDS layouts are gemm_dma_kernel's.
+__device__ __forceinline__ const char *uniform_ptr(const char *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const char *>(((uint64_t)hi << 32) | lo);
+}
+
+template <typename T, bool BCOL, typename Tout>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_wave_kernel(GemmArgs a) {
+    constexpr int BK = 64, SB = 256 * BK * 2;      // bytes per operand per stage
+    typedef typename Mfma<T>::frag frag;
+    __shared__ __attribute__((aligned(1024))) char sA0[SB], sB0[SB], sA1[SB], sB1[SB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn, bz;
+    tile_coords_batched(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn, bz);
+    const T *Ab = reinterpret_cast<const T *>(a.A) + bz * a.stride_a;
+    const T *Bb = reinterpret_cast<const T *>(a.B) + bz * a.stride_b;
+    const int64_t M = a.M, N = a.N, lda = a.lda, ldb = a.ldb, ldo = a.ldo, ldcin = a.ldcin;
+    const int c_kind = a.c_kind, vec_store = a.vec_store;
+    const float alpha = a.alpha, beta = a.beta;
+    const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
+    const int nk = (int)(a.K / BK);                // even, >= 2
+    auto swzK = [](int r) { return (r >> 1) & 7; };
+
+    // DMA: per stage and operand 32 blocks of 1 KB, 8 per wave.  Rows /
+    // columns past M / N are clamped (valid memory, results not stored).
+    const char *baseA = reinterpret_cast<const char *>(Ab + m0 * lda);
+    const char *baseB = BCOL ? reinterpret_cast<const char *>(Bb + n0 * ldb) : reinterpret_cast<const char *>(Bb + n0);
+    uint32_t goffA[8], goffB[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int blk = wave * 8 + j;
+        const int r = blk * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ swzK(r);
+        goffA[j] = (uint32_t)((min((int64_t)r, M - 1 - m0) * lda + c * 8) * 2);
+        if constexpr (BCOL) {
+            goffB[j] = (uint32_t)((min((int64_t)r, N - 1 - n0) * ldb + c * 8) * 2);
+        } else {
+            const int kr = blk * 2 + (lane >> 5);
+            const int cb = (lane & 31) ^ swzB(kr);
+            goffB[j] = (uint32_t)(((int64_t)kr * ldb + min((int64_t)cb * 8, N - 8 - n0)) * 2);
+        }
+    }
+    const uint32_t stepA = BK * 2;
+    const uint32_t stepB = BCOL ? (uint32_t)(BK * 2) : (uint32_t)(BK * ldb * 2);
+    // (the bases are uniform; readfirstlane keeps the descriptors in SGPRs,
+    // where the DMA needs them, instead of a per-lane waterfall loop)
+    const __amdgpu_buffer_rsrc_t rsA = make_rsrc(uniform_ptr(baseA), 0xffffffffu);
+    const __amdgpu_buffer_rsrc_t rsB = make_rsrc(uniform_ptr(baseB), 0xffffffffu);
+    auto issue = [&](int kt, char *sa, char *sb) __attribute__((always_inline)) {
+        const uint32_t ka = (uint32_t)kt * stepA, kb = (uint32_t)kt * stepB;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            dma16_buf(rsA, goffA[j], ka, sa + (wave * 8 + j) * 1024);
+            dma16_buf(rsB, goffB[j], kb, sb + (wave * 8 + j) * 1024);
+        }
+    };
+
+    // LDS byte offsets of this lane's fragments.
+    const int lrow = lane & 31, lk = lane >> 5;
+    int offA[4], offB[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const int r = wm * 128 + lrow;
+        offA[kk] = r * 128 + (((2 * kk + lk) ^ swzK(r)) << 4);
+    }
+    if constexpr (BCOL) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int r = wn * 128 + lrow;
+            offB[kk] = r * 128 + (((2 * kk + lk) ^ swzK(r)) << 4);
+        }
+    } else {
+        const int G = lane >> 4, q = lane & 15;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kr = 8 * (G >> 1) + (q >> 2);
+            const int n = wn * 128 + j * 32 + 16 * (G & 1) + 4 * (q & 3);
+            offB[j] = kr * 512 + (((n >> 3) ^ swzB(kr)) << 4) + ((n >> 2) & 1) * 8;
+        }
+    }
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    frag fa[2][4], fb[2][4];
+    auto rd = [&](const char *sa, const char *sb, int kk, int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            fa[slot][i] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(sa + offA[kk] + i * 32 * 128));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (BCOL) {
+                fb[slot][j] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(sb + offB[kk] + j * 32 * 128));
+            } else {
+                const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4 *)to_lds(sb + offB[j] + kk * 16 * 512));
+                const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4 *)to_lds(sb + offB[j] + kk * 16 * 512 + 4 * 512));
+                const u32x2 h0 = __builtin_bit_cast(u32x2, t0), h1 = __builtin_bit_cast(u32x2, t1);
+                fb[slot][j] = as_frag<frag>(u32x4{h0[0], h0[1], h1[0], h1[1]});
+            }
+        }
+    };
+    // swapped operands: acc[i][j] element e is row 32 i + lrow, column
+    // 32 j + 8 (e / 4) + 4 lk + e % 4 of the wave's quarter
+    auto mm = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::m32(fb[slot][j], fa[slot][i], acc[i][j]);
+    };
+    // scheduling groups of one k-step: MFMA, LDS read (12 of them: 8 for
+    // K-contiguous B), and the stage's DMA (16) when it is issued here
+    constexpr int NRD = BCOL ? 8 : 12;
+    auto pattern = [&](int nvmem) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (t < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (t < nvmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+    };
+    auto stage = [&](int s, const char *sa, const char *sb, const char *na, const char *nb, char *ra, char *rb,
+                     bool next, bool refill) __attribute__((always_inline)) {
+        rd(sa, sb, 1, 1);
+        mm(0);
+        pattern(0);
+        __builtin_amdgcn_sched_barrier(0);
+        rd(sa, sb, 2, 0);
+        mm(1);
+        pattern(0);
+        __builtin_amdgcn_sched_barrier(0);
+        rd(sa, sb, 3, 1);
+        mm(0);
+        pattern(0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (next) {
+            wait_vmcnt<0>();                         // this wave's DMA of stage s + 1
+            __builtin_amdgcn_s_waitcnt(0xc07f);      // and its LDS reads of stage s
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            rd(na, nb, 0, 0);
+            if (refill) issue(s + 2, ra, rb);
+        }
+        mm(1);
+        pattern(refill ? 16 : 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    issue(0, sA0, sB0);
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    rd(sA0, sB0, 0, 0);
+    issue(1, sA1, sB1);
+    int s = 0;
+    for (; s + 2 < nk; s += 2) {
+        stage(s, sA0, sB0, sA1, sB1, sA0, sB0, true, true);
+        stage(s + 1, sA1, sB1, sA0, sB0, sA1, sB1, true, true);
+    }
+    stage(s, sA0, sB0, sA1, sB1, sA0, sB0, true, false);
+    stage(s + 1, sA1, sB1, sA0, sB0, sA1, sB1, false, false);
+
+    // Epilogue: out = alpha * acc + beta * addend (fp32), one rounding.
+    const Tout *cin = reinterpret_cast<const Tout *>(a.cin);
+    Tout *out = reinterpret_cast<Tout *>(a.out) + bz * a.stride_o;
+    // beta * addend for 4 consecutive columns (8-byte loads where aligned)
+    auto addend4 = [&](int64_t row, int64_t col, float v[4]) __attribute__((always_inline)) {
+        const Tout *p = c_kind == KUIOPS_C_ROW ? cin + col : cin + row * ldcin + col;
+        if (sizeof(Tout) == 2 && col + 3 < N && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+            const u32x2 w = *reinterpret_cast<const u32x2 *>(p);
+            const Tout *h = reinterpret_cast<const Tout *>(&w);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = beta * to_f32(h[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = col + e < N ? beta * to_f32(p[e]) : 0.f;
+        }
+    };
+    // the 4 output values of (i, j, g); KIND is the addend kind
+    auto value4 = [&](auto kind, int i, int j, int g, int64_t row, int64_t col, const float brow[4], float v[4])
+        __attribute__((always_inline)) {
+        constexpr int KIND = decltype(kind)::value;
+        float add[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (KIND == KUIOPS_C_ROW) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) add[e] = brow[e];
+        } else if constexpr (KIND == KUIOPS_C_FULL) {
+            if (row < M) addend4(row, col, add);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = alpha * acc[i][j][4 * g + e] + add[e];
+    };
+    // runs body(kind_tag) with the addend kind as a compile-time constant
+    auto with_kind = [&](auto body) __attribute__((always_inline)) {
+        if (c_kind == KUIOPS_C_ROW) body(std::integral_constant<int, KUIOPS_C_ROW>{});
+        else if (c_kind == KUIOPS_C_FULL) body(std::integral_constant<int, KUIOPS_C_FULL>{});
+        else body(std::integral_constant<int, KUIOPS_C_NONE>{});
+    };
+    if constexpr (sizeof(Tout) == 2) {
+        // The tile's image in LDS: rows 64 b .. 64 b + 63 in stage array b,
+        // 512 bytes per row, 16-byte chunk c at position c ^ (row & 31).
+        auto stg = [&](int b) -> char * { return b == 0 ? sA0 : (b == 1 ? sB0 : (b == 2 ? sA1 : sB1)); };
+        __builtin_amdgcn_s_barrier();
+        with_kind([&](auto kind) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int cl = wn * 128 + j * 32 + 8 * g + 4 * lk;
+                    float brow[4] = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (decltype(kind)::value == KUIOPS_C_ROW) addend4(0, n0 + cl, brow);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = wm * 128 + i * 32 + lrow;
+                        float v[4];
+                        value4(kind, i, j, g, m0 + r, n0 + cl, brow, v);
+                        typedef Tout t4 __attribute__((ext_vector_type(4)));
+                        t4 w;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) w[e] = from_f32<Tout>(v[e]);
+                        *reinterpret_cast<u32x2 *>(stg(r >> 6) + (r & 63) * 512 + (((cl >> 3) ^ (r & 31)) << 4) +
+                                                   lk * 8) = __builtin_bit_cast(u32x2, w);
+                    }
+                }
+            }
+        });
+        __syncthreads();
+        if (vec_store && m0 + 256 <= M && n0 + 256 <= N) {
+#pragma unroll
+            for (int it = 0; it < 32; ++it) {
+                const int r = it * 8 + (tid >> 5), ch = tid & 31;
+                const u32x4 v =
+                    *reinterpret_cast<const u32x4 *>(stg(r >> 6) + (r & 63) * 512 + ((ch ^ (r & 31)) << 4));
+                // streaming store: the output is not read again here
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (m0 + r) * ldo + n0 + ch * 8));
+            }
+        } else {
+            for (int it = 0; it < 32; ++it) {
+                const int r = it * 8 + (tid >> 5), ch = tid & 31;
+                const int64_t grow = m0 + r, gcol = n0 + ch * 8;
+                if (grow >= M || gcol >= N) continue;
+                const u32x4 v =
+                    *reinterpret_cast<const u32x4 *>(stg(r >> 6) + (r & 63) * 512 + ((ch ^ (r & 31)) << 4));
+                if (vec_store) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + grow * ldo + gcol));
+                } else {
+                    const Tout *e8 = reinterpret_cast<const Tout *>(&v);
+                    for (int e = 0; e < 8; ++e)
+                        if (gcol + e < N) out[grow * ldo + gcol + e] = e8[e];
+                }
+            }
+        }
+    } else {
+        // fp32 output: 4 consecutive columns per lane, 16 bytes
+        with_kind([&](auto kind) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int64_t col = n0 + wn * 128 + j * 32 + 8 * g + 4 * lk;
+                    float brow[4] = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (decltype(kind)::value == KUIOPS_C_ROW) addend4(0, col, brow);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t row = m0 + wm * 128 + i * 32 + lrow;
+                        float v[4];
+                        value4(kind, i, j, g, row, col, brow, v);
+                        if (row >= M) continue;
+                        if (vec_store && col + 3 < N) {
+                            *reinterpret_cast<f32x4 *>(out + row * ldo + col) = f32x4{v[0], v[1], v[2], v[3]};
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (col + e < N) out[row * ldo + col + e] = from_f32<Tout>(v[e]);
+                        }
+                    }
+                }
+            }
+        });
+    }
+}
+
 // Sums split-K partials in split order, then applies alpha / beta / addend.
 template <typename Tout>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
@@ -689,6 +1005,17 @@ static void launch_mfma(const GemmArgs &a, TileCfg t, bool bcol, int64_t gz, hip
 #undef KUIOPS_GEMM_LAUNCH
 }
 
+// KUIOPS_GEMM_KERNEL=dma selects the 8-wave gemm_dma_kernel for the large
+// GEMMs (read once per process); the default is gemm_wave_kernel.
+static int gemm_kernel_choice() {
+    static int choice = -1;
+    if (choice < 0) {
+        const char *e = getenv("KUIOPS_GEMM_KERNEL");
+        choice = (e && e[0] == 'd') ? 1 : 0;
+    }
+    return choice;
+}
+
 static bool dma_eligible(const GemmArgs &a, int64_t batch, bool bcol) {
     // buffer offsets (tile rows x leading dim + K) must stay below 2^31 bytes
     const int64_t lim = (int64_t)1 << 30;
@@ -706,13 +1033,19 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
     if (splits_req <= 1 && dma_eligible(a, batch, bcol)) {
         a.tiles_m = (int)cdiv(a.M, 256);
         a.tiles_n = (int)cdiv(a.N, 256);
-        a.vec_store = sizeof(Tout) == 2 && a.N % 8 == 0 && a.ldo % 8 == 0 && a.stride_o % 8 == 0 && aligned16(a.out);
+        const int vec = sizeof(Tout) == 2 ? 8 : 4;    // elements per vector store
+        a.vec_store = a.N % vec == 0 && a.ldo % vec == 0 && a.stride_o % vec == 0 && aligned16(a.out);
         dim3 grid((unsigned)(a.tiles_m * a.tiles_n * batch));
-        // 8 waves (2 per SIMD, 128x64 each), BK = 64, two LDS stages: the best of
-        // the measured variants (4 waves x 128x128, BK = 32 with four stages,
-        // and an 8-wave ping-pong schedule were all slower at 4096^3 / 8192^3).
-        if (bcol) hipLaunchKernelGGL((gemm_dma_kernel<T, true, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
-        else hipLaunchKernelGGL((gemm_dma_kernel<T, false, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
+        // 4 waves of 128x128 (one per SIMD, explicit schedule); the 8-wave
+        // gemm_dma_kernel (128x64 per wave) stays selectable for comparison
+        if (gemm_kernel_choice() == 1) {
+            a.vec_store = sizeof(Tout) == 2 && a.vec_store;
+            if (bcol) hipLaunchKernelGGL((gemm_dma_kernel<T, true, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
+            else hipLaunchKernelGGL((gemm_dma_kernel<T, false, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
+        } else {
+            if (bcol) hipLaunchKernelGGL((gemm_wave_kernel<T, true, Tout>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((gemm_wave_kernel<T, false, Tout>), grid, dim3(256), 0, st, a);
+        }
         return launch_status();
     }
     TileCfg t = pick_tile(a.M, a.N, batch);
