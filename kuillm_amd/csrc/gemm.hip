@@ -1036,9 +1036,12 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
         const int vec = sizeof(Tout) == 2 ? 8 : 4;    // elements per vector store
         a.vec_store = a.N % vec == 0 && a.ldo % vec == 0 && a.stride_o % vec == 0 && aligned16(a.out);
         dim3 grid((unsigned)(a.tiles_m * a.tiles_n * batch));
-        // 4 waves of 128x128 (one per SIMD, explicit schedule); the 8-wave
-        // gemm_dma_kernel (128x64 per wave) stays selectable for comparison
-        if (gemm_kernel_choice() == 1) {
+        // 4 waves of 128x128 (one per SIMD, explicit schedule) for deep K;
+        // short K loops (bmm's K = 128: two stages, so the prologue and the
+        // epilogue dominate) run faster on the 8-wave gemm_dma_kernel, whose
+        // second wave per SIMD overlaps them.  KUIOPS_GEMM_KERNEL=dma forces
+        // the 8-wave kernel.
+        if (gemm_kernel_choice() == 1 || a.K < 512) {
             a.vec_store = sizeof(Tout) == 2 && a.vec_store;
             if (bcol) hipLaunchKernelGGL((gemm_dma_kernel<T, true, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
             else hipLaunchKernelGGL((gemm_dma_kernel<T, false, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);

@@ -59,9 +59,9 @@ def _dt(dtype) -> int:
 # A HIP graph records the raw address of the buffer it was captured with.
 # Growing during capture would put the new allocation and its zero fill
 # inside the graph, so it is refused: run the largest shape once eagerly
-# first.  A capture stream with no buffer of its own (the eager warm-up ran
-# on another stream, as torch.cuda.graph's default capture stream does)
-# takes the device's largest buffer of that kind; replays of that graph must
+# first.  A capture stream with no buffer of its own, or one too small (the
+# eager warm-up ran on another stream, as with torch.cuda.graph's default
+# capture stream), takes the device's largest buffer of that kind; replays of that graph must
 # then not overlap eager calls on the warm-up stream.  When a call needs more
 # bytes, the old buffer is released (stream-ordered, through torch's caching
 # allocator) unless a graph was captured with it: those are kept in
@@ -92,7 +92,7 @@ def workspace(device: torch.device, nbytes: int, kind: str = "scratch") -> torch
     capturing = _capturing(device)
     key = _ws_key(device, kind)
     buf = _WS.get(key)
-    if buf is None and capturing:
+    if capturing and (buf is None or buf.numel() < nbytes):
         same = [b for (d, _, k), b in _WS.items() if d == key[0] and k == kind and b.numel() >= nbytes]
         if same:
             buf = max(same, key=lambda t: t.numel())

@@ -51,5 +51,10 @@ def test_capture_stream_borrows_and_refuses_growth(fake_streams):
     assert ops.workspace(CPU, 1 << 20, "attn") is a
     with pytest.raises(RuntimeError, match="during HIP graph capture"):
         ops.workspace(CPU, 4 << 20, "attn")
+    fake_streams.update(stream=1, capturing=False)
+    b = ops.workspace(CPU, 4 << 20, "attn")         # a larger eager call on stream 1
+    fake_streams.update(stream=7, capturing=True)   # the capture stream's borrowed buffer is too small
+    assert ops.workspace(CPU, 3 << 20, "attn") is b
+    assert any(r is a for r in ops._RETIRED)        # `a` was handed to a capture: kept alive
     with pytest.raises(RuntimeError):
         ops.workspace(CPU, 16, "gemv")              # no buffer of that kind anywhere
