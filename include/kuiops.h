@@ -218,6 +218,26 @@ KUIOPS_API int kuiops_sdpa_fwd_bias(int64_t n, int64_t hq, int64_t hkv, int64_t 
                          float *lse, float scale, int causal,
                          const void *bias, const int64_t sb[3], void *stream);
 
+/* Every other SDPA: bf16 / f16 / fp32 / fp64 Q, K, V (one dtype), head dims
+ * e and ev independent and up to 1024, optional additive bias (element
+ * (b, h, i, j) at bias + b*sb[0] + h*sb[1] + i*sb[2] + j, the Q dtype, any
+ * alignment), causal top-left masking, grouped-query heads; same tensor
+ * conventions as kuiops_sdpa_fwd.  score = scale * q.k + bias (aten's
+ * order), accumulated in fp32 (fp64 for fp64 inputs); lse (optional, fp32
+ * [n, hq, l]) is the natural-log log-sum-exp; rows with no visible key give
+ * 0 and -inf.  A SIMT kernel (one wave per query row): the coverage path for
+ * what the MFMA kernels do not take.  Replaces the reference's sdpa launcher
+ * for its full dtype / shape range (kuiops/sdpa/wrapper_sdpa.cu.j2:21-30,
+ * gate kuipy/kuiops.py:640-648).                                            */
+KUIOPS_API int kuiops_sdpa_general(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s,
+                         int64_t e, int64_t ev, int dtype,
+                         const void *Q, const int64_t sq[3],
+                         const void *K, const int64_t sk[3],
+                         const void *V, const int64_t sv[3],
+                         void *O, const int64_t so[3],
+                         float *lse, double scale, int causal,
+                         const void *bias, const int64_t sb[3], void *stream);
+
 /* Decode attention (l small, typically 1) over a KV cache, split over the
  * key axis; same tensor conventions as kuiops_sdpa_fwd.  Causal masking with
  * l > 1 aligns the queries to the END of the keys (query i sees keys

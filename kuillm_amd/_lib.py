@@ -66,6 +66,8 @@ SIGNATURES = {
                                _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp]),
     "kuiops_sdpa_fwd_bias": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
                                     _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp, _i64p, _vp]),
+    "kuiops_sdpa_general": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
+                                   _vp, _i64p, _vp, _i64p, _vp, _dbl, _int, _vp, _i64p, _vp]),
     "kuiops_sdpa_decode": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _i64p, _vp, _i64p,
                                   _vp, _i64p, _vp, _i64p, _vp, _flt, _int, _vp, _vp, _sz, _vp]),
     "kuiops_softmax_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp]),

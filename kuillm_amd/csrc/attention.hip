@@ -28,6 +28,8 @@
 //
 // Semantics: aten scaled_dot_product_attention (the reference's fallthrough,
 // kuipy/kuiops.py:627-681 rejects is_causal; tests/test_jit_ops.py:173-193).
+#include <algorithm>
+
 #include "attn_decode.hpp"
 
 namespace kuiops {
@@ -444,6 +446,113 @@ __global__ __launch_bounds__(128) void fa_decode_combine_kernel(AttnArgs a) {
     if (a.lse && tid == 0) a.lse[grow] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
 }
 
+// ------------------------------------------------------------------------
+// sdpa_general_kernel -- every other SDPA: fp32 / fp64 (and 16-bit) inputs,
+// head dims e != ev, head dims past the MFMA kernels' 64 / 128, an optional
+// additive bias of any alignment.  The reference's own family takes any float
+// dtype and any (e, ev) (kuipy/kuiops.py:640-648), with a plain launcher
+// (sdpa/wrapper_sdpa.cu.j2:21-30); this is the matching coverage path, SIMT in
+// the accumulation type (fp32, fp64 for fp64 inputs).  One wave per query
+// row, 4 rows per work-group: the query row sits in LDS; keys go in chunks
+// of 64, lane j scoring key c0 + j (a dot product over its own K row), the
+// chunk's maximum moves the running maximum (online softmax, natural
+// exponent), the chunk's probabilities pass through LDS and each lane
+// accumulates its output columns d = lane + 64 t from the chunk's V rows
+// (coalesced).  score = scale * q.k + bias (aten's order), masked keys
+// (causal: key j > query i) weigh 0; rows with no visible key give 0 and
+// LSE = -inf.
+constexpr int kGenRows = 4;          // query rows (waves) per work-group
+constexpr int kGenMaxE = 1024;       // head dims served
+constexpr int kGenAcc = kGenMaxE / 64;
+
+template <typename T> struct GenAcc { typedef float type; };
+template <> struct GenAcc<double> { typedef double type; };
+
+__device__ __forceinline__ float gen_exp(float x) { return expf(x); }
+__device__ __forceinline__ double gen_exp(double x) { return exp(x); }
+__device__ __forceinline__ float gen_log(float x) { return logf(x); }
+__device__ __forceinline__ double gen_log(double x) { return log(x); }
+// accumulation type -> element type (fp64 stays fp64)
+template <typename T, typename Acc> __device__ __forceinline__ T gen_out(Acc v) {
+    if constexpr (sizeof(T) == 8) return v;
+    else return from_f32<T>((float)v);
+}
+
+struct GenArgs {
+    int64_t n, hq, hkv, l, s, e, ev;
+    const void *Q, *K, *V, *bias;
+    void *O;
+    float *lse;
+    int64_t sq0, sq1, sq2, sk0, sk1, sk2, sv0, sv1, sv2, so0, so1, so2, sb0, sb1, sb2;
+    double scale;
+    int causal;
+};
+
+template <typename T, int NACC>
+__global__ __launch_bounds__(kGenRows * 64) void sdpa_general_kernel(GenArgs a) {
+    typedef typename GenAcc<T>::type Acc;
+    __shared__ Acc s_q[kGenRows][kGenMaxE];
+    __shared__ Acc s_p[kGenRows][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row = (int64_t)blockIdx.x * kGenRows + wave;     // (b, h, i) flattened
+    if (row >= a.n * a.hq * a.l) return;                            // whole wave leaves
+    const int64_t i = row % a.l, bh = row / a.l, h = bh % a.hq, b = bh / a.hq;
+    const int64_t hk = h / (a.hq / a.hkv);
+    const T *Q = reinterpret_cast<const T *>(a.Q) + b * a.sq0 + h * a.sq1 + i * a.sq2;
+    const T *K = reinterpret_cast<const T *>(a.K) + b * a.sk0 + hk * a.sk1;
+    const T *V = reinterpret_cast<const T *>(a.V) + b * a.sv0 + hk * a.sv1;
+    const T *B = a.bias ? reinterpret_cast<const T *>(a.bias) + b * a.sb0 + h * a.sb1 + i * a.sb2 : nullptr;
+    for (int64_t d = lane; d < a.e; d += 64) s_q[wave][d] = (Acc)to_f32_or_self(Q[d]);
+    __builtin_amdgcn_wave_barrier();
+    const Acc scale = (Acc)a.scale;
+    const int64_t kend = a.causal ? min(a.s, i + 1) : a.s;
+    Acc m = -INFINITY, lsum = 0;
+    Acc o[NACC];
+#pragma unroll
+    for (int t = 0; t < NACC; ++t) o[t] = 0;
+    for (int64_t c0 = 0; c0 < kend; c0 += 64) {
+        const int64_t key = c0 + lane;
+        Acc sc = -INFINITY;
+        if (key < kend) {
+            const T *kr = K + key * a.sk2;
+            Acc dot = 0;
+            for (int64_t d = 0; d < a.e; ++d) dot += s_q[wave][d] * (Acc)to_f32_or_self(kr[d]);
+            sc = scale * dot;
+            if (B) sc += (Acc)to_f32_or_self(B[key]);
+        }
+        const Acc mc = wave_max(sc);
+        const Acc m_new = m > mc ? m : mc;
+        if (m_new == -INFINITY) continue;            // nothing visible yet (bias -inf)
+        const Acc alpha = m == -INFINITY ? (Acc)0 : gen_exp(m - m_new);
+        const Acc pj = sc == -INFINITY ? (Acc)0 : gen_exp(sc - m_new);
+        lsum = lsum * alpha + wave_sum(pj);
+#pragma unroll
+        for (int t = 0; t < NACC; ++t) o[t] *= alpha;
+        m = m_new;
+        s_p[wave][lane] = pj;
+        __builtin_amdgcn_wave_barrier();
+        const int nk = (int)min((int64_t)64, kend - c0);
+        for (int j = 0; j < nk; ++j) {
+            const Acc p = s_p[wave][j];
+            const T *vr = V + (c0 + j) * a.sv2;
+#pragma unroll
+            for (int t = 0; t < NACC; ++t) {
+                const int64_t d = lane + 64 * t;
+                if (d < a.ev) o[t] += p * (Acc)to_f32_or_self(vr[d]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    T *O = reinterpret_cast<T *>(a.O) + b * a.so0 + h * a.so1 + i * a.so2;
+    const Acc inv = lsum > 0 ? (Acc)1 / lsum : (Acc)0;
+#pragma unroll
+    for (int t = 0; t < NACC; ++t) {
+        const int64_t d = lane + 64 * t;
+        if (d < a.ev) O[d] = gen_out<T, Acc>(o[t] * inv);
+    }
+    if (a.lse && lane == 0) a.lse[row] = lsum > 0 ? (float)(m + gen_log(lsum)) : -INFINITY;
+}
+
 // ------------------------------------------------------------ host side
 
 static bool attn_common_ok(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, int64_t e, int64_t ev,
@@ -717,4 +826,52 @@ extern "C" int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l,
     hipStream_t st = as_stream(stream);
     if (dtype == KUIOPS_BF16) return e == 128 ? launch_decode<bf16_t, 128>(a, st) : launch_decode<bf16_t, 64>(a, st);
     return e == 128 ? launch_decode<f16_t, 128>(a, st) : launch_decode<f16_t, 64>(a, st);
+}
+
+// General SDPA entry point (any float dtype, e != ev, head dims up to 1024,
+// optional bias of any alignment); see sdpa_general_kernel.
+template <typename T>
+static int launch_general(const GenArgs &a, hipStream_t st) {
+    const int64_t rows = a.n * a.hq * a.l;
+    const dim3 grid((unsigned)cdiv(rows, kGenRows)), block(kGenRows * 64);
+    const int64_t w = std::max(a.ev, (int64_t)1);
+    if (w <= 64) hipLaunchKernelGGL((sdpa_general_kernel<T, 1>), grid, block, 0, st, a);
+    else if (w <= 128) hipLaunchKernelGGL((sdpa_general_kernel<T, 2>), grid, block, 0, st, a);
+    else if (w <= 256) hipLaunchKernelGGL((sdpa_general_kernel<T, 4>), grid, block, 0, st, a);
+    else if (w <= 512) hipLaunchKernelGGL((sdpa_general_kernel<T, 8>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((sdpa_general_kernel<T, 16>), grid, block, 0, st, a);
+    return launch_status();
+}
+
+extern "C" int kuiops_sdpa_general(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s, int64_t e, int64_t ev,
+                                   int dtype, const void *Q, const int64_t sq[3], const void *K, const int64_t sk[3],
+                                   const void *V, const int64_t sv[3], void *O, const int64_t so[3], float *lse,
+                                   double scale, int causal, const void *bias, const int64_t sb[3], void *stream) {
+    if (n < 0 || hq < 0 || hkv <= 0 || l < 0 || s < 0 || e <= 0 || ev <= 0 || !sq || !sk || !sv || !so)
+        return KUIOPS_E_INVALID;
+    if (hq % hkv || !Q || !K || !V || !O || (bias && !sb)) return KUIOPS_E_INVALID;
+    if (dtype != KUIOPS_BF16 && dtype != KUIOPS_F16 && dtype != KUIOPS_F32 && dtype != KUIOPS_F64)
+        return KUIOPS_E_UNSUPPORTED;
+    if (e > kGenMaxE || ev > kGenMaxE) return KUIOPS_E_UNSUPPORTED;
+    if (!(scale > 0.0)) return KUIOPS_E_UNSUPPORTED;
+    const int64_t rows = n * hq * l;
+    if (rows == 0) return KUIOPS_OK;
+    if (cdiv(rows, kGenRows) > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    GenArgs a{};
+    a.n = n; a.hq = hq; a.hkv = hkv; a.l = l; a.s = s; a.e = e; a.ev = ev;
+    a.Q = Q; a.K = K; a.V = V; a.O = O; a.lse = lse; a.bias = bias;
+    a.sq0 = sq[0]; a.sq1 = sq[1]; a.sq2 = sq[2];
+    a.sk0 = sk[0]; a.sk1 = sk[1]; a.sk2 = sk[2];
+    a.sv0 = sv[0]; a.sv1 = sv[1]; a.sv2 = sv[2];
+    a.so0 = so[0]; a.so1 = so[1]; a.so2 = so[2];
+    if (bias) { a.sb0 = sb[0]; a.sb1 = sb[1]; a.sb2 = sb[2]; }
+    a.scale = scale;
+    a.causal = causal ? 1 : 0;
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+        case KUIOPS_BF16: return launch_general<bf16_t>(a, st);
+        case KUIOPS_F16: return launch_general<f16_t>(a, st);
+        case KUIOPS_F32: return launch_general<float>(a, st);
+        default: return launch_general<double>(a, st);
+    }
 }

@@ -36,6 +36,7 @@ K = torch.ops.kuiops      # the custom ops: HIP kernels behind the C ABI
 
 _FLOAT_DTYPES = (torch.float16, torch.float32, torch.float64, torch.bfloat16)
 _HALF = (torch.float16, torch.bfloat16)
+_FLOATS = (torch.float16, torch.bfloat16, torch.float32, torch.float64)
 _SIZE_LIMIT = 2 ** 31 - 1
 
 
@@ -251,14 +252,16 @@ class SdpaImpl(_Family):
             return None
         if not (_is_dev(q, k, v) and q.dim() == 4 and k.dim() == 4 and v.dim() == 4):
             return None
-        if not (q.dtype == k.dtype == v.dtype and q.dtype in _HALF):
+        if not (q.dtype == k.dtype == v.dtype and q.dtype in _FLOATS):
             return None
         n, hq, l, e = (int(x) for x in q.shape)
         n2, hkv, s, e2 = (int(x) for x in k.shape)
         n3, hkv3, s3, ev = (int(x) for x in v.shape)
         if (n, e) != (n2, e2) or (n, hkv, s) != (n3, hkv3, s3) or hkv == 0 or hq % hkv:
             return None
-        if e != ev or not 0 < e <= 128 or n > 65535 or hq > 65535:
+        # the MFMA kernels take 16-bit e == ev <= 128; everything else up to
+        # 1024 (any float dtype, e != ev) runs on kuiops_sdpa_general
+        if not (0 < e <= 1024 and 0 < ev <= 1024) or n > 65535 or hq > 65535:
             return None
         if bias is not None:
             if not (_is_dev(bias) and bias.device == q.device and bias.dtype == q.dtype and bias.dim() <= 4):

@@ -313,6 +313,36 @@ def _bias_view(bias, n, hq, l, s, dtype):
     return b.expand(n, hq, l, s)
 
 
+def _sdpa_general(q, k, v, is_causal, scale, return_lse, out, bias, dims):
+    """kuiops_sdpa_general: fp32 / fp64 inputs, e != ev, head dims past 128."""
+    n, hq, hkv, l, s, e, ev = dims
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float16, torch.float32,
+                                                                torch.float64):
+        raise _lib.Unsupported("sdpa_general", _lib.E_UNSUPPORTED)
+    if out is None:
+        out = torch.empty((n, hq, l, ev), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (n, hq, l, ev) or out.stride(-1) != 1 or out.dtype != q.dtype:
+        raise _lib.KuiopsError("sdpa", _lib.E_INVALID)
+    lse = torch.empty((n, hq, l), dtype=torch.float32, device=q.device) if return_lse else None
+    if out.numel() == 0:
+        if lse is not None:
+            lse.fill_(-math.inf)
+        return out, lse
+    b = None
+    if bias is not None:
+        if bias.dtype != q.dtype or bias.dim() > 4:
+            raise _lib.Unsupported("sdpa_general", _lib.E_UNSUPPORTED)
+        b = bias.reshape((1,) * (4 - bias.dim()) + tuple(bias.shape)).expand(n, hq, l, s)
+        if s > 1 and b.stride(-1) != 1:
+            b = b.contiguous()
+    _lib.check("kuiops_sdpa_general", _lib_handle().kuiops_sdpa_general(
+        n, hq, hkv, l, s, e, ev, _dt(q.dtype), q.data_ptr(), _lib.strides3(*q.stride()[:3]), k.data_ptr(),
+        _lib.strides3(*k.stride()[:3]), v.data_ptr(), _lib.strides3(*v.stride()[:3]), out.data_ptr(),
+        _lib.strides3(*out.stride()[:3]), _ptr(lse), float(scale), 1 if is_causal else 0, _ptr(b),
+        _lib.strides3(*b.stride()[:3]) if b is not None else None, _stream(q.device)))
+    return out, lse
+
+
 def _pad_head(t, e_pad):
     e = t.shape[-1]
     return t if e == e_pad else torch.nn.functional.pad(t, (0, e_pad - e))
@@ -333,6 +363,8 @@ def sdpa(q, k, v, is_causal=False, scale=None, return_lse=True, decode_max_rows=
     q, k, v, (n, hq, hkv, l, s, e, ev) = _attn_prep(q, k, v)
     if scale is None:
         scale = 1.0 / math.sqrt(e)
+    if q.dtype not in HALF or e != ev or e > 128:
+        return _sdpa_general(q, k, v, is_causal, scale, return_lse, out, bias, (n, hq, hkv, l, s, e, ev))
     if e == ev and e < 128 and e not in (64,) and q.dtype in HALF:
         # other head dims: zero-pad to the kernels' 64 / 128 (q k^T and the
         # kept output columns are unchanged; the scale is the caller's)

@@ -234,3 +234,95 @@ def test_sdpa_causal_paired_blocks(cuda, n, hq, hkv, l, s, d):
         single, _ = ops.sdpa(q[b:b + 1, h:h + 1].contiguous(), k[b:b + 1, kh:kh + 1].contiguous(),
                              v[b:b + 1, kh:kh + 1].contiguous(), is_causal=True)
         assert (single.float() - out[b:b + 1, h:h + 1].float()).abs().max().item() < 2e-2
+
+
+# ------------------------------------------------ general SDPA (any float dtype, e != ev, wide heads)
+
+def test_sdpa_fp32_golden(cuda, golden):
+    """The reference family's own test case in fp32 (tests/test_jit_ops.py:173-193:
+    N, H, L, S = 2, 3, 8, 10, head dim 16, a full float bias, scale 0.3) on
+    kuiops_sdpa_general, against aten's fp32 outputs: the bias case, its LSE,
+    causal and full attention."""
+    Q, K, V, B = (torch.from_numpy(golden[k]).to(cuda) for k in ("sdpa_Q", "sdpa_K", "sdpa_V", "sdpa_bias"))
+    out, lse = ops.sdpa(Q, K, V, scale=0.3, bias=B)
+    assert out.dtype == torch.float32 and lse.dtype == torch.float32
+    np.testing.assert_allclose(npy(out), golden["sdpa_out_bias"], rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(npy(lse), golden["sdpa_lse_bias"], rtol=1e-5, atol=1e-5)
+    out, _ = ops.sdpa(Q, K, V, is_causal=True)
+    np.testing.assert_allclose(npy(out), golden["sdpa_out_causal"], rtol=1e-4, atol=1e-5)
+    out, _ = ops.sdpa(Q, K, V)
+    np.testing.assert_allclose(npy(out), golden["sdpa_out_full"], rtol=1e-4, atol=1e-5)
+
+
+GENERAL = [  # n, hq, hkv, l, s, e, ev
+    (2, 3, 3, 8, 10, 16, 12),            # the reference test's e != ev shape
+    (1, 4, 2, 37, 53, 64, 96),
+    (1, 2, 1, 20, 70, 160, 160),         # head dims past the MFMA kernels
+    (2, 2, 2, 9, 130, 256, 64),
+    (1, 1, 1, 3, 1, 8, 1100 // 2),
+]
+
+
+@pytest.mark.parametrize("n,hq,hkv,l,s,e,ev", GENERAL)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_sdpa_general_vs_oracle(cuda, n, hq, hkv, l, s, e, ev, dtype, causal, with_bias):
+    """kuiops_sdpa_general against the fp64 oracle: fp64 to 1e-12, fp32 to
+    1e-5, bf16 at the north-star tolerance; LSE in natural log."""
+    q, k, v = gen((n, hq, l, e), dtype, 31), gen((n, hkv, s, e), dtype, 32), gen((n, hkv, s, ev), dtype, 33)
+    bias = gen((n, hq, l, s), dtype, 34) if with_bias else None
+    scale = 0.3 if with_bias else None
+    out, lse = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda), is_causal=causal, scale=scale,
+                        bias=bias.to(cuda) if with_bias else None)
+    ref, lref = O.sdpa(q.double().numpy(), k.double().numpy(), v.double().numpy(), causal=causal, scale=scale,
+                       bias=bias.double().numpy() if with_bias else None)
+    assert out.shape == (n, hq, l, ev) and out.dtype == dtype
+    o = out.double().cpu().numpy()
+    tol = {torch.float64: 1e-12, torch.float32: 1e-5, torch.bfloat16: 1e-2}[dtype]
+    err = np.abs(o - ref) - (tol + tol * np.abs(ref))
+    assert err.max() <= 0, f"max excess {err.max():.3e}"
+    np.testing.assert_allclose(lse.double().cpu().numpy(), lref, rtol=1e-5, atol=1e-5)
+
+
+def test_sdpa_general_masked_rows_and_broadcast_bias(cuda):
+    """A broadcast padding mask (-inf on the first keys of one batch entry)
+    and a row with every key masked: that row gives 0 and LSE -inf, as the
+    oracle (and verify mode) treat it."""
+    n, h, l, s, e, ev = 2, 2, 6, 9, 24, 40
+    q, k, v = gen((n, h, l, e), torch.float32, 41), gen((n, h, s, e), torch.float32, 42), gen((n, h, s, ev), torch.float32, 43)
+    mask = torch.zeros(n, 1, 1, s)
+    mask[1, :, :, :4] = -math.inf
+    mask_full = mask.expand(n, h, l, s).clone()
+    mask_full[0, 1, 2, :] = -math.inf                 # one row sees no key
+    out, lse = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda), bias=mask_full.to(cuda))
+    ref, lref = O.sdpa(q.numpy(), k.numpy(), v.numpy(), bias=mask_full.numpy())
+    np.testing.assert_allclose(npy(out), ref, rtol=1e-5, atol=1e-5)
+    assert float(out[0, 1, 2].abs().max()) == 0.0 and math.isinf(float(lse[0, 1, 2]))
+    out2, _ = ops.sdpa(q.to(cuda), k.to(cuda), v.to(cuda), bias=mask.to(cuda))     # stride-0 broadcast
+    ref2, _ = O.sdpa(q.numpy(), k.numpy(), v.numpy(), bias=np.broadcast_to(mask.numpy(), (n, h, l, s)))
+    np.testing.assert_allclose(npy(out2), ref2, rtol=1e-5, atol=1e-5)
+
+
+def test_sdpa_general_under_kuiper_mode(cuda):
+    """The reference family's call (aten._scaled_dot_product_efficient_attention
+    with a full fp32 bias, e != ev, scale 0.3: tests/test_jit_ops.py:173-193)
+    is served by SdpaImpl (the general kernel) under KuiperMode instead of
+    falling through: output and LSE against the oracle."""
+    import kuillm_amd as kuipy
+    from kuillm_amd import kuiops as K
+    q, k = gen((2, 3, 8, 16), torch.float32, 51), gen((2, 3, 10, 16), torch.float32, 52)
+    v, bias = gen((2, 3, 10, 12), torch.float32, 53), gen((2, 3, 8, 10), torch.float32, 54)
+    func = torch.ops.aten._scaled_dot_product_efficient_attention.default
+    args = (q.to(cuda), k.to(cuda), v.to(cuda), bias.to(cuda), True)
+    impl = K.SdpaImpl({})
+    spec = impl.supported(func, args, {"scale": 0.3})
+    assert spec is not None
+    out, lse = impl.run(spec, args, {"scale": 0.3})[:2]
+    ref, lref = O.sdpa(q.double().numpy(), k.double().numpy(), v.double().numpy(), scale=0.3,
+                       bias=bias.double().numpy())
+    np.testing.assert_allclose(npy(out), ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(npy(lse)[..., :8], lref, rtol=1e-5, atol=1e-5)
+    with kuipy.KuiperMode():
+        out2 = func(*args, scale=0.3)[0]
+    assert torch.equal(out2, out)

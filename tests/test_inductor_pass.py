@@ -63,13 +63,13 @@ def test_every_hot_op_is_replaced():
 def test_unsupported_nodes_stay():
     def f(x, w, q, k, v, idx):
         y = aten.mm(x, w)                                         # int32: not served
-        a = aten._scaled_dot_product_flash_attention(q, k, v, 0.0, False)   # head dim 160
+        a = aten._scaled_dot_product_flash_attention(q, k, v, 0.0, False)   # head dim 2048
         s = aten._softmax(q, 2, False)                            # not the last dim
         e = aten.index(q, [idx, None, idx])                       # index axes not adjacent
         return y, a[0], s, e
     with FakeTensorMode():
-        args = (cu(4, 4, dtype=torch.int32), cu(4, 4, dtype=torch.int32), cu(1, 2, 8, 160), cu(1, 2, 8, 160),
-                cu(1, 2, 8, 160), cu(2, dtype=torch.int64))
+        args = (cu(4, 4, dtype=torch.int32), cu(4, 4, dtype=torch.int32), cu(1, 2, 8, 2048), cu(1, 2, 8, 2048),
+                cu(1, 2, 8, 2048), cu(2, dtype=torch.int64))
         gm = make_fx(f)(*args)
         assert KI.replace_in_graph(gm.graph) == 0
 

@@ -83,10 +83,15 @@ def test_sdpa_gate(fake):
     assert impl.supported(fl, (q, k, v, 0.0, False, True), {}) is None                   # debug mask
     assert impl.supported(fl, (cu(1, 3, 64, 128), k, v), {}) is None                     # 3 % 2 heads
     assert impl.supported(fl, (cu(1, 2, 8, 96), cu(1, 2, 8, 96), cu(1, 2, 8, 96)), {}) is not None  # padded
-    assert impl.supported(fl, (cu(1, 2, 8, 160), cu(1, 2, 8, 160), cu(1, 2, 8, 160)), {}) is None
-    f32 = torch.float32
-    assert impl.supported(fl, (cu(1, 2, 8, 64, dtype=f32), cu(1, 2, 8, 64, dtype=f32),
-                               cu(1, 2, 8, 64, dtype=f32)), {}) is None
+    # wide heads, e != ev and fp32 / fp64 (the reference gate's _FLOAT_DTYPES) take the general kernel
+    assert impl.supported(fl, (cu(1, 2, 8, 160), cu(1, 2, 8, 160), cu(1, 2, 8, 160)), {}) is not None
+    assert impl.supported(fl, (cu(1, 2, 8, 16), cu(1, 2, 8, 16), cu(1, 2, 8, 12)), {}) is not None
+    assert impl.supported(fl, (cu(1, 2, 8, 2048), cu(1, 2, 8, 2048), cu(1, 2, 8, 2048)), {}) is None
+    for dt in (torch.float32, torch.float64):
+        assert impl.supported(fl, (cu(1, 2, 8, 64, dtype=dt), cu(1, 2, 8, 64, dtype=dt),
+                                   cu(1, 2, 8, 64, dtype=dt)), {}) is not None
+    assert impl.supported(fl, (cu(1, 2, 8, 64, dtype=torch.int32), cu(1, 2, 8, 64, dtype=torch.int32),
+                               cu(1, 2, 8, 64, dtype=torch.int32)), {}) is None
 
 
 def test_topk_gate(fake):
