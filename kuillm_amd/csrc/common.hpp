@@ -352,7 +352,10 @@ constexpr unsigned kLLSpinLimit = 1u << 20;      // polls of one epoch-tagged wa
 // wait: a poll reads past the per-XCD L2, so a longer pause trades wake-up
 // latency for fabric traffic (persistent Llama-1B step: sleep 4 / 16 cost
 // 3 / 17 us per token more than 1)
-constexpr int kLLSleep = 1;
+#ifndef KUIOPS_LL_SLEEP
+#define KUIOPS_LL_SLEEP 1
+#endif
+constexpr int kLLSleep = KUIOPS_LL_SLEEP;
 
 // Epoch-tagged waits spin per wave: a wave polls its own input words until
 // all carry the expected epoch (a wave vote, no work-group reduction per

@@ -359,7 +359,17 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
                 if (l == 0) step_proj<T, kXRmsNorm, KCD, kOutRope, 0, PlainIO, LLIO>(args, 0, l, idx, tk, wl);
                 else step_proj<T, kXRmsNorm, KCD, kOutRope, 0, LLIO, LLIO>(args, 0, l, idx, tk, wl);
                 break;
-            case 1: step_attention<T, HD>(args, l, idx, tk); break;
+            case 1: {
+                // Work-group w runs on XCD w % 8, and job j on work-group
+                // j % G: jobs whose index agrees mod 8 share an XCD (and its
+                // L2).  Give them consecutive query heads, i.e. the heads of
+                // one KV head, so that head's cache rows are fetched into
+                // one L2 instead of one per query head.
+                const int hq = (int)args.hq;
+                const int head = (hq % 8 == 0) ? (idx % 8) * (hq / 8) + idx / 8 : idx;
+                step_attention<T, HD>(args, l, head, tk);
+                break;
+            }
             case 2: step_proj<T, kXPlain, KCD, kOutPlain, 0, LLIO, LLIO>(args, 2, l, idx, tk, wl); break;
             case 3: step_proj<T, kXRmsNorm, KCD, kOutSwiGlu, RLD, LLIO, LLIO>(args, 3, l, idx, tk, wl); break;
             case 4: step_proj<T, kXPlain, KCF, kOutPlain, RLF, LLIO, LLIO>(args, 4, l, idx, tk, wl); break;
