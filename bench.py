@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--summarize-trace", nargs=2, metavar=("DIR", "OUT_MD"),
                     help="write a kernel-duration table from a rocprofv3 --kernel-trace run")
     ap.add_argument("--command", default="", help="the profiling command, recorded in the summary")
+    ap.add_argument("--profile-decode-step", action="store_true",
+                    help="run 4 one-token persistent decode steps of BASELINE config 5 (512-token prompt), "
+                         "one dispatch each, for rocprofv3 --pmc passes")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="run only the dominant kernel of each workload 3x plus a 256 MiB copy "
                          "(the byte-counter calibration), for rocprofv3 --pmc runs")
@@ -601,6 +604,17 @@ def main():
     dev = torch.device("cuda:0")
     if args.profile_kernels:
         profile_kernels(torch, ops, dev)
+        return
+    if args.profile_decode_step:
+        from kuillm_amd.decoder import LlamaDecoder, LlamaShape
+        dec = LlamaDecoder(LlamaShape(**LLAMA1B), llama_state(torch, LLAMA1B, dev), capacity=640, device=dev)
+        if not dec.persistent:
+            sys.exit("bench.py: the persistent decode step is not available on this device")
+        dec.prefill(torch.randint(0, LLAMA1B["vocab"], (1, 512), generator=torch.Generator().manual_seed(0)))
+        torch.cuda.synchronize()
+        for _ in range(4):
+            dec._decode_step_fused(1)
+        dec.check_step_error()
         return
 
     # ---- headline: BASELINE config 2, bf16 addmm 4096^3 with a 1-D bias
