@@ -233,6 +233,7 @@ struct DecMArgs {
     void *vc; int64_t sv0, sv1, sv2;
     int64_t cap;
     int64_t kq;                              // k per wave, a multiple of 64
+    int64_t ldsx;                            // LDS row stride of the staged x rows (elements)
 };
 
 __device__ __forceinline__ int64_t pair_div_m(const DecMArgs &a, int64_t p) {
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     typedef typename Mfma<T>::frag frag;
     constexpr int PF = 32 / NW;                       // 64-k steps in flight per wave (64 KB per work-group)
     extern __shared__ __attribute__((aligned(16))) char dsm[];
-    T *sx = reinterpret_cast<T *>(dsm);               // [M][K] normalised rows of x
+    T *sx = reinterpret_cast<T *>(dsm);               // [M][ldsx] normalised rows of x
     __shared__ float red[NW][4][64];
     __shared__ float vals[16][17];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -329,7 +330,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     for (int m = wave; m < M; m += NW) {
         const T *in = reinterpret_cast<const T *>(a.in) +
                       (a.in_row ? max((int64_t)0, min(a.in_row[m], a.in_rows - 1)) : (int64_t)m) * a.ld_in;
-        T *srow = sx + (int64_t)m * a.K;
+        T *srow = sx + (int64_t)m * a.ldsx;
         float ss = 0.f;
         for (int c0 = lane; c0 < nch; c0 += 64 * XB) {
             u32x4 v0[XB], v1[XB];
@@ -416,7 +417,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
                 for (int h = 0; h < 2; ++h) {
                     const bool in_k = k + 32 * h < kend;
                     const u32x4 xa = (mrow && in_k)
-                                         ? *reinterpret_cast<const u32x4 *>(sx + (int64_t)n * a.K + k + 32 * h)
+                                         ? *reinterpret_cast<const u32x4 *>(sx + (int64_t)n * a.ldsx + k + 32 * h)
                                          : u32x4{0, 0, 0, 0};
                     acc = Mfma<T>::m16(as_frag<frag>(xa), as_frag<frag>(wr[j][h]), acc);
                 }
@@ -666,7 +667,12 @@ extern "C" int kuiops_decode_rows_batched(
     int nw = 4;
     while (nw < 16 && grid * nw < 2048 && K >= (int64_t)nw * 2 * 128) nw *= 2;
     a.kq = cdiv(cdiv(K, nw), 64) * 64;
-    const size_t lds = (size_t)M * K * 2;
+    // The 16 lanes of an MFMA A-operand read sit in 16 rows of x at one k:
+    // rows 16 bytes apart modulo the 64 banks (stride K + 8) spread them over
+    // the banks (a row stride of K, a multiple of 256 bytes, puts all 16 in
+    // one bank group); kept unpadded when the padding would not fit.
+    a.ldsx = (int64_t)M * (K + 8) * 2 <= kDecMaxLds ? K + 8 : K;
+    const size_t lds = (size_t)M * a.ldsx * 2;
     hipStream_t st = as_stream(stream);
 #define KUIOPS_DECM(T)                                                                                   \
     switch (x_kind) {                                                                                    \
