@@ -599,8 +599,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
 //   * before the last k-step of a stage each wave waits for its own DMA of
 //     the next stage, the work-group meets at one bare s_barrier (every wave
 //     has then read the current stage), and the next stage's first
-//     fragments plus the DMA refill of the current stage's buffers with
-//     stage s + 2 are issued under the last k-step's MFMAs;
+//     fragments plus half of the DMA refill of the current stage's buffers
+//     with stage s + 2 are issued under the last k-step's MFMAs, the other
+//     half under the next stage's first k-step (8 DMA instructions per
+//     k-step at most: 99 against 108 us at 4096^3 for all 16 in one);
 //   * the loop is unrolled over the two LDS stages with the last two stages
 //     peeled, so no conditional DMA sits inside it (the compiler's wait
 //     insertion is not path-sensitive: a conditional refill makes it wait
@@ -627,13 +629,18 @@ void gemm_wave_kernel(GemmArgs a) {
     const int wm = wave >> 1, wn = wave & 1;
     int tm, tn, bz;
     tile_coords_batched(blockIdx.x, gridDim.x, a.tiles_m, a.tiles_n, tm, tn, bz);
+    // (uniform: kept in SGPRs, so the epilogue's addressing does not hold
+    // VGPRs across the K loop, which would spill)
+    tm = __builtin_amdgcn_readfirstlane(tm);
+    tn = __builtin_amdgcn_readfirstlane(tn);
+    bz = __builtin_amdgcn_readfirstlane(bz);
     const T *Ab = reinterpret_cast<const T *>(a.A) + bz * a.stride_a;
     const T *Bb = reinterpret_cast<const T *>(a.B) + bz * a.stride_b;
     const int64_t M = a.M, N = a.N, lda = a.lda, ldb = a.ldb, ldo = a.ldo, ldcin = a.ldcin;
     const int c_kind = a.c_kind, vec_store = a.vec_store;
     const float alpha = a.alpha, beta = a.beta;
     const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
-    const int nk = (int)(a.K / BK);                // even, >= 2
+    const int nk = (int)(a.K / BK);                // even, >= 8 (K % 128 == 0, K >= 512)
     auto swzK = [](int r) { return (r >> 1) & 7; };
 
     // DMA: per stage and operand 32 blocks of 1 KB, 8 per wave.  Rows /
@@ -661,10 +668,11 @@ void gemm_wave_kernel(GemmArgs a) {
     // where the DMA needs them, instead of a per-lane waterfall loop)
     const __amdgpu_buffer_rsrc_t rsA = make_rsrc(uniform_ptr(baseA), 0xffffffffu);
     const __amdgpu_buffer_rsrc_t rsB = make_rsrc(uniform_ptr(baseB), 0xffffffffu);
-    auto issue = [&](int kt, char *sa, char *sb) __attribute__((always_inline)) {
+    // DMA blocks j0 .. j1 - 1 of both operands of stage kt
+    auto issue = [&](int kt, char *sa, char *sb, int j0, int j1) __attribute__((always_inline)) {
         const uint32_t ka = (uint32_t)kt * stepA, kb = (uint32_t)kt * stepB;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = j0; j < j1; ++j) {
             dma16_buf(rsA, goffA[j], ka, sa + (wave * 8 + j) * 1024);
             dma16_buf(rsB, goffB[j], kb, sb + (wave * 8 + j) * 1024);
         }
@@ -730,29 +738,39 @@ void gemm_wave_kernel(GemmArgs a) {
             for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::m32(fb[slot][j], fa[slot][i], acc[i][j]);
     };
     // scheduling groups of one k-step: MFMA, LDS read (12 of them: 8 for
-    // K-contiguous B), and the stage's DMA (16) when it is issued here
+    // K-contiguous B), and a DMA instruction after every second MFMA when
+    // half a stage's DMA (8 instructions) is issued in this k-step
     constexpr int NRD = BCOL ? 8 : 12;
-    auto pattern = [&](int nvmem) __attribute__((always_inline)) {
+    auto pattern = [&](bool dma) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (t < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            if (t < nvmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            if (dma && (t & 1)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
     };
+    // Stage s from buffers (sa, sb).  The DMA of a stage goes out in two
+    // halves: blocks 0-3 under the last k-step of stage s - 2 (right after
+    // the barrier that frees its buffers) and blocks 4-7 under the first
+    // k-step of stage s - 1, so no k-step carries more than 8 DMA
+    // instructions.  `half2`: issue blocks 4-7 of stage s + 1 into (pa, pb);
+    // `next`: wait for this wave's DMA of stage s + 1, meet at the barrier and
+    // read stage s + 1's first fragments from (na, nb); `half1`: issue blocks
+    // 0-3 of stage s + 2 into this stage's buffers (ra, rb).
     auto stage = [&](int s, const char *sa, const char *sb, const char *na, const char *nb, char *ra, char *rb,
-                     bool next, bool refill) __attribute__((always_inline)) {
+                     char *pa, char *pb, bool half2, bool next, bool half1) __attribute__((always_inline)) {
+        if (half2) issue(s + 1, pa, pb, 4, 8);
         rd(sa, sb, 1, 1);
         mm(0);
-        pattern(0);
+        pattern(half2);
         __builtin_amdgcn_sched_barrier(0);
         rd(sa, sb, 2, 0);
         mm(1);
-        pattern(0);
+        pattern(false);
         __builtin_amdgcn_sched_barrier(0);
         rd(sa, sb, 3, 1);
         mm(0);
-        pattern(0);
+        pattern(false);
         __builtin_amdgcn_sched_barrier(0);
         if (next) {
             wait_vmcnt<0>();                         // this wave's DMA of stage s + 1
@@ -760,32 +778,47 @@ void gemm_wave_kernel(GemmArgs a) {
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
             rd(na, nb, 0, 0);
-            if (refill) issue(s + 2, ra, rb);
+            if (half1) issue(s + 2, ra, rb, 0, 4);
         }
         mm(1);
-        pattern(refill ? 16 : 0);
+        pattern(half1);
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    issue(0, sA0, sB0);
+    // nk is even and >= 4: stage 0, pairs of stages, the last three peeled
+    // (no conditional DMA inside the loop)
+    // A row addend (bias) is loaded with the first stage and kept in LDS as
+    // beta * value, so the epilogue does not wait on memory for it.
+    const Tout *cin = reinterpret_cast<const Tout *>(a.cin);
+    __shared__ __attribute__((aligned(16))) float sRow[256];
+    float row_add = 0.f;
+    if (c_kind == KUIOPS_C_ROW && n0 + tid < N) row_add = beta * to_f32(cin[n0 + tid]);
+    issue(0, sA0, sB0, 0, 8);
     wait_vmcnt<0>();
+    sRow[tid] = row_add;      // visible at the epilogue: every stage barrier waits for LDS writes first
     __builtin_amdgcn_s_barrier();
     rd(sA0, sB0, 0, 0);
-    issue(1, sA1, sB1);
-    int s = 0;
-    for (; s + 2 < nk; s += 2) {
-        stage(s, sA0, sB0, sA1, sB1, sA0, sB0, true, true);
-        stage(s + 1, sA1, sB1, sA0, sB0, sA1, sB1, true, true);
+    issue(1, sA1, sB1, 0, 8);
+    stage(0, sA0, sB0, sA1, sB1, sA0, sB0, sA1, sB1, false, true, true);
+    int s = 1;
+    for (; s + 4 < nk; s += 2) {
+        stage(s, sA1, sB1, sA0, sB0, sA1, sB1, sA0, sB0, true, true, true);
+        stage(s + 1, sA0, sB0, sA1, sB1, sA0, sB0, sA1, sB1, true, true, true);
     }
-    stage(s, sA0, sB0, sA1, sB1, sA0, sB0, true, false);
-    stage(s + 1, sA1, sB1, sA0, sB0, sA1, sB1, false, false);
+    stage(s, sA1, sB1, sA0, sB0, sA1, sB1, sA0, sB0, true, true, true);
+    stage(s + 1, sA0, sB0, sA1, sB1, sA0, sB0, sA1, sB1, true, true, false);
+    stage(s + 2, sA1, sB1, sA0, sB0, sA1, sB1, sA0, sB0, false, false, false);
 
-    // Epilogue: out = alpha * acc + beta * addend (fp32), one rounding.
-    const Tout *cin = reinterpret_cast<const Tout *>(a.cin);
+    // Epilogue: out = alpha * acc + beta * addend (fp32), one rounding.  One
+    // code path for every addend kind: the row addend comes from LDS (zeros
+    // for the other kinds) and a full-matrix addend replaces it under a
+    // uniform branch, so the accumulator reads are not duplicated per kind
+    // (duplicated, the compiler hoists them and runs out of VGPRs).
     Tout *out = reinterpret_cast<Tout *>(a.out) + bz * a.stride_o;
-    // beta * addend for 4 consecutive columns (8-byte loads where aligned)
+    const bool full = c_kind == KUIOPS_C_FULL;
+    // beta * C[row, col .. col + 3] (8-byte loads where aligned)
     auto addend4 = [&](int64_t row, int64_t col, float v[4]) __attribute__((always_inline)) {
-        const Tout *p = c_kind == KUIOPS_C_ROW ? cin + col : cin + row * ldcin + col;
+        const Tout *p = cin + row * ldcin + col;
         if (sizeof(Tout) == 2 && col + 3 < N && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
             const u32x2 w = *reinterpret_cast<const u32x2 *>(p);
             const Tout *h = reinterpret_cast<const Tout *>(&w);
@@ -796,54 +829,38 @@ void gemm_wave_kernel(GemmArgs a) {
             for (int e = 0; e < 4; ++e) v[e] = col + e < N ? beta * to_f32(p[e]) : 0.f;
         }
     };
-    // the 4 output values of (i, j, g); KIND is the addend kind
-    auto value4 = [&](auto kind, int i, int j, int g, int64_t row, int64_t col, const float brow[4], float v[4])
-        __attribute__((always_inline)) {
-        constexpr int KIND = decltype(kind)::value;
-        float add[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (KIND == KUIOPS_C_ROW) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) add[e] = brow[e];
-        } else if constexpr (KIND == KUIOPS_C_FULL) {
-            if (row < M) addend4(row, col, add);
-        }
+    // the 4 output values of (i, j, g) at tile column cl
+    auto value4 = [&](int i, int j, int g, int64_t row, int cl, float v[4]) __attribute__((always_inline)) {
+        const f32x4 r4 = *reinterpret_cast<const f32x4 *>(sRow + cl);
+        float add[4] = {r4[0], r4[1], r4[2], r4[3]};
+        if (full && row < M) addend4(row, n0 + cl, add);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = alpha * acc[i][j][4 * g + e] + add[e];
-    };
-    // runs body(kind_tag) with the addend kind as a compile-time constant
-    auto with_kind = [&](auto body) __attribute__((always_inline)) {
-        if (c_kind == KUIOPS_C_ROW) body(std::integral_constant<int, KUIOPS_C_ROW>{});
-        else if (c_kind == KUIOPS_C_FULL) body(std::integral_constant<int, KUIOPS_C_FULL>{});
-        else body(std::integral_constant<int, KUIOPS_C_NONE>{});
     };
     if constexpr (sizeof(Tout) == 2) {
         // The tile's image in LDS: rows 64 b .. 64 b + 63 in stage array b,
         // 512 bytes per row, 16-byte chunk c at position c ^ (row & 31).
         auto stg = [&](int b) -> char * { return b == 0 ? sA0 : (b == 1 ? sB0 : (b == 2 ? sA1 : sB1)); };
         __builtin_amdgcn_s_barrier();
-        with_kind([&](auto kind) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; ++j) {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int cl = wn * 128 + j * 32 + 8 * g + 4 * lk;
-                    float brow[4] = {0.f, 0.f, 0.f, 0.f};
-                    if constexpr (decltype(kind)::value == KUIOPS_C_ROW) addend4(0, n0 + cl, brow);
+            for (int g = 0; g < 4; ++g) {
+                const int cl = wn * 128 + j * 32 + 8 * g + 4 * lk;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int r = wm * 128 + i * 32 + lrow;
-                        float v[4];
-                        value4(kind, i, j, g, m0 + r, n0 + cl, brow, v);
-                        typedef Tout t4 __attribute__((ext_vector_type(4)));
-                        t4 w;
+                for (int i = 0; i < 4; ++i) {
+                    const int r = wm * 128 + i * 32 + lrow;
+                    float v[4];
+                    value4(i, j, g, m0 + r, cl, v);
+                    typedef Tout t4 __attribute__((ext_vector_type(4)));
+                    t4 w;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) w[e] = from_f32<Tout>(v[e]);
-                        *reinterpret_cast<u32x2 *>(stg(r >> 6) + (r & 63) * 512 + (((cl >> 3) ^ (r & 31)) << 4) +
-                                                   lk * 8) = __builtin_bit_cast(u32x2, w);
-                    }
+                    for (int e = 0; e < 4; ++e) w[e] = from_f32<Tout>(v[e]);
+                    *reinterpret_cast<u32x2 *>(stg(r >> 6) + (r & 63) * 512 + (((cl >> 3) ^ (r & 31)) << 4) +
+                                               lk * 8) = __builtin_bit_cast(u32x2, w);
                 }
             }
-        });
+        }
         __syncthreads();
         if (vec_store && m0 + 256 <= M && n0 + 256 <= N) {
 #pragma unroll
@@ -872,31 +889,28 @@ void gemm_wave_kernel(GemmArgs a) {
         }
     } else {
         // fp32 output: 4 consecutive columns per lane, 16 bytes
-        with_kind([&](auto kind) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; ++j) {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int64_t col = n0 + wn * 128 + j * 32 + 8 * g + 4 * lk;
-                    float brow[4] = {0.f, 0.f, 0.f, 0.f};
-                    if constexpr (decltype(kind)::value == KUIOPS_C_ROW) addend4(0, col, brow);
+            for (int g = 0; g < 4; ++g) {
+                const int cl = wn * 128 + j * 32 + 8 * g + 4 * lk;
+                const int64_t col = n0 + cl;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t row = m0 + wm * 128 + i * 32 + lrow;
-                        float v[4];
-                        value4(kind, i, j, g, row, col, brow, v);
-                        if (row >= M) continue;
-                        if (vec_store && col + 3 < N) {
-                            *reinterpret_cast<f32x4 *>(out + row * ldo + col) = f32x4{v[0], v[1], v[2], v[3]};
-                        } else {
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t row = m0 + wm * 128 + i * 32 + lrow;
+                    float v[4];
+                    value4(i, j, g, row, cl, v);
+                    if (row >= M) continue;
+                    if (vec_store && col + 3 < N) {
+                        *reinterpret_cast<f32x4 *>(out + row * ldo + col) = f32x4{v[0], v[1], v[2], v[3]};
+                    } else {
 #pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (col + e < N) out[row * ldo + col + e] = from_f32<Tout>(v[e]);
-                        }
+                        for (int e = 0; e < 4; ++e)
+                            if (col + e < N) out[row * ldo + col + e] = from_f32<Tout>(v[e]);
                     }
                 }
             }
-        });
+        }
     }
 }
 
