@@ -100,6 +100,41 @@ def test_mm_closed_forms(cuda):
     assert torch.equal(ops.mm(A.to(cuda), eye.to(cuda)).cpu(), A)
 
 
+# Shapes that take the 4-wave 256x256 kernel (K % 128 == 0, K >= 512, at
+# least 128 tiles) with partial edge tiles in M and N.
+WAVE_SHAPES = [(2000, 4100, 640), (4096, 2056, 512), (1288, 6400, 1024)]
+
+
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("M,N,K", WAVE_SHAPES)
+@pytest.mark.parametrize("kind", ["row", "full", "none"])
+def test_addmm_wave_kernel_edges(cuda, layout, M, N, K, kind):
+    """Large-tile kernel paths: ragged last tiles, the three addend kinds
+    (bias row, full C, beta = 0) with alpha / beta != 1, and both B layouts,
+    every output against the oracle."""
+    A = gen((M, K), torch.bfloat16, seed=11)
+    B = gen((K, N), torch.bfloat16, 0.05, seed=12)
+    C = gen((N,) if kind == "row" else (M, N), torch.bfloat16, seed=13)
+    alpha, beta = (0.5, 0.0) if kind == "none" else (0.5, 2.0)
+    Bd = B.to(cuda) if layout == "row" else B.t().contiguous().to(cuda).t()
+    out = ops.addmm(C.to(cuda), A.to(cuda), Bd, beta=beta, alpha=alpha)
+    assert out.shape == (M, N)
+    assert_tol(out, O.addmm(npy(C), npy(A), npy(B), alpha, beta), torch.bfloat16)
+
+
+@pytest.mark.parametrize("layout", ["row", "col"])
+def test_mm_wave_kernel_f32_out(cuda, layout):
+    """bf16 operands, fp32 output, on the large-tile kernel (ragged N)."""
+    M, N, K = 2048, 4104, 768
+    A = gen((M, K), torch.bfloat16, seed=14)
+    B = gen((K, N), torch.bfloat16, 0.05, seed=15)
+    Bd = B.to(cuda) if layout == "row" else B.t().contiguous().to(cuda).t()
+    out = ops.mm(A.to(cuda), Bd, out_dtype=torch.float32)
+    assert out.dtype == torch.float32 and out.shape == (M, N)
+    ref = O.mm(npy(A), npy(B))
+    np.testing.assert_allclose(npy(out), ref, rtol=2e-3, atol=2e-3)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 1.0), (0.5, 2.0)])
 def test_addmm_golden(cuda, golden, dtype, alpha, beta):
