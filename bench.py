@@ -11,7 +11,10 @@ HBM.  Ten back-to-back steps are recorded in a HIP graph and the graph is
 replayed, so the timed region holds device work only and the per-replay
 launch cost is spread over ten kernels; HIP events on the launch stream
 bracket exactly K replays after W warm-up replays, and ``ms_per_step`` is the
-time per kernel.
+time per kernel.  The default W = 200 (about 0.2 s of addmm) lets the GPU's
+clocks settle under the load: with W = 10 the same kernel measures ~2% slower
+(and causal SDPA S=2048 ~8%), the clocks still ramping from the previous,
+lighter workload.
 
 ``workloads`` (extra keys of the same line) measures the other BASELINE.json
 configs the same way: decode split-K GEMM (HBM GB/s), bmm, causal SDPA at
@@ -41,7 +44,7 @@ def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline time budget")
