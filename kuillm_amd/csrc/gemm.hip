@@ -618,7 +618,7 @@ __device__ __forceinline__ const char *uniform_ptr(const char *p) {
     return reinterpret_cast<const char *>(((uint64_t)hi << 32) | lo);
 }
 
-template <typename T, bool BCOL, typename Tout>
+template <typename T, bool BCOL, typename Tout, bool FULLC>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_wave_kernel(GemmArgs a) {
     constexpr int BK = 64, SB = 256 * BK * 2;      // bytes per operand per stage
@@ -809,13 +809,13 @@ void gemm_wave_kernel(GemmArgs a) {
     stage(s + 1, sA0, sB0, sA1, sB1, sA0, sB0, sA1, sB1, true, true, false);
     stage(s + 2, sA1, sB1, sA0, sB0, sA1, sB1, sA0, sB0, false, false, false);
 
-    // Epilogue: out = alpha * acc + beta * addend (fp32), one rounding.  One
-    // code path for every addend kind: the row addend comes from LDS (zeros
-    // for the other kinds) and a full-matrix addend replaces it under a
-    // uniform branch, so the accumulator reads are not duplicated per kind
-    // (duplicated, the compiler hoists them and runs out of VGPRs).
+    // Epilogue: out = alpha * acc + beta * addend (fp32), one rounding.  The
+    // row addend comes from LDS (zeros when there is none); a full-matrix
+    // addend (FULLC, its own instance) replaces it.  Branching on the kind
+    // inside the kernel costs: per run, 64 scheduling regions (~1.5 us at
+    // 4096^3); per kind around the whole epilogue, the compiler hoists the
+    // accumulator reads above the branch and spills.
     Tout *out = reinterpret_cast<Tout *>(a.out) + bz * a.stride_o;
-    const bool full = c_kind == KUIOPS_C_FULL;
     // beta * C[row, col .. col + 3] (8-byte loads where aligned)
     auto addend4 = [&](int64_t row, int64_t col, float v[4]) __attribute__((always_inline)) {
         const Tout *p = cin + row * ldcin + col;
@@ -833,7 +833,9 @@ void gemm_wave_kernel(GemmArgs a) {
     auto value4 = [&](int i, int j, int g, int64_t row, int cl, float v[4]) __attribute__((always_inline)) {
         const f32x4 r4 = *reinterpret_cast<const f32x4 *>(sRow + cl);
         float add[4] = {r4[0], r4[1], r4[2], r4[3]};
-        if (full && row < M) addend4(row, n0 + cl, add);
+        if constexpr (FULLC) {
+            if (row < M) addend4(row, n0 + cl, add);
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = alpha * acc[i][j][4 * g + e] + add[e];
     };
@@ -1073,8 +1075,11 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
             if (bcol) hipLaunchKernelGGL((gemm_dma_kernel<T, true, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
             else hipLaunchKernelGGL((gemm_dma_kernel<T, false, Tout, 2, 4, 64, 2>), grid, dim3(512), 0, st, a);
         } else {
-            if (bcol) hipLaunchKernelGGL((gemm_wave_kernel<T, true, Tout>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((gemm_wave_kernel<T, false, Tout>), grid, dim3(256), 0, st, a);
+            const bool full = a.c_kind == KUIOPS_C_FULL;
+            if (bcol && full) hipLaunchKernelGGL((gemm_wave_kernel<T, true, Tout, true>), grid, dim3(256), 0, st, a);
+            else if (bcol) hipLaunchKernelGGL((gemm_wave_kernel<T, true, Tout, false>), grid, dim3(256), 0, st, a);
+            else if (full) hipLaunchKernelGGL((gemm_wave_kernel<T, false, Tout, true>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((gemm_wave_kernel<T, false, Tout, false>), grid, dim3(256), 0, st, a);
         }
         return launch_status();
     }
