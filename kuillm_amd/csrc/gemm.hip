@@ -843,37 +843,46 @@ void gemm_wave_kernel(GemmArgs a) {
         // The tile's image in LDS: rows 64 b .. 64 b + 63 in stage array b,
         // 512 bytes per row, 16-byte chunk c at position c ^ (row & 31).
         auto stg = [&](int b) -> char * { return b == 0 ? sA0 : (b == 1 ? sB0 : (b == 2 ? sA1 : sB1)); };
+        const bool fast = vec_store && m0 + 256 <= M && n0 + 256 <= N;
         __builtin_amdgcn_s_barrier();
+        // Two halves (accumulator rows i = 0, 1 and then 2, 3): the first
+        // half's stores go out while the second half is converted.
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int cl = wn * 128 + j * 32 + 8 * g + 4 * lk;
+            for (int j = 0; j < 4; ++j) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = wm * 128 + i * 32 + lrow;
-                    float v[4];
-                    value4(i, j, g, m0 + r, cl, v);
-                    typedef Tout t4 __attribute__((ext_vector_type(4)));
-                    t4 w;
+                for (int g = 0; g < 4; ++g) {
+                    const int cl = wn * 128 + j * 32 + 8 * g + 4 * lk;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) w[e] = from_f32<Tout>(v[e]);
-                    *reinterpret_cast<u32x2 *>(stg(r >> 6) + (r & 63) * 512 + (((cl >> 3) ^ (r & 31)) << 4) +
-                                               lk * 8) = __builtin_bit_cast(u32x2, w);
+                    for (int i = 2 * h; i < 2 * h + 2; ++i) {
+                        const int r = wm * 128 + i * 32 + lrow;
+                        float v[4];
+                        value4(i, j, g, m0 + r, cl, v);
+                        typedef Tout t4 __attribute__((ext_vector_type(4)));
+                        t4 w;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) w[e] = from_f32<Tout>(v[e]);
+                        *reinterpret_cast<u32x2 *>(stg(r >> 6) + (r & 63) * 512 + (((cl >> 3) ^ (r & 31)) << 4) +
+                                                   lk * 8) = __builtin_bit_cast(u32x2, w);
+                    }
+                }
+            }
+            __syncthreads();
+            if (fast) {
+                // this half's tile rows: 64 h .. 64 h + 63 of each 128-row band
+#pragma unroll
+                for (int it = 0; it < 16; ++it) {
+                    const int rr = it * 8 + (tid >> 5), ch = tid & 31;
+                    const int r = (rr >> 6) * 128 + 64 * h + (rr & 63);
+                    const u32x4 v =
+                        *reinterpret_cast<const u32x4 *>(stg(r >> 6) + (r & 63) * 512 + ((ch ^ (r & 31)) << 4));
+                    // streaming store: the output is not read again here
+                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (m0 + r) * ldo + n0 + ch * 8));
                 }
             }
         }
-        __syncthreads();
-        if (vec_store && m0 + 256 <= M && n0 + 256 <= N) {
-#pragma unroll
-            for (int it = 0; it < 32; ++it) {
-                const int r = it * 8 + (tid >> 5), ch = tid & 31;
-                const u32x4 v =
-                    *reinterpret_cast<const u32x4 *>(stg(r >> 6) + (r & 63) * 512 + ((ch ^ (r & 31)) << 4));
-                // streaming store: the output is not read again here
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (m0 + r) * ldo + n0 + ch * 8));
-            }
-        } else {
+        if (!fast) {
             for (int it = 0; it < 32; ++it) {
                 const int r = it * 8 + (tid >> 5), ch = tid & 31;
                 const int64_t grow = m0 + r, gcol = n0 + ch * 8;
