@@ -67,7 +67,7 @@ __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t vof
 // are rescaled: probabilities stay below 2^8 meanwhile.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename T, int HD, bool CAUSAL, int NWV, bool BIAS = false>
+template <typename T, int HD, bool CAUSAL, int NWV, bool BIAS = false, bool PRIO = true>
 __global__ __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(AttnArgs a) {
     constexpr int BQ = 32 * NWV, BKV = 64;          // 32 queries per wave
@@ -285,6 +285,12 @@ void fa_fwd_kernel(AttnArgs a) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) dst[t] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(pk + offKr[t] + pos));
         };
+        // With two waves per SIMD (PRIO), a wave in the MFMA phases (scores +
+        // exps, then P V) runs at raised priority, so the other wave's row max
+        // and rescale fill its gaps: 2% at causal S=4096.  With one wave per
+        // SIMD the priority changes only constrain the schedule (2% slower
+        // at S=2048), so that instance has none.
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kk = 0; kk < KPF - 1; ++kk) load_k(kk, kr[kk]);
 #pragma unroll
@@ -317,9 +323,6 @@ void fa_fwd_kernel(AttnArgs a) {
         };
 #pragma unroll
         for (int i = 0; i < VPF - 1; ++i) load_v(i, vr[i]);
-        // The MFMA-only phase runs at raised wave priority, so the other
-        // wave of the SIMD fills the gaps with its VALU work.
-        __builtin_amdgcn_s_setprio(1);
         frag pf;
 #pragma unroll
         for (int idx = 0; idx < NV; ++idx) {
@@ -334,7 +337,7 @@ void fa_fwd_kernel(AttnArgs a) {
             if (idx + VPF - 1 < NV) load_v(idx + VPF - 1, vr[(idx + VPF - 1) % VPF]);
             o[dt] = Mfma<T>::m32(vr[idx % VPF], pf, o[dt]);
         }
-        __builtin_amdgcn_s_setprio(0);
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
     // Software pipeline over KV blocks: step j runs the softmax of block j
@@ -683,6 +686,10 @@ static int launch_fwd(AttnArgs a, hipStream_t st) {
     if (a.bias) {
         if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
         else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false, 4, true>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+    } else if (blocks < 2 * (int64_t)num_cus()) {
+        // one work-group per CU: one wave per SIMD, no priority changes
+        if (a.causal) hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4, false, false>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((fa_fwd_kernel<T, HD, false, 4, false, false>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     } else if (a.causal) {
         hipLaunchKernelGGL((fa_fwd_kernel<T, HD, true, 4>), dim3((unsigned)blocks), dim3(256), 0, st, a);
     } else {
