@@ -211,7 +211,9 @@ def test_bmm_golden(cuda, golden, dtype):
     assert_tol(out, O.bmm(npy(t("A")), npy(t("B"))), dtype)
 
 
-@pytest.mark.parametrize("b,M,K,N", [(4, 64, 64, 64), (3, 130, 72, 200), (2, 256, 128, 512)])
+@pytest.mark.parametrize("b,M,K,N", [(4, 64, 64, 64), (3, 130, 72, 200), (2, 256, 128, 512),
+                                     (8, 1024, 640, 1024),     # batched 4-wave kernel (K >= 512)
+                                     (6, 600, 128, 1800)])     # short-K 8-wave kernel, ragged tiles
 def test_bmm_vs_oracle(cuda, b, M, K, N):
     A, B = gen((b, M, K), torch.bfloat16, seed=9), gen((b, K, N), torch.bfloat16, seed=10)
     assert_tol(ops.bmm(A.to(cuda), B.to(cuda)), O.bmm(npy(A), npy(B)), torch.bfloat16)
