@@ -9,7 +9,9 @@
 //   in LDS (one 1024-thread work-group per chunk); pass 2 gives each key its
 //   final rank = its position in its own chunk + the number of smaller keys in
 //   every other chunk (a binary search of each other chunk, staged in LDS in
-//   turn) and writes value and index there.  Values are copied bit-exactly.
+//   turn) and writes value and index there.  For rows of up to 32 chunks the
+//   searches run one work-group per (chunk, other chunk) pair and a third
+//   pass sums each key's counts and scatters.  Values are copied bit-exactly.
 // cumsum: one 1024-thread work-group per row, tiles of 4096 elements (four
 //   consecutive per thread, coalesced), block scans plus a running carry
 //   (fp32 accumulate for fp32, fp64 for fp64, exact for int64).
@@ -40,24 +42,57 @@ __device__ __forceinline__ uint32_t value_key(float v) {
 
 template <typename T> __device__ __forceinline__ float sort_val(T v) { return to_f32(v); }
 
-// Bitonic sort of kSortChunk keys in LDS, ascending (each thread handles
-// kSortPer / 2 compare-exchanges per stage).
+// 64-bit xor shuffle inside a wave (two 32-bit lane swaps).
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic sort of the kSortChunk keys in s (filled, and the work-group
+// synchronised, by the caller), ascending, left in s.  Thread t keeps keys
+// 2t and 2t + 1 in registers: stride 1 is an in-thread exchange, strides 2..64
+// pair thread t with thread t ^ (stride / 2) of the same wave (lane
+// shuffles, no barrier), and only the 15 stages of stride >= 128 pass through
+// LDS (two barriers each, against one per stage for all 66 in LDS).
 __device__ __forceinline__ void bitonic_chunk(uint64_t *s) {
+    static_assert(kSortChunk == 2 * kSortThreads, "two keys per thread");
     const int tid = threadIdx.x;
-    for (int size = 2; size <= kSortChunk; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+    uint64_t k0 = s[2 * tid], k1 = s[2 * tid + 1];
 #pragma unroll
-            for (int h = 0; h < kSortPer / 2; ++h) {
-                const int q = tid + h * kSortThreads;           // pair number
-                const int i = (q / stride) * 2 * stride + (q % stride);
-                const int j = i + stride;
-                const bool up = (i & size) == 0;
-                const uint64_t a = s[i], b = s[j];
-                if ((a > b) == up) { s[i] = b; s[j] = a; }
+    for (int size = 2; size <= kSortChunk; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const int pos = 2 * tid;
+            const bool up = (pos & size) == 0;
+            if (stride == 1) {
+                const uint64_t lo = k0 < k1 ? k0 : k1, hi = k0 < k1 ? k1 : k0;
+                k0 = up ? lo : hi;
+                k1 = up ? hi : lo;
+                continue;
             }
-            __syncthreads();
+            uint64_t p0, p1;
+            if (stride <= 64) {
+                p0 = shfl_xor64(k0, stride >> 1);
+                p1 = shfl_xor64(k1, stride >> 1);
+            } else {
+                __syncthreads();                     // earlier reads of s are done
+                s[pos] = k0;
+                s[pos + 1] = k1;
+                __syncthreads();
+                const int pt = 2 * (tid ^ (stride >> 1));
+                p0 = s[pt];
+                p1 = s[pt + 1];
+            }
+            // keys 2t and 2t + 1 share every bit above bit 0
+            const bool keep_min = ((pos & stride) == 0) == up;
+            k0 = keep_min ? (k0 < p0 ? k0 : p0) : (k0 < p0 ? p0 : k0);
+            k1 = keep_min ? (k1 < p1 ? k1 : p1) : (k1 < p1 ? p1 : k1);
         }
     }
+    __syncthreads();
+    s[2 * tid] = k0;
+    s[2 * tid + 1] = k1;
+    __syncthreads();
 }
 
 // Pass 1: chunk `blockIdx.x` of row `blockIdx.y` -> sorted keys in ws.  With a
@@ -157,6 +192,67 @@ __global__ __launch_bounds__(kSortThreads) void sort_rank_kernel(int64_t n, int 
         const int64_t src = (int64_t)(uint32_t)mine[h];
         vals[row * n + rank[h]] = x[src];
         inds[row * n + rank[h]] = src;
+    }
+}
+
+// Pass 2, wide form (rows of at most kSortWideChunks chunks): one
+// work-group per (own chunk c, other chunk o) counts, for every key of
+// chunk c, the keys of chunk o below it (a binary search of chunk o staged
+// in LDS; o == c: the key's own position), into part[row][o][c][p].  All
+// nc^2 searches run at once instead of nc - 1 in turn per work-group.
+constexpr int kSortWideChunks = 32;
+__global__ __launch_bounds__(kSortThreads) void sort_rank_part_kernel(int nchunks, const uint64_t *ws,
+                                                                       uint32_t *part) {
+    __shared__ uint64_t s[kSortChunk];
+    const int tid = threadIdx.x, c = blockIdx.x, o = blockIdx.y;
+    const int64_t row = blockIdx.z;
+    const uint64_t *base = ws + row * nchunks * (int64_t)kSortChunk;
+    uint32_t *out = part + ((row * nchunks + o) * nchunks + c) * (int64_t)kSortChunk;
+    if (o == c) {
+#pragma unroll
+        for (int h = 0; h < kSortPer; ++h) out[tid + h * kSortThreads] = tid + h * kSortThreads;
+        return;
+    }
+    uint64_t mine[kSortPer];
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) {
+        s[tid + h * kSortThreads] = base[(int64_t)o * kSortChunk + tid + h * kSortThreads];
+        mine[h] = base[(int64_t)c * kSortChunk + tid + h * kSortThreads];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) {
+        // keys are unique; padding ~0 is above every real key
+        int lo = 0, hi = kSortChunk;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (s[mid] < mine[h]) lo = mid + 1;
+            else hi = mid;
+        }
+        out[tid + h * kSortThreads] = (uint32_t)lo;
+    }
+}
+
+// Pass 3, wide form: each key's rank is the sum of its nc partial counts;
+// value and index go there.
+template <typename T>
+__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(int64_t n, int nchunks, const T *X, T *vals,
+                                                                     int64_t *inds, const uint64_t *ws,
+                                                                     const uint32_t *part) {
+    const int tid = threadIdx.x, c = blockIdx.x;
+    const int64_t row = blockIdx.y;
+    const uint64_t *keys = ws + (row * nchunks + c) * (int64_t)kSortChunk;
+    const T *x = X + row * n;
+#pragma unroll
+    for (int h = 0; h < kSortPer; ++h) {
+        const int p = tid + h * kSortThreads;
+        const uint64_t key = keys[p];
+        if (key == ~0ull) continue;                  // padding
+        int64_t rank = 0;
+        for (int o = 0; o < nchunks; ++o) rank += part[((row * nchunks + o) * nchunks + c) * (int64_t)kSortChunk + p];
+        const int64_t src = (int64_t)(uint32_t)key;
+        vals[row * n + rank] = x[src];
+        inds[row * n + rank] = src;
     }
 }
 
@@ -429,9 +525,17 @@ __global__ __launch_bounds__(kSortThreads) void multinomial_reg_kernel(int64_t n
 
 static int sort_nchunks(int64_t n) { return (int)cdiv(n, kSortChunk); }
 
+// The wide rank form while its partial counts stay small (m * nc^2 chunks of
+// counts: at most 128 MiB).
+static bool sort_wide(int64_t m, int nc) { return nc > 1 && nc <= kSortWideChunks && m * nc * nc <= 16384; }
+
+// keys, plus the partial counts of the wide form
 size_t sort_workspace_bytes(int64_t m, int64_t n) {
     const int nc = sort_nchunks(n);
-    return nc > 1 ? (size_t)m * nc * kSortChunk * sizeof(uint64_t) : 0;
+    if (nc <= 1) return 0;
+    size_t bytes = (size_t)m * nc * kSortChunk * sizeof(uint64_t);
+    if (sort_wide(m, nc)) bytes += (size_t)m * nc * nc * kSortChunk * sizeof(uint32_t);
+    return bytes;
 }
 
 }  // namespace kuiops
@@ -449,15 +553,22 @@ extern "C" int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *
     const size_t need = sort_workspace_bytes(m, n);
     if (need && (!workspace || workspace_bytes < need)) return KUIOPS_E_WORKSPACE;
     uint64_t *ws = reinterpret_cast<uint64_t *>(workspace);
+    uint32_t *part = sort_wide(m, nc) ? reinterpret_cast<uint32_t *>(ws + (size_t)m * nc * kSortChunk) : nullptr;
     hipStream_t st = as_stream(stream);
     const dim3 grid((unsigned)nc, (unsigned)m);
 #define KUIOPS_SORT(T)                                                                                        \
     do {                                                                                                      \
         hipLaunchKernelGGL(sort_chunk_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,        \
                            (T *)values, indices, ws, descending);                                              \
-        if (nc > 1)                                                                                           \
+        if (sort_wide(m, nc)) {                                                                               \
+            hipLaunchKernelGGL(sort_rank_part_kernel, dim3((unsigned)nc, (unsigned)nc, (unsigned)m),           \
+                               dim3(kSortThreads), 0, st, nc, (const uint64_t *)ws, part);                    \
+            hipLaunchKernelGGL(sort_scatter_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,  \
+                               (T *)values, indices, (const uint64_t *)ws, (const uint32_t *)part);          \
+        } else if (nc > 1) {                                                                                  \
             hipLaunchKernelGGL(sort_rank_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,     \
                                (T *)values, indices, (const uint64_t *)ws);                                   \
+        }                                                                                                     \
     } while (0)
     switch (dtype) {
         case KUIOPS_F32: KUIOPS_SORT(float); break;
