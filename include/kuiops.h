@@ -334,6 +334,20 @@ KUIOPS_API int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *
                         int64_t *indices, int descending, void *workspace,
                         size_t workspace_bytes, void *stream);
 
+/* The masking step of transformers' TopPLogitsWarper on fp32 scores[m, n],
+ * given their ascending stable sort (sorted_vals, sorted_idx [m, n], as
+ * kuiops_sort_lastdim returns them) and the fp32 cumulative softmax cum[m, n]
+ * of the sorted scores: out = scores with filter_value at sorted_idx[j] for
+ * every j < n - min_keep whose cum[j] <= (float)(1 - top_p) (min_keep == 0
+ * removes nothing, as the Python slice [-0:] does).  Written as a scatter of
+ * the sorted values, so out must not alias the inputs.  No reference kernel:
+ * it replaces the aten le.Scalar / setitem / scatter / masked_fill sequence
+ * the reference app runs after the sort (KERNELS.md rows aten.le.Scalar,
+ * aten.scatter.src; transformers' TopPLogitsWarper).                       */
+KUIOPS_API int kuiops_top_p_mask(int64_t m, int64_t n, const float *sorted_vals, const int64_t *sorted_idx,
+                                 const float *cum, double top_p, int64_t min_keep, double filter_value, float *out,
+                                 void *stream);
+
 /* Inclusive prefix sum of X[m, n] along the last dim into Y (aten.cumsum):
  * dtype F32 (fp32 accumulate), F64, I64 (exact).  No reference kernel
  * (KERNELS.md rows aten.cumsum.default).                                   */

@@ -77,6 +77,7 @@ SIGNATURES = {
     "kuiops_scatter": (_int, [_int, _i64p, _i64p, _int, _int, _vp, _vp, _vp, _vp, _vp]),
     "kuiops_sort_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp, _int, _vp, _sz, _vp]),
     "kuiops_cumsum_lastdim": (_int, [_i64, _i64, _int, _vp, _vp, _vp]),
+    "kuiops_top_p_mask": (_int, [_i64, _i64, _vp, _vp, _vp, _dbl, _i64, _dbl, _vp, _vp]),
     "kuiops_multinomial": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
     "kuiops_index": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "kuiops_index_multi": (_int, [_i64, _int, _i64p, _i64, _i64, ctypes.POINTER(_vp), _int, _vp, _vp, _vp, _vp]),

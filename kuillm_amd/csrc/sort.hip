@@ -256,6 +256,25 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(int64_t n, i
     }
 }
 
+// ------------------------------------------------------------ top-p mask
+
+// The masking step of transformers' TopPLogitsWarper after its sort and
+// cumsum, fused: out[sorted_idx[j]] = filter if j < keep_from and the sorted
+// cumulative probability cum[j] <= thr, else the sorted value sv[j] (the sort
+// copies values bit-exactly, so this is scores[sorted_idx[j]]).  Every
+// position of a row is written once (sorted_idx is a permutation): the aten
+// sequence le.Scalar, setitem of the kept tail, scatter, masked_fill in one
+// pass, spread over the whole grid.
+__global__ __launch_bounds__(256) void top_p_mask_kernel(int64_t n, const float *sv, const int64_t *sidx,
+                                                          const float *cum, float thr, int64_t keep_from, float fill,
+                                                          float *out) {
+    const int64_t row = blockIdx.y;
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= n) return;
+    const int64_t o = row * n + j;
+    out[row * n + sidx[o]] = (j < keep_from && cum[o] <= thr) ? fill : sv[o];
+}
+
 // ------------------------------------------------------------------ scans
 
 template <typename A>
@@ -577,6 +596,23 @@ extern "C" int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *
         default: return KUIOPS_E_UNSUPPORTED;
     }
 #undef KUIOPS_SORT
+    return launch_status();
+}
+
+extern "C" int kuiops_top_p_mask(int64_t m, int64_t n, const float *sorted_vals, const int64_t *sorted_idx,
+                                 const float *cum, double top_p, int64_t min_keep, double filter_value, float *out,
+                                 void *stream) {
+    if (m < 0 || n < 0 || min_keep < 0) return KUIOPS_E_INVALID;
+    if (m == 0 || n == 0) return KUIOPS_OK;
+    if (!sorted_vals || !sorted_idx || !cum || !out) return KUIOPS_E_INVALID;
+    if (m > 65535 || cdiv(n, 256) > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    // thr: the Python float 1 - top_p, compared with fp32 probabilities in fp32;
+    // remove[..., -min_keep:] = False keeps the last min_keep sorted positions
+    // (all of them for min_keep == 0, as Python's [-0:] slice does)
+    const float thr = (float)(1.0 - top_p);
+    const int64_t keep_from = min_keep == 0 ? 0 : (min_keep >= n ? 0 : n - min_keep);
+    hipLaunchKernelGGL(top_p_mask_kernel, dim3((unsigned)cdiv(n, 256), (unsigned)m), dim3(256), 0, as_stream(stream),
+                       n, sorted_vals, sorted_idx, cum, thr, keep_from, (float)filter_value, out);
     return launch_status();
 }
 

@@ -711,6 +711,15 @@ def top_p_filter(scores: torch.Tensor, top_p: float, filter_value: float = -floa
     and fill the dropped scores with filter_value."""
     sorted_logits, sorted_idx = sort(scores, -1, descending=False)
     cum = cumsum(softmax(sorted_logits), -1)
+    if scores.dtype == torch.float32 and scores.dim() == 2 and cum.dtype == torch.float32:
+        # le / setitem / scatter / masked_fill as one scatter of the sorted values
+        m, n = scores.shape
+        out = torch.empty((m, n), dtype=scores.dtype, device=scores.device)
+        _lib.check("kuiops_top_p_mask", _lib_handle().kuiops_top_p_mask(
+            m, n, sorted_logits.contiguous().data_ptr(), sorted_idx.contiguous().data_ptr(),
+            cum.contiguous().data_ptr(), float(top_p), int(min_tokens_to_keep), float(filter_value),
+            out.data_ptr(), _stream(scores.device)))
+        return out
     remove = cum <= (1 - top_p)
     remove[..., -min_tokens_to_keep:] = False
     mask = scatter(remove, 1, sorted_idx, remove)

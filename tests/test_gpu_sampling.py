@@ -307,6 +307,28 @@ def test_top_p_filter_and_sampler_vs_oracle(cuda):
     np.testing.assert_array_equal(tok, O.multinomial(probs, u.numpy())[:, 0])
 
 
+@pytest.mark.parametrize("min_keep", [1, 5, 0, 40000])
+def test_top_p_mask_kernel_matches_aten_sequence(cuda, min_keep):
+    """The fused top-p mask equals the aten sequence it replaces (le.Scalar,
+    setitem of the kept tail, scatter, masked_fill) on the same sorted
+    indices and cumulative probabilities, bit for bit, including a NaN score
+    (sorts last, never removed), ties and min_tokens_to_keep edge values."""
+    g = torch.Generator().manual_seed(min_keep + 7)
+    scores = (torch.randn(3, 32000, generator=g) * 3).to(cuda)
+    scores[1, 100] = float("nan")
+    scores[2, :50] = 1.0                                   # ties
+    for top_p in (0.3, 0.9, 1.0):
+        sv, si = ops.sort(scores, -1, descending=False)
+        cum = ops.cumsum(ops.softmax(sv), -1)
+        remove = cum <= (1 - top_p)
+        remove[..., -min_keep:] = False
+        mask = ops.scatter(remove, 1, si, remove)
+        ref = scores.masked_fill(mask, -float("inf"))
+        got = ops.top_p_filter(scores, top_p, min_tokens_to_keep=min_keep)
+        assert torch.equal(torch.isnan(got), torch.isnan(ref))
+        assert torch.equal(got.nan_to_num(0.0), ref.nan_to_num(0.0))
+
+
 @pytest.mark.parametrize("m,n,dtype", [(1, 32000, torch.bfloat16), (3, 32000, torch.float32), (2, 1000, torch.float16),
                                        (1, 32768, torch.float32), (4, 7, torch.float32)])
 def test_softmax_top1_matches_softmax_topk(cuda, m, n, dtype):
