@@ -24,6 +24,8 @@
 // Semantics: aten.sort / aten.cumsum / aten.multinomial, the reference's
 // fallthrough results (no kuiops kernels exist for them: KERNELS.md rows
 // "aten.sort.default", "aten.cumsum.default", "aten.multinomial.default").
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace kuiops {
@@ -46,6 +48,17 @@ template <typename T> __device__ __forceinline__ float sort_val(T v) { return to
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
     const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
     return ((uint64_t)hi << 32) | lo;
+}
+
+// atomicMin of v into *dst for the whole wave with one LDS atomic (the wave's
+// minimum): 1024 same-address atomics serialise.
+__device__ __forceinline__ void wave_atomic_min(unsigned long long *dst, uint64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t o = shfl_xor64(v, off);
+        v = o < v ? o : v;
+    }
+    if ((threadIdx.x & 63) == 0 && v != ~0ull) atomicMin(dst, (unsigned long long)v);
 }
 
 // Bitonic sort of the kSortChunk keys in s (filled, and the work-group
@@ -248,8 +261,12 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(int64_t n, i
         const int p = tid + h * kSortThreads;
         const uint64_t key = keys[p];
         if (key == ~0ull) continue;                  // padding
-        int64_t rank = 0;
-        for (int o = 0; o < nchunks; ++o) rank += part[((row * nchunks + o) * nchunks + c) * (int64_t)kSortChunk + p];
+        // (all nc counts load at once: the loop is unrolled to the chunk limit)
+        uint32_t rank = 0;
+        const uint32_t *pp = part + (row * nchunks * nchunks + c) * (int64_t)kSortChunk + p;
+#pragma unroll
+        for (int o = 0; o < kSortWideChunks; ++o)
+            if (o < nchunks) rank += pp[(int64_t)o * nchunks * kSortChunk];
         const int64_t src = (int64_t)(uint32_t)key;
         vals[row * n + rank] = x[src];
         inds[row * n + rank] = src;
@@ -355,6 +372,76 @@ __device__ __forceinline__ void store_run(T *y, int64_t b, int64_t n, const A *v
     }
 }
 
+// Rows of 8K..32K elements through LDS: coalesced 16-byte loads (lane q takes
+// elements E q .. E q + E - 1, E per 16 bytes) into a [1024][33] float array,
+// then each thread reads its 32-element run at the 33-float pitch (bank
+// conflict free).  Loading the runs straight from memory touches 64 cache
+// lines per load instruction (a 128-byte lane stride), which the texture
+// path serves one line at a time.  Elements past n read as 0.
+constexpr int kStageRP = 32, kStagePitch = 33;
+template <typename T>
+__device__ __forceinline__ void stage_row_in(const T *x, int64_t n, float *sm, float *v) {
+    constexpr int E = 16 / sizeof(T);
+    constexpr int Q = kSortThreads * kStageRP / E;              // 16-byte chunks of a full row
+    const int tid = threadIdx.x;
+    const bool vec = n % E == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+#pragma unroll
+    for (int k = 0; k < Q / kSortThreads; ++k) {
+        const int q = k * kSortThreads + tid, e0 = q * E;
+        float t[E];
+        if (vec && e0 + E <= n) {
+            typedef T tv __attribute__((ext_vector_type(E)));
+            const tv r = __builtin_bit_cast(tv, *reinterpret_cast<const u32x4 *>(x + e0));
+#pragma unroll
+            for (int e = 0; e < E; ++e) t[e] = to_f32(r[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) t[e] = e0 + e < n ? to_f32(x[e0 + e]) : 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) sm[((e0 + e) >> 5) * kStagePitch + ((e0 + e) & 31)] = t[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kStageRP; ++j) v[j] = sm[tid * kStagePitch + j];
+}
+
+// fp32 cumsum of rows of 8K..32K elements: the row comes in through LDS
+// (stage_row_in), each run is scanned in registers and offset by one block
+// scan, and the result goes out through LDS as coalesced 16-byte stores.
+__global__ __launch_bounds__(kSortThreads) void cumsum_stage_kernel(int64_t n, const float *X, float *Y) {
+    __shared__ float sm[kSortThreads * kStagePitch];
+    __shared__ float s_wave[kSortThreads / 64 + 1];
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const float *x = X + row * n;
+    float *y = Y + row * n;
+    float v[kStageRP];
+    stage_row_in<float>(x, n, sm, v);
+#pragma unroll
+    for (int j = 1; j < kStageRP; ++j) v[j] += v[j - 1];
+    float total;
+    const float excl = block_scan_excl<float>(v[kStageRP - 1], s_wave, total);   // (ends with a barrier)
+#pragma unroll
+    for (int j = 0; j < kStageRP; ++j) sm[tid * kStagePitch + j] = excl + v[j];
+    __syncthreads();
+    const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+    for (int k = 0; k < kStageRP / 4; ++k) {
+        const int e0 = (k * kSortThreads + tid) * 4;
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = sm[((e0 + e) >> 5) * kStagePitch + ((e0 + e) & 31)];
+        if (vec && e0 + 4 <= n) {
+            *reinterpret_cast<f32x4 *>(y + e0) = f32x4{t[0], t[1], t[2], t[3]};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (e0 + e < n) y[e0 + e] = t[e];
+        }
+    }
+}
+
 // Rows of at most 1024 x RP elements: thread t owns the contiguous run
 // [RP t, RP t + RP), loaded at once (every cache line is used whole by its
 // lane), scanned in registers, offset by one block scan.
@@ -439,7 +526,15 @@ __global__ __launch_bounds__(kSortThreads) void multinomial_kernel(int64_t n, in
     __syncthreads();
     // the last positive weight of the row: draws whose target the rounded
     // prefix sums never exceed (u rounding onto the total) take it
-    if (last_pos >= 0) atomicMax(&s_pick, (unsigned long long)last_pos);
+    {
+        uint64_t lp = (uint64_t)(last_pos + 1);      // 0: none; one atomic per wave
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const uint64_t o = shfl_xor64(lp, off);
+            lp = o > lp ? o : lp;
+        }
+        if ((tid & 63) == 0 && lp > 0) atomicMax(&s_pick, (unsigned long long)(lp - 1));
+    }
     __syncthreads();
     const int64_t row_last = (int64_t)s_pick;
     const bool row_bad = s_bad != 0 || !(total > 0.0);
@@ -466,12 +561,11 @@ __global__ __launch_bounds__(kSortThreads) void multinomial_kernel(int64_t n, in
             const double excl = block_scan_excl<double>(c[kScanVPT - 1], s_wave, tile_total) + carry;
             if (tid == 0) s_pick = ~0ull;
             __syncthreads();
+            uint64_t cand = ~0ull;                   // this thread's first qualifying index
 #pragma unroll
-            for (int j = 0; j < kScanVPT; ++j)
-                if (b + j < n && v[j] > 0.0 && excl + c[j] > target) {
-                    atomicMin(&s_pick, (unsigned long long)(b + j));
-                    break;
-                }
+            for (int j = kScanVPT - 1; j >= 0; --j)
+                if (b + j < n && v[j] > 0.0 && excl + c[j] > target) cand = (uint64_t)(b + j);
+            wave_atomic_min(&s_pick, cand);
             __syncthreads();
             if (s_pick != ~0ull) pick = (int64_t)s_pick;
             carry += tile_total;
@@ -493,11 +587,13 @@ __global__ __launch_bounds__(kSortThreads) void multinomial_reg_kernel(int64_t n
     __shared__ unsigned long long s_pick, s_last;
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
+    static_assert(RP == kStageRP, "staged run length");
+    __shared__ float sm[kSortThreads * kStagePitch];
     const T *p = P + row * n;
     const int64_t b = (int64_t)tid * RP;
     if (tid == 0) { s_bad = 0; s_last = 0ull; }
     float v[RP];
-    load_run<T, float, RP>(p, b, n, v);
+    stage_row_in<T>(p, n, sm, v);
     double sum = 0.0;
     int64_t last_pos = -1;
     bool bad = false;
@@ -507,9 +603,17 @@ __global__ __launch_bounds__(kSortThreads) void multinomial_reg_kernel(int64_t n
         if (v[j] > 0.f) last_pos = b + j;
         sum += (double)v[j];
     }
+    // the row's last positive weight: a wave maximum, then one LDS atomic per
+    // wave (1024 same-address atomics serialise: ~5 us)
+    uint64_t lp = (uint64_t)(last_pos + 1);          // 0: none
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t o = shfl_xor64(lp, off);
+        lp = o > lp ? o : lp;
+    }
     __syncthreads();
     if (bad) s_bad = 1;
-    if (last_pos >= 0) atomicMax(&s_last, (unsigned long long)last_pos);
+    if ((tid & 63) == 0 && lp > 0) atomicMax(&s_last, (unsigned long long)(lp - 1));
     double total;
     const double excl = block_scan_excl<double>(sum, s_wave, total);
     const bool row_bad = s_bad != 0 || !(total > 0.0);
@@ -525,17 +629,19 @@ __global__ __launch_bounds__(kSortThreads) void multinomial_reg_kernel(int64_t n
         const double target = (double)U[row * ns + sidx] * total;
         if (tid == 0) s_pick = ~0ull;
         __syncthreads();
+        uint64_t cand = ~0ull;                       // this thread's first qualifying index
         if (excl + sum > target) {
             double run = excl;
 #pragma unroll
             for (int j = 0; j < RP; ++j) {
                 run += (double)v[j];
                 if (run > target && v[j] > 0.f) {
-                    atomicMin(&s_pick, (unsigned long long)(b + j));
+                    cand = (uint64_t)(b + j);
                     break;
                 }
             }
         }
+        wave_atomic_min(&s_pick, cand);
         __syncthreads();
         if (tid == 0) out[row * ns + sidx] = s_pick != ~0ull ? (int64_t)s_pick : row_last;
         __syncthreads();
@@ -627,6 +733,9 @@ extern "C" int kuiops_cumsum_lastdim(int64_t m, int64_t n, int dtype, const void
     do {                                                                                                      \
         if (n <= kSortThreads * 8)                                                                            \
             hipLaunchKernelGGL((cumsum_reg_kernel<T, 8>), grid, dim3(kSortThreads), 0, st, n, (const T *)X, (T *)Y); \
+        else if (n <= kSortThreads * 32 && std::is_same<T, float>::value)                                     \
+            hipLaunchKernelGGL(cumsum_stage_kernel, grid, dim3(kSortThreads), 0, st, n, (const float *)X,     \
+                               (float *)Y);                                                                   \
         else if (n <= kSortThreads * 32)                                                                      \
             hipLaunchKernelGGL((cumsum_reg_kernel<T, 32>), grid, dim3(kSortThreads), 0, st, n, (const T *)X, (T *)Y); \
         else                                                                                                  \
