@@ -340,7 +340,8 @@ KUIOPS_API int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *
  * of the sorted scores: out = scores with filter_value at sorted_idx[j] for
  * every j < n - min_keep whose cum[j] <= (float)(1 - top_p) (min_keep == 0
  * removes nothing, as the Python slice [-0:] does).  Written as a scatter of
- * the sorted values, so out must not alias the inputs.  No reference kernel:
+ * the sorted values, so out must not alias the inputs; indices outside
+ * [0, n) are skipped (out is then incomplete).  No reference kernel:
  * it replaces the aten le.Scalar / setitem / scatter / masked_fill sequence
  * the reference app runs after the sort (KERNELS.md rows aten.le.Scalar,
  * aten.scatter.src; transformers' TopPLogitsWarper).                       */

@@ -289,7 +289,9 @@ __global__ __launch_bounds__(256) void top_p_mask_kernel(int64_t n, const float 
     const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (j >= n) return;
     const int64_t o = row * n + j;
-    out[row * n + sidx[o]] = (j < keep_from && cum[o] <= thr) ? fill : sv[o];
+    const int64_t dst = sidx[o];
+    if (dst < 0 || dst >= n) return;                 // not a permutation of the row: no stray store
+    out[row * n + dst] = (j < keep_from && cum[o] <= thr) ? fill : sv[o];
 }
 
 // ------------------------------------------------------------------ scans
