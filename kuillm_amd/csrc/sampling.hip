@@ -224,6 +224,34 @@ __device__ uint32_t block_kth_largest(uint32_t v, bool part, int k, int *hist, u
     return t;
 }
 
+// Descending bitonic sort of 128 keys held two per lane by one wave (lane l:
+// positions 2l, 2l + 1): stride 1 in-lane, strides 2..64 by lane shuffles,
+// no barriers.
+__device__ __forceinline__ uint64_t topk_shfl_xor64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ void wave_bitonic128_desc(uint64_t &k0, uint64_t &k1) {
+    const int pos = 2 * (threadIdx.x & 63);
+#pragma unroll
+    for (int size = 2; size <= 128; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const bool desc = (pos & size) == 0;
+            if (stride == 1) {
+                const uint64_t hi = k0 > k1 ? k0 : k1, lo = k0 > k1 ? k1 : k0;
+                k0 = desc ? hi : lo;
+                k1 = desc ? lo : hi;
+                continue;
+            }
+            const uint64_t p0 = topk_shfl_xor64(k0, stride >> 1), p1 = topk_shfl_xor64(k1, stride >> 1);
+            const bool keep_max = ((pos & stride) == 0) == desc;
+            k0 = keep_max ? (k0 > p0 ? k0 : p0) : (k0 > p0 ? p0 : k0);
+            k1 = keep_max ? (k1 > p1 ? k1 : p1) : (k1 > p1 ? p1 : k1);
+        }
+    }
+}
+
 constexpr int kTopkFastPer = 32;       // keys per thread held in registers (n <= 32768)
 constexpr int kTopkFastMaxK = 512;
 constexpr int kTopkCandCap = 2048;     // candidates the fast path sorts
@@ -239,6 +267,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(int64_t n, int k, co
     if (k == 1) {
         // arg-max with lowest-index tie break: composite (key, ~index) maximum.
         uint64_t best = 0;
+        // (unrolled: eight loads in flight per thread)
+#pragma unroll 8
         for (int64_t i = tid; i < n; i += kTopkThreads) {
             const uint64_t c = ((uint64_t)order_key(load_f(x + i), lg) << 32) | (uint32_t)~(uint32_t)i;
             best = c > best ? c : best;
@@ -294,6 +324,24 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(int64_t n, int k, co
             for (int j = 0; j < kTopkFastPer; ++j) {
                 const int64_t i = (int64_t)j * kTopkThreads + tid;
                 if (i < n && key[j] >= thr) s_cand[pos++] = ((uint64_t)key[j] << 32) | (uint32_t)~(uint32_t)i;
+            }
+            __syncthreads();
+            if (total <= 128) {
+                // up to 128 candidates: one wave sorts them in registers
+                if (wave == 0) {
+                    uint64_t k0 = 2 * lane < total ? s_cand[2 * lane] : 0, k1 = 2 * lane + 1 < total ? s_cand[2 * lane + 1] : 0;
+                    wave_bitonic128_desc(k0, k1);
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int j = 2 * lane + e;
+                        if (j < k) {
+                            const int64_t idx = (int64_t)(uint32_t)~(uint32_t)((e ? k1 : k0) & 0xffffffffu);
+                            vals[row * k + j] = x[idx];
+                            inds[row * k + j] = idx;
+                        }
+                    }
+                }
+                return;
             }
             int P = 1;
             while (P < total) P <<= 1;
