@@ -61,18 +61,19 @@ __device__ __forceinline__ void wave_atomic_min(unsigned long long *dst, uint64_
     if ((threadIdx.x & 63) == 0 && v != ~0ull) atomicMin(dst, (unsigned long long)v);
 }
 
-// Bitonic sort of the kSortChunk keys in s (filled, and the work-group
-// synchronised, by the caller), ascending, left in s.  Thread t keeps keys
-// 2t and 2t + 1 in registers: stride 1 is an in-thread exchange, strides 2..64
-// pair thread t with thread t ^ (stride / 2) of the same wave (lane
-// shuffles, no barrier), and only the 15 stages of stride >= 128 pass through
-// LDS (two barriers each, against one per stage for all 66 in LDS).
+// Bitonic sort of the CH keys in s (filled, and the work-group synchronised,
+// by the caller; CH / 2 threads), ascending, left in s.  Thread t keeps keys
+// 2t and 2t + 1 in registers: stride 1 is an in-thread exchange, strides
+// 2..64 pair thread t with thread t ^ (stride / 2) of the same wave (lane
+// shuffles, no barrier), and only the stages of stride >= 128 pass through
+// LDS (two barriers each; 15 of 66 stages for 2048 keys, against one
+// barrier per stage for all of them in LDS).
+template <int CH>
 __device__ __forceinline__ void bitonic_chunk(uint64_t *s) {
-    static_assert(kSortChunk == 2 * kSortThreads, "two keys per thread");
     const int tid = threadIdx.x;
     uint64_t k0 = s[2 * tid], k1 = s[2 * tid + 1];
 #pragma unroll
-    for (int size = 2; size <= kSortChunk; size <<= 1) {
+    for (int size = 2; size <= CH; size <<= 1) {
 #pragma unroll
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             const int pos = 2 * tid;
@@ -110,17 +111,18 @@ __device__ __forceinline__ void bitonic_chunk(uint64_t *s) {
 
 // Pass 1: chunk `blockIdx.x` of row `blockIdx.y` -> sorted keys in ws.  With a
 // single chunk per row the outputs are written directly.
-template <typename T>
-__global__ __launch_bounds__(kSortThreads) void sort_chunk_kernel(int64_t n, int nchunks, const T *X, T *vals,
-                                                                   int64_t *inds, uint64_t *ws, int descending) {
-    __shared__ uint64_t s[kSortChunk];
+template <typename T, int CH>
+__global__ __launch_bounds__(CH / 2) void sort_chunk_kernel(int64_t n, int nchunks, const T *X, T *vals,
+                                                             int64_t *inds, uint64_t *ws, int descending) {
+    constexpr int NT = CH / 2;                       // two keys per thread
+    __shared__ uint64_t s[CH];
     const int tid = threadIdx.x, c = blockIdx.x;
     const int64_t row = blockIdx.y;
     const T *x = X + row * n;
 #pragma unroll
-    for (int h = 0; h < kSortPer; ++h) {
-        const int p = tid + h * kSortThreads;
-        const int64_t i = (int64_t)c * kSortChunk + p;
+    for (int h = 0; h < 2; ++h) {
+        const int p = tid + h * NT;
+        const int64_t i = (int64_t)c * CH + p;
         uint64_t key = ~0ull;                        // padding sorts last
         if (i < n) {
             uint32_t k = value_key(sort_val<T>(x[i]));
@@ -130,11 +132,11 @@ __global__ __launch_bounds__(kSortThreads) void sort_chunk_kernel(int64_t n, int
         s[p] = key;
     }
     __syncthreads();
-    bitonic_chunk(s);
+    bitonic_chunk<CH>(s);
     if (nchunks == 1) {
 #pragma unroll
-        for (int h = 0; h < kSortPer; ++h) {
-            const int p = tid + h * kSortThreads;
+        for (int h = 0; h < 2; ++h) {
+            const int p = tid + h * NT;
             if (p < n) {
                 const int64_t src = (int64_t)(uint32_t)s[p];
                 vals[row * n + p] = x[src];
@@ -143,9 +145,9 @@ __global__ __launch_bounds__(kSortThreads) void sort_chunk_kernel(int64_t n, int
         }
         return;
     }
-    uint64_t *w = ws + (row * nchunks + c) * kSortChunk;
+    uint64_t *w = ws + (row * nchunks + c) * CH;
 #pragma unroll
-    for (int h = 0; h < kSortPer; ++h) w[tid + h * kSortThreads] = s[tid + h * kSortThreads];
+    for (int h = 0; h < 2; ++h) w[tid + h * NT] = s[tid + h * NT];
 }
 
 // Pass 2: rank of each key of chunk blockIdx.x among all keys of the row.
@@ -214,59 +216,61 @@ __global__ __launch_bounds__(kSortThreads) void sort_rank_kernel(int64_t n, int 
 // in LDS; o == c: the key's own position), into part[row][o][c][p].  All
 // nc^2 searches run at once instead of nc - 1 in turn per work-group.
 constexpr int kSortWideChunks = 32;
-__global__ __launch_bounds__(kSortThreads) void sort_rank_part_kernel(int nchunks, const uint64_t *ws,
-                                                                       uint32_t *part) {
-    __shared__ uint64_t s[kSortChunk];
+template <int CH>
+__global__ __launch_bounds__(CH / 2) void sort_rank_part_kernel(int nchunks, const uint64_t *ws, uint32_t *part) {
+    constexpr int NT = CH / 2;
+    __shared__ uint64_t s[CH];
     const int tid = threadIdx.x, c = blockIdx.x, o = blockIdx.y;
     const int64_t row = blockIdx.z;
-    const uint64_t *base = ws + row * nchunks * (int64_t)kSortChunk;
-    uint32_t *out = part + ((row * nchunks + o) * nchunks + c) * (int64_t)kSortChunk;
+    const uint64_t *base = ws + row * nchunks * (int64_t)CH;
+    uint32_t *out = part + ((row * nchunks + o) * nchunks + c) * (int64_t)CH;
     if (o == c) {
 #pragma unroll
-        for (int h = 0; h < kSortPer; ++h) out[tid + h * kSortThreads] = tid + h * kSortThreads;
+        for (int h = 0; h < 2; ++h) out[tid + h * NT] = tid + h * NT;
         return;
     }
-    uint64_t mine[kSortPer];
+    uint64_t mine[2];
 #pragma unroll
-    for (int h = 0; h < kSortPer; ++h) {
-        s[tid + h * kSortThreads] = base[(int64_t)o * kSortChunk + tid + h * kSortThreads];
-        mine[h] = base[(int64_t)c * kSortChunk + tid + h * kSortThreads];
+    for (int h = 0; h < 2; ++h) {
+        s[tid + h * NT] = base[(int64_t)o * CH + tid + h * NT];
+        mine[h] = base[(int64_t)c * CH + tid + h * NT];
     }
     __syncthreads();
 #pragma unroll
-    for (int h = 0; h < kSortPer; ++h) {
+    for (int h = 0; h < 2; ++h) {
         // keys are unique; padding ~0 is above every real key
-        int lo = 0, hi = kSortChunk;
+        int lo = 0, hi = CH;
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
             if (s[mid] < mine[h]) lo = mid + 1;
             else hi = mid;
         }
-        out[tid + h * kSortThreads] = (uint32_t)lo;
+        out[tid + h * NT] = (uint32_t)lo;
     }
 }
 
 // Pass 3, wide form: each key's rank is the sum of its nc partial counts;
 // value and index go there.
-template <typename T>
-__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(int64_t n, int nchunks, const T *X, T *vals,
-                                                                     int64_t *inds, const uint64_t *ws,
-                                                                     const uint32_t *part) {
+template <typename T, int CH>
+__global__ __launch_bounds__(CH / 2) void sort_scatter_kernel(int64_t n, int nchunks, const T *X, T *vals,
+                                                               int64_t *inds, const uint64_t *ws,
+                                                               const uint32_t *part) {
+    constexpr int NT = CH / 2;
     const int tid = threadIdx.x, c = blockIdx.x;
     const int64_t row = blockIdx.y;
-    const uint64_t *keys = ws + (row * nchunks + c) * (int64_t)kSortChunk;
+    const uint64_t *keys = ws + (row * nchunks + c) * (int64_t)CH;
     const T *x = X + row * n;
 #pragma unroll
-    for (int h = 0; h < kSortPer; ++h) {
-        const int p = tid + h * kSortThreads;
+    for (int h = 0; h < 2; ++h) {
+        const int p = tid + h * NT;
         const uint64_t key = keys[p];
         if (key == ~0ull) continue;                  // padding
         // (all nc counts load at once: the loop is unrolled to the chunk limit)
         uint32_t rank = 0;
-        const uint32_t *pp = part + (row * nchunks * nchunks + c) * (int64_t)kSortChunk + p;
+        const uint32_t *pp = part + (row * nchunks * nchunks + c) * (int64_t)CH + p;
 #pragma unroll
         for (int o = 0; o < kSortWideChunks; ++o)
-            if (o < nchunks) rank += pp[(int64_t)o * nchunks * kSortChunk];
+            if (o < nchunks) rank += pp[(int64_t)o * nchunks * CH];
         const int64_t src = (int64_t)(uint32_t)key;
         vals[row * n + rank] = x[src];
         inds[row * n + rank] = src;
@@ -650,18 +654,24 @@ __global__ __launch_bounds__(kSortThreads) void multinomial_reg_kernel(int64_t n
     }
 }
 
-static int sort_nchunks(int64_t n) { return (int)cdiv(n, kSortChunk); }
-
 // The wide rank form while its partial counts stay small (m * nc^2 chunks of
-// counts: at most 128 MiB).
-static bool sort_wide(int64_t m, int nc) { return nc > 1 && nc <= kSortWideChunks && m * nc * nc <= 16384; }
+// counts: at most 64 MiB of 1024-key chunks, 128 MiB of 2048-key ones).
+static bool sort_wide(int64_t m, int64_t nc) { return nc > 1 && nc <= kSortWideChunks && m * nc * nc <= 16384; }
+
+// Keys per chunk: 1024 (512 threads; the bitonic pass is about half as
+// long) whenever the wide rank form takes the row at that size, else 2048.
+static int sort_chunk_for(int64_t m, int64_t n) {
+    const int64_t nc = cdiv(n, 1024);
+    return nc <= 1 || sort_wide(m, nc) ? 1024 : kSortChunk;
+}
 
 // keys, plus the partial counts of the wide form
 size_t sort_workspace_bytes(int64_t m, int64_t n) {
-    const int nc = sort_nchunks(n);
+    const int ch = sort_chunk_for(m, n);
+    const int64_t nc = cdiv(n, ch);
     if (nc <= 1) return 0;
-    size_t bytes = (size_t)m * nc * kSortChunk * sizeof(uint64_t);
-    if (sort_wide(m, nc)) bytes += (size_t)m * nc * nc * kSortChunk * sizeof(uint32_t);
+    size_t bytes = (size_t)m * nc * ch * sizeof(uint64_t);
+    if (sort_wide(m, nc)) bytes += (size_t)m * nc * nc * ch * sizeof(uint32_t);
     return bytes;
 }
 
@@ -675,27 +685,36 @@ extern "C" int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *
     if (m == 0 || n == 0) return KUIOPS_OK;
     if (!X || !values || !indices) return KUIOPS_E_INVALID;
     if (n >= (int64_t)UINT32_MAX || m > 65535) return KUIOPS_E_UNSUPPORTED;
-    const int nc = sort_nchunks(n);
-    if (nc > 65535) return KUIOPS_E_UNSUPPORTED;
+    const int ch = sort_chunk_for(m, n);
+    const int64_t nc64 = cdiv(n, ch);
+    if (nc64 > 65535) return KUIOPS_E_UNSUPPORTED;
+    const int nc = (int)nc64;
     const size_t need = sort_workspace_bytes(m, n);
     if (need && (!workspace || workspace_bytes < need)) return KUIOPS_E_WORKSPACE;
     uint64_t *ws = reinterpret_cast<uint64_t *>(workspace);
-    uint32_t *part = sort_wide(m, nc) ? reinterpret_cast<uint32_t *>(ws + (size_t)m * nc * kSortChunk) : nullptr;
+    const bool wide = sort_wide(m, nc);
+    uint32_t *part = wide ? reinterpret_cast<uint32_t *>(ws + (size_t)m * nc * ch) : nullptr;
     hipStream_t st = as_stream(stream);
     const dim3 grid((unsigned)nc, (unsigned)m);
-#define KUIOPS_SORT(T)                                                                                        \
+    const dim3 pairs((unsigned)nc, (unsigned)nc, (unsigned)m);
+#define KUIOPS_SORT_CH(T, CH)                                                                                 \
     do {                                                                                                      \
-        hipLaunchKernelGGL(sort_chunk_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,        \
+        hipLaunchKernelGGL((sort_chunk_kernel<T, CH>), grid, dim3(CH / 2), 0, st, n, nc, (const T *)X,       \
                            (T *)values, indices, ws, descending);                                              \
-        if (sort_wide(m, nc)) {                                                                               \
-            hipLaunchKernelGGL(sort_rank_part_kernel, dim3((unsigned)nc, (unsigned)nc, (unsigned)m),           \
-                               dim3(kSortThreads), 0, st, nc, (const uint64_t *)ws, part);                    \
-            hipLaunchKernelGGL(sort_scatter_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,  \
+        if (wide) {                                                                                           \
+            hipLaunchKernelGGL((sort_rank_part_kernel<CH>), pairs, dim3(CH / 2), 0, st, nc,                   \
+                               (const uint64_t *)ws, part);                                                   \
+            hipLaunchKernelGGL((sort_scatter_kernel<T, CH>), grid, dim3(CH / 2), 0, st, n, nc, (const T *)X,  \
                                (T *)values, indices, (const uint64_t *)ws, (const uint32_t *)part);          \
         } else if (nc > 1) {                                                                                  \
             hipLaunchKernelGGL(sort_rank_kernel<T>, grid, dim3(kSortThreads), 0, st, n, nc, (const T *)X,     \
                                (T *)values, indices, (const uint64_t *)ws);                                   \
         }                                                                                                     \
+    } while (0)
+#define KUIOPS_SORT(T)                                                                                        \
+    do {                                                                                                      \
+        if (ch == 1024) KUIOPS_SORT_CH(T, 1024);                                                              \
+        else KUIOPS_SORT_CH(T, 2048);                                                                         \
     } while (0)
     switch (dtype) {
         case KUIOPS_F32: KUIOPS_SORT(float); break;
@@ -704,6 +723,7 @@ extern "C" int kuiops_sort_lastdim(int64_t m, int64_t n, int dtype, const void *
         default: return KUIOPS_E_UNSUPPORTED;
     }
 #undef KUIOPS_SORT
+#undef KUIOPS_SORT_CH
     return launch_status();
 }
 

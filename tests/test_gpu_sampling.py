@@ -207,7 +207,8 @@ def test_sort_golden(cuda, golden):
 @pytest.mark.parametrize("m,n,dtype", [(1, 32000, torch.float32), (3, 2048, torch.float32), (2, 2049, torch.float32), (1, 4097, torch.float32),
                                        (5, 1, torch.float32), (4, 7000, torch.bfloat16), (2, 513, torch.float16),
                                        (1, 131072, torch.float32),
-                                       (17, 65536, torch.bfloat16)])   # 32 chunks x 17 rows: the per-chunk rank pass
+                                       (17, 65536, torch.bfloat16),    # 32 chunks x 17 rows: the per-chunk rank pass
+                                       (20, 32000, torch.float32)])    # 2048-key chunks, pairwise rank pass
 def test_sort_vs_oracle(cuda, m, n, dtype):
     g = torch.Generator().manual_seed(n)
     x = (torch.randn(m, n, generator=g) * 4).to(dtype)
