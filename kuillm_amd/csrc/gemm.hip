@@ -586,6 +586,190 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
             store_tile32<Tout>(a, acc[i][j], m0 + wm * WTM + i * 32, n0 + wn * WTN + j * 32 + lrow, lk);
 }
 
+// Uniform (wave-invariant) pointer kept in SGPRs: buffer descriptors built
+// from it need no per-lane waterfall loop around each DMA.
+__device__ __forceinline__ const char *uniform_ptr(const char *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const char *>(((uint64_t)hi << 32) | lo);
+}
+
+// ------------------------------------------------------------------------
+// gemm_stream_kernel: short-K batched GEMMs (K <= 128, so a tile's whole K
+// fits the two 64-k LDS stages; bmm 32 x 2048x128x2048 writes 268 MB and
+// reads 33 MB, so the output stores bound it).  A persistent grid of one
+// 8-wave work-group per CU walks the tiles in row-by-row order (at step i
+// the grid holds tiles 256 i .. 256 i + 255, whose 512-byte row segments
+// make whole output rows).  The DMA of the next tile is issued before the
+// current tile's output stores, so each CU loads and stores at the same
+// time; the waits leave the stores in flight (vmcnt counts the 16 stores of
+// a tile, younger than the DMA) and the barriers are bare s_barrier (a
+// __syncthreads() fence would wait for the stores).  Operand layouts and
+// fragments are gemm_dma_kernel's (2 x 4 waves of 128x64); the output goes
+// through a separate 32 KB LDS band (two 32-row bands of 512-byte rows,
+// 16-byte chunks XOR-swizzled by row), so the stage buffers are free for
+// the next tile's DMA.  Full 256x256 tiles, row-major B, 16-bit output, no
+// addend.
+template <typename T, typename Tout, int NK>
+__global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_tiles) {
+    constexpr int BK = 64, WTM = 128, WTN = 64, TM = 4, TN = 2, KK = BK / 16;
+    constexpr int RB = BK * 2, RPB = 1024 / RB, CPR = BK / 8;
+    constexpr int SBYTES = 256 * BK * 2;           // 32 KB per operand per stage
+    constexpr int DPW = SBYTES / 1024 / 8;         // 1 KB DMA blocks per wave per operand
+    constexpr int NSTORE = TM * 4;                 // 16-byte output stores per thread per tile
+    typedef typename Mfma<T>::frag frag;
+    __shared__ __attribute__((aligned(1024))) char sA0[SBYTES], sB0[SBYTES], sA1[SBYTES], sB1[SBYTES];
+    __shared__ __attribute__((aligned(1024))) char sOut[2 * 32 * 512];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / 4, wn = wave % 4;
+    const int per = a.tiles_m * a.tiles_n;
+    // work-group -> first tile: ids on one XCD (dispatched round-robin) take a
+    // contiguous range of each step's 256 tiles
+    const int G = gridDim.x, bid = blockIdx.x;
+    const int pid = __builtin_amdgcn_readfirstlane((bid & 7) * (G >> 3) + min(bid & 7, G & 7) + (bid >> 3));
+    auto swzK = [](int r) { return (r >> 1) & 7; };
+
+    uint32_t goffA[DPW], goffB[DPW];
+#pragma unroll
+    for (int j = 0; j < DPW; ++j) {
+        const int blk = wave * DPW + j;
+        const int r = blk * RPB + lane / CPR;
+        const int c = (lane % CPR) ^ swzK(r);
+        goffA[j] = (uint32_t)((r * a.lda + c * 8) * 2);
+        const int kr = blk * 2 + (lane >> 5);
+        const int cb = (lane & 31) ^ swzB(kr);
+        goffB[j] = (uint32_t)((kr * a.ldb + cb * 8) * 2);
+    }
+    const uint32_t stepB = (uint32_t)(BK * a.ldb * 2);
+    // both K stages of tile t (the tile's operand bases are uniform)
+    auto issue = [&](int t) __attribute__((always_inline)) {
+        const int bz = t / per, rr = t - bz * per;
+        const int tm = rr / a.tiles_n, tn = rr - tm * a.tiles_n;
+        const char *ba = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.A) + bz * a.stride_a +
+                                                        (int64_t)tm * 256 * a.lda);
+        const char *bb = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.B) + bz * a.stride_b +
+                                                        (int64_t)tn * 256);
+        const __amdgpu_buffer_rsrc_t rsA = make_rsrc(uniform_ptr(ba), 0xffffffffu);
+        const __amdgpu_buffer_rsrc_t rsB = make_rsrc(uniform_ptr(bb), 0xffffffffu);
+#pragma unroll
+        for (int j = 0; j < DPW; ++j) {
+            dma16_buf(rsA, goffA[j], 0, sA0 + (wave * DPW + j) * 1024);
+            dma16_buf(rsB, goffB[j], 0, sB0 + (wave * DPW + j) * 1024);
+        }
+        if constexpr (NK > 1) {
+#pragma unroll
+            for (int j = 0; j < DPW; ++j) {
+                dma16_buf(rsA, goffA[j], BK * 2, sA1 + (wave * DPW + j) * 1024);
+                dma16_buf(rsB, goffB[j], stepB, sB1 + (wave * DPW + j) * 1024);
+            }
+        }
+    };
+
+    const int lrow = lane & 31, lk = lane >> 5;
+    const int Gq = lane >> 4, q = lane & 15;
+    int offA[KK], offB[TN];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        const int r = wm * WTM + lrow;
+        offA[kk] = r * RB + (((2 * kk + lk) ^ swzK(r)) << 4);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int kr = 8 * (Gq >> 1) + (q >> 2);
+        const int n = wn * WTN + j * 32 + 16 * (Gq & 1) + 4 * (q & 3);
+        offB[j] = kr * 512 + (((n >> 3) ^ swzB(kr)) << 4) + ((n >> 2) & 1) * 8;
+    }
+    auto load_frags = [&](const char *sa, const char *sb, int kk, frag *fa, frag *fb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            fa[i] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(sa + offA[kk] + i * 32 * RB));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)to_lds(sb + offB[j] + kk * 16 * 512));
+            const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)to_lds(sb + offB[j] + kk * 16 * 512 + 4 * 512));
+            const u32x2 h0 = __builtin_bit_cast(u32x2, t0), h1 = __builtin_bit_cast(u32x2, t1);
+            fb[j] = as_frag<frag>(u32x4{h0[0], h0[1], h1[0], h1[1]});
+        }
+    };
+    f32x16 acc[TM][TN];
+    auto compute = [&](const char *sa, const char *sb) __attribute__((always_inline)) {
+        frag fa[2][TM], fb[2][TN];
+        load_frags(sa, sb, 0, fa[0], fb[0]);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            if (kk + 1 < KK) load_frags(sa, sb, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::m32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+        }
+    };
+
+    // One tile: its DMA has landed (the caller waited), MFMAs, then the DMA
+    // of tile `next` (the last tile again when there is none: the stage
+    // buffers are not read after the loop, and no DMA is conditional, so the
+    // compiler's waits stay those below), then this tile's output.
+    auto tile = [&](int t, int next) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_barrier();
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+        compute(sA0, sB0);
+        if constexpr (NK > 1) compute(sA1, sB1);
+        __builtin_amdgcn_s_waitcnt(0xc07f);        // this wave's LDS reads are done
+        __builtin_amdgcn_s_barrier();              // (every wave's): the stages are free
+        issue(next);
+        // epilogue: per accumulator row band i, the two 32-row bands (wm =
+        // 0, 1) through sOut, then 512-byte row segments to memory
+        const int bz = t / per, rr = t - bz * per;
+        const int tm = rr / a.tiles_n, tn = rr - tm * a.tiles_n;
+        Tout *out = reinterpret_cast<Tout *>(a.out) + bz * a.stride_o;
+        const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
+        char *band = sOut + wm * 32 * 512;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);    // this wave's reads of the previous band are done
+            __builtin_amdgcn_s_barrier();
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int cl = wn * WTN + j * 32 + lrow;            // column within the tile
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = (e >> 2) * 8 + lk * 4 + (e & 3);   // row within the band
+                    *reinterpret_cast<Tout *>(band + r * 512 + (((cl >> 3) ^ r) << 4) + (cl & 7) * 2) =
+                        from_f32<Tout>(a.alpha * acc[i][j][e]);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);    // this wave's band writes are done
+            __builtin_amdgcn_s_barrier();
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int idx = u * 512 + tid;                       // 2 bands x 32 rows x 32 chunks
+                const int bnd = idx >> 10, r = (idx >> 5) & 31, ch = idx & 31;
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(sOut + bnd * 32 * 512 + r * 512 + ((ch ^ r) << 4));
+                __builtin_nontemporal_store(
+                    v, reinterpret_cast<u32x4 *>(out + (m0 + bnd * WTM + i * 32 + r) * a.ldo + n0 + ch * 8));
+            }
+        }
+    };
+    // (the host launches at most total_tiles work-groups: pid < total_tiles)
+    const int last = total_tiles - 1;
+    issue(pid);
+    wait_vmcnt<0>();
+    for (int t = pid; t < total_tiles; t += G) {
+        wait_vmcnt<NSTORE>();          // this tile's DMA; the previous tile's stores stay in flight
+        tile(t, min(t + G, last));
+    }
+
+}
+
 // ------------------------------------------------------------------------
 // gemm_wave_kernel: 256x256x64 work-group tiles, 4 waves (one per SIMD),
 // each wave a 128x128 quarter built from 32x32x16 MFMAs whose 256 fp32
@@ -612,11 +796,6 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dma_kernel(GemmArgs a) {
 // 8-column group: the epilogue writes 8-byte runs into an LDS image of the
 // tile (16-byte chunks XOR-swizzled by row) and the work-group stores whole
 // 512-byte row segments.  Loads and the LDS layouts are gemm_dma_kernel's.
-__device__ __forceinline__ const char *uniform_ptr(const char *p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<const char *>(((uint64_t)hi << 32) | lo);
-}
 
 template <typename T, bool BCOL, typename Tout, bool FULLC>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
@@ -1074,6 +1253,17 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
         // epilogue dominate) run faster on the 8-wave gemm_dma_kernel, whose
         // second wave per SIMD overlaps them.  KUIOPS_GEMM_KERNEL=dma forces
         // the 8-wave kernel.
+        const int64_t total = (int64_t)a.tiles_m * a.tiles_n * batch;
+        if (gemm_kernel_choice() != 1 && a.K <= 128 && a.K % 64 == 0 && !bcol && sizeof(Tout) == 2 &&
+            a.c_kind == KUIOPS_C_NONE && a.M % 256 == 0 && a.N % 256 == 0 && a.vec_store &&
+            total >= 2 * (int64_t)num_cus()) {
+            // short K, several tiles per CU: the persistent kernel overlaps each
+            // tile's output stores with the next tile's loads
+            const int wgs = (int)min(total, (int64_t)num_cus());
+            if (a.K == 128) hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 2>), dim3(wgs), dim3(512), 0, st, a, (int)total);
+            else hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 1>), dim3(wgs), dim3(512), 0, st, a, (int)total);
+            return launch_status();
+        }
         if (gemm_kernel_choice() == 1 || a.K < 512) {
             // Short K is bound by the output stores (bmm 32 x 2048x128x2048
             // writes 268 MB): rasterise row by row so the tiles running
