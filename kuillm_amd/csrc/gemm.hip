@@ -705,7 +705,7 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::m32(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+                for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::m32(fb[kk & 1][j], fa[kk & 1][i], acc[i][j]);
         }
     };
 
@@ -737,14 +737,19 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
         for (int i = 0; i < TM; ++i) {
             __builtin_amdgcn_s_waitcnt(0xc07f);    // this wave's reads of the previous band are done
             __builtin_amdgcn_s_barrier();
+            // (operands swapped in the MFMA: a lane holds row lrow of the band
+            // and 4 consecutive columns per 8-column group, one 8-byte write)
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int cl = wn * WTN + j * 32 + lrow;            // column within the tile
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int r = (e >> 2) * 8 + lk * 4 + (e & 3);   // row within the band
-                    *reinterpret_cast<Tout *>(band + r * 512 + (((cl >> 3) ^ r) << 4) + (cl & 7) * 2) =
-                        from_f32<Tout>(a.alpha * acc[i][j][e]);
+                for (int g = 0; g < 4; ++g) {
+                    const int c0 = wn * WTN + j * 32 + 8 * g + 4 * lk;   // first of the 4 columns
+                    typedef Tout t4 __attribute__((ext_vector_type(4)));
+                    t4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = from_f32<Tout>(a.alpha * acc[i][j][4 * g + e]);
+                    *reinterpret_cast<u32x2 *>(band + lrow * 512 + (((c0 >> 3) ^ lrow) << 4) + lk * 8) =
+                        __builtin_bit_cast(u32x2, w);
                 }
             }
             __builtin_amdgcn_s_waitcnt(0xc07f);    // this wave's band writes are done
@@ -1254,15 +1259,19 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
         // second wave per SIMD overlaps them.  KUIOPS_GEMM_KERNEL=dma forces
         // the 8-wave kernel.
         const int64_t total = (int64_t)a.tiles_m * a.tiles_n * batch;
-        if (gemm_kernel_choice() != 1 && a.K <= 128 && a.K % 64 == 0 && !bcol && sizeof(Tout) == 2 &&
-            a.c_kind == KUIOPS_C_NONE && a.M % 256 == 0 && a.N % 256 == 0 && a.vec_store &&
-            total >= 2 * (int64_t)num_cus()) {
-            // short K, several tiles per CU: the persistent kernel overlaps each
-            // tile's output stores with the next tile's loads
-            const int wgs = (int)min(total, (int64_t)num_cus());
-            if (a.K == 128) hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 2>), dim3(wgs), dim3(512), 0, st, a, (int)total);
-            else hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 1>), dim3(wgs), dim3(512), 0, st, a, (int)total);
-            return launch_status();
+        if constexpr (sizeof(Tout) == 2) {
+            if (gemm_kernel_choice() != 1 && a.K <= 128 && a.K % 64 == 0 && !bcol &&
+                a.c_kind == KUIOPS_C_NONE && a.M % 256 == 0 && a.N % 256 == 0 && a.vec_store &&
+                total >= 2 * (int64_t)num_cus()) {
+                // short K, several tiles per CU: the persistent kernel overlaps
+                // each tile's output stores with the next tile's loads
+                const int wgs = (int)min(total, (int64_t)num_cus());
+                if (a.K == 128)
+                    hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 2>), dim3(wgs), dim3(512), 0, st, a, (int)total);
+                else
+                    hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 1>), dim3(wgs), dim3(512), 0, st, a, (int)total);
+                return launch_status();
+            }
         }
         if (gemm_kernel_choice() == 1 || a.K < 512) {
             // Short K is bound by the output stores (bmm 32 x 2048x128x2048
