@@ -1247,6 +1247,27 @@ static bool dma_eligible(const GemmArgs &a, int64_t batch, bool bcol) {
 template <typename T, typename Tout>
 static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *ws, size_t ws_bytes,
                     hipStream_t st) {
+    if constexpr (sizeof(Tout) == 2) {
+        // short K (64 or 128), full 256x256 tiles, several tiles per CU: the
+        // persistent kernel overlaps each tile's output stores with the next
+        // tile's loads
+        const int64_t lim = (int64_t)1 << 30;
+        const int64_t total = (a.M / 256) * (a.N / 256) * batch;
+        if (splits_req <= 1 && gemm_kernel_choice() != 1 && (a.K == 64 || a.K == 128) && !bcol &&
+            a.c_kind == KUIOPS_C_NONE && a.M % 256 == 0 && a.N % 256 == 0 && 256 * a.lda + a.K < lim &&
+            a.K * a.ldb + 256 < lim && a.lda % 8 == 0 && a.ldb % 8 == 0 && a.stride_a % 8 == 0 && a.stride_b % 8 == 0 && a.ldo % 8 == 0 &&
+            a.stride_o % 8 == 0 && aligned16(a.out) && total >= 2 * (int64_t)num_cus() && total < INT32_MAX) {
+            a.tiles_m = (int)(a.M / 256);
+            a.tiles_n = (int)(a.N / 256);
+            a.vec_store = true;
+            const int wgs = (int)min(total, (int64_t)num_cus());
+            if (a.K == 128)
+                hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 2>), dim3(wgs), dim3(512), 0, st, a, (int)total);
+            else
+                hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 1>), dim3(wgs), dim3(512), 0, st, a, (int)total);
+            return launch_status();
+        }
+    }
     if (splits_req <= 1 && dma_eligible(a, batch, bcol)) {
         a.tiles_m = (int)cdiv(a.M, 256);
         a.tiles_n = (int)cdiv(a.N, 256);
@@ -1258,21 +1279,6 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
         // epilogue dominate) run faster on the 8-wave gemm_dma_kernel, whose
         // second wave per SIMD overlaps them.  KUIOPS_GEMM_KERNEL=dma forces
         // the 8-wave kernel.
-        const int64_t total = (int64_t)a.tiles_m * a.tiles_n * batch;
-        if constexpr (sizeof(Tout) == 2) {
-            if (gemm_kernel_choice() != 1 && a.K <= 128 && a.K % 64 == 0 && !bcol &&
-                a.c_kind == KUIOPS_C_NONE && a.M % 256 == 0 && a.N % 256 == 0 && a.vec_store &&
-                total >= 2 * (int64_t)num_cus()) {
-                // short K, several tiles per CU: the persistent kernel overlaps
-                // each tile's output stores with the next tile's loads
-                const int wgs = (int)min(total, (int64_t)num_cus());
-                if (a.K == 128)
-                    hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 2>), dim3(wgs), dim3(512), 0, st, a, (int)total);
-                else
-                    hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 1>), dim3(wgs), dim3(512), 0, st, a, (int)total);
-                return launch_status();
-            }
-        }
         if (gemm_kernel_choice() == 1 || a.K < 512) {
             // Short K is bound by the output stores (bmm 32 x 2048x128x2048
             // writes 268 MB): rasterise row by row so the tiles running

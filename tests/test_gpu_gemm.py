@@ -222,6 +222,17 @@ def test_bmm_vs_oracle(cuda, b, M, K, N):
     assert torch.equal(ops.bmm(A.to(cuda), Bt), ops.bmm(A.to(cuda), B.to(cuda)))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,M,K,N", [(8, 1024, 64, 4096),      # one 64-k stage
+                                     (9, 1024, 128, 3840)])    # 540 tiles: uneven tiles per work-group
+def test_bmm_persistent_short_k(cuda, dtype, b, M, K, N):
+    """Short-K batched GEMM with at least two full tiles per CU: the
+    persistent kernel that stores each tile while loading the next."""
+    A, B = gen((b, M, K), dtype, seed=21), gen((b, K, N), dtype, seed=22)
+    out = ops.bmm(A.to(cuda), B.to(cuda))
+    assert_tol(out, O.bmm(npy(A), npy(B)), dtype)
+
+
 def test_bmm_full_size(cuda):
     """BASELINE config 2b: bmm 32 x [2048,128] x [128,2048]: every batch
     against the oracle in full."""
