@@ -51,6 +51,21 @@ def test_mm_vs_oracle(cuda, dtype, layout, M, N, K):
     assert_tol(out, ref, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("M,N,K", [(4096, 8192, 64), (2048, 16384, 128)])
+def test_mm_short_k_many_tiles(cuda, dtype, layout, M, N, K):
+    """K of one or two 64-k stages and at least two 256x256 tiles per CU:
+    row-major B takes the persistent short-K kernel, column-major B the
+    8-wave LDS-DMA kernel (K = 128) or the register-staged one (K = 64)."""
+    A = gen((M, K), dtype, seed=5)
+    B = gen((K, N), dtype, 0.5, seed=6)
+    Bd = B.to(cuda) if layout == "row" else B.t().contiguous().to(cuda).t()
+    out = ops.mm(A.to(cuda), Bd)
+    assert out.dtype == dtype and out.shape == (M, N)
+    assert_tol(out, O.mm(npy(A), npy(B)), dtype)
+
+
 @pytest.mark.parametrize("layout", ["row", "col"])
 @pytest.mark.parametrize("M,N,K", [(256, 512, 2048), (130, 384, 4096)])
 def test_mm_few_tiles_splitk(cuda, layout, M, N, K):
