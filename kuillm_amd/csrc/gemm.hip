@@ -608,9 +608,10 @@ __device__ __forceinline__ const char *uniform_ptr(const char *p) {
 // fragments are gemm_dma_kernel's (2 x 4 waves of 128x64); the output goes
 // through a separate 32 KB LDS band (two 32-row bands of 512-byte rows,
 // 16-byte chunks XOR-swizzled by row), so the stage buffers are free for
-// the next tile's DMA.  Full 256x256 tiles, row-major B, 16-bit output, no
-// addend.
-template <typename T, typename Tout, int NK>
+// the next tile's DMA.  Full 256x256 tiles, 16-bit output, no addend; B
+// row-major (transposing fragment reads) or column-major (B^T rows staged
+// and read like A's).
+template <typename T, bool BCOL, typename Tout, int NK>
 __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_tiles) {
     constexpr int BK = 64, WTM = 128, WTN = 64, TM = 4, TN = 2, KK = BK / 16;
     constexpr int RB = BK * 2, RPB = 1024 / RB, CPR = BK / 8;
@@ -638,11 +639,15 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
         const int r = blk * RPB + lane / CPR;
         const int c = (lane % CPR) ^ swzK(r);
         goffA[j] = (uint32_t)((r * a.lda + c * 8) * 2);
-        const int kr = blk * 2 + (lane >> 5);
-        const int cb = (lane & 31) ^ swzB(kr);
-        goffB[j] = (uint32_t)((kr * a.ldb + cb * 8) * 2);
+        if constexpr (BCOL) {
+            goffB[j] = (uint32_t)((r * a.ldb + c * 8) * 2);     // B^T rows: A's layout
+        } else {
+            const int kr = blk * 2 + (lane >> 5);
+            const int cb = (lane & 31) ^ swzB(kr);
+            goffB[j] = (uint32_t)((kr * a.ldb + cb * 8) * 2);
+        }
     }
-    const uint32_t stepB = (uint32_t)(BK * a.ldb * 2);
+    const uint32_t stepB = BCOL ? (uint32_t)(BK * 2) : (uint32_t)(BK * a.ldb * 2);
     // both K stages of tile t (the tile's operand bases are uniform)
     auto issue = [&](int t) __attribute__((always_inline)) {
         const int bz = t / per, rr = t - bz * per;
@@ -650,7 +655,7 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
         const char *ba = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.A) + bz * a.stride_a +
                                                         (int64_t)tm * 256 * a.lda);
         const char *bb = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.B) + bz * a.stride_b +
-                                                        (int64_t)tn * 256);
+                                                        (int64_t)tn * 256 * (BCOL ? a.ldb : 1));
         const __amdgpu_buffer_rsrc_t rsA = make_rsrc(uniform_ptr(ba), 0xffffffffu);
         const __amdgpu_buffer_rsrc_t rsB = make_rsrc(uniform_ptr(bb), 0xffffffffu);
 #pragma unroll
@@ -675,11 +680,20 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
         const int r = wm * WTM + lrow;
         offA[kk] = r * RB + (((2 * kk + lk) ^ swzK(r)) << 4);
     }
+    int offKc[KK];                                  // (column-major B) chunk of k-step kk
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) offKc[kk] = ((2 * kk + lk) ^ swzK(lrow)) << 4;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        const int kr = 8 * (Gq >> 1) + (q >> 2);
-        const int n = wn * WTN + j * 32 + 16 * (Gq & 1) + 4 * (q & 3);
-        offB[j] = kr * 512 + (((n >> 3) ^ swzB(kr)) << 4) + ((n >> 2) & 1) * 8;
+        if constexpr (BCOL) {
+            // B^T row wn * WTN + 32 j + lrow in A's layout; its k-chunk
+            // offset is offKc (the swizzle repeats every 16 rows)
+            offB[j] = (wn * WTN + j * 32 + lrow) * RB;
+        } else {
+            const int kr = 8 * (Gq >> 1) + (q >> 2);
+            const int n = wn * WTN + j * 32 + 16 * (Gq & 1) + 4 * (q & 3);
+            offB[j] = kr * 512 + (((n >> 3) ^ swzB(kr)) << 4) + ((n >> 2) & 1) * 8;
+        }
     }
     auto load_frags = [&](const char *sa, const char *sb, int kk, frag *fa, frag *fb) __attribute__((always_inline)) {
 #pragma unroll
@@ -687,6 +701,10 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
             fa[i] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(sa + offA[kk] + i * 32 * RB));
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
+            if constexpr (BCOL) {
+                fb[j] = as_frag<frag>(*reinterpret_cast<const u32x4 *>(sb + offB[j] + offKc[kk]));
+                continue;
+            }
             const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4 *)to_lds(sb + offB[j] + kk * 16 * 512));
             const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -1253,18 +1271,19 @@ static int run_mfma(GemmArgs a, int64_t batch, bool bcol, int splits_req, void *
         // tile's loads
         const int64_t lim = (int64_t)1 << 30;
         const int64_t total = (a.M / 256) * (a.N / 256) * batch;
-        if (splits_req <= 1 && gemm_kernel_choice() != 1 && (a.K == 64 || a.K == 128) && !bcol &&
+        if (splits_req <= 1 && gemm_kernel_choice() != 1 && (a.K == 64 || a.K == 128) &&
             a.c_kind == KUIOPS_C_NONE && a.M % 256 == 0 && a.N % 256 == 0 && 256 * a.lda + a.K < lim &&
-            a.K * a.ldb + 256 < lim && a.lda % 8 == 0 && a.ldb % 8 == 0 && a.stride_a % 8 == 0 && a.stride_b % 8 == 0 && a.ldo % 8 == 0 &&
+            (bcol ? 256 * a.ldb + a.K : a.K * a.ldb + 256) < lim && a.lda % 8 == 0 && a.ldb % 8 == 0 && a.stride_a % 8 == 0 && a.stride_b % 8 == 0 && a.ldo % 8 == 0 &&
             a.stride_o % 8 == 0 && aligned16(a.out) && total >= 2 * (int64_t)num_cus() && total < INT32_MAX) {
             a.tiles_m = (int)(a.M / 256);
             a.tiles_n = (int)(a.N / 256);
             a.vec_store = true;
             const int wgs = (int)min(total, (int64_t)num_cus());
-            if (a.K == 128)
-                hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 2>), dim3(wgs), dim3(512), 0, st, a, (int)total);
-            else
-                hipLaunchKernelGGL((gemm_stream_kernel<T, Tout, 1>), dim3(wgs), dim3(512), 0, st, a, (int)total);
+            const dim3 g(wgs), blk(512);
+            if (bcol && a.K == 128) hipLaunchKernelGGL((gemm_stream_kernel<T, true, Tout, 2>), g, blk, 0, st, a, (int)total);
+            else if (bcol) hipLaunchKernelGGL((gemm_stream_kernel<T, true, Tout, 1>), g, blk, 0, st, a, (int)total);
+            else if (a.K == 128) hipLaunchKernelGGL((gemm_stream_kernel<T, false, Tout, 2>), g, blk, 0, st, a, (int)total);
+            else hipLaunchKernelGGL((gemm_stream_kernel<T, false, Tout, 1>), g, blk, 0, st, a, (int)total);
             return launch_status();
         }
     }

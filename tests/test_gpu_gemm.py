@@ -56,8 +56,8 @@ def test_mm_vs_oracle(cuda, dtype, layout, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(4096, 8192, 64), (2048, 16384, 128)])
 def test_mm_short_k_many_tiles(cuda, dtype, layout, M, N, K):
     """K of one or two 64-k stages and at least two 256x256 tiles per CU:
-    row-major B takes the persistent short-K kernel, column-major B the
-    8-wave LDS-DMA kernel (K = 128) or the register-staged one (K = 64)."""
+    the persistent short-K kernel, with B row-major (transposing fragment
+    reads) or column-major (B^T rows staged like A)."""
     A = gen((M, K), dtype, seed=5)
     B = gen((K, N), dtype, 0.5, seed=6)
     Bd = B.to(cuda) if layout == "row" else B.t().contiguous().to(cuda).t()
@@ -240,11 +240,14 @@ def test_bmm_vs_oracle(cuda, b, M, K, N):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("b,M,K,N", [(8, 1024, 64, 4096),      # one 64-k stage
                                      (9, 1024, 128, 3840)])    # 540 tiles: uneven tiles per work-group
-def test_bmm_persistent_short_k(cuda, dtype, b, M, K, N):
+@pytest.mark.parametrize("layout", ["row", "col"])
+def test_bmm_persistent_short_k(cuda, dtype, b, M, K, N, layout):
     """Short-K batched GEMM with at least two full tiles per CU: the
-    persistent kernel that stores each tile while loading the next."""
+    persistent kernel that stores each tile while loading the next (B as
+    given, or a K-contiguous transposed view as in q @ k^T)."""
     A, B = gen((b, M, K), dtype, seed=21), gen((b, K, N), dtype, seed=22)
-    out = ops.bmm(A.to(cuda), B.to(cuda))
+    Bd = B.to(cuda) if layout == "row" else B.transpose(1, 2).contiguous().to(cuda).transpose(1, 2)
+    out = ops.bmm(A.to(cuda), Bd)
     assert_tol(out, O.bmm(npy(A), npy(B)), dtype)
 
 
