@@ -327,65 +327,82 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     constexpr int XB = 4;
     const int nch = (int)(a.K / 8);
     const T *addp = reinterpret_cast<const T *>(a.in_add);
-    for (int m = wave; m < M; m += NW) {
-        const T *in = reinterpret_cast<const T *>(a.in) +
-                      (a.in_row ? max((int64_t)0, min(a.in_row[m], a.in_rows - 1)) : (int64_t)m) * a.ld_in;
+    auto x_row = [&](int m) __attribute__((always_inline)) {
+        return reinterpret_cast<const T *>(a.in) +
+               (a.in_row ? max((int64_t)0, min(a.in_row[m], a.in_rows - 1)) : (int64_t)m) * a.ld_in;
+    };
+    // (every load is issued, from chunk 0 when the chunk is past the row or
+    // there is no residual; consume_x skips those values.  With no
+    // conditional loads and no use right after them, the compiler waits for
+    // exactly these, leaving younger W loads in flight.)
+    auto issue_x = [&](int m, int c0, u32x4 *v0, u32x4 *v1) __attribute__((always_inline)) {
+        const T *in = x_row(m);
+        const T *ap = addp ? addp + m * a.ld_add : in;
+#pragma unroll
+        for (int j = 0; j < XB; ++j) {
+            const int c = c0 + 64 * j;
+            const int cc = c < nch ? c : 0;
+            v0[j] = *reinterpret_cast<const u32x4 *>(in + cc * 8);
+            v1[j] = u32x4{0, 0, 0, 0};
+            if constexpr (XK == kXSwiGlu) v1[j] = *reinterpret_cast<const u32x4 *>(in + a.K + cc * 8);
+            if constexpr (XK == kXRmsNorm) v1[j] = *reinterpret_cast<const u32x4 *>(ap + cc * 8);
+        }
+    };
+    auto consume_x = [&](int m, int c0, const u32x4 *v0, const u32x4 *v1, float &ss) __attribute__((always_inline)) {
         T *srow = sx + (int64_t)m * a.ldsx;
-        float ss = 0.f;
-        for (int c0 = lane; c0 < nch; c0 += 64 * XB) {
-            u32x4 v0[XB], v1[XB];
 #pragma unroll
-            for (int j = 0; j < XB; ++j) {
-                const int c = c0 + 64 * j;
-                v0[j] = v1[j] = u32x4{0, 0, 0, 0};
-                if (c < nch) {
-                    v0[j] = *reinterpret_cast<const u32x4 *>(in + c * 8);
-                    if constexpr (XK == kXSwiGlu) v1[j] = *reinterpret_cast<const u32x4 *>(in + a.K + c * 8);
-                    if constexpr (XK == kXRmsNorm)
-                        if (addp) v1[j] = *reinterpret_cast<const u32x4 *>(addp + m * a.ld_add + c * 8);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < XB; ++j) {
-                const int c = c0 + 64 * j;
-                if (c >= nch) continue;
-                float h[8], o[8];
-                unpack8<T>(v0[j], h);
-                if constexpr (XK == kXRmsNorm) {
-                    if (addp) {
-                        unpack8<T>(v1[j], o);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) h[e] = rnd<T>(h[e] + o[e]);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) ss += h[e] * h[e];
-                    // the summed row goes to LDS first (rounded: exact), normalised below
-                    *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(h);
-                    if (a.h_out && blockIdx.x == 0)
-                        *reinterpret_cast<u32x4 *>(reinterpret_cast<T *>(a.h_out) + m * a.ld_h + c * 8) = pack8f<T>(h);
-                } else if constexpr (XK == kXSwiGlu) {
+        for (int j = 0; j < XB; ++j) {
+            const int c = c0 + 64 * j;
+            if (c >= nch) continue;
+            float h[8], o[8];
+            unpack8<T>(v0[j], h);
+            if constexpr (XK == kXRmsNorm) {
+                if (addp) {
                     unpack8<T>(v1[j], o);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) h[e] = rnd<T>(h[e] / (1.f + expf(-h[e]))) * o[e];
-                    *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(h);
-                } else {
-                    *reinterpret_cast<u32x4 *>(srow + c * 8) = v0[j];
+                    for (int e = 0; e < 8; ++e) h[e] = rnd<T>(h[e] + o[e]);
                 }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += h[e] * h[e];
+                // the summed row goes to LDS first (rounded: exact), normalised below
+                *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(h);
+                if (a.h_out && blockIdx.x == 0)
+                    *reinterpret_cast<u32x4 *>(reinterpret_cast<T *>(a.h_out) + m * a.ld_h + c * 8) = pack8f<T>(h);
+            } else if constexpr (XK == kXSwiGlu) {
+                unpack8<T>(v1[j], o);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = rnd<T>(h[e] / (1.f + expf(-h[e]))) * o[e];
+                *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(h);
+            } else {
+                *reinterpret_cast<u32x4 *>(srow + c * 8) = v0[j];
             }
         }
+    };
+    auto norm_pass = [&](int m, float ss, const u32x4 *nw) __attribute__((always_inline)) {
+        // RMSNorm's second pass over a staged row; the norm weight chunks
+        // come from `nw` (loaded with the row: one chunk batch) or memory
         if constexpr (XK == kXRmsNorm) {
+            T *srow = sx + (int64_t)m * a.ldsx;
             ss = wave_sum(ss);
             const float inv = rsqrtf(ss / (float)a.K + a.eps);
-            for (int c = lane; c < nch; c += 64) {
+            auto one = [&](int c, u32x4 wv) __attribute__((always_inline)) {
                 float h[8], w8[8], xo[8];
                 unpack8<T>(*reinterpret_cast<const u32x4 *>(srow + c * 8), h);
-                unpack8<T>(*reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.norm_w) + c * 8), w8);
+                unpack8<T>(wv, w8);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) xo[e] = w8[e] * rnd<T>(h[e] * inv);
                 *reinterpret_cast<u32x4 *>(srow + c * 8) = pack8f<T>(xo);
+            };
+            if (nw) {
+#pragma unroll
+                for (int j = 0; j < XB; ++j)
+                    if (lane + 64 * j < nch) one(lane + 64 * j, nw[j]);
+            } else {
+                for (int c = lane; c < nch; c += 64)
+                    one(c, *reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.norm_w) + c * 8));
             }
         }
-    }
+    };
     u32x4 wr[PF][2];
     auto load_w = [&](const T *Wr, int st, u32x4 *dst) __attribute__((always_inline)) {
         const int64_t k = kbeg + (int64_t)st * 64 + 8 * cq;
@@ -396,8 +413,56 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     const int64_t G = gridDim.x;
     int64_t g = blockIdx.x;
     const T *Wc = w_row(g);
+    const bool one_batch = nch <= 64 * XB;
+    int m_rest = wave;                                // first row still to stage
+    if (one_batch) {
+        // one chunk batch per row: this wave's first row (and the norm
+        // weights) is loaded, then the first group's W steps, and the row is
+        // staged while those are in flight (loads return in issue order)
+        u32x4 v0[XB], v1[XB], nw[XB];
+        const bool has = wave < M;
+        if (has) {
+            issue_x(wave, lane, v0, v1);
+            if constexpr (XK == kXRmsNorm) {
 #pragma unroll
-    for (int st = 0; st < PF; ++st) load_w(Wc, st, wr[st]);
+                for (int j = 0; j < XB; ++j) {
+                    const int c = lane + 64 * j;        // (chunks past the row are not used)
+                    nw[j] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.norm_w) + (c < nch ? c : 0) * 8);
+                }
+            }
+        }
+        // (unconditional as well: a step past this wave's K range loads
+        // the row's first chunk and is zeroed)
+#pragma unroll
+        for (int st = 0; st < PF; ++st) {
+            const int64_t k = kbeg + (int64_t)st * 64 + 8 * cq;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const bool ok = k + 32 * h < kend;
+                const u32x4 t = *reinterpret_cast<const u32x4 *>(Wc + (ok ? k + 32 * h : 0));
+                wr[st][h] = ok ? t : u32x4{0, 0, 0, 0};
+            }
+        }
+        if (has) {
+            float ss = 0.f;
+            consume_x(wave, lane, v0, v1, ss);
+            norm_pass(wave, ss, nw);
+        }
+        m_rest = wave + NW;
+    }
+    for (int m = m_rest; m < M; m += NW) {
+        float ss = 0.f;
+        for (int c0 = lane; c0 < nch; c0 += 64 * XB) {
+            u32x4 v0[XB], v1[XB];
+            issue_x(m, c0, v0, v1);
+            consume_x(m, c0, v0, v1, ss);
+        }
+        norm_pass(m, ss, nullptr);
+    }
+    if (!one_batch) {
+#pragma unroll
+        for (int st = 0; st < PF; ++st) load_w(Wc, st, wr[st]);
+    }
 
     __syncthreads();
 
