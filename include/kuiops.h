@@ -630,6 +630,7 @@ KUIOPS_API int kuiops_cat(int n_inputs, const void *const *inputs, const int64_t
  * products differ from them only in fp32 summation order).
  * Input stages (RMSNorm, SwiGLU) and embedding rows need M <= 16 and
  * M * K * 2 <= 140 KiB (x staged in LDS); plain x takes any M <= 64.
+ * With x staged (M <= 16), W must span less than 2 GiB.
  * Otherwise KUIOPS_E_UNSUPPORTED.  No reference
  * counterpart: it fuses the mm launcher with the RMSNorm / SwiGLU / rotary /
  * KV-cache cat launches of a batched decode step (infer.py:57-89 generates

@@ -298,7 +298,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
     // W row of this lane's logical output n in group g (row 0, never
     // stored, for outputs past N)
-    auto w_row = [&](int64_t g) __attribute__((always_inline)) -> const T * {
+    auto w_row = [&](int64_t g) __attribute__((always_inline)) -> uint32_t {
         int64_t wrow;
         bool wvalid;
         if constexpr (OK == kOutPlain) {
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
                 wrow = head * a.hd + (p - head * half) + e * half;
             }
         }
-        return reinterpret_cast<const T *>(a.W) + (wvalid ? wrow : 0) * a.ldw;
+        return (uint32_t)((wvalid ? wrow : 0) * a.ldw * 2);   // byte offset (W spans < 2 GiB)
     };
     // every wave runs the same padded step count (steps past its K range
     // load nothing), so group boundaries line up for the barriers
@@ -403,16 +403,24 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
             }
         }
     };
+    // W steps as buffer loads: a step that is switched off (past this
+    // wave's K range, or past the work-group's last group) gets an offset
+    // past the descriptor's range and reads zeros without touching memory,
+    // so no load is conditional and the compiler's waits count them exactly
     u32x4 wr[PF][2];
-    auto load_w = [&](const T *Wr, int st, u32x4 *dst) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rsW =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.W), (short)0, 0x7fffffff, 0x00020000);
+    auto load_w = [&](uint32_t wrow, int st, bool live, u32x4 *dst) __attribute__((always_inline)) {
         const int64_t k = kbeg + (int64_t)st * 64 + 8 * cq;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-            dst[h] = k + 32 * h < kend ? *reinterpret_cast<const u32x4 *>(Wr + k + 32 * h) : u32x4{0, 0, 0, 0};
+        for (int h = 0; h < 2; ++h) {
+            const bool ok = live && k + 32 * h < kend;
+            dst[h] = __builtin_amdgcn_raw_buffer_load_b128(rsW, ok ? wrow + (uint32_t)((k + 32 * h) * 2) : 0x80000000u, 0, 0);
+        }
     };
     const int64_t G = gridDim.x;
     int64_t g = blockIdx.x;
-    const T *Wc = w_row(g);
+    uint32_t Wc = w_row(g);
     const bool one_batch = nch <= 64 * XB;
     int m_rest = wave;                                // first row still to stage
     if (one_batch) {
@@ -431,18 +439,8 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
                 }
             }
         }
-        // (unconditional as well: a step past this wave's K range loads
-        // the row's first chunk and is zeroed)
 #pragma unroll
-        for (int st = 0; st < PF; ++st) {
-            const int64_t k = kbeg + (int64_t)st * 64 + 8 * cq;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const bool ok = k + 32 * h < kend;
-                const u32x4 t = *reinterpret_cast<const u32x4 *>(Wc + (ok ? k + 32 * h : 0));
-                wr[st][h] = ok ? t : u32x4{0, 0, 0, 0};
-            }
-        }
+        for (int st = 0; st < PF; ++st) load_w(Wc, st, true, wr[st]);
         if (has) {
             float ss = 0.f;
             consume_x(wave, lane, v0, v1, ss);
@@ -461,7 +459,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     }
     if (!one_batch) {
 #pragma unroll
-        for (int st = 0; st < PF; ++st) load_w(Wc, st, wr[st]);
+        for (int st = 0; st < PF; ++st) load_w(Wc, st, true, wr[st]);
     }
 
     __syncthreads();
@@ -471,9 +469,11 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
         // ---- MFMAs over this wave's K range; the last PF steps prefetch
         // the next group's first PF
         const bool has_next = g + G < ngroups;
-        const T *Wn = w_row(has_next ? g + G : g);
+        const uint32_t Wn = w_row(has_next ? g + G : g);
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < nsp; s0 += PF) {
+        // PF steps: MFMAs on the loaded W, each step's registers refilled
+        // with step nst0 + j of W row offset nrow (switched off: zeros)
+        auto steps = [&](int s0, uint32_t nrow, int nst0, bool live) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < PF; ++j) {
                 const int st = s0 + j;
@@ -486,10 +486,12 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
                                          : u32x4{0, 0, 0, 0};
                     acc = Mfma<T>::m16(as_frag<frag>(xa), as_frag<frag>(wr[j][h]), acc);
                 }
-                if (st + PF < nsp) load_w(Wc, st + PF, wr[j]);
-                else if (has_next) load_w(Wn, st + PF - nsp, wr[j]);
+                load_w(nrow, nst0 + j, live, wr[j]);
             }
-        }
+        };
+        int s0 = 0;
+        for (; s0 + PF < nsp; s0 += PF) steps(s0, Wc, s0 + PF, true);
+        steps(s0, Wn, 0, has_next);               // the last PF steps prefetch the next group's first
         // acc[i]: x row 4 * cq + i, output n.  Waves summed in wave order.
 #pragma unroll
         for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
@@ -699,6 +701,8 @@ extern "C" int kuiops_decode_rows_batched(
     // wide kernel takes 17..64 rows of plain x read from L2
     const bool wide = M > 16 || (int64_t)M * K * 2 > kDecMaxLds;
     if (wide ? (x_kind != kXPlain || in_row) : (int64_t)M * K * 2 > kDecMaxLds) return KUIOPS_E_UNSUPPORTED;
+    // the staged kernel addresses W by 32-bit buffer offsets
+    if (!wide && N > 0 && ((N - 1) * ldw + K) * 2 >= 0x7fffffff) return KUIOPS_E_UNSUPPORTED;
     if (!aligned16(in) || !aligned16(W) || (in_add && !aligned16(in_add)) || (norm_w && !aligned16(norm_w)) ||
         (h_out && !aligned16(h_out)))
         return KUIOPS_E_UNSUPPORTED;
