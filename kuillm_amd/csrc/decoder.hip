@@ -723,12 +723,15 @@ extern "C" int kuiops_decode_rows_batched(
         a.vc = v_cache; a.sv0 = sv[0]; a.sv1 = sv[1]; a.sv2 = sv[2];
     }
     a.cap = cache_cap;
-    // Output groups per work-group: enough work-groups for every CU, each
-    // staging x once for up to 8 groups (one per work-group in the wide
-    // kernel, which stages nothing).
+    // At most one work-group per CU, each staging x once and taking every
+    // G-th output group (one group per work-group in the wide kernel, which
+    // stages nothing).  A second work-group on a CU queues its x loads
+    // behind the first one's W loads and doubles that CU's groups: with 704
+    // groups on 352 work-groups (batch 8 gate|up), 96 CUs carried 4 groups
+    // and staged x 6 us late (17.3 us); 256 work-groups carry at most 3
+    // (13.9 us).
     const int64_t ngroups = out_kind == kOutPlain ? cdiv(N, 16) : cdiv(N / 2, 8);
-    const int64_t gpw = wide ? 1 : std::max<int64_t>(1, std::min<int64_t>(8, ngroups / 256));
-    const int64_t grid = cdiv(ngroups, gpw);
+    const int64_t grid = wide ? ngroups : std::min<int64_t>(ngroups, (int64_t)num_cus());
     if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
     // Waves per work-group: K is split over more waves when the output
     // groups alone would leave CUs idle (N = 2048 is 128 work-groups), as
