@@ -84,7 +84,8 @@ typedef enum kuiops_op {
     KUIOPS_OP_GEMV_SPLITK = 2,
     KUIOPS_OP_SDPA_DECODE = 3,
     KUIOPS_OP_TOPK = 4,
-    KUIOPS_OP_SORT = 5          /* (m, n, 0): rows x row length */
+    KUIOPS_OP_SORT = 5,         /* (m, n, 0): rows x row length */
+    KUIOPS_OP_DECODE_ROWS_BATCHED = 6   /* (M, N, K) */
 } kuiops_op;
 
 KUIOPS_API int kuiops_abi_version(void);
@@ -96,6 +97,7 @@ KUIOPS_API const char *kuiops_status_string(int status);
  *   GEMV_SPLITK:  a = M, b = N, c = K
  *   SDPA_DECODE:  a = batch * q_heads * q_len, b = kv_len, c = head_dim_v
  *   TOPK:         a = rows, b = row length, c = k
+ *   DECODE_ROWS_BATCHED: a = M, b = N, c = K
  * Workspace contents need no initialisation, except GEMV_SPLITK's first
  * 16 KB (arrival counters): zero before the first call, and every call
  * leaves them zero.  Calls that share one workspace must be ordered on one
@@ -631,7 +633,11 @@ KUIOPS_API int kuiops_cat(int n_inputs, const void *const *inputs, const int64_t
  * Input stages (RMSNorm, SwiGLU) and embedding rows need M <= 16 and
  * M * K * 2 <= 140 KiB (x staged in LDS); plain x takes any M <= 64.
  * With x staged (M <= 16), W must span less than 2 GiB.
- * Otherwise KUIOPS_E_UNSUPPORTED.  No reference
+ * Otherwise KUIOPS_E_UNSUPPORTED.  The unstaged (wide) form splits K over
+ * work-groups when given the workspace of
+ * kuiops_query_workspace(KUIOPS_OP_DECODE_ROWS_BATCHED, M, N, K) (fp32
+ * partial sums, summed in split order by a second launch; no
+ * initialisation needed); with none, or less, it runs unsplit.  No reference
  * counterpart: it fuses the mm launcher with the RMSNorm / SwiGLU / rotary /
  * KV-cache cat launches of a batched decode step (infer.py:57-89 generates
  * in batches).                                                              */
@@ -641,7 +647,8 @@ KUIOPS_API int kuiops_decode_rows_batched(int64_t M, int64_t N, int64_t K, int d
                                void *h_out, int64_t ld_h, const void *W, int64_t ldw, void *out, int64_t ld_out,
                                int64_t pair_off, int64_t hq, int64_t hkv, int64_t hd, const float *inv_freq,
                                const int32_t *pos, void *k_cache, const int64_t sk[3], void *v_cache,
-                               const int64_t sv[3], int64_t cache_cap, void *stream);
+                               const int64_t sv[3], int64_t cache_cap, void *workspace,
+                               size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -31,7 +31,7 @@ C_NONE, C_FULL, C_ROW = 0, 1, 2
 EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_NEG, EW_SILU, EW_RSQRT, EW_COS, EW_SIN, EW_EXP, EW_SQRT, EW_POW_SCALAR, \
     EW_EQ, EW_NE, EW_LE, EW_LT, EW_GE, EW_GT, EW_WHERE, EW_BITWISE_NOT, EW_BITWISE_AND, EW_BITWISE_OR = range(22)
 # kuiops_op
-OP_ADDMM, OP_GEMV_SPLITK, OP_SDPA_DECODE, OP_TOPK, OP_SORT = 1, 2, 3, 4, 5
+OP_ADDMM, OP_GEMV_SPLITK, OP_SDPA_DECODE, OP_TOPK, OP_SORT, OP_DECODE_ROWS_BATCHED = 1, 2, 3, 4, 5, 6
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -83,7 +83,7 @@ SIGNATURES = {
     "kuiops_index_multi": (_int, [_i64, _int, _i64p, _i64, _i64, ctypes.POINTER(_vp), _int, _vp, _vp, _vp, _vp]),
     "kuiops_decode_rows_batched": (_int, [_i64, _i64, _i64, _int, _int, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
                                           _flt, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp,
-                                          _vp, _vp, _i64p, _vp, _i64p, _i64, _vp]),
+                                          _vp, _vp, _i64p, _vp, _i64p, _i64, _vp, _sz, _vp]),
     "kuiops_rmsnorm": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _flt, _vp, _i64, _vp]),
     "kuiops_silu_mul": (_int, [_i64, _i64, _int, _vp, _i64, _vp, _i64, _vp]),
     "kuiops_rope_kv_append": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _vp, _vp,

@@ -8,6 +8,7 @@ size_t gemv_workspace_bytes(int64_t M, int64_t N, int64_t K);
 size_t decode_workspace_bytes(int64_t rows, int64_t kv_len, int64_t ev);
 size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 size_t sort_workspace_bytes(int64_t m, int64_t n);
+size_t decode_rows_batched_workspace_bytes(int64_t M, int64_t N, int64_t K);
 }  // namespace kuiops
 
 extern "C" int kuiops_abi_version(void) { return KUIOPS_ABI_VERSION; }
@@ -31,6 +32,7 @@ extern "C" size_t kuiops_query_workspace(int op, int64_t a, int64_t b, int64_t c
         case KUIOPS_OP_SDPA_DECODE: return kuiops::decode_workspace_bytes(a, b, c);
         case KUIOPS_OP_TOPK: return kuiops::topk_workspace_bytes(a, b, c);
         case KUIOPS_OP_SORT: return kuiops::sort_workspace_bytes(a, b);
+        case KUIOPS_OP_DECODE_ROWS_BATCHED: return kuiops::decode_rows_batched_workspace_bytes(a, b, c);
         default: return 0;
     }
 }

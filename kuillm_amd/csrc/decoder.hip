@@ -234,6 +234,8 @@ struct DecMArgs {
     int64_t cap;
     int64_t kq;                              // k per wave, a multiple of 64
     int64_t ldsx;                            // LDS row stride of the staged x rows (elements)
+    float *part;                             // (wide kernel, K split over work-groups) fp32 sums
+    int64_t ks;                              //   [split][group][row][16]; k per split (multiple of 64)
 };
 
 __device__ __forceinline__ int64_t pair_div_m(const DecMArgs &a, int64_t p) {
@@ -517,7 +519,7 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
 // fragment.  A work-group owns GW consecutive 16-output groups, its NW waves
 // split K, the wave sums meet in LDS in wave order and the plain / SwiGLU /
 // rotary epilogues follow.  PF = 2 steps of W and x in flight per wave.
-template <typename T, int OK, int NW, int MB, int GW>
+template <typename T, int OK, int NW, int MB, int GW, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64) void decode_mrows_wide_kernel(DecMArgs a) {
     typedef typename Mfma<T>::frag frag;
     constexpr int PF = 2;
@@ -550,8 +552,11 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_wide_kernel(DecMArgs a) 
         Wr[gi] = reinterpret_cast<const T *>(a.W) + (wvalid ? wrow : 0) * a.ldw;
     }
     const T *X = reinterpret_cast<const T *>(a.in);
-    const int64_t kbeg = (int64_t)wave * a.kq;
-    const int64_t kend = min(a.K, kbeg + a.kq);
+    // (SPLIT: this work-group's K slice is split blockIdx.y)
+    const int64_t kb0 = SPLIT ? (int64_t)blockIdx.y * a.ks : 0;
+    const int64_t kfin = SPLIT ? min(a.K, kb0 + a.ks) : a.K;
+    const int64_t kbeg = kb0 + (int64_t)wave * a.kq;
+    const int64_t kend = min(kfin, kbeg + a.kq);
     const int nsp = (int)(((a.kq / 64) + PF - 1) / PF) * PF;
     u32x4 wr[PF][GW][2], xr[PF][MB][2];
     auto load = [&](int st, int j) __attribute__((always_inline)) {
@@ -610,19 +615,45 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_wide_kernel(DecMArgs a) 
             vals[m][o] = v;
         }
         __syncthreads();
-        if (g0 + gi < ngroups)
-            for (int idx = tid; idx < M * 16; idx += NW * 64)
-                decode_mrows_epilogue<T, OK>(a, g0 + gi, idx >> 4, idx & 15, vals);
+        if (g0 + gi < ngroups) {
+            if constexpr (SPLIT) {
+                float *pp = a.part + (((int64_t)blockIdx.y * ngroups + g0 + gi) * M) * 16;
+                for (int idx = tid; idx < M * 16; idx += NW * 64) pp[idx] = vals[idx >> 4][idx & 15];
+            } else {
+                for (int idx = tid; idx < M * 16; idx += NW * 64)
+                    decode_mrows_epilogue<T, OK>(a, g0 + gi, idx >> 4, idx & 15, vals);
+            }
+        }
     }
 }
 
-template <typename T, int OK, int NW, int GW>
-static void decode_wide_launch2(const DecMArgs &a, unsigned grid, hipStream_t st) {
+// The K splits of decode_mrows_wide_kernel<..., SPLIT>: one work-group per
+// output group sums the splits' fp32 sums in split order and runs the
+// group's epilogue.
+template <typename T, int OK>
+__global__ __launch_bounds__(256) void decode_wide_merge_kernel(DecMArgs a, int splits) {
+    __shared__ float vals[64][17];
+    const int tid = threadIdx.x;
+    const int M = (int)a.M;
+    const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
+    const int64_t g = blockIdx.x;
+    for (int idx = tid; idx < M * 16; idx += 256) {
+        const float *pp = a.part + (g * M) * 16 + idx;
+        float v = pp[0];
+        for (int sp = 1; sp < splits; ++sp) v += pp[(int64_t)sp * ngroups * M * 16];
+        vals[idx >> 4][idx & 15] = v;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < M * 16; idx += 256) decode_mrows_epilogue<T, OK>(a, g, idx >> 4, idx & 15, vals);
+}
+
+template <typename T, int OK, int NW, int GW, bool SPLIT = false>
+static void decode_wide_launch2(const DecMArgs &a, dim3 grid, hipStream_t st) {
     switch ((a.M + 15) / 16) {
-        case 1: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 1, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 2, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
-        case 3: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 3, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
-        default: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 4, GW>), dim3(grid), dim3(NW * 64), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 1, GW, SPLIT>), grid, dim3(NW * 64), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 2, GW, SPLIT>), grid, dim3(NW * 64), 0, st, a); break;
+        case 3: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 3, GW, SPLIT>), grid, dim3(NW * 64), 0, st, a); break;
+        default: hipLaunchKernelGGL((decode_mrows_wide_kernel<T, OK, NW, 4, GW, SPLIT>), grid, dim3(NW * 64), 0, st, a); break;
     }
 }
 
@@ -630,23 +661,57 @@ static void decode_wide_launch2(const DecMArgs &a, unsigned grid, hipStream_t st
 // waves per work-group (K split), within the registers of a lane:
 // (GW, NW) = (4, 4) or (1, 16).
 template <typename T, int OK>
-static void decode_wide_launch1(const DecMArgs &a, int gw, unsigned grid, hipStream_t st) {
-    if (gw == 4) decode_wide_launch2<T, OK, 4, 4>(a, grid, st);
-    else decode_wide_launch2<T, OK, 16, 1>(a, grid, st);
+static void decode_wide_launch1(const DecMArgs &a, int gw, unsigned grid, int splits, hipStream_t st) {
+    if (splits > 1) {
+        // K split over grid.y work-groups (4 groups x 4 waves each), then the merge
+        decode_wide_launch2<T, OK, 4, 4, true>(a, dim3(grid, (unsigned)splits), st);
+        const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
+        hipLaunchKernelGGL((decode_wide_merge_kernel<T, OK>), dim3((unsigned)ngroups), dim3(256), 0, st, a, splits);
+    } else if (gw == 4) {
+        decode_wide_launch2<T, OK, 4, 4>(a, dim3(grid), st);
+    } else {
+        decode_wide_launch2<T, OK, 16, 1>(a, dim3(grid), st);
+    }
 }
 
 template <typename T>
-static void decode_wide_launch(const DecMArgs &a, int out_kind, int gw, unsigned grid, hipStream_t st) {
+static void decode_wide_launch(const DecMArgs &a, int out_kind, int gw, unsigned grid, int splits, hipStream_t st) {
     switch (out_kind) {
-        case kOutPlain: decode_wide_launch1<T, kOutPlain>(a, gw, grid, st); break;
-        case kOutSwiGlu: decode_wide_launch1<T, kOutSwiGlu>(a, gw, grid, st); break;
-        default: decode_wide_launch1<T, kOutRope>(a, gw, grid, st); break;
+        case kOutPlain: decode_wide_launch1<T, kOutPlain>(a, gw, grid, splits, st); break;
+        case kOutSwiGlu: decode_wide_launch1<T, kOutSwiGlu>(a, gw, grid, splits, st); break;
+        default: decode_wide_launch1<T, kOutRope>(a, gw, grid, splits, st); break;
     }
 }
 
 // dynamic LDS for the staged rows of x; with the 17 KiB of static reduction
 // arrays of 16 waves it stays within the CU's 160 KiB
 constexpr int64_t kDecMaxLds = 140 * 1024;
+
+// K split of the wide kernel over work-groups, for K >= 4096: 4 output
+// groups per work-group (x read once per 64 outputs) and enough K slices (of
+// at least 256 k, at most 16) for about one work-group per CU, so each
+// work-group reads only its slice of x.  Measured at M = 64 with cold W:
+// 2048 x 5632 (down) 32.0 -> 24.1 us (25.7 at half the slices, 35.7 at
+// twice); at K = 2048 the merge launch outweighs it (11264 x 2048: 27.2 ->
+// 35.3 us, 2048 x 2048: 12.2 -> 19.3 us), so those stay unsplit.
+struct WideSplit { int64_t splits, ks; };
+static WideSplit wide_split_plan(int64_t ngroups, int64_t K) {
+    if (K < 4096) return {1, K};
+    const int64_t ngs = cdiv(ngroups, 4);
+    const int64_t sp = std::max<int64_t>(1, std::min<int64_t>({(int64_t)16, K / 256, cdiv((int64_t)num_cus(), ngs)}));
+    const int64_t ks = cdiv(cdiv(K, sp), 64) * 64;
+    return {cdiv(K, ks), ks};
+}
+// Workspace of kuiops_decode_rows_batched (the wide kernel's K split).
+size_t decode_rows_batched_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || M > 64) return 0;
+    const bool wide = M > 16 || M * K * 2 > kDecMaxLds;
+    if (!wide) return 0;
+    const int64_t ngroups = cdiv(N, 16);
+    const WideSplit p = wide_split_plan(ngroups, K);
+    return p.splits > 1 ? (size_t)(p.splits * ngroups * M * 16 * sizeof(float)) : 0;
+}
+
 
 template <typename T, int XK, int OK, int NW>
 static hipError_t decode_mrows_launch1(const DecMArgs &a, unsigned grid, size_t lds, hipStream_t st) {
@@ -686,7 +751,8 @@ extern "C" int kuiops_decode_rows_batched(
     const int64_t *in_row, int64_t in_rows, const void *in_add, int64_t ld_add, const void *norm_w, float eps,
     void *h_out, int64_t ld_h, const void *W, int64_t ldw, void *out, int64_t ld_out, int64_t pair_off,
     int64_t hq, int64_t hkv, int64_t hd, const float *inv_freq, const int32_t *pos, void *k_cache,
-    const int64_t sk[3], void *v_cache, const int64_t sv[3], int64_t cache_cap, void *stream) {
+    const int64_t sk[3], void *v_cache, const int64_t sv[3], int64_t cache_cap, void *workspace,
+    size_t workspace_bytes, void *stream) {
     if (M < 0 || N < 0 || K < 0) return KUIOPS_E_INVALID;
     if (x_kind != kXPlain && x_kind != kXRmsNorm && x_kind != kXSwiGlu) return KUIOPS_E_INVALID;
     if (out_kind != kOutPlain && out_kind != kOutSwiGlu && out_kind != kOutRope) return KUIOPS_E_INVALID;
@@ -759,12 +825,25 @@ extern "C" int kuiops_decode_rows_batched(
         // 4 groups against 32.5 / 22.5 (2) and 37.7 / 25.2 (1); 32000 x 2048
         // 50.8 / 37.1 against 93.4 / 62.6; 2048-output shapes are fastest
         // with 1 group (2048 x 5632: 31.5 against 55.1 with 4).
+        // With a workspace, K is split over work-groups instead (each reads
+        // only its slice of x; see wide_split_plan).
+        const WideSplit sp = wide_split_plan(ngroups, K);
+        const size_t need = sp.splits > 1 ? (size_t)(sp.splits * ngroups * M * 16 * sizeof(float)) : 0;
+        if (need > 0 && workspace && workspace_bytes >= need && aligned16(workspace)) {
+            a.part = static_cast<float *>(workspace);
+            a.ks = sp.ks;
+            a.kq = cdiv(cdiv(sp.ks, 4), 64) * 64;
+            const unsigned sgrid = (unsigned)cdiv(ngroups, 4);
+            if (dtype == KUIOPS_BF16) decode_wide_launch<bf16_t>(a, out_kind, 4, sgrid, (int)sp.splits, st);
+            else decode_wide_launch<f16_t>(a, out_kind, 4, sgrid, (int)sp.splits, st);
+            return launch_status();
+        }
         const int gw = ngroups >= 512 ? 4 : 1;
         const int wnw = gw == 4 ? 4 : 16;
         a.kq = cdiv(cdiv(K, wnw), 64) * 64;
         const unsigned wgrid = (unsigned)cdiv(ngroups, gw);
-        if (dtype == KUIOPS_BF16) decode_wide_launch<bf16_t>(a, out_kind, gw, wgrid, st);
-        else decode_wide_launch<f16_t>(a, out_kind, gw, wgrid, st);
+        if (dtype == KUIOPS_BF16) decode_wide_launch<bf16_t>(a, out_kind, gw, wgrid, 1, st);
+        else decode_wide_launch<f16_t>(a, out_kind, gw, wgrid, 1, st);
         return launch_status();
     }
     hipError_t err;

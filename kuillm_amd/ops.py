@@ -1125,7 +1125,7 @@ _OUT_KIND = {"plain": 0, "swiglu": 1, "rope": 2}
 
 def decode_rows_batched(x, W, x_kind="plain", out_kind="plain", in_add=None, norm_w=None, eps=1e-5,
                         h_out=None, out=None, row=None, pair_off=0, hq=0, hkv=0, hd=0, inv_freq=None,
-                        pos=None, k_cache=None, v_cache=None):
+                        pos=None, k_cache=None, v_cache=None, split=True):
     """Batched (M <= 16 rows) decode projection with the fused input stage and
     epilogue of ``decode_linear`` / ``decode_gate_up`` / ``decode_qkv_rope``
     (one launch; see kuiops_decode_rows_batched).  W is an nn.Linear weight
@@ -1133,7 +1133,9 @@ def decode_rows_batched(x, W, x_kind="plain", out_kind="plain", in_add=None, nor
     [rows, K] table read at the device rows ``row`` (int64 [M]).
     ``out_kind``: ``plain`` -> out [M, N]; ``swiglu`` (rows p, p + pair_off)
     -> out [M, pair_off]; ``rope`` (fused [q; k; v] heads) -> q into out
-    [M, hq * hd], k / v into the caches [M, hkv, capacity, hd] at pos[m]."""
+    [M, hq * hd], k / v into the caches [M, hkv, capacity, hd] at pos[m].
+    ``split``: give the unstaged (17..64-row) form its workspace, so it
+    splits K over work-groups (False: one pass, no workspace)."""
     N, K = W.shape
     if x.dtype != W.dtype or W.stride(1) != 1 or x.stride(-1) != 1 or x.dim() != 2:
         raise _lib.KuiopsError("decode_rows_batched", _lib.E_INVALID)
@@ -1167,10 +1169,13 @@ def decode_rows_batched(x, W, x_kind="plain", out_kind="plain", in_add=None, nor
     elif out_kind == "swiglu":
         pair_off = N // 2
     lib = _lib_handle()
+    ws_bytes = lib.kuiops_query_workspace(_lib.OP_DECODE_ROWS_BATCHED, M, N, K) if split else 0
+    ws = workspace(x.device, ws_bytes, "decode_rows") if ws_bytes else None
     _lib.check("kuiops_decode_rows_batched", lib.kuiops_decode_rows_batched(
         M, N, K, _dt(x.dtype), _X_KIND[x_kind], _OUT_KIND[out_kind], x.data_ptr(), x.stride(0), _ptr(row), rows,
         _ptr(in_add), in_add.stride(0) if in_add is not None else 0, _ptr(norm_w), float(eps), _ptr(h_out),
         h_out.stride(0) if h_out is not None else 0, W.data_ptr(), W.stride(0), out.data_ptr(), out.stride(0),
         int(pair_off), int(hq), int(hkv), int(hd), _ptr(inv_freq), _ptr(pos),
-        _ptr(k_cache), sk, _ptr(v_cache), sv, k_cache.shape[2] if k_cache is not None else 0, _stream(x.device)))
+        _ptr(k_cache), sk, _ptr(v_cache), sv, k_cache.shape[2] if k_cache is not None else 0,
+        _ptr(ws), ws.numel() if ws is not None else 0, _stream(x.device)))
     return out

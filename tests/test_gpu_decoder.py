@@ -487,6 +487,24 @@ def test_decode_rows_batched_wide_epilogues(cuda, M):
     assert not kc1[0].any() and not vc1[0].any()
 
 
+@pytest.mark.parametrize("M", [17, 64])
+@pytest.mark.parametrize("out_kind", ["plain", "swiglu"])
+def test_decode_rows_batched_wide_k_split(cuda, M, out_kind):
+    """The unstaged form with K split over work-groups (K >= 4096, fp32
+    partials summed in split order by a second launch) against the same call
+    in one pass and the one-row projection; repeated calls are bitwise equal."""
+    K, N = 5632, 2048
+    x = bf((M, K), 140 + M).to(cuda)
+    W = bf((N, K), 141, 0.02).to(cuda)
+    ref, _ = _ref_rows(x, W, "plain")
+    s1 = ops.decode_rows_batched(x, W, "plain", out_kind)
+    s2 = ops.decode_rows_batched(x, W, "plain", out_kind)
+    one = ops.decode_rows_batched(x, W, "plain", out_kind, split=False)
+    assert torch.equal(s1, s2)
+    close(f(s1), f(one), 2e-2)
+    close(f(s1), f(ref if out_kind == "plain" else ops.silu_mul(ref)), 2e-2)
+
+
 @pytest.mark.parametrize("batch", [24, 64])
 def test_wide_decode_step_matches_unfused(cuda, batch):
     """The wide batched decode step (separate RMSNorm, projections on the
