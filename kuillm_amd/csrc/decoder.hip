@@ -283,7 +283,7 @@ __device__ __forceinline__ void decode_mrows_epilogue(const DecMArgs &a, int64_t
     }
 }
 
-template <typename T, int XK, int OK, int NW>
+template <typename T, int XK, int OK, int NW, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     typedef typename Mfma<T>::frag frag;
     constexpr int PF = 32 / NW;                       // 64-k steps in flight per wave (64 KB per work-group)
@@ -320,17 +320,21 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
     };
     // every wave runs the same padded step count (steps past its K range
     // load nothing), so group boundaries line up for the barriers
+    // (SPLIT, plain x only: this work-group's K slice is split blockIdx.y;
+    // k below counts from the slice's start, x is staged for the slice)
+    const int64_t kb0 = SPLIT ? (int64_t)blockIdx.y * a.ks : 0;
+    const int64_t klen = SPLIT ? min(a.K - kb0, a.ks) : a.K;
     const int64_t kbeg = (int64_t)wave * a.kq;
-    const int64_t kend = min(a.K, kbeg + a.kq);
+    const int64_t kend = min(klen, kbeg + a.kq);
     const int nsp = (int)(((a.kq / 64) + PF - 1) / PF) * PF;
     // ---- input stage: wave w normalises rows w, w + NW, ... into LDS.  A
     // lane issues XB chunk loads (and their residual / up halves) before it
     // uses any, so a row costs one memory round trip per 64 * XB chunks.
     constexpr int XB = 4;
-    const int nch = (int)(a.K / 8);
+    const int nch = (int)(klen / 8);
     const T *addp = reinterpret_cast<const T *>(a.in_add);
     auto x_row = [&](int m) __attribute__((always_inline)) {
-        return reinterpret_cast<const T *>(a.in) +
+        return reinterpret_cast<const T *>(a.in) + kb0 +
                (a.in_row ? max((int64_t)0, min(a.in_row[m], a.in_rows - 1)) : (int64_t)m) * a.ld_in;
     };
     // (every load is issued, from chunk 0 when the chunk is past the row or
@@ -417,7 +421,8 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const bool ok = live && k + 32 * h < kend;
-            dst[h] = __builtin_amdgcn_raw_buffer_load_b128(rsW, ok ? wrow + (uint32_t)((k + 32 * h) * 2) : 0x80000000u, 0, 0);
+            dst[h] = __builtin_amdgcn_raw_buffer_load_b128(rsW, ok ? wrow + (uint32_t)((kb0 + k + 32 * h) * 2) : 0x80000000u,
+                                                           0, 0);
         }
     };
     const int64_t G = gridDim.x;
@@ -507,7 +512,12 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_kernel(DecMArgs a) {
             vals[m][o] = v;
         }
         __syncthreads();
-        if (tid < 256 && (tid >> 4) < M) decode_mrows_epilogue<T, OK>(a, g, tid >> 4, tid & 15, vals);
+        if (tid < 256 && (tid >> 4) < M) {
+            if constexpr (SPLIT)
+                a.part[(((int64_t)blockIdx.y * ngroups + g) * M) * 16 + tid] = vals[tid >> 4][tid & 15];
+            else
+                decode_mrows_epilogue<T, OK>(a, g, tid >> 4, tid & 15, vals);
+        }
         Wc = Wn;
     }
 }
@@ -628,8 +638,10 @@ __global__ __launch_bounds__(NW * 64) void decode_mrows_wide_kernel(DecMArgs a) 
 }
 
 // The K splits of decode_mrows_wide_kernel<..., SPLIT>: one work-group per
-// output group sums the splits' fp32 sums in split order and runs the
-// group's epilogue.
+// output group and 16 rows, one thread per (row, output); a thread loads
+// all its splits' sums before adding them in split order, then the group's
+// epilogue runs for those rows.
+constexpr int kMaxWideSplits = 16;
 template <typename T, int OK>
 __global__ __launch_bounds__(256) void decode_wide_merge_kernel(DecMArgs a, int splits) {
     __shared__ float vals[64][17];
@@ -637,14 +649,21 @@ __global__ __launch_bounds__(256) void decode_wide_merge_kernel(DecMArgs a, int 
     const int M = (int)a.M;
     const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
     const int64_t g = blockIdx.x;
-    for (int idx = tid; idx < M * 16; idx += 256) {
-        const float *pp = a.part + (g * M) * 16 + idx;
-        float v = pp[0];
-        for (int sp = 1; sp < splits; ++sp) v += pp[(int64_t)sp * ngroups * M * 16];
-        vals[idx >> 4][idx & 15] = v;
+    const int m = (int)blockIdx.y * 16 + (tid >> 4), o = tid & 15;
+    if (m < M) {
+        const float *pp = a.part + (g * M + m) * 16 + o;
+        const int64_t stride = ngroups * M * 16;
+        float p[kMaxWideSplits];
+#pragma unroll
+        for (int sp = 0; sp < kMaxWideSplits; ++sp) p[sp] = sp < splits ? pp[sp * stride] : 0.f;
+        float v = p[0];
+#pragma unroll
+        for (int sp = 1; sp < kMaxWideSplits; ++sp)
+            if (sp < splits) v += p[sp];
+        vals[m][o] = v;
     }
     __syncthreads();
-    for (int idx = tid; idx < M * 16; idx += 256) decode_mrows_epilogue<T, OK>(a, g, idx >> 4, idx & 15, vals);
+    if (m < M) decode_mrows_epilogue<T, OK>(a, g, m, o, vals);
 }
 
 template <typename T, int OK, int NW, int GW, bool SPLIT = false>
@@ -666,7 +685,8 @@ static void decode_wide_launch1(const DecMArgs &a, int gw, unsigned grid, int sp
         // K split over grid.y work-groups (4 groups x 4 waves each), then the merge
         decode_wide_launch2<T, OK, 4, 4, true>(a, dim3(grid, (unsigned)splits), st);
         const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
-        hipLaunchKernelGGL((decode_wide_merge_kernel<T, OK>), dim3((unsigned)ngroups), dim3(256), 0, st, a, splits);
+        hipLaunchKernelGGL((decode_wide_merge_kernel<T, OK>), dim3((unsigned)ngroups, (unsigned)((a.M + 15) / 16)),
+                           dim3(256), 0, st, a, splits);
     } else if (gw == 4) {
         decode_wide_launch2<T, OK, 4, 4>(a, dim3(grid), st);
     } else {
@@ -698,38 +718,64 @@ struct WideSplit { int64_t splits, ks; };
 static WideSplit wide_split_plan(int64_t ngroups, int64_t K) {
     if (K < 4096) return {1, K};
     const int64_t ngs = cdiv(ngroups, 4);
-    const int64_t sp = std::max<int64_t>(1, std::min<int64_t>({(int64_t)16, K / 256, cdiv((int64_t)num_cus(), ngs)}));
+    const int64_t sp = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kMaxWideSplits, K / 256, cdiv((int64_t)num_cus(), ngs)}));
     const int64_t ks = cdiv(cdiv(K, sp), 64) * 64;
     return {cdiv(K, ks), ks};
 }
-// Workspace of kuiops_decode_rows_batched (the wide kernel's K split).
+// K split of the staged kernel (plain x, K >= 4096, fewer output groups than
+// CUs): enough slices for about one work-group per CU.
+static WideSplit staged_split_plan(int64_t ngroups, int64_t K) {
+    if (K < 4096 || ngroups >= num_cus()) return {1, K};
+    const int64_t sp = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kMaxWideSplits, K / 512,
+                                                               cdiv((int64_t)num_cus(), ngroups)}));
+    const int64_t ks = cdiv(cdiv(K, sp), 64) * 64;
+    return {cdiv(K, ks), ks};
+}
+
+// Workspace of kuiops_decode_rows_batched (the K splits; a plain-x bound).
 size_t decode_rows_batched_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || M > 64) return 0;
     const bool wide = M > 16 || M * K * 2 > kDecMaxLds;
-    if (!wide) return 0;
     const int64_t ngroups = cdiv(N, 16);
-    const WideSplit p = wide_split_plan(ngroups, K);
+    const WideSplit p = wide ? wide_split_plan(ngroups, K) : staged_split_plan(ngroups, K);
     return p.splits > 1 ? (size_t)(p.splits * ngroups * M * 16 * sizeof(float)) : 0;
 }
 
 
-template <typename T, int XK, int OK, int NW>
-static hipError_t decode_mrows_launch1(const DecMArgs &a, unsigned grid, size_t lds, hipStream_t st) {
+template <typename T, int XK, int OK, int NW, bool SPLIT = false>
+static hipError_t decode_mrows_launch1(const DecMArgs &a, dim3 grid, size_t lds, hipStream_t st) {
     // more than 64 KB of dynamic LDS has to be allowed per kernel first
     if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_mrows_kernel<T, XK, OK, NW>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecMaxLds);
+        const hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&decode_mrows_kernel<T, XK, OK, NW, SPLIT>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDecMaxLds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((decode_mrows_kernel<T, XK, OK, NW>), dim3(grid), dim3(NW * 64), lds, st, a);
+    hipLaunchKernelGGL((decode_mrows_kernel<T, XK, OK, NW, SPLIT>), grid, dim3(NW * 64), lds, st, a);
+    return hipSuccess;
+}
+
+// Plain x with K split over grid.y work-groups, then the split merge.
+template <typename T, int OK>
+static hipError_t decode_mrows_split_launch(const DecMArgs &a, int nw, unsigned grid, int splits, size_t lds,
+                                            hipStream_t st) {
+    const dim3 g(grid, (unsigned)splits);
+    hipError_t e;
+    if (nw == 16) e = decode_mrows_launch1<T, kXPlain, OK, 16, true>(a, g, lds, st);
+    else if (nw == 8) e = decode_mrows_launch1<T, kXPlain, OK, 8, true>(a, g, lds, st);
+    else e = decode_mrows_launch1<T, kXPlain, OK, 4, true>(a, g, lds, st);
+    if (e != hipSuccess) return e;
+    const int64_t ngroups = OK == kOutPlain ? (a.N + 15) / 16 : (a.N / 2 + 7) / 8;
+    hipLaunchKernelGGL((decode_wide_merge_kernel<T, OK>), dim3((unsigned)ngroups, (unsigned)((a.M + 15) / 16)),
+                       dim3(256), 0, st, a, splits);
     return hipSuccess;
 }
 
 template <typename T, int XK, int OK>
 static hipError_t decode_mrows_launch2(const DecMArgs &a, int nw, unsigned grid, size_t lds, hipStream_t st) {
-    if (nw == 16) return decode_mrows_launch1<T, XK, OK, 16>(a, grid, lds, st);
-    if (nw == 8) return decode_mrows_launch1<T, XK, OK, 8>(a, grid, lds, st);
-    return decode_mrows_launch1<T, XK, OK, 4>(a, grid, lds, st);
+    if (nw == 16) return decode_mrows_launch1<T, XK, OK, 16>(a, dim3(grid), lds, st);
+    if (nw == 8) return decode_mrows_launch1<T, XK, OK, 8>(a, dim3(grid), lds, st);
+    return decode_mrows_launch1<T, XK, OK, 4>(a, dim3(grid), lds, st);
 }
 
 template <typename T, int XK>
@@ -799,6 +845,40 @@ extern "C" int kuiops_decode_rows_batched(
     const int64_t ngroups = out_kind == kOutPlain ? cdiv(N, 16) : cdiv(N / 2, 8);
     const int64_t grid = wide ? ngroups : std::min<int64_t>(ngroups, (int64_t)num_cus());
     if (grid > INT32_MAX) return KUIOPS_E_UNSUPPORTED;
+    hipStream_t st = as_stream(stream);
+    if (!wide && x_kind == kXPlain) {
+        // Plain x with K >= 4096 and fewer output groups than CUs (batch
+        // down projection): K split over work-groups, each staging only its
+        // slice of x, when the workspace allows (see staged_split_plan).
+        const WideSplit sp = staged_split_plan(ngroups, K);
+        const size_t need = sp.splits > 1 ? (size_t)(sp.splits * ngroups * M * 16 * sizeof(float)) : 0;
+        if (need > 0 && workspace && workspace_bytes >= need && aligned16(workspace)) {
+            a.part = static_cast<float *>(workspace);
+            a.ks = sp.ks;
+            int snw = 4;
+            while (snw < 16 && grid * sp.splits * snw < 2048 && sp.ks >= (int64_t)snw * 2 * 128) snw *= 2;
+            a.kq = cdiv(cdiv(sp.ks, snw), 64) * 64;
+            a.ldsx = (int64_t)M * (sp.ks + 8) * 2 <= kDecMaxLds ? sp.ks + 8 : sp.ks;
+            const size_t slds = (size_t)M * a.ldsx * 2;
+            hipError_t e;
+            switch (out_kind) {
+                case kOutPlain:
+                    e = dtype == KUIOPS_BF16 ? decode_mrows_split_launch<bf16_t, kOutPlain>(a, snw, (unsigned)grid, (int)sp.splits, slds, st)
+                                             : decode_mrows_split_launch<f16_t, kOutPlain>(a, snw, (unsigned)grid, (int)sp.splits, slds, st);
+                    break;
+                case kOutSwiGlu:
+                    e = dtype == KUIOPS_BF16 ? decode_mrows_split_launch<bf16_t, kOutSwiGlu>(a, snw, (unsigned)grid, (int)sp.splits, slds, st)
+                                             : decode_mrows_split_launch<f16_t, kOutSwiGlu>(a, snw, (unsigned)grid, (int)sp.splits, slds, st);
+                    break;
+                default:
+                    e = dtype == KUIOPS_BF16 ? decode_mrows_split_launch<bf16_t, kOutRope>(a, snw, (unsigned)grid, (int)sp.splits, slds, st)
+                                             : decode_mrows_split_launch<f16_t, kOutRope>(a, snw, (unsigned)grid, (int)sp.splits, slds, st);
+                    break;
+            }
+            if (e != hipSuccess) return KUIOPS_E_HIP;
+            return launch_status();
+        }
+    }
     // Waves per work-group: K is split over more waves when the output
     // groups alone would leave CUs idle (N = 2048 is 128 work-groups), as
     // long as each wave keeps at least two 64-k steps.
@@ -811,7 +891,6 @@ extern "C" int kuiops_decode_rows_batched(
     // one bank group); kept unpadded when the padding would not fit.
     a.ldsx = (int64_t)M * (K + 8) * 2 <= kDecMaxLds ? K + 8 : K;
     const size_t lds = (size_t)M * a.ldsx * 2;
-    hipStream_t st = as_stream(stream);
 #define KUIOPS_DECM(T)                                                                                   \
     switch (x_kind) {                                                                                    \
         case kXPlain: err = decode_mrows_launch<T, kXPlain>(a, out_kind, nw, (unsigned)grid, lds, st); break;     \

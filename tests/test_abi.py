@@ -60,10 +60,12 @@ def test_workspace_queries(lib):
     assert lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, 32, 4096, 128) >= 32 * 32 * 130 * 4
     assert lib.kuiops_query_workspace(99, 1, 1, 1) == 0
     assert lib.kuiops_query_workspace(_lib.OP_ADDMM, -1, 1, 1) == 0
-    # batched decode rows: only the unstaged form with K >= 4096 splits K
+    # batched decode rows: K >= 4096 splits K (staged: only with fewer output
+    # groups than CUs)
     assert lib.kuiops_query_workspace(_lib.OP_DECODE_ROWS_BATCHED, 64, 2048, 5632) > 0
+    assert lib.kuiops_query_workspace(_lib.OP_DECODE_ROWS_BATCHED, 8, 2048, 5632) > 0
     assert lib.kuiops_query_workspace(_lib.OP_DECODE_ROWS_BATCHED, 64, 2048, 2048) == 0
-    assert lib.kuiops_query_workspace(_lib.OP_DECODE_ROWS_BATCHED, 8, 2048, 5632) == 0
+    assert lib.kuiops_query_workspace(_lib.OP_DECODE_ROWS_BATCHED, 8, 2048, 2048) == 0
 
 
 def test_host_side_argument_validation(lib):

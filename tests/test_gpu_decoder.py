@@ -487,12 +487,13 @@ def test_decode_rows_batched_wide_epilogues(cuda, M):
     assert not kc1[0].any() and not vc1[0].any()
 
 
-@pytest.mark.parametrize("M", [17, 64])
+@pytest.mark.parametrize("M", [3, 8, 17, 64])
 @pytest.mark.parametrize("out_kind", ["plain", "swiglu"])
-def test_decode_rows_batched_wide_k_split(cuda, M, out_kind):
-    """The unstaged form with K split over work-groups (K >= 4096, fp32
-    partials summed in split order by a second launch) against the same call
-    in one pass and the one-row projection; repeated calls are bitwise equal."""
+def test_decode_rows_batched_k_split(cuda, M, out_kind):
+    """Plain x with K split over work-groups (K >= 4096; staged slices up to
+    16 rows, the unstaged form above; fp32 partials summed in split order by
+    a second launch) against the same call in one pass and the one-row
+    projection; repeated calls are bitwise equal."""
     K, N = 5632, 2048
     x = bf((M, K), 140 + M).to(cuda)
     W = bf((N, K), 141, 0.02).to(cuda)
