@@ -94,6 +94,9 @@ void fa_fwd_kernel(AttnArgs a) {
     const int G = lane >> 4, qq = lane & 15;
 
     const int nblocks = gridDim.x, bid = blockIdx.x;
+    // (PRIO: the work-groups dispatched second to a CU run one priority level
+    // above the first ones, which otherwise win the age-ordered issue ties)
+    const bool young = PRIO && bid >= nblocks / 2;
     int w = bid;
     if ((nblocks & 7) == 0) w = (bid & 7) * (nblocks >> 3) + (bid >> 3);
     // Work units per (batch, head): one query block each, or (causal, paired)
@@ -290,7 +293,10 @@ void fa_fwd_kernel(AttnArgs a) {
         // and rescale fill its gaps: 2% at causal S=4096.  With one wave per
         // SIMD the priority changes only constrain the schedule (2% slower
         // at S=2048), so that instance has none.
-        if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
+        if constexpr (PRIO) {
+            if (young) __builtin_amdgcn_s_setprio(2);
+            else __builtin_amdgcn_s_setprio(1);
+        }
 #pragma unroll
         for (int kk = 0; kk < KPF - 1; ++kk) load_k(kk, kr[kk]);
 #pragma unroll
@@ -337,7 +343,10 @@ void fa_fwd_kernel(AttnArgs a) {
             if (idx + VPF - 1 < NV) load_v(idx + VPF - 1, vr[(idx + VPF - 1) % VPF]);
             o[dt] = Mfma<T>::m32(vr[idx % VPF], pf, o[dt]);
         }
-        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+        if constexpr (PRIO) {
+            if (young) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        }
     };
 
     // Software pipeline over KV blocks: step j runs the softmax of block j
