@@ -728,11 +728,13 @@ static int launch_decode(AttnArgs a, hipStream_t st) {
     dim3 grid((unsigned)a.splits, (unsigned)(a.hkv * a.row_groups), (unsigned)a.n);
     if (a.splits == 1) {
         // short caches: one work-group per row group streams every key (no
-        // workspace round trip)
+        // workspace round trip).  Four rows take 4-wave work-groups: at 180
+        // VGPRs two of them fit a CU, so batch 64's 512 row groups run in one
+        // round instead of two 8-wave rounds (27 -> ~22 us per layer).
         switch (R) {
             case 1: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 1, 16>), grid, dim3(1024), 0, st, a); break;
             case 2: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 2, 16>), grid, dim3(1024), 0, st, a); break;
-            case 4: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 4, 8>), grid, dim3(512), 0, st, a); break;
+            case 4: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 4, 4>), grid, dim3(256), 0, st, a); break;
             default: hipLaunchKernelGGL((fa_decode_kernel<T, HD, 8, 4>), grid, dim3(256), 0, st, a); break;
         }
         return launch_status();
