@@ -37,6 +37,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
     T *ro = a.res_out ? reinterpret_cast<T *>(a.res_out) + row * a.ldro : nullptr;
     float h[NC][8];
     float ss = 0.f;
+    // the norm weight is loaded with x (one memory round trip, not two)
+    const T *w = reinterpret_cast<const T *>(a.w);
+    u32x4 wr[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int64_t i = ((int64_t)c * 256 + tid) * 8;
+        wr[c] = i < a.n ? *reinterpret_cast<const u32x4 *>(w + i) : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int64_t i = ((int64_t)c * 256 + tid) * 8;
@@ -59,14 +67,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsArgs a) {
     __syncthreads();
     const float tot = (part[0] + part[1]) + (part[2] + part[3]);
     const float inv = rsqrtf(tot / (float)a.n + a.eps);
-    const T *w = reinterpret_cast<const T *>(a.w);
     T *y = reinterpret_cast<T *>(a.y) + row * a.ldy;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int64_t i = ((int64_t)c * 256 + tid) * 8;
         if (i < a.n) {
             float wv[8], o[8];
-            unpack8<T>(*reinterpret_cast<const u32x4 *>(w + i), wv);
+            unpack8<T>(wr[c], wv);
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = wv[e] * rnd<T>(h[c][e] * inv);
             *reinterpret_cast<u32x4 *>(y + i) = pack8f<T>(o);
