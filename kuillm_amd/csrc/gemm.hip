@@ -649,7 +649,8 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
     }
     const uint32_t stepB = BCOL ? (uint32_t)(BK * 2) : (uint32_t)(BK * a.ldb * 2);
     // both K stages of tile t (the tile's operand bases are uniform)
-    auto issue = [&](int t) __attribute__((always_inline)) {
+    // stage st (0 or 1) of tile t
+    auto issue = [&](int t, int st) __attribute__((always_inline)) {
         const int bz = t / per, rr = t - bz * per;
         const int tm = rr / a.tiles_n, tn = rr - tm * a.tiles_n;
         const char *ba = reinterpret_cast<const char *>(reinterpret_cast<const T *>(a.A) + bz * a.stride_a +
@@ -658,12 +659,13 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
                                                         (int64_t)tn * 256 * (BCOL ? a.ldb : 1));
         const __amdgpu_buffer_rsrc_t rsA = make_rsrc(uniform_ptr(ba), 0xffffffffu);
         const __amdgpu_buffer_rsrc_t rsB = make_rsrc(uniform_ptr(bb), 0xffffffffu);
+        if (st == 0) {
 #pragma unroll
-        for (int j = 0; j < DPW; ++j) {
-            dma16_buf(rsA, goffA[j], 0, sA0 + (wave * DPW + j) * 1024);
-            dma16_buf(rsB, goffB[j], 0, sB0 + (wave * DPW + j) * 1024);
-        }
-        if constexpr (NK > 1) {
+            for (int j = 0; j < DPW; ++j) {
+                dma16_buf(rsA, goffA[j], 0, sA0 + (wave * DPW + j) * 1024);
+                dma16_buf(rsB, goffB[j], 0, sB0 + (wave * DPW + j) * 1024);
+            }
+        } else {
 #pragma unroll
             for (int j = 0; j < DPW; ++j) {
                 dma16_buf(rsA, goffA[j], BK * 2, sA1 + (wave * DPW + j) * 1024);
@@ -739,11 +741,18 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
             for (int j = 0; j < TN; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+        // each stage is refilled with the next tile's as soon as every wave
+        // has read it (stage 0 under stage 1's MFMAs)
         compute(sA0, sB0);
-        if constexpr (NK > 1) compute(sA1, sB1);
         __builtin_amdgcn_s_waitcnt(0xc07f);        // this wave's LDS reads are done
-        __builtin_amdgcn_s_barrier();              // (every wave's): the stages are free
-        issue(next);
+        __builtin_amdgcn_s_barrier();              // (every wave's): stage 0 is free
+        issue(next, 0);
+        if constexpr (NK > 1) {
+            compute(sA1, sB1);
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_s_barrier();
+            issue(next, 1);
+        }
         // epilogue: per accumulator row band i, the two 32-row bands (wm =
         // 0, 1) through sOut, then 512-byte row segments to memory
         const int bz = t / per, rr = t - bz * per;
@@ -784,7 +793,8 @@ __global__ __launch_bounds__(512) void gemm_stream_kernel(GemmArgs a, int total_
     };
     // (the host launches at most total_tiles work-groups: pid < total_tiles)
     const int last = total_tiles - 1;
-    issue(pid);
+    issue(pid, 0);
+    if constexpr (NK > 1) issue(pid, 1);
     wait_vmcnt<0>();
     for (int t = pid; t < total_tiles; t += G) {
         wait_vmcnt<NSTORE>();          // this tile's DMA; the previous tile's stores stay in flight
