@@ -626,7 +626,7 @@ static int decode_rows_per_group(int rows_kv) {
 }
 
 // Waves of the single-split kernel (as many as the row state's registers allow).
-static int decode_single_waves(int R) { return R <= 2 ? 16 : (R == 4 ? 8 : 4); }
+static int decode_single_waves(int R) { return R <= 2 ? 16 : 4; }   // the one-split launch's waves
 
 // A cache that one work-group streams in a single step takes a single split
 // (no workspace round trip): keys per step = waves x keys per wave-step.

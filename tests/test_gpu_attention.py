@@ -188,6 +188,8 @@ DECODE = [  # n, hq, hkv, l, s, d
     (1, 16, 4, 1, 384, 128),    # row-wide at head dim 128 (longest)
     (2, 8, 2, 1, 77, 128),
     (1, 4, 4, 1, 1, 64),
+    (64, 32, 8, 1, 300, 64),    # 512 row groups of 4 rows: one split, 4-wave work-groups
+    (70, 32, 8, 1, 520, 64),
 ]
 
 

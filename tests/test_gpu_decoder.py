@@ -506,6 +506,33 @@ def test_decode_rows_batched_k_split(cuda, M, out_kind):
     close(f(s1), f(ref if out_kind == "plain" else ops.silu_mul(ref)), 2e-2)
 
 
+@pytest.mark.parametrize("M", [6, 40])
+def test_decode_rows_batched_k_split_rope(cuda, M):
+    """The rotary + KV-append epilogue after a K split (plain x, K = 4096:
+    staged slices for M <= 16, the unstaged form above) against the same call
+    in one pass: q and both caches, including a position past the capacity."""
+    hq, hkv, hd, cap, K = 8, 2, 64, 24, 4096
+    N = (hq + 2 * hkv) * hd
+    x = bf((M, K), 150 + M).to(cuda)
+    W = bf((N, K), 151, 0.02).to(cuda)
+    inv = torch.from_numpy(O.rope_inv_freq(hd, 10000.0)).to(cuda)
+    posl = [(3 * m + 1) % cap for m in range(M)]
+    posl[0] = cap
+    pos = torch.tensor(posl, dtype=torch.int32, device=cuda)
+    outs = []
+    for split in (True, False):
+        kc = torch.zeros(M, hkv, cap, hd, dtype=torch.bfloat16, device=cuda)
+        vc = kc.clone()
+        q = ops.decode_rows_batched(x, W, "plain", "rope", hq=hq, hkv=hkv, hd=hd, inv_freq=inv, pos=pos,
+                                    k_cache=kc, v_cache=vc, split=split)
+        outs.append((q, kc, vc))
+    for a_, b_ in zip(outs[0], outs[1]):
+        close(f(a_), f(b_), 2e-2)
+    assert not outs[0][1][0].any() and not outs[0][2][0].any()
+    for m in range(1, M):
+        assert outs[0][1][m, :, posl[m]].abs().sum() > 0
+
+
 @pytest.mark.parametrize("batch", [24, 64])
 def test_wide_decode_step_matches_unfused(cuda, batch):
     """The wide batched decode step (separate RMSNorm, projections on the
