@@ -663,7 +663,7 @@ static int64_t decode_chunk_for(int64_t s, int64_t groups) {
 
 // Workspace: split arrival counters (one per work-group row group, at most
 // one per query row; zero between calls), then the split states.
-static size_t decode_counter_bytes(int64_t rows) { return (size_t)cdiv(rows * 4, 256) * 256; }
+static size_t decode_counter_bytes(int64_t rows) { return (size_t)cdiv(rows * 4 * kAttnCounterStride, 256) * 256; }
 
 size_t decode_workspace_bytes(int64_t rows, int64_t kv_len, int64_t ev) {
     const int64_t splits = cdiv(kv_len > 0 ? kv_len : 1, decode_chunk(kv_len));
