@@ -71,10 +71,12 @@ __device__ __forceinline__ void merge_state(float &m1, float &l1, float *o1, flo
 // One work-group of fa_decode_kernel: split `split` of the row group `unit`
 // (KV head * row_groups + row group) of batch entry b.  The query is read
 // first, then every step loads its keys.
-template <typename T, int HD, int R, int NWV = 4, int NB = 4>
+template <typename T, int HD, int R, int NWV = 4, int NB = 4, bool KVFIRST = true>
 __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, int unit, int64_t b) {
     // NB: keys per lane group per step; all K / V loads of a step are issued
-    // before any is used, so a step is one memory round trip.
+    // before any is used, so a step is one memory round trip.  KVFIRST: the
+    // first step's loads are issued with the query's (else after the query
+    // is converted: fewer registers live across the query's arrival).
     constexpr int NT = NWV * 64;
     constexpr int LPK = HD / 8;       // lanes per key (8 d values each)
     constexpr int KPW = 64 / LPK;     // keys per wave step
@@ -113,7 +115,7 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
     auto load_kv = [&](int64_t kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int64_t key = min(kb + j * KPW + kg, kend_cap - 1);    // in-bounds address
+            const int64_t key = min(kb + j * KPW + kg, kend_cap - 1);    // in-bounds address (s = 0: zero strides)
             kr[j] = *reinterpret_cast<const u32x4 *>(Kp + key * a.sk2 + dl * 8);
             vr[j] = *reinterpret_cast<const u32x4 *>(Vp + key * a.sv2 + dl * 8);
         }
@@ -134,6 +136,15 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
                                                         qi * a.sq2 + dl * 8)
                      : u32x4{0, 0, 0, 0};
     }
+    // The first step's K / V loads go out right behind the query's, so the
+    // query's conversion waits for the query alone and the key stream does
+    // not start a memory round trip later (later steps load at the end of
+    // the previous one).  Unconditional (a conditional load makes the
+    // compiler wait for every load before the query is used): addresses are
+    // clamped into the split's keys, and an empty cache (s = 0) is given K / V
+    // pointers into the workspace with zero strides by the host.
+    const int64_t kstep = (int64_t)NWV * KPW * NB;
+    if constexpr (KVFIRST) load_kv(kb0);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int rr = r0 + r;
@@ -147,9 +158,9 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
         last_key[r] = ok ? (a.causal ? s_b - a.l + qi + 1 : s_b) : 0;
     }
 
-    for (int64_t kb = kb0; kb < kend_cap; kb += NWV * KPW * NB) {
+    for (int64_t kb = kb0; kb < kend_cap; kb += kstep) {
         float s[R][NB];
-        load_kv(kb);
+        if constexpr (!KVFIRST) load_kv(kb);
         // keys past the device count are zeroed (their scores are masked
         // below; a zero V keeps a NaN in unused cache rows out of the sum)
 #pragma unroll
@@ -205,6 +216,8 @@ __device__ __forceinline__ void fa_decode_block(const AttnArgs &a, int split, in
                 for (int e = 0; e < 8; ++e) o[r][e] += p[j] * to_f32(vv[e]);
             }
         }
+        if constexpr (KVFIRST)
+            if (kb + kstep < kend_cap) load_kv(kb + kstep);
     }
 
     // Merge the KPW key slots of a wave (lanes with equal dl) by a butterfly
@@ -573,7 +586,7 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_onepass_kernel(AttnArgs a)
     fa_decode_onepass_block<T, HD, NWV, NB>(a, unit, blockIdx.z);
 }
 
-template <typename T, int HD, int R, int NWV = 4, int NB = 4>
+template <typename T, int HD, int R, int NWV = 4, int NB = 4, bool KVFIRST = true>
 __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     // One split, many row groups: work-groups are dispatched round-robin
     // over the 8 XCDs, so consecutive (KV head, row group) units are spread
@@ -581,7 +594,7 @@ __global__ __launch_bounds__(NWV * 64) void fa_decode_kernel(AttnArgs a) {
     // that XCD's L2 after the first read).
     int unit = blockIdx.y;
     if (gridDim.x == 1 && (gridDim.y & 7) == 0) unit = (unit & 7) * (gridDim.y >> 3) + (unit >> 3);
-    fa_decode_block<T, HD, R, NWV, NB>(a, blockIdx.x, unit, blockIdx.z);
+    fa_decode_block<T, HD, R, NWV, NB, KVFIRST>(a, blockIdx.x, unit, blockIdx.z);
 }
 
 }  // namespace kuiops
