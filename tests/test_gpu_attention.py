@@ -204,6 +204,36 @@ def test_sdpa_decode_vs_oracle(cuda, n, hq, hkv, l, s, d):
     assert torch.equal(out, again)
 
 
+def test_sdpa_decode_empty_keys(cuda):
+    """No visible keys.  A batch entry whose device kv_len is 0, on the
+    split kernel over a 4096-key cache (its K / V loads are issued before the
+    key count is known), and s = 0 through the C ABI with non-null K / V
+    pointers: zero outputs and lse = -inf, the other entry unchanged."""
+    from kuillm_amd import _lib
+    q, k, v = gen((2, 32, 1, 128), seed=21), gen((2, 32, 4096, 128), seed=22), gen((2, 32, 4096, 128), seed=23)
+    lens = torch.tensor([0, 4096], dtype=torch.int32, device=cuda)
+    out, lse = ops.sdpa_decode(q.to(cuda), k.to(cuda), v.to(cuda), causal=False, return_lse=True, kv_len=lens)
+    assert not out[0].float().any() and bool(torch.isneginf(lse[0]).all())
+    ref, lref = O.sdpa(npy(q[1:]), npy(k[1:]), npy(v[1:]))
+    close(out[1:], ref)
+    np.testing.assert_allclose(npy(lse[1:]), lref, atol=1e-3, rtol=1e-4)
+
+    lib = ops._lib_handle()
+    q0 = q[:1, :4, :, :64].contiguous().to(cuda)
+    kz = torch.zeros(1, 4, 1, 64, dtype=q0.dtype, device=cuda)
+    o0 = torch.full((1, 4, 1, 64), 7.0, dtype=q0.dtype, device=cuda)
+    l0 = torch.zeros(1, 4, 1, dtype=torch.float32, device=cuda)
+    ws = ops.workspace(q0.device, lib.kuiops_query_workspace(_lib.OP_SDPA_DECODE, 4, 0, 64), "attn")
+    st = _lib.strides3(*kz.stride()[:3])
+    rc = lib.kuiops_sdpa_decode(1, 4, 4, 1, 0, 64, 64, _lib.BF16, q0.data_ptr(), _lib.strides3(*q0.stride()[:3]),
+                                kz.data_ptr(), st, kz.data_ptr(), st, o0.data_ptr(), _lib.strides3(*o0.stride()[:3]),
+                                l0.data_ptr(), 0.125, 0, None,
+                                ws.data_ptr(), ws.numel(), None)
+    torch.cuda.synchronize()
+    assert rc == _lib.OK
+    assert not o0.float().any() and bool(torch.isneginf(l0).all())
+
+
 @pytest.mark.parametrize("l", [1, 2, 4])
 def test_sdpa_decode_bottom_right_causal(cuda, l):
     # KV-cache decode step: the l new queries are the last l positions
