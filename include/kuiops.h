@@ -252,7 +252,9 @@ KUIOPS_API int kuiops_sdpa_general(int64_t n, int64_t hq, int64_t hkv, int64_t l
  * aligned, whose first bytes hold the split arrival counters: they must be
  * zero before the first call and every call leaves them zero (calls that
  * share a workspace must not overlap).  One launch: the last split
- * work-group of each query-row group merges the splits.
+ * work-group of each query-row group merges the splits.  Rows with no
+ * visible key (s = 0, or kv_len[b] = 0) give zero output and lse = -inf;
+ * K / V must still be non-null.  Counters sit 64 bytes apart.
  * Replaces the decode use of the reference sdpa launcher
  * (kuiops/sdpa/wrapper_sdpa.cu.j2:21-30), which has no KV-cache form.     */
 KUIOPS_API int kuiops_sdpa_decode(int64_t n, int64_t hq, int64_t hkv, int64_t l, int64_t s,
