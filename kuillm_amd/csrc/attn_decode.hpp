@@ -475,6 +475,10 @@ __device__ __forceinline__ void fa_decode_onepass_block(const AttnArgs &a, int u
     } else {
         load_q();
     }
+    // the query's load stays ahead of the K / V loads in issue order (the
+    // compiler would hoist them above it), so its wait leaves them in flight
+    // and the scores start as K arrives (batch-8 step 0.779 -> 0.777 ms)
+    if constexpr (!PF) __builtin_amdgcn_sched_barrier(0);
     if constexpr (!PF) load_kv();
     if (PF && fresh >= 0) {
 #pragma unroll
